@@ -1,0 +1,186 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 B1_0 1-bit linear (one MI355X).
+
+Default workload: the B1_0 GEMM at M=4096 (tokens), K=3072, N=12288 on
+synthetic data (activations N(0,1) fp32, random sign words, fp16 scales
+U[0.005, 0.05]), inputs resident in HBM before timing.  One step = one
+B1_0 linear over that batch.  Prints ONE JSON line (rank 0) with the metric,
+the MFMA roofline of the GEMM kernel, the small-M GEMV bandwidth (M=8,
+K=3072, N=18432, weight copies rotated past the 256 MB Infinity Cache) and
+the CPU baseline (the oracle's restatement of the reference AVX2 path) timed
+on this host on a bounded sample.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--all] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT), str(ROOT / "bonsai.cpp_amd")]
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+HEADLINE = (4096, 3072, 12288)
+GEMV = (8, 3072, 18432)
+MALL_BYTES = 256 << 20
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_launches(torch, fn, steps, warmup):
+    """Average GPU time per call (ms) from events on the launch stream, plus
+    the host wall time of the timed region."""
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(s)
+    for i in range(steps):
+        fn(i)
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / steps, wall
+
+
+def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto"):
+    a = synth.device_activations(m, k, 1)
+    w = synth.device_packed_weights(n, k, 2)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ms, wall = time_launches(torch, lambda i: b1.linear(a, w, n, out=y, mode=mode), steps, warmup)
+    flop = 2.0 * m * n * k
+    return {"shape": [m, k, n], "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12,
+            "frac": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "wall_s": wall,
+            "inputs": (a, w)}
+
+
+def bench_gemv(torch, b1, synth, m, k, n, steps, warmup):
+    nbytes = n * (k // 32) * 6
+    copies = max(2, (2 * MALL_BYTES) // nbytes + 1)      # rotate > 2x the MALL
+    ws = [synth.device_packed_weights(n, k, 100 + c) for c in range(copies)]
+    a = synth.device_activations(m, k, 3)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ms, wall = time_launches(torch, lambda i: b1.linear(a, ws[i % copies], n, out=y, mode="gemv"),
+                             steps, warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"shape": [m, k, n], "ms": ms, "us": ms * 1e3, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
+            "packed_bytes": nbytes, "weight_copies": copies, "wall_s": wall}
+
+
+def cpu_baseline(a_dev, w_dev, n, rows, threads, reps=3):
+    """The oracle's AVX2 restatement of src/b1_0_kernel.h:79-239 (ggml row
+    split, nth = threads) on the first `rows` rows of the same device inputs
+    the GPU leg timed (copied to host)."""
+    import numpy as np
+    from oracle import b1_oracle as o
+    k = a_dev.shape[1]
+    act = a_dev[:rows].cpu().numpy()
+    raw = w_dev.cpu().numpy().reshape(n, -1)
+    o.linear(act[:4], raw, n, variant="avx2", nth=threads, nthreads=threads)   # warm-up
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        o.linear(act, raw, n, variant="avx2", nth=threads, nthreads=threads)
+        ts.append(time.perf_counter() - t0)
+    dt = float(np.median(ts))
+    return 2.0 * rows * n * k / dt / 1e12, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--all", action="store_true", help="also time the other config shapes (stderr)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the B1_0 linear is built and timed on a single "
+              "MI355X; multi-GPU sharding is design-only (see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import bonsai_b1 as b1
+    from bonsai_b1 import synth
+    b1.load()
+    torch.cuda.init()
+
+    m, k, n = HEADLINE
+    log(f"[bench] GEMM M={m} K={k} N={n} steps={args.steps} warmup={args.warmup}")
+    g = bench_gemm(torch, b1, synth, m, k, n, args.steps, args.warmup)
+    log(f"[bench] GEMM {g['ms']*1e3:.1f} us  {g['tflops']:.1f} TFLOP/s  {100*g['frac']:.1f}% of fp16 MFMA peak")
+
+    gm, gk, gn = GEMV
+    log(f"[bench] GEMV M={gm} K={gk} N={gn}")
+    v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), args.warmup)
+    log(f"[bench] GEMV {v['us']:.2f} us/call  {v['gbs']:.0f} GB/s packed  {100*v['frac']:.1f}% of HBM peak")
+    v1 = bench_gemv(torch, b1, synth, 1, gk, gn, max(args.steps, 200), args.warmup)
+    log(f"[bench] GEMV M=1 {v1['us']:.2f} us/call  {v1['gbs']:.0f} GB/s packed")
+
+    extra = {}
+    if args.all:
+        for name, shp in [("c1_parity", (256, 3072, 3072)),
+                          ("c3_qkv", (4608, 3072, 9216)), ("c3_out", (4608, 3072, 3072)),
+                          ("c4_up", (4608, 3072, 12288)), ("c4_down", (4608, 12288, 3072)),
+                          ("c5_linear1", (4608, 3072, 21504)), ("c5_linear2", (4608, 15360, 3072))]:
+            r = bench_gemm(torch, b1, synth, *shp, max(10, args.steps // 2), 3)
+            extra[name] = {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 1),
+                           "frac": round(r["frac"], 4)}
+            log(f"[bench] {name} {shp}: {r['ms']*1e3:.1f} us {r['tflops']:.1f} TFLOP/s")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        rows = 256
+        log(f"[bench] CPU baseline: oracle AVX2, {threads} threads, {rows} of {m} rows")
+        tf, dt = cpu_baseline(*g["inputs"], n, rows, threads)
+        cpu = {"value": round(tf, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+               "sample": f"M={rows} of {m} rows, K={k}, N={n}; AVX2 restatement of "
+                         f"src/b1_0_kernel.h:79-239, gcc -O3 -mavx2 -mfma -mf16c -ffp-contract=off, "
+                         f"ggml row split nth={threads}; median of 3 ({dt:.2f} s)"}
+        log(f"[bench] CPU {tf*1e3:.1f} GFLOP/s")
+
+    flop = 2.0 * m * n * k
+    line = {
+        "metric": "B1_0 GEMM TFLOP/s & % roofline at M4096 K3072 N12288; GEMV GB/s % HBM peak",
+        "value": round(g["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16-mfma/fp32-acc",
+        "data": "synthetic (N(0,1) fp32 activations, random B1_0 packed weights)",
+        "config": {"workload": "b1_0_gemm", "M": m, "K": k, "N": n, "mode": "fast",
+                   "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "achieved": round(g["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(g["frac"], 4), "traffic": None,
+                     "algorithmic_flop": flop},
+        "gemv": {"M": gm, "K": gk, "N": gn, "us_per_call": round(v["us"], 3),
+                 "GBps_packed": round(v["gbs"], 1), "frac_hbm": round(v["frac"], 4),
+                 "packed_bytes": v["packed_bytes"], "weight_copies": v["weight_copies"],
+                 "M1_us_per_call": round(v1["us"], 3), "M1_GBps_packed": round(v1["gbs"], 1)},
+        "cpu_baseline": cpu,
+    }
+    if extra:
+        line["configs"] = extra
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,18 @@
+"""Python plumbing over the gfx950 B1_0 linear C ABI (include/bonsai_b1.h).
+
+The compute lives in lib/libbonsai_b1.so (HIP kernels for gfx950); this
+module only passes torch device pointers and the current torch stream to it
+through ctypes.  There is no CPU fallback: if the library is missing or the
+device is not gfx950, calls raise.
+"""
+from .capi import (  # noqa: F401
+    B1Error,
+    MODES,
+    Weights,
+    declared_symbols,
+    library_path,
+    linear,
+    linear_raw,
+    load,
+)
+from . import synth  # noqa: F401

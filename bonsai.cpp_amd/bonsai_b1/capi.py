@@ -1,0 +1,159 @@
+"""ctypes binding of libbonsai_b1.so (declarations in include/bonsai_b1.h)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+_PKG = Path(__file__).resolve().parent.parent          # bonsai.cpp_amd/
+_REPO = _PKG.parent
+_LIB = _PKG / "lib" / "libbonsai_b1.so"
+_HDR = _REPO / "include" / "bonsai_b1.h"
+
+BLOCK_SIZE = 32
+BLOCK_BYTES = 6
+MAGIC = 0x31423142
+
+OK, ERR_ARG, ERR_HIP, ERR_NONFINITE, ERR_DEVICE = 0, 1, 2, 3, 4
+MODES = {"auto": 0, "fast": 1, "exact": 2, "gemm": 3, "gemv": 4}
+
+_lib = None
+
+
+class B1Error(RuntimeError):
+    def __init__(self, status: int, what: str = ""):
+        self.status = status
+        text = load().bonsai_b1_status_string(status).decode()
+        super().__init__(f"{what}: {text} (status {status})" if what else text)
+
+
+class B1LinearUserData(ctypes.Structure):
+    _fields_ = [("magic", ctypes.c_int), ("in_dim", ctypes.c_int), ("out_dim", ctypes.c_int)]
+
+
+class B1WeightsC(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("in_dim", ctypes.c_int), ("out_dim", ctypes.c_int),
+                ("nbytes", ctypes.c_size_t), ("device", ctypes.c_int)]
+
+
+def library_path() -> Path:
+    return _LIB
+
+
+def declared_symbols() -> list[str]:
+    """Every extern "C" function declared in include/bonsai_b1.h."""
+    text = _HDR.read_text()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(bonsai_b1_\w+)\s*\(", text, re.M)))
+
+
+def load():
+    """Load the HIP library (torch first, so both share one HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    import torch  # noqa: F401  -- loads torch's libamdhip64 before ours
+    if not _LIB.exists():
+        raise FileNotFoundError(f"{_LIB} is not built; run __graft_entry__.build() or make -C bonsai.cpp_amd")
+    L = ctypes.CDLL(str(_LIB))
+    vp, i, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    L.bonsai_b1_linear_f32.argtypes = [vp, i64, vp, i, i, i, vp, i64, i, vp, vp]
+    L.bonsai_b1_linear_f32.restype = i
+    L.bonsai_b1_linear.argtypes = [vp, ctypes.POINTER(B1WeightsC), i, vp,
+                                   ctypes.POINTER(B1LinearUserData), i, vp, vp]
+    L.bonsai_b1_linear.restype = i
+    L.bonsai_b1_weights_upload.argtypes = [vp, ctypes.c_size_t, i, i, vp, ctypes.POINTER(B1WeightsC)]
+    L.bonsai_b1_weights_upload.restype = i
+    L.bonsai_b1_weights_free.argtypes = [ctypes.POINTER(B1WeightsC)]
+    L.bonsai_b1_weights_free.restype = i
+    L.bonsai_b1_status_string.argtypes = [i]
+    L.bonsai_b1_status_string.restype = ctypes.c_char_p
+    L.bonsai_b1_version.restype = i
+    L.bonsai_b1_linear_f32_f32.argtypes = [vp, i, i, vp]
+    L.bonsai_b1_linear_f32_f32.restype = None
+    _lib = L
+    return L
+
+
+def _stream_handle(stream):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def linear_raw(act_ptr: int, lda: int, w_ptr: int, in_dim: int, out_dim: int, batch: int,
+               out_ptr: int, ldo: int, mode: str = "auto", nonfinite_ptr: int = 0,
+               stream_handle: int = 0) -> int:
+    """Direct call with raw device pointers; returns the status code."""
+    return load().bonsai_b1_linear_f32(act_ptr, lda, w_ptr, in_dim, out_dim, batch, out_ptr, ldo,
+                                       MODES[mode], nonfinite_ptr or None, stream_handle or None)
+
+
+def linear(act, w_packed, out_dim: int, out=None, mode: str = "auto", nonfinite=None, stream=None):
+    """out[M, N] = B1_0 linear of act[M, K] (fp32, cuda, row stride >= K)
+    with packed weights w_packed (uint8, cuda, N*(K/32)*6 bytes).
+    Returns `out` (allocated if None).  Stream-ordered; does not sync."""
+    import torch
+    if act.dim() != 2 or act.dtype != torch.float32 or not act.is_cuda or act.stride(1) != 1:
+        raise ValueError("act must be a 2-D fp32 cuda tensor with unit column stride")
+    m, k = act.shape
+    if w_packed.dtype != torch.uint8 or not w_packed.is_cuda or not w_packed.is_contiguous():
+        raise ValueError("w_packed must be a contiguous uint8 cuda tensor")
+    if w_packed.numel() != out_dim * (k // BLOCK_SIZE) * BLOCK_BYTES:
+        raise ValueError("w_packed size does not match out_dim * in_dim/32 * 6")
+    if out is None:
+        out = torch.empty((m, out_dim), dtype=torch.float32, device=act.device)
+    if out.dim() != 2 or out.shape[0] != m or out.shape[1] < out_dim or out.stride(1) != 1:
+        raise ValueError("out must be [M, >=N] fp32 with unit column stride")
+    nf = nonfinite.data_ptr() if nonfinite is not None else None
+    st = load().bonsai_b1_linear_f32(act.data_ptr(), act.stride(0), w_packed.data_ptr(), k, out_dim, m,
+                                     out.data_ptr(), out.stride(0), MODES[mode], nf, _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_linear_f32")
+    return out
+
+
+class Weights:
+    """Device-resident packed weights via bonsai_b1_weights_upload."""
+
+    def __init__(self, host_packed, in_dim: int, out_dim: int, stream=None):
+        import numpy as np
+        self._host = np.ascontiguousarray(host_packed, dtype=np.uint8)
+        self.c = B1WeightsC()
+        st = load().bonsai_b1_weights_upload(self._host.ctypes.data, self._host.nbytes, in_dim, out_dim,
+                                             _stream_handle(stream), ctypes.byref(self.c))
+        if st != OK:
+            raise B1Error(st, "bonsai_b1_weights_upload")
+
+    @property
+    def in_dim(self):
+        return self.c.in_dim
+
+    @property
+    def out_dim(self):
+        return self.c.out_dim
+
+    def linear(self, act, out=None, mode: str = "auto", nonfinite=None, stream=None, ud=None):
+        import torch
+        m = act.shape[0]
+        if out is None:
+            out = torch.empty((m, self.out_dim), dtype=torch.float32, device=act.device)
+        if ud is None:
+            ud = B1LinearUserData()
+        nf = nonfinite.data_ptr() if nonfinite is not None else None
+        st = load().bonsai_b1_linear(act.data_ptr(), ctypes.byref(self.c), m, out.data_ptr(), ctypes.byref(ud),
+                                     MODES[mode], nf, _stream_handle(stream))
+        if st != OK:
+            raise B1Error(st, "bonsai_b1_linear")
+        return out
+
+    def free(self):
+        if self.c.data:
+            st = load().bonsai_b1_weights_free(ctypes.byref(self.c))
+            if st != OK:
+                raise B1Error(st, "bonsai_b1_weights_free")
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

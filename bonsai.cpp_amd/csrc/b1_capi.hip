@@ -1,0 +1,224 @@
+// C ABI of the B1_0 linear (declared in include/bonsai_b1.h): argument
+// checks, device checks, kernel dispatch, weight residency and the
+// ggml-style custom-op callback.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "bonsai_b1.h"
+#include "b1_internal.h"
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceInfo {
+    int state = 0; // 0 unknown, 1 usable gfx950, -1 unusable
+    int num_cus = 0;
+    int32_t *cb_counter = nullptr; // non-finite counter for the callback
+};
+
+std::mutex g_mu;
+DeviceInfo g_dev[kMaxDevices];
+
+// Returns the current device's info, probing it once.
+DeviceInfo *current_device(int *dev_out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    if (dev_out) *dev_out = dev;
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceInfo &d = g_dev[dev];
+    if (d.state == 0) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+            d.state = -1;
+        } else {
+            d.state = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+            d.num_cus = prop.multiProcessorCount;
+        }
+    }
+    return d.state == 1 ? &d : nullptr;
+}
+
+int check_args(const float *act, int64_t lda, const void *w, int in_dim,
+               int out_dim, int batch, const float *out, int64_t ldo) {
+    if (in_dim <= 0 || out_dim <= 0 || batch < 0) return BONSAI_B1_ERR_ARG;
+    if (in_dim % BONSAI_B1_BLOCK_SIZE != 0) return BONSAI_B1_ERR_ARG;
+    if (lda < in_dim || ldo < out_dim) return BONSAI_B1_ERR_ARG;
+    if (batch > 0 && (!act || !w || !out)) return BONSAI_B1_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(act) & 3u) || (reinterpret_cast<uintptr_t>(out) & 3u) ||
+        (reinterpret_cast<uintptr_t>(w) & 1u))
+        return BONSAI_B1_ERR_ARG;
+    return BONSAI_B1_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int bonsai_b1_version(void) { return 100; }
+
+const char *bonsai_b1_status_string(int status) {
+    switch (status) {
+    case BONSAI_B1_OK: return "ok";
+    case BONSAI_B1_ERR_ARG: return "invalid argument";
+    case BONSAI_B1_ERR_HIP: return "HIP runtime error";
+    case BONSAI_B1_ERR_NONFINITE: return "non-finite output";
+    case BONSAI_B1_ERR_DEVICE: return "no usable gfx950 device";
+    default: return "unknown status";
+    }
+}
+
+int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
+                         int in_dim, int out_dim, int batch, float *out,
+                         int64_t ldo, int mode, int32_t *nonfinite,
+                         hipStream_t stream) {
+    int st = check_args(act, lda, w, in_dim, out_dim, batch, out, ldo);
+    if (st != BONSAI_B1_OK) return st;
+    if (mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_GEMV) return BONSAI_B1_ERR_ARG;
+    DeviceInfo *dev = current_device(nullptr);
+    if (!dev) return BONSAI_B1_ERR_DEVICE;
+    if (batch == 0) return BONSAI_B1_OK;
+
+    b1::LinearArgs a;
+    a.act = act;
+    a.lda = lda;
+    a.w = static_cast<const uint8_t *>(w);
+    a.K = in_dim;
+    a.N = out_dim;
+    a.M = batch;
+    a.out = out;
+    a.ldo = ldo;
+    a.nonfinite = nonfinite;
+
+    hipError_t e;
+    switch (mode) {
+    case BONSAI_B1_MODE_EXACT:
+        e = b1::launch_exact(a, stream);
+        break;
+    case BONSAI_B1_MODE_GEMM:
+        if (!b1::gemm_supported(a)) return BONSAI_B1_ERR_ARG;
+        e = b1::launch_gemm(a, dev->num_cus, stream);
+        break;
+    case BONSAI_B1_MODE_GEMV:
+        if (!b1::gemv_supported(a)) return BONSAI_B1_ERR_ARG;
+        e = b1::launch_gemv(a, dev->num_cus, stream);
+        break;
+    default: // AUTO, FAST
+        if (b1::gemv_supported(a))
+            e = b1::launch_gemv(a, dev->num_cus, stream);
+        else if (b1::gemm_supported(a))
+            e = b1::launch_gemm(a, dev->num_cus, stream);
+        else
+            e = b1::launch_exact(a, stream); // unaligned / K % 64 != 0
+        break;
+    }
+    return e == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
+}
+
+int bonsai_b1_linear(const float *act, const B1Weights *w, int batch,
+                     float *out, B1LinearUserData *ud, int mode,
+                     int32_t *nonfinite, hipStream_t stream) {
+    if (!w) return BONSAI_B1_ERR_ARG;
+    if (ud) {
+        ud->magic = BONSAI_B1_MAGIC;
+        ud->in_dim = w->in_dim;
+        ud->out_dim = w->out_dim;
+    }
+    return bonsai_b1_linear_f32(act, w->in_dim, w->data, w->in_dim, w->out_dim,
+                                batch, out, w->out_dim, mode, nonfinite, stream);
+}
+
+void bonsai_b1_linear_f32_f32(bonsai_b1_tensor *dst, int ith, int nth,
+                              void *userdata) {
+    (void)nth;
+    if (ith != 0) return;
+    const B1LinearUserData *ud = static_cast<const B1LinearUserData *>(userdata);
+    const bonsai_b1_tensor *act = dst->src[0];
+    const bonsai_b1_tensor *wt = dst->src[1];
+    if (!ud || ud->magic != BONSAI_B1_MAGIC || !act || !wt || !wt->data) {
+        fprintf(stderr, "B1_FATAL: bad custom-op arguments (userdata/src)\n");
+        abort();
+    }
+    const int in_dim = ud->in_dim, out_dim = ud->out_dim;
+    const int batch = (int)act->ne[1];
+    const int64_t lda = act->nb[1] ? (int64_t)(act->nb[1] / sizeof(float)) : in_dim;
+    const int64_t ldo = dst->nb[1] ? (int64_t)(dst->nb[1] / sizeof(float)) : out_dim;
+    int dev = 0;
+    DeviceInfo *di = current_device(&dev);
+    if (!di) {
+        fprintf(stderr, "B1_FATAL: no usable gfx950 device\n");
+        abort();
+    }
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!di->cb_counter && hipMalloc(reinterpret_cast<void **>(&di->cb_counter), sizeof(int32_t)) != hipSuccess) {
+            fprintf(stderr, "B1_FATAL: hipMalloc of the status counter failed\n");
+            abort();
+        }
+    }
+    hipStream_t s = hipStreamPerThread;
+    int32_t bad = 0;
+    int st = hipMemsetAsync(di->cb_counter, 0, sizeof(int32_t), s) == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
+    if (st == BONSAI_B1_OK)
+        st = bonsai_b1_linear_f32(static_cast<const float *>(act->data), lda, wt->data, in_dim, out_dim,
+                                  batch, static_cast<float *>(dst->data), ldo, BONSAI_B1_MODE_AUTO,
+                                  di->cb_counter, s);
+    if (st == BONSAI_B1_OK &&
+        (hipMemcpyAsync(&bad, di->cb_counter, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+         hipStreamSynchronize(s) != hipSuccess))
+        st = BONSAI_B1_ERR_HIP;
+    if (st != BONSAI_B1_OK) {
+        fprintf(stderr, "B1_FATAL: b1_linear failed: %s (in_dim=%d out_dim=%d)\n",
+                bonsai_b1_status_string(st), in_dim, out_dim);
+        abort();
+    }
+    if (bad) {
+        fprintf(stderr, "B1_FATAL_OUT: NaN generated in b1_linear! in_dim=%d out_dim=%d (%d non-finite)\n",
+                in_dim, out_dim, bad);
+        abort();
+    }
+}
+
+int bonsai_b1_weights_upload(const void *host_packed, size_t nbytes,
+                             int in_dim, int out_dim, hipStream_t stream,
+                             B1Weights *out) {
+    if (!out || !host_packed || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE)
+        return BONSAI_B1_ERR_ARG;
+    const size_t want = (size_t)out_dim * (size_t)(in_dim / BONSAI_B1_BLOCK_SIZE) * BONSAI_B1_BLOCK_BYTES;
+    if (nbytes != want) return BONSAI_B1_ERR_ARG;
+    int dev = 0;
+    if (!current_device(&dev)) return BONSAI_B1_ERR_DEVICE;
+    void *d = nullptr;
+    if (hipMalloc(&d, nbytes) != hipSuccess) return BONSAI_B1_ERR_HIP;
+    if (hipMemcpyAsync(d, host_packed, nbytes, hipMemcpyHostToDevice, stream) != hipSuccess) {
+        (void)hipFree(d);
+        return BONSAI_B1_ERR_HIP;
+    }
+    out->data = d;
+    out->in_dim = in_dim;
+    out->out_dim = out_dim;
+    out->nbytes = nbytes;
+    out->device = dev;
+    return BONSAI_B1_OK;
+}
+
+int bonsai_b1_weights_free(B1Weights *w) {
+    if (!w) return BONSAI_B1_ERR_ARG;
+    if (w->data) {
+        int cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess) return BONSAI_B1_ERR_HIP;
+        if (cur != w->device && hipSetDevice(w->device) != hipSuccess) return BONSAI_B1_ERR_HIP;
+        hipError_t e = hipFree(w->data);
+        if (cur != w->device) (void)hipSetDevice(cur);
+        if (e != hipSuccess) return BONSAI_B1_ERR_HIP;
+    }
+    w->data = nullptr;
+    w->nbytes = 0;
+    return BONSAI_B1_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,36 @@
+// Internal launcher interface between the C ABI (b1_capi.hip) and the
+// gfx950 kernels (b1_kernels.hip).  Not installed; no HIP types beyond the
+// stream.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace b1 {
+
+struct LinearArgs {
+    const float *act;   // [M][lda] fp32
+    int64_t lda;        // elements
+    const uint8_t *w;   // packed [N][K/32*6]
+    int K, N, M;
+    float *out;         // [M][ldo] fp32
+    int64_t ldo;        // elements
+    int32_t *nonfinite; // optional device counter
+};
+
+// fp32 VALU kernel in the reference scalar order; any K % 32 == 0.
+hipError_t launch_exact(const LinearArgs &a, hipStream_t s);
+
+// fp16 MFMA GEMM; requires K % 64 == 0, lda % 4 == 0, act 16-byte aligned.
+bool gemm_supported(const LinearArgs &a);
+hipError_t launch_gemm(const LinearArgs &a, int num_cus, hipStream_t s);
+
+// Small-M (M <= 16) bandwidth-bound kernel; requires K % 64 == 0,
+// lda % 4 == 0, act 16-byte aligned.
+bool gemv_supported(const LinearArgs &a);
+hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s);
+
+constexpr int kGemvMaxM = 16;
+
+} // namespace b1

@@ -1,0 +1,462 @@
+// B1_0 1-bit linear kernels for MI355X (gfx950, CDNA4, wave64).
+//
+// Arithmetic being reproduced (src/b1_0_kernel.h:37-288 of the reference):
+//   out[m][n] = sum_blk fp32(scale[n][blk]) *
+//               sum_{i<32} (bit_i ? +a[m][32 blk + i] : -a[m][32 blk + i])
+// Packed block (convert_to_b1_0_packed.py:21-43): bytes 0-1 fp16 scale,
+// bytes 2-5 little-endian u32 sign word; row n starts at byte n*(K/32)*6.
+//
+// Three kernels:
+//  * b1_exact_kernel — fp32 VALU, the reference's scalar summation order
+//    (src/b1_0_kernel.h:253-277) with contraction off: bit-identical output.
+//  * b1_gemm_kernel  — wide-tile MFMA GEMM for large M.  Activations are
+//    converted fp32 -> fp16 while being staged into LDS; each weight block
+//    is expanded in registers to fp16 +-scale (exact: a sign flip of an fp16
+//    value), so the per-block scale rides inside the MFMA operand and no
+//    per-block rescale of fp32 partial sums is needed.
+//  * b1_gemv_kernel  — small M (<= 16): persistent work-groups, split-K over
+//    the waves of a work-group, activations held in registers, packed
+//    weights streamed once from HBM; MFMA 16x16x32 with M padded to 16.
+//
+// K-slot pairing shared by both MFMA kernels.  Inside a 32-element block,
+// fp16 dword d (d = 0..15) holds elements (d, d+16).  On the weight side the
+// two sign bits for dword d are then bits d and d+16 of the sign word, which
+// one left shift by (15 - d) lands on bits 15 and 31 — the two fp16 sign bits
+// — so a single v_bfi_b32 against the replicated scale builds the pair.  The
+// activation side is written in the same pairing when it is packed to fp16.
+// Any consistent permutation of K inside the MFMA leaves the dot product
+// unchanged.  The bit value 1 lands on the fp16 sign, i.e. the expanded
+// weight is -(reference weight); the activations are negated when packed to
+// fp16 so that the product keeps the reference sign.
+#include <hip/hip_runtime.h>
+
+#include "b1_internal.h"
+
+namespace b1 {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kSignPair = 0x80008000u;
+
+// (x & m) | (y & ~m) in one VALU op.  Written as asm because gfx950 VOP3
+// takes no literal and the compiler otherwise emits shift/and/or triples.
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(x), "v"(y));
+    return r;
+}
+
+// (-lo, -hi) -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t neg_pack_f16(float lo, float hi) {
+    float2v v = {-lo, -hi};
+    half2v h = __builtin_convertvector(v, half2v);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ uint32_t dup_lo16(uint32_t d) {
+    return __builtin_amdgcn_perm(d, d, 0x01000100u);
+}
+__device__ __forceinline__ uint32_t dup_hi16(uint32_t d) {
+    return __builtin_amdgcn_perm(d, d, 0x03020302u);
+}
+
+// Weight dword for fp16 pair slot (bits p and p+16 of `w`, p = 15 - sh).
+__device__ __forceinline__ uint32_t wpair(uint32_t w, int sh, uint32_t scale2) {
+    return bfi(kSignPair, w << sh, scale2);
+}
+
+__device__ __forceinline__ void count_nonfinite(int32_t *ctr, int bad) {
+    if (bad && ctr) atomicAdd(ctr, bad);
+}
+
+// ---------------------------------------------------------------- exact --
+
+constexpr int kExTN = 256; // output columns per work-group (one per thread)
+constexpr int kExTM = 4;   // output rows per work-group
+constexpr int kExKC = 256; // K staged in LDS per pass
+
+__global__ __launch_bounds__(kExTN) void b1_exact_kernel(LinearArgs p) {
+#pragma clang fp contract(off)
+    __shared__ float As[kExTM][kExKC];
+    const int n = blockIdx.x * kExTN + threadIdx.x;
+    const int m0 = blockIdx.y * kExTM;
+    const int nb = p.K / 32;
+    const int nrow = n < p.N ? n : p.N - 1;
+    const uint16_t *wr = reinterpret_cast<const uint16_t *>(p.w + (size_t)nrow * nb * 6);
+    float sum[kExTM];
+#pragma unroll
+    for (int r = 0; r < kExTM; ++r) sum[r] = 0.0f;
+
+    for (int kc = 0; kc < p.K; kc += kExKC) {
+        const int klen = min(kExKC, p.K - kc);
+        __syncthreads();
+        for (int i = threadIdx.x; i < kExTM * kExKC; i += kExTN) {
+            const int r = i / kExKC, c = i - r * kExKC;
+            As[r][c] = (m0 + r < p.M && c < klen)
+                           ? p.act[(size_t)(m0 + r) * p.lda + kc + c]
+                           : 0.0f;
+        }
+        __syncthreads();
+        const int nbk = klen / 32;
+        for (int b = 0; b < nbk; ++b) {
+            const uint16_t *blk = wr + (size_t)(kc / 32 + b) * 3;
+            const float scale = (float)__builtin_bit_cast(_Float16, blk[0]);
+            const uint32_t bits = (uint32_t)blk[1] | ((uint32_t)blk[2] << 16);
+#pragma unroll
+            for (int r = 0; r < kExTM; ++r) {
+                float bs = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const float a = As[r][b * 32 + i];
+                    bs = ((bits >> i) & 1u) ? bs + a : bs - a;
+                }
+                sum[r] = sum[r] + scale * bs;
+            }
+        }
+    }
+    if (n >= p.N) return;
+    int bad = 0;
+#pragma unroll
+    for (int r = 0; r < kExTM; ++r) {
+        if (m0 + r < p.M) {
+            bad += !__builtin_isfinite(sum[r]);
+            p.out[(size_t)(m0 + r) * p.ldo + n] = sum[r];
+        }
+    }
+    count_nonfinite(p.nonfinite, bad);
+}
+
+// ----------------------------------------------------------------- gemm --
+
+template <int BM, int BN, int WM, int WN>
+struct GemmCfg {
+    static constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN;
+    static constexpr int NT = NW * 64;
+    static constexpr int MT = WM / 32, NTL = WN / 32; // 32x32 sub-tiles/wave
+    static constexpr int KC = 64;                     // K per stage (2 blocks)
+    static constexpr int ROW = KC * 2 + 16;           // LDS bytes per A row
+    static constexpr int STAGE = BM * ROW;
+    static constexpr int UNITS = BM * 8; // (row, block, quad) staging units
+    static constexpr int UPT = UNITS / NT;
+    static_assert(UNITS % NT == 0, "staging units must divide evenly");
+    static_assert(WM % 32 == 0 && WN % 32 == 0, "32x32 sub-tiles");
+};
+
+// Work-groups are dispatched round-robin over the 8 XCDs (bid % 8).  Give
+// each XCD a contiguous run of tiles (N-fastest) so the work-groups resident
+// on one XCD share activation rows in that XCD's L2.
+__device__ __forceinline__ int xcd_tile(int bid, int nblk) {
+    const int xcd = bid & 7, loc = bid >> 3;
+    const int q = nblk >> 3, r = nblk & 7;
+    return xcd * q + min(xcd, r) + loc;
+}
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_kernel(LinearArgs p, int tiles_n) {
+    using C = GemmCfg<BM, BN, WM, WN>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * C::STAGE];
+
+    const int t = xcd_tile(blockIdx.x, gridDim.x);
+    const int tm = t / tiles_n, tn = t - tm * tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / C::NWN, wn = wave - wm * C::NWN;
+    const int li = lane & 31, g = lane >> 5;
+    const size_t rs = (size_t)(p.K / 32) * 6;
+    const int nstage = p.K / C::KC;
+
+    // ---- activation staging: unit id -> (row, block, quad c) -------------
+    floatx4 ar[C::UPT][2];
+    auto load_a = [&](int ks) {
+#pragma unroll
+        for (int u = 0; u < C::UPT; ++u) {
+            const int id = tid + u * C::NT;
+            const int c = id & 3, blk = (id >> 2) & 1, row = id >> 3;
+            const int gm = m0 + row;
+            if (gm < p.M) {
+                const float *src = p.act + (size_t)gm * p.lda + ks * C::KC + blk * 32 + c * 4;
+                ar[u][0] = *reinterpret_cast<const floatx4 *>(src);
+                ar[u][1] = *reinterpret_cast<const floatx4 *>(src + 16);
+            } else {
+                ar[u][0] = floatx4{0.f, 0.f, 0.f, 0.f};
+                ar[u][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < C::UPT; ++u) {
+            const int id = tid + u * C::NT;
+            const int c = id & 3, blk = (id >> 2) & 1, row = id >> 3;
+            u32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = neg_pack_f16(ar[u][0][j], ar[u][1][j]);
+            *reinterpret_cast<u32x4 *>(lds + buf * C::STAGE + row * C::ROW + blk * 64 + c * 16) = v;
+        }
+    };
+
+    // ---- packed weights: lane column n, 12 bytes (2 blocks) per stage ----
+    uint32_t br[C::NTL][3];
+    const int ncol = n0 + wn * WN + li;
+    auto load_b = [&](int ks) {
+#pragma unroll
+        for (int nt = 0; nt < C::NTL; ++nt) {
+            const int n = ncol + nt * 32;
+            if (n < p.N) {
+                const uint32_t *src = reinterpret_cast<const uint32_t *>(p.w + (size_t)n * rs + (size_t)ks * 12);
+                br[nt][0] = src[0];
+                br[nt][1] = src[1];
+                br[nt][2] = src[2];
+            } else {
+                br[nt][0] = br[nt][1] = br[nt][2] = 0u;
+            }
+        }
+    };
+
+    floatx16 acc[C::MT][C::NTL];
+#pragma unroll
+    for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < C::NTL; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    auto compute = [&](int buf, const uint32_t (&bq)[C::NTL][3]) {
+        const uint8_t *base = lds + buf * C::STAGE + (wm * WM + li) * C::ROW + g * 16;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            uint32_t s2[C::NTL], wg[C::NTL];
+#pragma unroll
+            for (int nt = 0; nt < C::NTL; ++nt) {
+                uint32_t wd;
+                if (b == 0) {
+                    s2[nt] = dup_lo16(bq[nt][0]);
+                    wd = __builtin_amdgcn_alignbit(bq[nt][1], bq[nt][0], 16);
+                } else {
+                    s2[nt] = dup_hi16(bq[nt][1]);
+                    wd = bq[nt][2];
+                }
+                wg[nt] = wd >> (4 * g);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                half8 af[C::MT];
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+                    af[mt] = *reinterpret_cast<const half8 *>(base + mt * 32 * C::ROW + b * 64 + h * 32);
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt) {
+                    u32x4 bd;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) bd[j] = wpair(wg[nt], 15 - 8 * h - j, s2[nt]);
+                    const half8 bf = __builtin_bit_cast(half8, bd);
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt], bf, acc[mt][nt], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    load_a(0);
+    load_b(0);
+    store_a(0);
+    __syncthreads();
+    for (int s = 0; s < nstage; ++s) {
+        uint32_t bc[C::NTL][3];
+#pragma unroll
+        for (int nt = 0; nt < C::NTL; ++nt) {
+            bc[nt][0] = br[nt][0];
+            bc[nt][1] = br[nt][1];
+            bc[nt][2] = br[nt][2];
+        }
+        const bool more = s + 1 < nstage;
+        if (more) {
+            load_a(s + 1);
+            load_b(s + 1);
+        }
+        compute(s & 1, bc);
+        if (more) store_a((s + 1) & 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: 32x32 accumulator layout: lane column li, rows
+    // 8*(v/4) + 4*g + v%4 of each sub-tile ------------------------------
+    int bad = 0;
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < C::NTL; ++nt) {
+            const int n = ncol + nt * 32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + wm * WM + mt * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+                if (m < p.M && n < p.N) {
+                    const float y = acc[mt][nt][v];
+                    bad += !__builtin_isfinite(y);
+                    p.out[(size_t)m * p.ldo + n] = y;
+                }
+            }
+        }
+    }
+    count_nonfinite(p.nonfinite, bad);
+}
+
+// ----------------------------------------------------------------- gemv --
+
+constexpr int kGvWaves = 8;                    // waves per work-group
+constexpr int kGvBPW = 12;                     // blocks per wave per pass
+constexpr int kGvChunk = kGvWaves * kGvBPW;    // blocks per pass (K 3072)
+constexpr int kGvMaxRG = 6;                    // 16-row groups per WG, max
+
+__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, int groups) {
+    __shared__ floatx4 red[kGvWaves][kGvMaxRG][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, g = lane >> 4;
+    const int nwg = gridDim.x, bid = blockIdx.x;
+    const int rg0 = (int)(((int64_t)groups * bid) / nwg);
+    const int rg1 = (int)(((int64_t)groups * (bid + 1)) / nwg);
+    const int nrg = rg1 - rg0;
+    const int nb = p.K / 32;
+    const size_t rs = (size_t)nb * 6;
+    const bool tok_ok = col < p.M;
+    const float *arow = p.act + (size_t)(tok_ok ? col : 0) * p.lda;
+
+    floatx4 acc[kGvMaxRG];
+#pragma unroll
+    for (int r = 0; r < kGvMaxRG; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb0 = 0; kb0 < nb; kb0 += kGvChunk) {
+        const int wb0 = kb0 + wave * kGvBPW;
+        // Activation fragments for this wave's blocks: lane row = token col,
+        // k-slots 8g..8g+7 = dwords 4g..4g+3 of each block.
+        u32x4 af[kGvBPW];
+#pragma unroll
+        for (int b = 0; b < kGvBPW; ++b) {
+            const int blk = wb0 + b;
+            if (tok_ok && blk < nb) {
+                const float *src = arow + blk * 32 + 4 * g;
+                const floatx4 lo = *reinterpret_cast<const floatx4 *>(src);
+                const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + 16);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) af[b][j] = neg_pack_f16(lo[j], hi[j]);
+            } else {
+                af[b] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+
+        // Packed bytes of this wave's 12 blocks of row n: 18 dwords.
+        auto load_row = [&](int r, uint32_t (&d)[kGvBPW * 3 / 2]) {
+            const int n = (rg0 + r) * 16 + col;
+            const uint32_t *src = reinterpret_cast<const uint32_t *>(p.w + (size_t)(n < p.N ? n : 0) * rs + (size_t)wb0 * 6);
+#pragma unroll
+            for (int q = 0; q < kGvBPW / 2; ++q) {
+                if (n < p.N && wb0 + 2 * q < nb) {
+                    d[3 * q] = src[3 * q];
+                    d[3 * q + 1] = src[3 * q + 1];
+                    d[3 * q + 2] = src[3 * q + 2];
+                } else {
+                    d[3 * q] = d[3 * q + 1] = d[3 * q + 2] = 0u;
+                }
+            }
+        };
+
+        uint32_t dcur[kGvBPW * 3 / 2], dnext[kGvBPW * 3 / 2];
+        if (nrg > 0) load_row(0, dcur);
+#pragma unroll
+        for (int r = 0; r < kGvMaxRG; ++r) {
+            if (r < nrg) {
+                if (r + 1 < nrg) load_row(r + 1, dnext);
+#pragma unroll
+                for (int b = 0; b < kGvBPW; ++b) {
+                    if (wb0 + b < nb) {
+                        uint32_t s2, wd;
+                        if ((b & 1) == 0) {
+                            s2 = dup_lo16(dcur[3 * b / 2]);
+                            wd = __builtin_amdgcn_alignbit(dcur[3 * b / 2 + 1], dcur[3 * b / 2], 16);
+                        } else {
+                            s2 = dup_hi16(dcur[(3 * b - 1) / 2]);
+                            wd = dcur[(3 * b + 1) / 2];
+                        }
+                        const uint32_t wg = wd >> (4 * g);
+                        u32x4 bd;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) bd[j] = wpair(wg, 15 - j, s2);
+                        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8, af[b]), __builtin_bit_cast(half8, bd), acc[r], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < kGvBPW * 3 / 2; ++i) dcur[i] = dnext[i];
+            }
+        }
+    }
+
+    // Cross-wave (split-K) reduction in a fixed order, then store.
+#pragma unroll
+    for (int r = 0; r < kGvMaxRG; ++r)
+        if (r < nrg) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    int bad = 0;
+    for (int e = tid; e < nrg * 256; e += kGvWaves * 64) {
+        const int c = e & 15, tok = (e >> 4) & 15, r = e >> 8;
+        const int ln = 16 * (tok >> 2) + c, v = tok & 3;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kGvWaves; ++w) s += red[w][r][ln][v];
+        const int n = (rg0 + r) * 16 + c;
+        if (tok < p.M && n < p.N) {
+            bad += !__builtin_isfinite(s);
+            p.out[(size_t)tok * p.ldo + n] = s;
+        }
+    }
+    count_nonfinite(p.nonfinite, bad);
+}
+
+} // namespace
+
+// ------------------------------------------------------------- launchers --
+
+hipError_t launch_exact(const LinearArgs &a, hipStream_t s) {
+    dim3 grid((a.N + kExTN - 1) / kExTN, (a.M + kExTM - 1) / kExTM);
+    hipLaunchKernelGGL(b1_exact_kernel, grid, dim3(kExTN), 0, s, a);
+    return hipGetLastError();
+}
+
+static bool fast_layout_ok(const LinearArgs &a) {
+    return a.K % 64 == 0 && a.lda % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(a.act) & 15u) == 0 &&
+           (reinterpret_cast<uintptr_t>(a.w) & 3u) == 0;
+}
+
+bool gemm_supported(const LinearArgs &a) { return fast_layout_ok(a); }
+
+hipError_t launch_gemm(const LinearArgs &a, int num_cus, hipStream_t s) {
+    (void)num_cus;
+    constexpr int BM = 128, BN = 512, WM = 128, WN = 64;
+    using C = GemmCfg<BM, BN, WM, WN>;
+    const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
+    hipLaunchKernelGGL((b1_gemm_kernel<BM, BN, WM, WN>), dim3(tiles_m * tiles_n), dim3(C::NT), 0, s, a, tiles_n);
+    return hipGetLastError();
+}
+
+bool gemv_supported(const LinearArgs &a) { return a.M <= kGemvMaxM && fast_layout_ok(a); }
+
+hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
+    const int groups = (a.N + 15) / 16;
+    int nwg = num_cus > 0 ? num_cus : 256;
+    const int need = (groups + kGvMaxRG - 1) / kGvMaxRG;
+    if (nwg < need) nwg = need;
+    if (nwg > groups) nwg = groups;
+    hipLaunchKernelGGL(b1_gemv_kernel, dim3(nwg), dim3(kGvWaves * 64), 0, s, a, groups);
+    return hipGetLastError();
+}
+
+} // namespace b1

@@ -1,0 +1,154 @@
+/*
+ * bonsai_b1.h — C ABI of the MI355X (gfx950) B1_0 1-bit linear.
+ *
+ * Drop-in for the B1_0 weight matmul of Juste-Leo2/bonsai.cpp:
+ *   out[m][n] = sum_blk fp32(scale[n][blk]) *
+ *               sum_{i<32} (bit_i ? +act[m][32*blk+i] : -act[m][32*blk+i])
+ * with the packed layout written by convert_to_b1_0_packed.py:21-43:
+ * rows are N-major, row n starts at byte n*(K/32)*6, and each 32-weight block
+ * is 6 bytes: fp16 scale (little-endian) then the u32 sign word (bit i set ->
+ * +scale for element i, clear -> -scale).
+ *
+ * Everything here is plain C: pointers, sizes and a HIP stream.  Device
+ * pointers are HIP device (or managed) addresses on the current device.
+ * All compute entry points are stream-ordered and never synchronise the host.
+ */
+#ifndef BONSAI_B1_H
+#define BONSAI_B1_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* src/diffuser_types.h:10-11 */
+#define BONSAI_B1_BLOCK_SIZE 32
+#define BONSAI_B1_BLOCK_BYTES 6
+/* src/b1_0_kernel.h:32 — "1B1B", how GPU backends recognise the op */
+#define BONSAI_B1_MAGIC 0x31423142
+
+/* Op descriptor; replaces bonsai::B1LinearUserData (src/b1_0_kernel.h:31-35).
+ * Same field order and sizes: {int magic; int in_dim; int out_dim;}. */
+typedef struct B1LinearUserData {
+    int magic;
+    int in_dim;
+    int out_dim;
+} B1LinearUserData;
+
+/* Device-resident packed weights; replaces bonsai::B1Weights
+ * (src/diffuser_types.h:32-36), whose `data` was a GGML_TYPE_I8 [nbytes,1]
+ * tensor.  Here `data` is a hipMalloc'd buffer of out_dim*(in_dim/32)*6
+ * bytes, 256-byte aligned. */
+typedef struct B1Weights {
+    void *data;
+    int in_dim;
+    int out_dim;
+    size_t nbytes;
+    int device;
+} B1Weights;
+
+/* Status codes.  The reference has none: it abort()s on a non-finite output
+ * (src/b1_0_kernel.h:194-198,230-233,279-282) and leaves its preconditions
+ * unchecked (K % 32 == 0, act->ne[0] == in_dim). */
+enum {
+    BONSAI_B1_OK = 0,
+    BONSAI_B1_ERR_ARG = 1,       /* bad shape, stride, pointer or mode */
+    BONSAI_B1_ERR_HIP = 2,       /* a HIP runtime call failed */
+    BONSAI_B1_ERR_NONFINITE = 3, /* output held NaN/Inf (reference: abort) */
+    BONSAI_B1_ERR_DEVICE = 4     /* no usable gfx950 device */
+};
+
+/* Arithmetic modes.
+ *  AUTO  : FAST numerics; small batches (M <= 16) take the bandwidth-bound
+ *          kernel, larger ones the MFMA GEMM.
+ *  FAST  : activations rounded to fp16 (RNE), weights expanded to exactly
+ *          +-scale in fp16, fp32 MFMA accumulation.  Requires |act| < 65504.
+ *          Per-element error vs the reference <= 1e-2 of max(|y|, rms(y)).
+ *  EXACT : fp32 VALU in the reference's scalar summation order
+ *          (src/b1_0_kernel.h:253-277); bit-identical to that path.
+ *  GEMM / GEMV : FAST numerics with the kernel forced (for benchmarks). */
+enum {
+    BONSAI_B1_MODE_AUTO = 0,
+    BONSAI_B1_MODE_FAST = 1,
+    BONSAI_B1_MODE_EXACT = 2,
+    BONSAI_B1_MODE_GEMM = 3,
+    BONSAI_B1_MODE_GEMV = 4
+};
+
+/*
+ * The B1_0 linear on device buffers; the compute of the reference CPU custom
+ * op b1_linear_f32_f32(dst, ith, nth, userdata) (src/b1_0_kernel.h:37-288),
+ * done for all rows by one stream-ordered launch.
+ *   act      [batch][lda] fp32, rows of in_dim used (reference: src[0], rows
+ *            contiguous with stride in_dim, src/b1_0_kernel.h:103)
+ *   w        packed B1_0 [out_dim][in_dim/32*6] bytes (reference: src[1])
+ *   out      [batch][ldo] fp32, columns [0,out_dim) written
+ *            (reference: out[b*out_dim + r], src/b1_0_kernel.h:200-203)
+ *   nonfinite  optional device int32 counter; every non-finite output adds 1
+ *            (NULL: not counted).  Replaces the reference's abort().
+ * Preconditions checked on the host: in_dim % 32 == 0, in_dim, out_dim > 0,
+ * batch >= 0, lda >= in_dim, ldo >= out_dim, non-NULL pointers.
+ * Returns BONSAI_B1_OK or an error code; never blocks the host.
+ */
+int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
+                         int in_dim, int out_dim, int batch, float *out,
+                         int64_t ldo, int mode, int32_t *nonfinite,
+                         hipStream_t stream);
+
+/*
+ * Builder-style call; replaces bonsai::b1_linear(ctx, act, w, n_threads, ud)
+ * (src/b1_0_kernel.h:290-300): fills ud from w (magic, in_dim, out_dim) and
+ * runs the op for `batch` rows of act (the reference's act->ne[1]).
+ * ud may be NULL.
+ */
+int bonsai_b1_linear(const float *act, const B1Weights *w, int batch,
+                     float *out, B1LinearUserData *ud, int mode,
+                     int32_t *nonfinite, hipStream_t stream);
+
+/*
+ * ggml custom-op callback over a device-side stand-in tensor; same signature
+ * and meaning as the reference's b1_linear_f32_f32 (src/b1_0_kernel.h:37):
+ * dst->src[0] = act, dst->src[1] = packed weights, the userdata holds
+ * {magic, in_dim, out_dim}.  Task ith == 0 runs the whole op on the calling
+ * thread's current stream (hipStreamPerThread) and synchronises it; other
+ * tasks return at once.  Like the reference, a non-finite output prints
+ * "B1_FATAL_OUT" to stderr and abort()s.  Returns nothing.
+ */
+typedef struct bonsai_b1_tensor {
+    int64_t ne[4];                    /* ne[0] = in_dim/out_dim, ne[1] = rows */
+    size_t nb[4];                     /* byte strides; nb[1] = row stride */
+    struct bonsai_b1_tensor *src[2];  /* act, packed weights */
+    void *data;                       /* device pointer */
+} bonsai_b1_tensor;
+
+void bonsai_b1_linear_f32_f32(bonsai_b1_tensor *dst, int ith, int nth,
+                              void *userdata);
+
+/*
+ * Weight residency; replaces load_b1 (src/diffuser.cpp:39-50, memcpy of the
+ * safetensors U8 [out_dim, in_dim/32*6] tensor into a ggml I8 tensor) and the
+ * deferred upload of the WebGPU driver (src/diffuser_webgpu.cpp:49-64,
+ * 246-250).  Allocates device memory on the current device and enqueues the
+ * host->device copy of nbytes on `stream`.  The host buffer must stay valid
+ * until the stream has passed the copy.  nbytes must equal
+ * out_dim*(in_dim/32)*6.
+ */
+int bonsai_b1_weights_upload(const void *host_packed, size_t nbytes,
+                             int in_dim, int out_dim, hipStream_t stream,
+                             B1Weights *out);
+int bonsai_b1_weights_free(B1Weights *w);
+
+/* Human-readable text for a status code (static storage). */
+const char *bonsai_b1_status_string(int status);
+
+/* Library version, major*10000 + minor*100 + patch. */
+int bonsai_b1_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BONSAI_B1_H */

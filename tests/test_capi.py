@@ -1,0 +1,64 @@
+"""Host-side checks of the C ABI library (no GPU compute).
+
+The library must load, export every function include/bonsai_b1.h declares,
+keep the reference's struct layouts, and reject bad arguments before it
+touches the device.
+"""
+import ctypes
+
+import pytest
+
+import bonsai_b1
+from bonsai_b1 import capi
+
+
+def test_library_exports_every_declared_symbol():
+    lib = bonsai_b1.load()
+    names = bonsai_b1.declared_symbols()
+    assert len(names) >= 7
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in include/bonsai_b1.h but not exported"
+
+
+def test_struct_layouts_match_reference():
+    # B1LinearUserData {int magic; int in_dim; int out_dim;} src/b1_0_kernel.h:31-35
+    assert ctypes.sizeof(capi.B1LinearUserData) == 12
+    assert capi.B1LinearUserData.magic.offset == 0
+    assert capi.MAGIC == 0x31423142
+
+
+def test_version_and_status_strings():
+    lib = bonsai_b1.load()
+    assert lib.bonsai_b1_version() >= 100
+    assert lib.bonsai_b1_status_string(0) == b"ok"
+    assert lib.bonsai_b1_status_string(3) == b"non-finite output"
+    assert lib.bonsai_b1_status_string(99) == b"unknown status"
+
+
+@pytest.mark.parametrize("args", [
+    # (lda, in_dim, out_dim, batch, ldo, mode)
+    (64, 63, 32, 1, 32, 0),      # in_dim % 32 != 0 (reference precondition)
+    (64, 0, 32, 1, 32, 0),       # empty in_dim
+    (64, 64, 0, 1, 32, 0),       # empty out_dim
+    (64, 64, 32, -1, 32, 0),     # negative batch
+    (32, 64, 32, 1, 32, 0),      # lda < in_dim
+    (64, 64, 32, 1, 16, 0),      # ldo < out_dim
+    (64, 64, 32, 1, 32, 9),      # unknown mode
+])
+def test_bad_arguments_rejected_before_device(args):
+    lda, k, n, m, ldo, mode = args
+    lib = bonsai_b1.load()
+    fake = 0x10000  # never dereferenced: validation precedes any device call
+    st = lib.bonsai_b1_linear_f32(fake, lda, fake, k, n, m, fake, ldo, mode, None, None)
+    assert st == capi.ERR_ARG
+
+
+def test_null_pointers_rejected():
+    lib = bonsai_b1.load()
+    assert lib.bonsai_b1_linear_f32(None, 64, None, 64, 32, 1, None, 32, 0, None, None) == capi.ERR_ARG
+    w = capi.B1WeightsC()
+    assert lib.bonsai_b1_weights_upload(None, 0, 64, 32, None, ctypes.byref(w)) == capi.ERR_ARG
+    # wrong byte count for the packed layout
+    buf = (ctypes.c_uint8 * 10)()
+    assert lib.bonsai_b1_weights_upload(buf, 10, 64, 32, None, ctypes.byref(w)) == capi.ERR_ARG
+    assert lib.bonsai_b1_weights_free(None) == capi.ERR_ARG

@@ -1,0 +1,286 @@
+"""GPU parity of the gfx950 B1_0 linear against the CPU oracle.
+
+Bars (stated here, used below):
+  EXACT mode  : bit-identical to the oracle's scalar path (the reference's
+                src/b1_0_kernel.h:240-287 summation order).
+  FAST modes  : per element |y - ref| / max(|ref|, rms(ref)) <= 1e-2 and
+                cosine(y, ref) >= 0.9999, ref = fp64 brute force or the
+                oracle's AVX2 path.
+Full-size shapes use size-independent properties (exact scaling by 2,
+exact negation under complemented sign words, sampled rows vs fp64).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL_REL = 1e-2
+TOL_COS = 0.9999
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "GPU tests need the MI355X"
+    return t
+
+
+@pytest.fixture(scope="module")
+def b1(torch):
+    import bonsai_b1
+    bonsai_b1.load()
+    return bonsai_b1
+
+
+def rel_to_rms(y, ref):
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.maximum(np.abs(ref), np.sqrt(np.mean(ref * ref)))
+    return float(np.max(np.abs(np.asarray(y, np.float64) - ref) / den))
+
+
+def cosine(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def assert_fast_close(y, ref, what=""):
+    r, c = rel_to_rms(y, ref), cosine(y, ref)
+    say(f"  {what}: rel_to_rms={r:.3e} cos={c:.8f}")
+    assert r <= TOL_REL, what
+    assert c >= TOL_COS, what
+
+
+def gpu_run(torch, b1, act, raw, n, mode, lda=None, ldo=None, nonfinite=None):
+    m, k = act.shape
+    if lda is None:
+        a = torch.from_numpy(np.ascontiguousarray(act)).cuda()
+    else:
+        big = torch.zeros((m, lda), dtype=torch.float32)
+        big[:, :k] = torch.from_numpy(act)
+        a = big.cuda()[:, :k]
+    w = torch.from_numpy(np.ascontiguousarray(raw).ravel()).cuda()
+    out = None
+    if ldo is not None:
+        out = torch.full((m, ldo), 7.0, dtype=torch.float32, device="cuda")
+    y = b1.linear(a, w, n, out=out, mode=mode, nonfinite=nonfinite)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+# ------------------------------------------------------ golden fixtures ----
+
+def test_golden_exact_bit_exact(torch, b1):
+    from tests.golden import make_golden
+    for name, c in make_golden.load_all().items():
+        say(f"golden exact {name}")
+        y = gpu_run(torch, b1, c["act"], c["w"], int(c["n"]), "exact")
+        assert np.array_equal(y.view(np.uint32), c["y_scalar"].view(np.uint32)), name
+
+
+@pytest.mark.parametrize("mode", ["auto", "gemm", "gemv"])
+def test_golden_fast(torch, b1, mode):
+    from tests.golden import make_golden
+    for name, c in make_golden.load_all().items():
+        m, k = c["act"].shape
+        if mode == "gemv" and (m > 16 or k % 64):
+            continue
+        if mode == "gemm" and k % 64:
+            continue
+        say(f"golden {mode} {name}")
+        y = gpu_run(torch, b1, c["act"], c["w"], int(c["n"]), mode)
+        assert_fast_close(y, c["y_f64"], f"{mode} {name}")
+
+
+# ------------------------------------------------------------ configs ----
+
+def test_c1_parity_config(torch, b1, oracle):
+    """M=256, K=3072, N=3072: EXACT bit-exact vs the scalar oracle; FAST vs
+    the AVX2 oracle (the reference's optimised path)."""
+    from bonsai_b1 import synth
+    m, k, n = 256, 3072, 3072
+    act = synth.activations(m, k, 42)
+    raw = synth.packed_weights(n, k, 43)
+    say("c1 oracle scalar")
+    ys, _ = oracle.linear(act, raw, n, variant="scalar", nth=16, nthreads=16)
+    say("c1 gpu exact")
+    ye = gpu_run(torch, b1, act, raw, n, "exact")
+    assert np.array_equal(ye.view(np.uint32), ys.view(np.uint32))
+    say("c1 oracle avx2")
+    ya, _ = oracle.linear(act, raw, n, variant="avx2", nth=16, nthreads=16)
+    for mode in ("auto", "gemm"):
+        say(f"c1 gpu {mode}")
+        assert_fast_close(gpu_run(torch, b1, act, raw, n, mode), ya, f"c1 {mode}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
+def test_small_m_config(torch, b1, oracle, m):
+    """Small-M GEMV shape: K=3072, N=18432."""
+    from bonsai_b1 import synth
+    k, n = 3072, 18432
+    act = synth.activations(m, k, 100 + m)
+    raw = synth.packed_weights(n, k, 200)
+    ya, _ = oracle.linear(act, raw, n, variant="avx2", nth=16, nthreads=16)
+    for mode in ("gemv", "gemm", "auto"):
+        say(f"small-m M={m} {mode}")
+        assert_fast_close(gpu_run(torch, b1, act, raw, n, mode), ya, f"M={m} {mode}")
+
+
+@pytest.mark.parametrize("shape", [
+    (4096, 3072, 12288),   # headline GEMM
+    (4608, 3072, 9216),    # fused QKV projection
+    (4608, 12288, 3072),   # MLP down projection
+    (4608, 15360, 3072),   # single-stream linear2
+])
+def test_full_size_properties(torch, b1, shape):
+    from bonsai_b1 import synth
+    m, k, n = shape
+    say(f"full-size {shape}")
+    a = synth.device_activations(m, k, 7)
+    w = synth.device_packed_weights(n, k, 8)
+    y = b1.linear(a, w, n, mode="auto")
+    # exact scaling: fp16(2a) = 2 fp16(a) and the fp32 MFMA sums scale exactly
+    y2 = b1.linear(a * 2.0, w, n, mode="auto")
+    assert torch.equal(y2, 2.0 * y)
+    # complemented sign words: every expanded weight flips sign exactly
+    wc = w.view(n, k // 32, 6).clone()
+    wc[:, :, 2:6] ^= 0xFF
+    yc = b1.linear(a, wc.view(-1), n, mode="auto")
+    assert torch.equal(yc, -y)
+    # sampled rows vs fp64
+    rows = torch.linspace(0, m - 1, 24).long()
+    from oracle import b1_oracle as o
+    raw = w.cpu().numpy().reshape(n, -1)
+    ref = o.linear_f64(a[rows].cpu().numpy(), raw, n)
+    torch.cuda.synchronize()
+    assert_fast_close(y[rows].cpu().numpy(), ref, f"{shape} sampled rows")
+
+
+def test_exact_mode_full_size_agrees(torch, b1):
+    from bonsai_b1 import synth
+    m, k, n = 1024, 3072, 3072
+    a = synth.device_activations(m, k, 17)
+    w = synth.device_packed_weights(n, k, 18)
+    ye = b1.linear(a, w, n, mode="exact")
+    yf = b1.linear(a, w, n, mode="gemm")
+    torch.cuda.synchronize()
+    assert_fast_close(yf.cpu().numpy(), ye.cpu().numpy(), "gemm vs exact 1024x3072x3072")
+
+
+# --------------------------------------------------------------- edges ----
+
+def test_edges(torch, b1, oracle):
+    from bonsai_b1 import capi, synth
+    k, n = 256, 40
+    act = synth.activations(5, k, 1)
+    raw = synth.packed_weights(n, k, 2)
+    ys, _ = oracle.linear(act, raw, n, variant="scalar")
+    yf = oracle.linear_f64(act, raw, n)
+
+    say("edge: M=0 is a no-op")
+    a = torch.zeros((0, k), device="cuda")
+    out = b1.linear(a, torch.from_numpy(raw.ravel()).cuda(), n)
+    assert out.shape == (0, n)
+
+    say("edge: strided rows (lda > K, ldo > N)")
+    for mode in ("exact", "auto", "gemm", "gemv"):
+        y = gpu_run(torch, b1, act, raw, n, mode, lda=k + 36, ldo=n + 24)
+        if mode == "exact":
+            assert np.array_equal(y[:, :n], ys)
+        else:
+            assert_fast_close(y[:, :n], yf, f"strided {mode}")
+        assert np.all(y[:, n:] == 7.0), "columns beyond out_dim must be untouched"
+
+    say("edge: K=32 (one block) and K=96 take the exact path in auto")
+    for kk in (32, 96):
+        a1 = synth.activations(3, kk, 5)
+        r1 = synth.packed_weights(16, kk, 6)
+        s1, _ = oracle.linear(a1, r1, 16, variant="scalar")
+        assert np.array_equal(gpu_run(torch, b1, a1, r1, 16, "auto"), s1)
+        with pytest.raises(b1.B1Error):
+            gpu_run(torch, b1, a1, r1, 16, "gemm")
+
+    say("edge: unaligned activation pointer")
+    base = torch.zeros((5 * k + 1,), device="cuda")
+    base[1:] = torch.from_numpy(act.ravel()).cuda()
+    a_un = base[1:].view(5, k)
+    wdev = torch.from_numpy(raw.ravel()).cuda()
+    y = b1.linear(a_un, wdev, n, mode="auto")
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), ys)
+    with pytest.raises(b1.B1Error) as ei:
+        b1.linear(a_un, wdev, n, mode="gemm")
+    assert ei.value.status == capi.ERR_ARG
+
+
+@pytest.mark.parametrize("mode", ["exact", "gemm", "gemv"])
+def test_nonfinite_counter(torch, b1, mode):
+    """Replaces the reference's abort (src/b1_0_kernel.h:194-198): NaN in one
+    activation row poisons that row; an Inf fp16 scale poisons a column."""
+    from bonsai_b1 import synth
+    m, k, n = 4, 128, 48
+    act = synth.activations(m, k, 3)
+    raw = synth.packed_weights(n, k, 4)
+    ctr = torch.zeros(1, dtype=torch.int32, device="cuda")
+    gpu_run(torch, b1, act, raw, n, mode, nonfinite=ctr)
+    assert int(ctr.item()) == 0
+    act[2, 7] = np.nan
+    gpu_run(torch, b1, act, raw, n, mode, nonfinite=ctr)
+    assert int(ctr.item()) == n
+    ctr.zero_()
+    act[2, 7] = 0.5
+    r3 = raw.reshape(n, k // 32, 6).copy()
+    r3[5, 2, 0:2] = [0x00, 0x7C]     # +Inf scale for row 5, block 2
+    gpu_run(torch, b1, act, r3.reshape(n, -1), n, mode, nonfinite=ctr)
+    assert int(ctr.item()) == m
+
+
+def test_residency_builder_and_callback(torch, b1, oracle):
+    """bonsai_b1_weights_upload + bonsai_b1_linear (b1_linear builder, fills
+    the userdata) + the ggml-style callback over stand-in tensors."""
+    import ctypes
+    from bonsai_b1 import capi, synth
+    m, k, n = 6, 512, 96
+    act = synth.activations(m, k, 9)
+    raw = synth.packed_weights(n, k, 10)
+    ys, _ = oracle.linear(act, raw, n, variant="scalar")
+    W = b1.Weights(raw, k, n)
+    torch.cuda.synchronize()
+    a = torch.from_numpy(act).cuda()
+    ud = capi.B1LinearUserData()
+    y = W.linear(a, mode="exact", ud=ud)
+    torch.cuda.synchronize()
+    assert (ud.magic, ud.in_dim, ud.out_dim) == (0x31423142, k, n)
+    assert np.array_equal(y.cpu().numpy(), ys)
+
+    class T(ctypes.Structure):
+        pass
+    T._fields_ = [("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_size_t * 4),
+                  ("src", ctypes.POINTER(T) * 2), ("data", ctypes.c_void_p)]
+    out = torch.empty((m, n), device="cuda")
+    ta, tw, td = T(), T(), T()
+    ta.ne[:] = [k, m, 1, 1]
+    ta.nb[:] = [4, 4 * k, 4 * k * m, 4 * k * m]
+    ta.data = a.data_ptr()
+    tw.ne[:] = [W.c.nbytes, 1, 1, 1]
+    tw.data = W.c.data
+    td.ne[:] = [n, m, 1, 1]
+    td.nb[:] = [4, 4 * n, 4 * n * m, 4 * n * m]
+    td.src[0] = ctypes.pointer(ta)
+    td.src[1] = ctypes.pointer(tw)
+    td.data = out.data_ptr()
+    ud2 = capi.B1LinearUserData(0x31423142, k, n)
+    lib = b1.load()
+    for ith in range(1, 4):        # other ggml tasks return at once
+        lib.bonsai_b1_linear_f32_f32(ctypes.byref(td), ith, 4, ctypes.byref(ud2))
+    lib.bonsai_b1_linear_f32_f32(ctypes.byref(td), 0, 4, ctypes.byref(ud2))
+    torch.cuda.synchronize()
+    assert_fast_close(out.cpu().numpy(), oracle.linear_f64(act, raw, n), "callback")
+    W.free()
