@@ -66,17 +66,39 @@ def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto"):
 
 
 def bench_gemv(torch, b1, synth, m, k, n, steps, warmup):
+    """Small-M kernel, weight copies rotated past the MALL.  The launches are
+    captured once into a HIP graph (one launch per weight copy) and the graph
+    is replayed, so the GPU runs the kernels back to back with no host in the
+    loop; the per-launch time is the event time over the replays / launches."""
     nbytes = n * (k // 32) * 6
     copies = max(2, (2 * MALL_BYTES) // nbytes + 1)      # rotate > 2x the MALL
     ws = [synth.device_packed_weights(n, k, 100 + c) for c in range(copies)]
     a = synth.device_activations(m, k, 3)
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    b1.linear(a, ws[0], n, out=y, mode="gemv")          # load the code object
     torch.cuda.synchronize()
-    ms, wall = time_launches(torch, lambda i: b1.linear(a, ws[i % copies], n, out=y, mode="gemv"),
-                             steps, warmup)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in range(copies):
+            b1.linear(a, ws[c], n, out=y, mode="gemv")
+    reps = max(1, steps // copies)
+    ms, wall = time_launches(torch, lambda i: graph.replay(), reps, max(1, warmup // copies))
+    ms /= copies
+    eager_ms, _ = time_launches(torch, lambda i: b1.linear(a, ws[i % copies], n, out=y, mode="gemv"),
+                                steps, warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"shape": [m, k, n], "ms": ms, "us": ms * 1e3, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
-            "packed_bytes": nbytes, "weight_copies": copies, "wall_s": wall}
+            "packed_bytes": nbytes, "weight_copies": copies, "launches": reps * copies,
+            "eager_us": eager_ms * 1e3, "wall_s": wall}
+
+
+def bench_copy(torch, nbytes, steps, warmup):
+    """Plain device copy of known size: calibrates the FETCH_SIZE/WRITE_SIZE
+    counters (bytes moved = nbytes read + nbytes written per launch)."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+    ms, _ = time_launches(torch, lambda i: dst.copy_(src), steps, warmup)
+    return {"bytes": nbytes, "ms": ms, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
 
 
 def cpu_baseline(a_dev, w_dev, n, rows, threads, reps=3):
@@ -105,6 +127,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--all", action="store_true", help="also time the other config shapes (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["gemm", "gemv", "copy"], default=None,
+                    help="run one leg only (profiler runs); prints that leg's numbers")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the B1_0 linear is built and timed on a single "
@@ -118,14 +142,27 @@ def main():
     torch.cuda.init()
 
     m, k, n = HEADLINE
+    if args.only == "copy":
+        c = bench_copy(torch, 256 << 20, args.steps, args.warmup)
+        print(json.dumps({"copy": c}), flush=True)
+        return
+    if args.only == "gemv":
+        gm, gk, gn = GEMV
+        v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), args.warmup)
+        print(json.dumps({"gemv": {x: v[x] for x in v}}), flush=True)
+        return
     log(f"[bench] GEMM M={m} K={k} N={n} steps={args.steps} warmup={args.warmup}")
     g = bench_gemm(torch, b1, synth, m, k, n, args.steps, args.warmup)
     log(f"[bench] GEMM {g['ms']*1e3:.1f} us  {g['tflops']:.1f} TFLOP/s  {100*g['frac']:.1f}% of fp16 MFMA peak")
+    if args.only == "gemm":
+        print(json.dumps({"gemm": {x: g[x] for x in g if x != "inputs"}}), flush=True)
+        return
 
     gm, gk, gn = GEMV
     log(f"[bench] GEMV M={gm} K={gk} N={gn}")
     v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), args.warmup)
-    log(f"[bench] GEMV {v['us']:.2f} us/call  {v['gbs']:.0f} GB/s packed  {100*v['frac']:.1f}% of HBM peak")
+    log(f"[bench] GEMV {v['us']:.2f} us/launch (graph)  {v['gbs']:.0f} GB/s packed  "
+        f"{100*v['frac']:.1f}% of HBM peak; eager {v['eager_us']:.2f} us/call")
     v1 = bench_gemv(torch, b1, synth, 1, gk, gn, max(args.steps, 200), args.warmup)
     log(f"[bench] GEMV M=1 {v1['us']:.2f} us/call  {v1['gbs']:.0f} GB/s packed")
 
@@ -143,7 +180,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
-        rows = 256
+        rows = m
         log(f"[bench] CPU baseline: oracle AVX2, {threads} threads, {rows} of {m} rows")
         tf, dt = cpu_baseline(*g["inputs"], n, rows, threads)
         cpu = {"value": round(tf, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
@@ -174,6 +211,8 @@ def main():
         "gemv": {"M": gm, "K": gk, "N": gn, "us_per_call": round(v["us"], 3),
                  "GBps_packed": round(v["gbs"], 1), "frac_hbm": round(v["frac"], 4),
                  "packed_bytes": v["packed_bytes"], "weight_copies": v["weight_copies"],
+                 "timing": "hip graph of back-to-back launches, one per weight copy",
+                 "eager_us_per_call": round(v["eager_us"], 3),
                  "M1_us_per_call": round(v1["us"], 3), "M1_GBps_packed": round(v1["gbs"], 1)},
         "cpu_baseline": cpu,
     }

@@ -310,9 +310,24 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_kernel(Lin
 }
 
 // ----------------------------------------------------------------- gemv --
+//
+// Small M (<= 16).  Persistent work-groups (one per CU); wave w owns a K
+// slice of kGvBPW blocks and accumulates every 16-row group of its
+// work-group over that slice (split-K); the waves' partial tiles are then
+// summed in LDS in a fixed order.  MFMA 16x16x32 f16 with the tokens on the
+// A side (rows >= M are zero) and the weight rows on the B side.
+//
+// Block-interleaved K: inside a quad of 4 consecutive blocks, lane group g
+// (lanes 16g..16g+15) always works on block 4q+g, and MFMA t (t = 0..3) of
+// the quad covers fp16 dwords 4t..4t+3 of that block (elements d and d+16,
+// d = 4t..4t+3).  Each lane therefore needs only its own 6-byte block of its
+// own row, which it fetches as two aligned dwords; all of a wave's weight
+// loads are issued before any is consumed, so the kernel pays one HBM round
+// trip rather than one per row group.
 
 constexpr int kGvWaves = 8;                    // waves per work-group
-constexpr int kGvBPW = 12;                     // blocks per wave per pass
+constexpr int kGvQuads = 3;                    // 4-block quads per wave per pass
+constexpr int kGvBPW = 4 * kGvQuads;           // blocks per wave per pass
 constexpr int kGvChunk = kGvWaves * kGvBPW;    // blocks per pass (K 3072)
 constexpr int kGvMaxRG = 6;                    // 16-row groups per WG, max
 
@@ -328,6 +343,12 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
     const size_t rs = (size_t)nb * 6;
     const bool tok_ok = col < p.M;
     const float *arow = p.act + (size_t)(tok_ok ? col : 0) * p.lda;
+    // Block 4q+g has the parity of g (the slice start and 4q are even).  An
+    // even block starts a 4-byte aligned 8-byte window; an odd block sits at
+    // byte 2 of the window that starts 2 bytes before it.
+    const int odd = g & 1;
+    const uint32_t sel_word = odd ? 0x07060504u : 0x05040302u;
+    const uint32_t sel_scale = odd ? 0x03020302u : 0x01000100u;
 
     floatx4 acc[kGvMaxRG];
 #pragma unroll
@@ -335,71 +356,70 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
 
     for (int kb0 = 0; kb0 < nb; kb0 += kGvChunk) {
         const int wb0 = kb0 + wave * kGvBPW;
-        // Activation fragments for this wave's blocks: lane row = token col,
-        // k-slots 8g..8g+7 = dwords 4g..4g+3 of each block.
-        u32x4 af[kGvBPW];
+
+        uint32_t wd[kGvMaxRG][kGvQuads][2];
 #pragma unroll
-        for (int b = 0; b < kGvBPW; ++b) {
-            const int blk = wb0 + b;
-            if (tok_ok && blk < nb) {
-                const float *src = arow + blk * 32 + 4 * g;
-                const floatx4 lo = *reinterpret_cast<const floatx4 *>(src);
-                const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + 16);
+        for (int r = 0; r < kGvMaxRG; ++r) {
+            const int n = (rg0 + r) * 16 + col;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) af[b][j] = neg_pack_f16(lo[j], hi[j]);
-            } else {
-                af[b] = u32x4{0u, 0u, 0u, 0u};
+            for (int q = 0; q < kGvQuads; ++q) {
+                const int blk = wb0 + 4 * q + g;
+                if (r < nrg && n < p.N && blk < nb) {
+                    const uint32_t *src = reinterpret_cast<const uint32_t *>(
+                        p.w + (size_t)n * rs + (size_t)blk * 6 - 2 * odd);
+                    wd[r][q][0] = src[0];
+                    wd[r][q][1] = src[1];
+                } else {
+                    wd[r][q][0] = wd[r][q][1] = 0u;
+                }
             }
         }
 
-        // Packed bytes of this wave's 12 blocks of row n: 18 dwords.
-        auto load_row = [&](int r, uint32_t (&d)[kGvBPW * 3 / 2]) {
-            const int n = (rg0 + r) * 16 + col;
-            const uint32_t *src = reinterpret_cast<const uint32_t *>(p.w + (size_t)(n < p.N ? n : 0) * rs + (size_t)wb0 * 6);
+        u32x4 af[kGvQuads][4];
 #pragma unroll
-            for (int q = 0; q < kGvBPW / 2; ++q) {
-                if (n < p.N && wb0 + 2 * q < nb) {
-                    d[3 * q] = src[3 * q];
-                    d[3 * q + 1] = src[3 * q + 1];
-                    d[3 * q + 2] = src[3 * q + 2];
+        for (int q = 0; q < kGvQuads; ++q) {
+            const int blk = wb0 + 4 * q + g;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (tok_ok && blk < nb) {
+                    const float *src = arow + (size_t)blk * 32 + 4 * t;
+                    const floatx4 lo = *reinterpret_cast<const floatx4 *>(src);
+                    const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + 16);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) af[q][t][j] = neg_pack_f16(lo[j], hi[j]);
                 } else {
-                    d[3 * q] = d[3 * q + 1] = d[3 * q + 2] = 0u;
+                    af[q][t] = u32x4{0u, 0u, 0u, 0u};
                 }
             }
-        };
+        }
 
-        uint32_t dcur[kGvBPW * 3 / 2], dnext[kGvBPW * 3 / 2];
-        if (nrg > 0) load_row(0, dcur);
 #pragma unroll
-        for (int r = 0; r < kGvMaxRG; ++r) {
-            if (r < nrg) {
-                if (r + 1 < nrg) load_row(r + 1, dnext);
+        for (int q = 0; q < kGvQuads; ++q) {
+            uint32_t s2[kGvMaxRG], w[kGvMaxRG];
 #pragma unroll
-                for (int b = 0; b < kGvBPW; ++b) {
-                    if (wb0 + b < nb) {
-                        uint32_t s2, wd;
-                        if ((b & 1) == 0) {
-                            s2 = dup_lo16(dcur[3 * b / 2]);
-                            wd = __builtin_amdgcn_alignbit(dcur[3 * b / 2 + 1], dcur[3 * b / 2], 16);
-                        } else {
-                            s2 = dup_hi16(dcur[(3 * b - 1) / 2]);
-                            wd = dcur[(3 * b + 1) / 2];
-                        }
-                        const uint32_t wg = wd >> (4 * g);
+            for (int r = 0; r < kGvMaxRG; ++r) {
+                s2[r] = __builtin_amdgcn_perm(wd[r][q][1], wd[r][q][0], sel_scale);
+                w[r] = __builtin_amdgcn_perm(wd[r][q][1], wd[r][q][0], sel_word);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int r = 0; r < kGvMaxRG; ++r) {
+                    if (r < nrg) {
                         u32x4 bd;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) bd[j] = wpair(wg, 15 - j, s2);
+                        for (int j = 0; j < 4; ++j) bd[j] = wpair(w[r], 15 - 4 * t - j, s2[r]);
                         acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(half8, af[b]), __builtin_bit_cast(half8, bd), acc[r], 0, 0, 0);
+                            __builtin_bit_cast(half8, af[q][t]), __builtin_bit_cast(half8, bd), acc[r], 0, 0, 0);
                     }
                 }
-#pragma unroll
-                for (int i = 0; i < kGvBPW * 3 / 2; ++i) dcur[i] = dnext[i];
             }
         }
     }
 
-    // Cross-wave (split-K) reduction in a fixed order, then store.
+    // Cross-wave (split-K) reduction in a fixed order, then store.  16x16
+    // accumulator layout: lane column = lane & 15 (weight row), rows
+    // 4*(lane >> 4) + v (tokens).
 #pragma unroll
     for (int r = 0; r < kGvMaxRG; ++r)
         if (r < nrg) red[wave][r][lane] = acc[r];

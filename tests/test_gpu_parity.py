@@ -145,15 +145,28 @@ def test_full_size_properties(torch, b1, shape):
     say(f"full-size {shape}")
     a = synth.device_activations(m, k, 7)
     w = synth.device_packed_weights(n, k, 8)
+    # keep activations out of the fp16 subnormal range, where fp16(2a) and
+    # 2 fp16(a) round at different granularity
+    a = torch.where(a.abs() < 2.0 ** -12, torch.zeros_like(a), a)
     y = b1.linear(a, w, n, mode="auto")
-    # exact scaling: fp16(2a) = 2 fp16(a) and the fp32 MFMA sums scale exactly
+    # exact scaling of the activations: fp16(2a) = 2 fp16(a) for normal
+    # fp16 values and the fp32 MFMA sums scale exactly
     y2 = b1.linear(a * 2.0, w, n, mode="auto")
     assert torch.equal(y2, 2.0 * y)
-    # complemented sign words: every expanded weight flips sign exactly
+    # exact scaling of every fp16 block scale by 2 (exponent + 1)
+    w2 = w.view(n, k // 32, 6).clone()
+    sc = w2[:, :, 0:2].contiguous().view(torch.float16) * 2
+    w2[:, :, 0:2] = sc.view(torch.uint8).view(n, k // 32, 2)
+    y3 = b1.linear(a, w2.view(-1), n, mode="auto")
+    assert torch.equal(y3, 2.0 * y)
+    # complemented sign words: every expanded weight flips sign exactly; the
+    # MFMA's internal rounding is not sign-symmetric bit for bit, so the
+    # negation is checked to 1e-6 of rms(y), far below any sign/index slip
     wc = w.view(n, k // 32, 6).clone()
     wc[:, :, 2:6] ^= 0xFF
     yc = b1.linear(a, wc.view(-1), n, mode="auto")
-    assert torch.equal(yc, -y)
+    rms = float(y.pow(2).mean().sqrt())
+    assert float((yc + y).abs().max()) <= 1e-6 * rms
     # sampled rows vs fp64
     rows = torch.linspace(0, m - 1, 24).long()
     from oracle import b1_oracle as o
@@ -284,3 +297,25 @@ def test_residency_builder_and_callback(torch, b1, oracle):
     torch.cuda.synchronize()
     assert_fast_close(out.cpu().numpy(), oracle.linear_f64(act, raw, n), "callback")
     W.free()
+
+
+@pytest.mark.parametrize("mode,m", [("gemv", 8), ("gemm", 256)])
+def test_graph_replay_matches_eager(torch, b1, mode, m):
+    """Launches captured into a HIP graph (as the benchmark does) give the
+    eager result on every replay, with eager work between replays."""
+    from bonsai_b1 import synth
+    k, n = 3072, 4096
+    a = synth.device_activations(m, k, 31)
+    w = synth.device_packed_weights(n, k, 32)
+    ref = b1.linear(a, w, n, mode=mode).clone()
+    y = torch.empty((m, n), device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        b1.linear(a, w, n, out=y, mode=mode)
+    for i in range(4):
+        y.fill_(float(i + 1))
+        b1.linear(a * 0.5, w, n, mode=mode)        # unrelated eager work
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {i}"
