@@ -15,10 +15,22 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 
+constexpr int kWsSlots = 8; // cached workspaces per device (one per stream)
+
+struct Workspace {
+    hipStream_t stream = nullptr;
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    uint64_t last_use = 0;
+    bool used = false;
+};
+
 struct DeviceInfo {
     int state = 0; // 0 unknown, 1 usable gfx950, -1 unusable
     int num_cus = 0;
     int32_t *cb_counter = nullptr; // non-finite counter for the callback
+    Workspace ws[kWsSlots];
+    uint64_t tick = 0;
 };
 
 std::mutex g_mu;
@@ -41,6 +53,47 @@ DeviceInfo *current_device(int *dev_out) {
         }
     }
     return d.state == 1 ? &d : nullptr;
+}
+
+// Library-owned workspace for `stream` on the current device, grown to at
+// least `need` bytes.  Returns nullptr (the caller then uses a kernel that
+// needs none) when the stream is being captured and no large enough buffer
+// exists yet, or when allocation fails.  Growing frees the old buffer
+// (hipFree waits for work that may still use it).
+void *stream_workspace(DeviceInfo *d, hipStream_t stream, size_t need) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Workspace *hit = nullptr, *victim = &d->ws[0];
+    for (Workspace &w : d->ws) {
+        if (w.used && w.stream == stream) hit = &w;
+        if (!w.used) {
+            if (victim->used) victim = &w;
+        } else if (victim->used && w.last_use < victim->last_use) {
+            victim = &w;
+        }
+    }
+    if (hit && hit->bytes >= need) {
+        hit->last_use = ++d->tick;
+        return hit->ptr;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    Workspace *w = hit ? hit : victim;
+    if (w->ptr) {
+        (void)hipFree(w->ptr);
+        w->ptr = nullptr;
+        w->bytes = 0;
+        w->used = false;
+    }
+    const size_t bytes = (need + (2u << 20) - 1) & ~((size_t)(2u << 20) - 1);
+    if (hipMalloc(&w->ptr, bytes) != hipSuccess) {
+        w->ptr = nullptr;
+        return nullptr;
+    }
+    w->stream = stream;
+    w->bytes = bytes;
+    w->used = true;
+    w->last_use = ++d->tick;
+    return w->ptr;
 }
 
 int check_args(const float *act, int64_t lda, const void *w, int in_dim,
@@ -72,10 +125,11 @@ const char *bonsai_b1_status_string(int status) {
     }
 }
 
-int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
-                         int in_dim, int out_dim, int batch, float *out,
-                         int64_t ldo, int mode, int32_t *nonfinite,
-                         hipStream_t stream) {
+// Shared body of the two linear entry points.  ws_mode: 0 = library-owned
+// workspace, 1 = caller's (ws, ws_bytes; may be NULL / too small).
+static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim, int out_dim, int batch,
+                       float *out, int64_t ldo, int mode, int32_t *nonfinite, int ws_mode, void *ws,
+                       size_t ws_bytes, hipStream_t stream) {
     int st = check_args(act, lda, w, in_dim, out_dim, batch, out, ldo);
     if (st != BONSAI_B1_OK) return st;
     if (mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_GEMV) return BONSAI_B1_ERR_ARG;
@@ -94,6 +148,15 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
     a.ldo = ldo;
     a.nonfinite = nonfinite;
 
+    auto gemm = [&]() {
+        const size_t need = b1::gemm_workspace_bytes(a);
+        if (need > 0 && ws_mode == 0) {
+            ws = stream_workspace(dev, stream, need);
+            ws_bytes = ws ? need : 0;
+        }
+        return b1::launch_gemm(a, dev->num_cus, ws, ws_bytes, stream);
+    };
+
     hipError_t e;
     switch (mode) {
     case BONSAI_B1_MODE_EXACT:
@@ -101,7 +164,7 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
         break;
     case BONSAI_B1_MODE_GEMM:
         if (!b1::gemm_supported(a)) return BONSAI_B1_ERR_ARG;
-        e = b1::launch_gemm(a, dev->num_cus, stream);
+        e = gemm();
         break;
     case BONSAI_B1_MODE_GEMV:
         if (!b1::gemv_supported(a)) return BONSAI_B1_ERR_ARG;
@@ -111,12 +174,45 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
         if (b1::gemv_supported(a))
             e = b1::launch_gemv(a, dev->num_cus, stream);
         else if (b1::gemm_supported(a))
-            e = b1::launch_gemm(a, dev->num_cus, stream);
+            e = gemm();
         else
             e = b1::launch_exact(a, stream); // unaligned / K % 64 != 0
         break;
     }
     return e == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
+}
+
+int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
+                         int in_dim, int out_dim, int batch, float *out,
+                         int64_t ldo, int mode, int32_t *nonfinite,
+                         hipStream_t stream) {
+    return linear_impl(act, lda, w, in_dim, out_dim, batch, out, ldo, mode, nonfinite, 0, nullptr, 0, stream);
+}
+
+size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode) {
+    if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
+    if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return 0;
+    if ((mode == BONSAI_B1_MODE_AUTO || mode == BONSAI_B1_MODE_FAST) && batch <= b1::kGemvMaxM) return 0;
+    return in_dim % 256 == 0 ? (size_t)batch * (size_t)in_dim * 2 : 0;
+}
+
+int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
+                            int in_dim, int out_dim, int batch, float *out,
+                            int64_t ldo, int mode, int32_t *nonfinite,
+                            void *workspace, size_t workspace_bytes,
+                            hipStream_t stream) {
+    return linear_impl(act, lda, w, in_dim, out_dim, batch, out, ldo, mode, nonfinite, 1, workspace,
+                       workspace_bytes, stream);
+}
+
+void bonsai_b1_release_workspaces(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (DeviceInfo &d : g_dev) {
+        for (Workspace &w : d.ws) {
+            if (w.ptr) (void)hipFree(w.ptr);
+            w = Workspace();
+        }
+    }
 }
 
 int bonsai_b1_linear(const float *act, const B1Weights *w, int batch,

@@ -23,8 +23,13 @@ struct LinearArgs {
 hipError_t launch_exact(const LinearArgs &a, hipStream_t s);
 
 // fp16 MFMA GEMM; requires K % 64 == 0, lda % 4 == 0, act 16-byte aligned.
+// With a workspace of gemm_workspace_bytes(a) bytes (> 0 when K % 256 == 0
+// and the weights are 8-byte aligned) the activations are packed to fp16
+// once and streamed into LDS directly; otherwise the kernel converts them
+// while staging each tile.
 bool gemm_supported(const LinearArgs &a);
-hipError_t launch_gemm(const LinearArgs &a, int num_cus, hipStream_t s);
+size_t gemm_workspace_bytes(const LinearArgs &a);
+hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s);
 
 // Small-M (M <= 16) bandwidth-bound kernel; requires K % 64 == 0,
 // lda % 4 == 0, act 16-byte aligned.

@@ -9,11 +9,13 @@
 // Three kernels:
 //  * b1_exact_kernel — fp32 VALU, the reference's scalar summation order
 //    (src/b1_0_kernel.h:253-277) with contraction off: bit-identical output.
-//  * b1_gemm_kernel  — wide-tile MFMA GEMM for large M.  Activations are
-//    converted fp32 -> fp16 while being staged into LDS; each weight block
-//    is expanded in registers to fp16 +-scale (exact: a sign flip of an fp16
-//    value), so the per-block scale rides inside the MFMA operand and no
-//    per-block rescale of fp32 partial sums is needed.
+//  * b1_gemm_kernel  — wide-tile MFMA GEMM for large M over activations
+//    packed to fp16 once (b1_pack_act_kernel) and streamed global -> LDS
+//    directly; each weight block is expanded in registers to fp16 +-scale
+//    (exact: a sign flip of an fp16 value), so the per-block scale rides
+//    inside the MFMA operand and no per-block rescale of fp32 partial sums
+//    is needed.  b1_gemm_fused_kernel is the same GEMM converting fp32
+//    activations while staging each tile (used when no workspace is given).
 //  * b1_gemv_kernel  — small M (<= 16): persistent work-groups, split-K over
 //    the waves of a work-group, activations held in registers, packed
 //    weights streamed once from HBM; MFMA 16x16x32 with M padded to 16.
@@ -26,9 +28,11 @@
 // activation side is written in the same pairing when it is packed to fp16.
 // Any consistent permutation of K inside the MFMA leaves the dot product
 // unchanged.  The bit value 1 lands on the fp16 sign, i.e. the expanded
-// weight is -(reference weight); the activations are negated when packed to
-// fp16 so that the product keeps the reference sign.
+// weight is -(reference weight); the MFMA kernels store the negated
+// accumulator so that the output keeps the reference sign.
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 
 #include "b1_internal.h"
 
@@ -52,12 +56,31 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {
     return r;
 }
 
-// (-lo, -hi) -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32).
-__device__ __forceinline__ uint32_t neg_pack_f16(float lo, float hi) {
-    float2v v = {-lo, -hi};
+// (lo, hi) -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+    float2v v = {lo, hi};
     half2v h = __builtin_convertvector(v, half2v);
     return __builtin_bit_cast(uint32_t, h);
 }
+
+// s_waitcnt vmcnt(N) leaving expcnt and lgkmcnt alone (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Work-group barrier that does not drain outstanding global->LDS loads
+// (__syncthreads() would add s_waitcnt vmcnt(0) while LDS-DMA is pending).
+// Each wave waits for its own loads with wait_vmcnt<> before arriving.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ uint32_t dup_lo16(uint32_t d) {
     return __builtin_amdgcn_perm(d, d, 0x01000100u);
@@ -158,7 +181,7 @@ __device__ __forceinline__ int xcd_tile(int bid, int nblk) {
 }
 
 template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_kernel(LinearArgs p, int tiles_n) {
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_fused_kernel(LinearArgs p, int tiles_n) {
     using C = GemmCfg<BM, BN, WM, WN>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * C::STAGE];
 
@@ -197,7 +220,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_kernel(Lin
             const int c = id & 3, blk = (id >> 2) & 1, row = id >> 3;
             u32x4 v;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = neg_pack_f16(ar[u][0][j], ar[u][1][j]);
+            for (int j = 0; j < 4; ++j) v[j] = pack_f16(ar[u][0][j], ar[u][1][j]);
             *reinterpret_cast<u32x4 *>(lds + buf * C::STAGE + row * C::ROW + blk * 64 + c * 16) = v;
         }
     };
@@ -299,7 +322,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_kernel(Lin
             for (int v = 0; v < 16; ++v) {
                 const int m = m0 + wm * WM + mt * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
                 if (m < p.M && n < p.N) {
-                    const float y = acc[mt][nt][v];
+                    const float y = -acc[mt][nt][v];
                     bad += !__builtin_isfinite(y);
                     p.out[(size_t)m * p.ldo + n] = y;
                 }
@@ -307,6 +330,219 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_kernel(Lin
         }
     }
     count_nonfinite(p.nonfinite, bad);
+}
+
+// ------------------------------------------------------- pack activations --
+//
+// fp32 activations -> fp16 (RNE) in the K-slot pairing, once per call: u32
+// word (row, 16 blk + d) holds (a[row][32 blk + d], a[row][32 blk + d + 16]).
+// The GEMM then streams this straight into LDS with no per-tile conversion.
+
+__global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restrict__ act, int64_t lda,
+                                                          uint32_t *__restrict__ ah, int M, int K) {
+    const int nb = K / 32;
+    const int units = M * nb * 4; // (row, block, quad)
+    for (int u = blockIdx.x * 256 + threadIdx.x; u < units; u += gridDim.x * 256) {
+        const int c = u & 3, rb = u >> 2;
+        const int row = rb / nb, blk = rb - row * nb;
+        const float *src = act + (size_t)row * lda + blk * 32 + c * 4;
+        const floatx4 lo = *reinterpret_cast<const floatx4 *>(src);
+        const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + 16);
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = pack_f16(lo[j], hi[j]);
+        *reinterpret_cast<u32x4 *>(ah + (size_t)row * (K / 2) + blk * 16 + c * 4) = v;
+    }
+}
+
+// ------------------------------------------------------------- gemm (lds) --
+//
+// Wide-tile GEMM over pre-packed fp16 activations.  Work-group tile BM x BN,
+// NW = BN/WN waves side by side along N (each wave BM x WN; all waves share
+// the activation rows, so no weight column is expanded twice).  K advances
+// in stages of 128 (4 blocks).  Both operands of a stage go global -> LDS
+// directly (global_load_lds_dwordx4 for activations, _dwordx3 for the 24
+// packed bytes per weight column), with no VGPR staging, into a two-slot
+// ring: stage s+1 is fetched while stage s is computed.
+// Activation rows are 256 bytes in LDS with 16-byte chunk c of row r stored
+// at position c ^ (r & 7), so the 8 lanes of a ds_read_b128 phase hit 8
+// different bank groups.  Weight bytes sit per wave as two planes of
+// 64 columns x 12 bytes (blocks 0-1 and blocks 2-3 of the stage).
+
+template <int BM, int BN, int WN, int STAGES>
+struct Gemm2Cfg {
+    static constexpr int NW = BN / WN, NT = NW * 64;
+    static constexpr int MT = BM / 32, NTL = WN / 32;
+    static constexpr int KC = 128;                   // K per stage (4 blocks)
+    static constexpr int ROWB = KC * 2;              // LDS bytes per row
+    static constexpr int ASTAGE = BM * ROWB;         // activation bytes per slot
+    static constexpr int BWAVE = WN * 24;            // weight bytes per wave per slot
+    static constexpr int BSTAGE = NW * BWAVE;        // weight bytes per slot
+    static constexpr int BBASE = STAGES * ASTAGE;    // weight slots follow the activation slots
+    static constexpr int LPW = ASTAGE / 1024 / NW;   // 1 KB activation loads per wave
+    static constexpr int LDS = STAGES * (ASTAGE + BSTAGE);
+    static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
+    static_assert(WN == 64, "one weight column per lane");
+    static_assert((STAGES - 1) * ASTAGE + (MT - 1) * 32 * ROWB + 128 < 65536,
+                  "fragment offsets fit the ds_read immediate");
+};
+
+template <int BM, int BN, int WN, int STAGES>
+__global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t *__restrict__ ah,
+                                                                 const uint8_t *__restrict__ w, int K, int N,
+                                                                 int M, float *__restrict__ out, int64_t ldo,
+                                                                 int32_t *nonfinite, int tiles_n) {
+    using C = Gemm2Cfg<BM, BN, WN, STAGES>;
+    static_assert(STAGES == 2, "two-slot ring");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+
+    const int t = xcd_tile(blockIdx.x, gridDim.x);
+    const int tm = t / tiles_n, tn = t - tm * tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    // The wave index is made visibly uniform: LDS-DMA destinations go
+    // through M0 and must not depend on the lane.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 31, g = lane >> 5;
+    const int nstage = K / C::KC;
+    const uint32_t rs = (uint32_t)(K / 32) * 6;
+    const uint8_t *abase = reinterpret_cast<const uint8_t *>(ah);
+
+    // Activation loads: load j of a stage fills LDS bytes [1024 j, +1024)
+    // = rows 4j..4j+3; lane L writes position L % 16 of row 4j + L / 16,
+    // which holds chunk (L % 16) ^ (row & 7).  Rows past M read row M-1.
+    uint32_t aoff[C::LPW];
+#pragma unroll
+    for (int i = 0; i < C::LPW; ++i) {
+        const int j = wave * C::LPW + i;
+        const int row = 4 * j + (lane >> 4);
+        const int c = (lane & 15) ^ (row & 7);
+        aoff[i] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + (uint32_t)c * 8) * 2;
+    }
+    // Weight loads: lane L fetches 12 bytes of column n0 + 64 wave + L per
+    // plane.  Columns past N read row N-1 and are never stored.
+    const uint32_t boff = (uint32_t)min(n0 + wave * WN + lane, N - 1) * rs;
+    auto issue = [&](int ks, int slot) {
+        uint8_t *sa = smem + slot * C::ASTAGE;
+        uint8_t *sw = smem + C::BBASE + slot * C::BSTAGE + wave * C::BWAVE;
+#pragma unroll
+        for (int i = 0; i < C::LPW; ++i)
+            __builtin_amdgcn_global_load_lds(abase + aoff[i] + (uint32_t)ks * C::ROWB,
+                                             (lds_void_t *)(sa + (wave * C::LPW + i) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+            __builtin_amdgcn_global_load_lds(w + boff + (uint32_t)ks * 24 + pl * 12,
+                                             (lds_void_t *)(sw + pl * 768), 12, 0, 0);
+    };
+
+    // Fragment offsets: lane (li, g) reads row li (+32 mt) at chunk
+    // c = 4b + 2h + g, stored at position c ^ (li & 7).
+    uint32_t foff[2][2];
+#pragma unroll
+    for (int b1 = 0; b1 < 2; ++b1)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            foff[b1][h] = li * C::ROWB + (((4 * b1 + 2 * h + g) ^ (li & 7)) * 16);
+    const uint32_t bq_off = C::BBASE + wave * C::BWAVE + li * 12;
+
+    floatx16 acc[C::MT][C::NTL];
+#pragma unroll
+    for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < C::NTL; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    // One stage = 8 steps (block b = step/2, half h = step%2).  The fragment
+    // reads of step+1 are issued before the MFMAs of step, into a second
+    // buffer; a scheduling fence per step keeps the compiler from hoisting
+    // every read of the stage.
+    auto compute = [&](int slot) {
+        const uint8_t *sb = smem + slot * C::ASTAGE;
+        const uint8_t *sq = smem + slot * C::BSTAGE + bq_off;
+        auto read_frags = [&](int step, half8 (&af)[C::MT]) {
+            const int b = step >> 1, h = step & 1;
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt)
+                af[mt] = *reinterpret_cast<const half8 *>(sb + mt * 32 * C::ROWB + foff[b & 1][h] + (b >> 1) * 128);
+        };
+        half8 afa[C::MT], afb[C::MT];
+        uint32_t d[C::NTL][3], s2[C::NTL], wg[C::NTL];
+        read_frags(0, afa);
+#pragma unroll
+        for (int step = 0; step < 8; ++step) {
+            const int b = step >> 1, h = step & 1;
+            half8 (&cur)[C::MT] = (step & 1) ? afb : afa;
+            half8 (&nxt)[C::MT] = (step & 1) ? afa : afb;
+            if (step + 1 < 8) read_frags(step + 1, nxt);
+            if (h == 0) {
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt) {
+                    if ((b & 1) == 0) {
+                        const uint32_t *src = reinterpret_cast<const uint32_t *>(sq + nt * 384 + (b >> 1) * 768);
+                        d[nt][0] = src[0];
+                        d[nt][1] = src[1];
+                        d[nt][2] = src[2];
+                        s2[nt] = dup_lo16(d[nt][0]);
+                        wg[nt] = __builtin_amdgcn_alignbit(d[nt][1], d[nt][0], 16) >> (4 * g);
+                    } else {
+                        s2[nt] = dup_hi16(d[nt][1]);
+                        wg[nt] = d[nt][2] >> (4 * g);
+                    }
+                }
+            }
+#pragma unroll
+            for (int nt = 0; nt < C::NTL; ++nt) {
+                u32x4 bd;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bd[j] = wpair(wg[nt], 15 - 8 * h - j, s2[nt]);
+                const half8 bf = __builtin_bit_cast(half8, bd);
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[mt], bf, acc[mt][nt], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Pipeline (stage s in slot s % 2): at the top of stage s the wave waits
+    // for its own loads of stage s, then the barrier publishes every wave's
+    // part and retires all reads of slot (s+1) % 2 (stage s-1's), which
+    // stage s+1's loads then refill while stage s is computed.  The loop is
+    // unrolled by two so that slot offsets are compile-time; the stage count
+    // K/128 is even (K % 256 == 0), so the loop has no exit mid-body.
+    issue(0, 0);
+    for (int s = 0; s < nstage; s += 2) {
+        wait_vmcnt<0>();
+        lds_barrier();
+        issue(s + 1, 1);
+        compute(0);
+        wait_vmcnt<0>();
+        lds_barrier();
+        if (s + 2 < nstage) issue(s + 2, 0);
+        compute(1);
+    }
+
+    // Epilogue.  32x32 accumulator layout: lane column li, rows
+    // 8*(v/4) + 4*g + v%4 of each sub-tile; stored negated (see top).
+    const int ncol = n0 + wave * WN + li;
+    int bad = 0;
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < C::NTL; ++nt) {
+            const int n = ncol + nt * 32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+                if (m < M && n < N) {
+                    const float y = -acc[mt][nt][v];
+                    bad += !__builtin_isfinite(y);
+                    out[(size_t)m * ldo + n] = y;
+                }
+            }
+        }
+    }
+    count_nonfinite(nonfinite, bad);
 }
 
 // ----------------------------------------------------------------- gemv --
@@ -375,22 +611,29 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
             }
         }
 
+        // Activation fragments.  All loads are issued unconditionally (row and
+        // block clamped into range) before any is converted, so they overlap;
+        // out-of-range tokens/blocks are zeroed afterwards.
+        floatx4 araw[kGvQuads][4][2];
+#pragma unroll
+        for (int q = 0; q < kGvQuads; ++q) {
+            const int blk = min(wb0 + 4 * q + g, nb - 1);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float *src = arow + (size_t)blk * 32 + 4 * t;
+                araw[q][t][0] = *reinterpret_cast<const floatx4 *>(src);
+                araw[q][t][1] = *reinterpret_cast<const floatx4 *>(src + 16);
+            }
+        }
         u32x4 af[kGvQuads][4];
 #pragma unroll
         for (int q = 0; q < kGvQuads; ++q) {
-            const int blk = wb0 + 4 * q + g;
+            const bool ok = tok_ok && wb0 + 4 * q + g < nb;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                if (tok_ok && blk < nb) {
-                    const float *src = arow + (size_t)blk * 32 + 4 * t;
-                    const floatx4 lo = *reinterpret_cast<const floatx4 *>(src);
-                    const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + 16);
+            for (int t = 0; t < 4; ++t)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) af[q][t][j] = neg_pack_f16(lo[j], hi[j]);
-                } else {
-                    af[q][t] = u32x4{0u, 0u, 0u, 0u};
-                }
-            }
+                for (int j = 0; j < 4; ++j)
+                    af[q][t][j] = ok ? pack_f16(araw[q][t][0][j], araw[q][t][1][j]) : 0u;
         }
 
 #pragma unroll
@@ -431,6 +674,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
         float s = 0.0f;
 #pragma unroll
         for (int w = 0; w < kGvWaves; ++w) s += red[w][r][ln][v];
+        s = -s; // the expanded weights carry the opposite sign
         const int n = (rg0 + r) * 16 + c;
         if (tok < p.M && n < p.N) {
             bad += !__builtin_isfinite(s);
@@ -458,12 +702,48 @@ static bool fast_layout_ok(const LinearArgs &a) {
 
 bool gemm_supported(const LinearArgs &a) { return fast_layout_ok(a); }
 
-hipError_t launch_gemm(const LinearArgs &a, int num_cus, hipStream_t s) {
+// GEMM over pre-packed activations: K % 256 == 0 (every 4-block weight
+// chunk is 8-byte aligned) and 8-byte aligned weights.
+static bool packed_gemm_ok(const LinearArgs &a) {
+    return a.K % 256 == 0 && (reinterpret_cast<uintptr_t>(a.w) & 7u) == 0;
+}
+
+size_t gemm_workspace_bytes(const LinearArgs &a) {
+    return packed_gemm_ok(a) && fast_layout_ok(a) ? (size_t)a.M * a.K * 2 : 0;
+}
+
+namespace {
+constexpr int kBM = 128, kBN = 512, kWN = 64, kStages = 2;
+using KCfg = Gemm2Cfg<kBM, kBN, kWN, kStages>;
+} // namespace
+
+hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s) {
     (void)num_cus;
-    constexpr int BM = 128, BN = 512, WM = 128, WN = 64;
-    using C = GemmCfg<BM, BN, WM, WN>;
-    const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
-    hipLaunchKernelGGL((b1_gemm_kernel<BM, BN, WM, WN>), dim3(tiles_m * tiles_n), dim3(C::NT), 0, s, a, tiles_n);
+    const size_t need = gemm_workspace_bytes(a);
+    if (need == 0 || workspace == nullptr || ws_bytes < need) {
+        // Fused-conversion kernel: no workspace needed.
+        constexpr int BM = 128, BN = 512, WM = 128, WN = 64;
+        using C = GemmCfg<BM, BN, WM, WN>;
+        const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
+        hipLaunchKernelGGL((b1_gemm_fused_kernel<BM, BN, WM, WN>), dim3(tiles_m * tiles_n), dim3(C::NT), 0, s, a,
+                           tiles_n);
+        return hipGetLastError();
+    }
+    static std::once_flag attr_once;
+    static hipError_t attr_err = hipSuccess;
+    std::call_once(attr_once, [] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemm_kernel<kBM, kBN, kWN, kStages>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, KCfg::LDS);
+    });
+    if (attr_err != hipSuccess) return attr_err;
+    uint32_t *ah = static_cast<uint32_t *>(workspace);
+    const int units = a.M * (a.K / 32) * 4;
+    const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
+    hipLaunchKernelGGL(b1_pack_act_kernel, dim3(pgrid), dim3(256), 0, s, a.act, a.lda, ah, a.M, a.K);
+    const int tiles_m = (a.M + kBM - 1) / kBM, tiles_n = (a.N + kBN - 1) / kBN;
+    hipLaunchKernelGGL((b1_gemm_kernel<kBM, kBN, kWN, kStages>), dim3(tiles_m * tiles_n), dim3(KCfg::NT), KCfg::LDS,
+                       s, reinterpret_cast<const uint16_t *>(ah), a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite,
+                       tiles_n);
     return hipGetLastError();
 }
 

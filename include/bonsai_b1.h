@@ -100,6 +100,29 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
                          hipStream_t stream);
 
 /*
+ * The FAST GEMM packs the activations to fp16 once into a device workspace
+ * of bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) bytes (0 when
+ * the call needs none).  bonsai_b1_linear_f32 keeps one library-owned
+ * workspace per (device, stream), grown on demand with hipMalloc; while a
+ * stream is being captured it never allocates and, lacking a large enough
+ * buffer, runs the GEMM variant that converts activations tile by tile.
+ * bonsai_b1_linear_f32_ws takes the caller's workspace instead (NULL or too
+ * small selects that same variant) and never allocates.  Results do not
+ * depend on the variant.  Concurrent calls on one stream are ordered; calls
+ * on different streams use different workspaces.
+ */
+size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode);
+
+int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
+                            int in_dim, int out_dim, int batch, float *out,
+                            int64_t ldo, int mode, int32_t *nonfinite,
+                            void *workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+
+/* Frees every library-owned workspace (all devices); waits for the device. */
+void bonsai_b1_release_workspaces(void);
+
+/*
  * Builder-style call; replaces bonsai::b1_linear(ctx, act, w, n_threads, ud)
  * (src/b1_0_kernel.h:290-300): fills ud from w (magic, in_dim, out_dim) and
  * runs the op for `batch` rows of act (the reference's act->ne[1]).
