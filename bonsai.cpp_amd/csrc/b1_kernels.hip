@@ -82,6 +82,17 @@ __device__ __forceinline__ void lds_barrier() {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Global -> LDS copies without VGPR staging (global_load_lds_dwordx4 / x3).
+// `lds` must be wave-uniform (it goes through M0); lane i lands at
+// lds + i * size.  Kept as plain device functions so that kernel templates
+// using them still instantiate on the host pass.
+__device__ __forceinline__ void dma_lds16(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma_lds12(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 12, 0, 0);
+}
+
 __device__ __forceinline__ uint32_t dup_lo16(uint32_t d) {
     return __builtin_amdgcn_perm(d, d, 0x01000100u);
 }
@@ -426,12 +437,10 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
         uint8_t *sw = smem + C::BBASE + slot * C::BSTAGE + wave * C::BWAVE;
 #pragma unroll
         for (int i = 0; i < C::LPW; ++i)
-            __builtin_amdgcn_global_load_lds(abase + aoff[i] + (uint32_t)ks * C::ROWB,
-                                             (lds_void_t *)(sa + (wave * C::LPW + i) * 1024), 16, 0, 0);
+            dma_lds16(abase + aoff[i] + (uint32_t)ks * C::ROWB, sa + (wave * C::LPW + i) * 1024);
 #pragma unroll
         for (int pl = 0; pl < 2; ++pl)
-            __builtin_amdgcn_global_load_lds(w + boff + (uint32_t)ks * 24 + pl * 12,
-                                             (lds_void_t *)(sw + pl * 768), 12, 0, 0);
+            dma_lds12(w + boff + (uint32_t)ks * 24 + pl * 12, sw + pl * 768);
     };
 
     // Fragment offsets: lane (li, g) reads row li (+32 mt) at chunk
@@ -702,10 +711,13 @@ static bool fast_layout_ok(const LinearArgs &a) {
 
 bool gemm_supported(const LinearArgs &a) { return fast_layout_ok(a); }
 
-// GEMM over pre-packed activations: K % 256 == 0 (every 4-block weight
-// chunk is 8-byte aligned) and 8-byte aligned weights.
+// GEMM over pre-packed activations: K % 256 == 0 (an even number of 4-block
+// stages) and byte offsets into the packed activations and the weights that
+// fit the kernel's 32-bit offsets.
 static bool packed_gemm_ok(const LinearArgs &a) {
-    return a.K % 256 == 0 && (reinterpret_cast<uintptr_t>(a.w) & 7u) == 0;
+    const uint64_t act_bytes = (uint64_t)a.M * (uint64_t)a.K * 2;
+    const uint64_t w_bytes = (uint64_t)a.N * (uint64_t)(a.K / 32) * 6;
+    return a.K % 256 == 0 && act_bytes < (1ull << 32) && w_bytes < (1ull << 32);
 }
 
 size_t gemm_workspace_bytes(const LinearArgs &a) {
@@ -729,10 +741,11 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
                            tiles_n);
         return hipGetLastError();
     }
+    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages>;
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
-    std::call_once(attr_once, [] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemm_kernel<kBM, kBN, kWN, kStages>),
+    std::call_once(attr_once, [kernel] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, KCfg::LDS);
     });
     if (attr_err != hipSuccess) return attr_err;
@@ -741,9 +754,8 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
     const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
     hipLaunchKernelGGL(b1_pack_act_kernel, dim3(pgrid), dim3(256), 0, s, a.act, a.lda, ah, a.M, a.K);
     const int tiles_m = (a.M + kBM - 1) / kBM, tiles_n = (a.N + kBN - 1) / kBN;
-    hipLaunchKernelGGL((b1_gemm_kernel<kBM, kBN, kWN, kStages>), dim3(tiles_m * tiles_n), dim3(KCfg::NT), KCfg::LDS,
-                       s, reinterpret_cast<const uint16_t *>(ah), a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite,
-                       tiles_n);
+    hipLaunchKernelGGL(kernel, dim3(tiles_m * tiles_n), dim3(KCfg::NT), KCfg::LDS, s,
+                       reinterpret_cast<const uint16_t *>(ah), a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, tiles_n);
     return hipGetLastError();
 }
 
