@@ -82,15 +82,12 @@ __device__ __forceinline__ void lds_barrier() {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Global -> LDS copies without VGPR staging (global_load_lds_dwordx4 / x3).
+// Global -> LDS copy without VGPR staging (global_load_lds_dwordx4).
 // `lds` must be wave-uniform (it goes through M0); lane i lands at
 // lds + i * size.  Kept as plain device functions so that kernel templates
 // using them still instantiate on the host pass.
 __device__ __forceinline__ void dma_lds16(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 16, 0, 0);
-}
-__device__ __forceinline__ void dma_lds12(const void *src, void *lds) {
-    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 12, 0, 0);
 }
 
 __device__ __forceinline__ uint32_t dup_lo16(uint32_t d) {
@@ -371,14 +368,13 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
 // Wide-tile GEMM over pre-packed fp16 activations.  Work-group tile BM x BN,
 // NW = BN/WN waves side by side along N (each wave BM x WN; all waves share
 // the activation rows, so no weight column is expanded twice).  K advances
-// in stages of 128 (4 blocks).  Both operands of a stage go global -> LDS
-// directly (global_load_lds_dwordx4 for activations, _dwordx3 for the 24
-// packed bytes per weight column), with no VGPR staging, into a two-slot
-// ring: stage s+1 is fetched while stage s is computed.
-// Activation rows are 256 bytes in LDS with 16-byte chunk c of row r stored
-// at position c ^ (r & 7), so the 8 lanes of a ds_read_b128 phase hit 8
-// different bank groups.  Weight bytes sit per wave as two planes of
-// 64 columns x 12 bytes (blocks 0-1 and blocks 2-3 of the stage).
+// in stages of 128 (4 blocks).  Activation stages go global -> LDS directly
+// (global_load_lds_dwordx4, no VGPR staging) into a two-slot ring that
+// fills exactly the first 64 KB of LDS; the 24 packed bytes per weight
+// column and stage go to VGPRs.  Stage s+1 is fetched while stage s is
+// computed.  Activation rows are 256 bytes in LDS with 16-byte chunk c of
+// row r stored at position c ^ (r & 7), so the 8 lanes of a ds_read_b128
+// phase hit 8 different bank groups.
 
 template <int BM, int BN, int WN, int STAGES>
 struct Gemm2Cfg {
@@ -387,13 +383,10 @@ struct Gemm2Cfg {
     static constexpr int KC = 128;                   // K per stage (4 blocks)
     static constexpr int ROWB = KC * 2;              // LDS bytes per row
     static constexpr int ASTAGE = BM * ROWB;         // activation bytes per slot
-    static constexpr int BWAVE = WN * 24;            // weight bytes per wave per slot
-    static constexpr int BSTAGE = NW * BWAVE;        // weight bytes per slot
-    static constexpr int BBASE = STAGES * ASTAGE;    // weight slots follow the activation slots
     static constexpr int LPW = ASTAGE / 1024 / NW;   // 1 KB activation loads per wave
-    static constexpr int LDS = STAGES * (ASTAGE + BSTAGE);
+    static constexpr int LDS = STAGES * ASTAGE;
     static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
-    static_assert(WN == 64, "one weight column per lane");
+    static_assert(LDS <= 65536, "LDS-DMA destinations stay below 64 KB");
     static_assert((STAGES - 1) * ASTAGE + (MT - 1) * 32 * ROWB + 128 < 65536,
                   "fragment offsets fit the ds_read immediate");
 };
@@ -429,18 +422,25 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
         const int c = (lane & 15) ^ (row & 7);
         aoff[i] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + (uint32_t)c * 8) * 2;
     }
-    // Weight loads: lane L fetches 12 bytes of column n0 + 64 wave + L per
-    // plane.  Columns past N read row N-1 and are never stored.
-    const uint32_t boff = (uint32_t)min(n0 + wave * WN + lane, N - 1) * rs;
-    auto issue = [&](int ks, int slot) {
+    auto issue_a = [&](int ks, int slot) {
         uint8_t *sa = smem + slot * C::ASTAGE;
-        uint8_t *sw = smem + C::BBASE + slot * C::BSTAGE + wave * C::BWAVE;
 #pragma unroll
         for (int i = 0; i < C::LPW; ++i)
             dma_lds16(abase + aoff[i] + (uint32_t)ks * C::ROWB, sa + (wave * C::LPW + i) * 1024);
+    };
+    // Packed weights: lane column n, 24 bytes (4 blocks) per stage, into
+    // VGPRs.  Columns past N read row N-1 and are never stored.
+    const int ncol = n0 + wave * WN + li;
+    uint32_t boff[C::NTL];
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl)
-            dma_lds12(w + boff + (uint32_t)ks * 24 + pl * 12, sw + pl * 768);
+    for (int nt = 0; nt < C::NTL; ++nt) boff[nt] = (uint32_t)min(ncol + nt * 32, N - 1) * rs;
+    auto load_b = [&](int ks, uint32_t (&d)[C::NTL][6]) {
+#pragma unroll
+        for (int nt = 0; nt < C::NTL; ++nt) {
+            const uint32_t *src = reinterpret_cast<const uint32_t *>(w + boff[nt] + (uint32_t)ks * 24);
+#pragma unroll
+            for (int q = 0; q < 6; ++q) d[nt][q] = src[q];
+        }
     };
 
     // Fragment offsets: lane (li, g) reads row li (+32 mt) at chunk
@@ -451,7 +451,6 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
 #pragma unroll
         for (int h = 0; h < 2; ++h)
             foff[b1][h] = li * C::ROWB + (((4 * b1 + 2 * h + g) ^ (li & 7)) * 16);
-    const uint32_t bq_off = C::BBASE + wave * C::BWAVE + li * 12;
 
     floatx16 acc[C::MT][C::NTL];
 #pragma unroll
@@ -465,9 +464,8 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
     // reads of step+1 are issued before the MFMAs of step, into a second
     // buffer; a scheduling fence per step keeps the compiler from hoisting
     // every read of the stage.
-    auto compute = [&](int slot) {
+    auto compute = [&](int slot, const uint32_t (&d)[C::NTL][6]) {
         const uint8_t *sb = smem + slot * C::ASTAGE;
-        const uint8_t *sq = smem + slot * C::BSTAGE + bq_off;
         auto read_frags = [&](int step, half8 (&af)[C::MT]) {
             const int b = step >> 1, h = step & 1;
 #pragma unroll
@@ -475,7 +473,7 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
                 af[mt] = *reinterpret_cast<const half8 *>(sb + mt * 32 * C::ROWB + foff[b & 1][h] + (b >> 1) * 128);
         };
         half8 afa[C::MT], afb[C::MT];
-        uint32_t d[C::NTL][3], s2[C::NTL], wg[C::NTL];
+        uint32_t s2[C::NTL], wg[C::NTL];
         read_frags(0, afa);
 #pragma unroll
         for (int step = 0; step < 8; ++step) {
@@ -486,16 +484,13 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
             if (h == 0) {
 #pragma unroll
                 for (int nt = 0; nt < C::NTL; ++nt) {
+                    const int q = (b >> 1) * 3;
                     if ((b & 1) == 0) {
-                        const uint32_t *src = reinterpret_cast<const uint32_t *>(sq + nt * 384 + (b >> 1) * 768);
-                        d[nt][0] = src[0];
-                        d[nt][1] = src[1];
-                        d[nt][2] = src[2];
-                        s2[nt] = dup_lo16(d[nt][0]);
-                        wg[nt] = __builtin_amdgcn_alignbit(d[nt][1], d[nt][0], 16) >> (4 * g);
+                        s2[nt] = dup_lo16(d[nt][q]);
+                        wg[nt] = __builtin_amdgcn_alignbit(d[nt][q + 1], d[nt][q], 16) >> (4 * g);
                     } else {
-                        s2[nt] = dup_hi16(d[nt][1]);
-                        wg[nt] = d[nt][2] >> (4 * g);
+                        s2[nt] = dup_hi16(d[nt][q + 1]);
+                        wg[nt] = d[nt][q + 2] >> (4 * g);
                     }
                 }
             }
@@ -519,21 +514,26 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
     // stage s+1's loads then refill while stage s is computed.  The loop is
     // unrolled by two so that slot offsets are compile-time; the stage count
     // K/128 is even (K % 256 == 0), so the loop has no exit mid-body.
-    issue(0, 0);
+    uint32_t bq0[C::NTL][6], bq1[C::NTL][6];
+    issue_a(0, 0);
+    load_b(0, bq0);
     for (int s = 0; s < nstage; s += 2) {
         wait_vmcnt<0>();
         lds_barrier();
-        issue(s + 1, 1);
-        compute(0);
+        issue_a(s + 1, 1);
+        load_b(s + 1, bq1);
+        compute(0, bq0);
         wait_vmcnt<0>();
         lds_barrier();
-        if (s + 2 < nstage) issue(s + 2, 0);
-        compute(1);
+        if (s + 2 < nstage) {
+            issue_a(s + 2, 0);
+            load_b(s + 2, bq0);
+        }
+        compute(1, bq1);
     }
 
     // Epilogue.  32x32 accumulator layout: lane column li, rows
     // 8*(v/4) + 4*g + v%4 of each sub-tile; stored negated (see top).
-    const int ncol = n0 + wave * WN + li;
     int bad = 0;
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt) {
