@@ -373,8 +373,8 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
 // fills exactly the first 64 KB of LDS; the 24 packed bytes per weight
 // column and stage go to VGPRs.  Stage s+1 is fetched while stage s is
 // computed.  Activation rows are 256 bytes in LDS with 16-byte chunk c of
-// row r stored at position c ^ (r & 7), so the 8 lanes of a ds_read_b128
-// phase hit 8 different bank groups.
+// row r stored at position c ^ (r & 15), so the 16 lanes that one
+// ds_read_b128 phase serves (64 banks) hit 16 different bank groups.
 
 template <int BM, int BN, int WN, int STAGES>
 struct Gemm2Cfg {
@@ -413,13 +413,13 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
 
     // Activation loads: load j of a stage fills LDS bytes [1024 j, +1024)
     // = rows 4j..4j+3; lane L writes position L % 16 of row 4j + L / 16,
-    // which holds chunk (L % 16) ^ (row & 7).  Rows past M read row M-1.
+    // which holds chunk (L % 16) ^ (row & 15).  Rows past M read row M-1.
     uint32_t aoff[C::LPW];
 #pragma unroll
     for (int i = 0; i < C::LPW; ++i) {
         const int j = wave * C::LPW + i;
         const int row = 4 * j + (lane >> 4);
-        const int c = (lane & 15) ^ (row & 7);
+        const int c = (lane & 15) ^ (row & 15);
         aoff[i] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + (uint32_t)c * 8) * 2;
     }
     auto issue_a = [&](int ks, int slot) {
@@ -444,13 +444,13 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
     };
 
     // Fragment offsets: lane (li, g) reads row li (+32 mt) at chunk
-    // c = 4b + 2h + g, stored at position c ^ (li & 7).
-    uint32_t foff[2][2];
+    // c = 4b + 2h + g, stored at position c ^ (li & 15).
+    uint32_t foff[4][2];
 #pragma unroll
-    for (int b1 = 0; b1 < 2; ++b1)
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-            foff[b1][h] = li * C::ROWB + (((4 * b1 + 2 * h + g) ^ (li & 7)) * 16);
+            foff[b][h] = li * C::ROWB + (((4 * b + 2 * h + g) ^ (li & 15)) * 16);
 
     floatx16 acc[C::MT][C::NTL];
 #pragma unroll
@@ -470,7 +470,7 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
             const int b = step >> 1, h = step & 1;
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt)
-                af[mt] = *reinterpret_cast<const half8 *>(sb + mt * 32 * C::ROWB + foff[b & 1][h] + (b >> 1) * 128);
+                af[mt] = *reinterpret_cast<const half8 *>(sb + mt * 32 * C::ROWB + foff[b][h]);
         };
         half8 afa[C::MT], afb[C::MT];
         uint32_t s2[C::NTL], wg[C::NTL];
@@ -575,9 +575,18 @@ constexpr int kGvQuads = 3;                    // 4-block quads per wave per pas
 constexpr int kGvBPW = 4 * kGvQuads;           // blocks per wave per pass
 constexpr int kGvChunk = kGvWaves * kGvBPW;    // blocks per pass (K 3072)
 constexpr int kGvMaxRG = 6;                    // 16-row groups per WG, max
+constexpr int kGvAUnits = 6;                   // activation units per lane per batch
+constexpr int kGvWaveLds = kGvBPW * 4 * 16 * 16; // fp16 fragments of one wave (12 KB)
+constexpr int kGvLds = kGvWaves * kGvWaveLds;  // 96 KB; the reduction reuses it
 
-__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, int groups) {
-    __shared__ floatx4 red[kGvWaves][kGvMaxRG][64];
+// The activation slice of a wave (Mp token slots x 12 blocks) is read with
+// coalesced float4 loads in units (block, t, token) -- token fastest, so
+// each unit pair covers 64 contiguous bytes of one token row -- converted to
+// fp16 pairs and written to the wave's LDS area already in MFMA fragment
+// order (fragment (q, t) = 64 lanes x 16 bytes), from which every lane then
+// reads its 12 fragments with ds_read_b128.
+__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, int groups, int mp_log2) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, g = lane >> 4;
     const int nwg = gridDim.x, bid = blockIdx.x;
@@ -586,8 +595,8 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
     const int nrg = rg1 - rg0;
     const int nb = p.K / 32;
     const size_t rs = (size_t)nb * 6;
-    const bool tok_ok = col < p.M;
-    const float *arow = p.act + (size_t)(tok_ok ? col : 0) * p.lda;
+    const int mp = 1 << mp_log2; // token slots, power of two >= M
+    uint8_t *abuf = gsm + wave * kGvWaveLds;
     // Block 4q+g has the parity of g (the slice start and 4q are even).  An
     // even block starts a 4-byte aligned 8-byte window; an odd block sits at
     // byte 2 of the window that starts 2 bytes before it.
@@ -602,6 +611,8 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
     for (int kb0 = 0; kb0 < nb; kb0 += kGvChunk) {
         const int wb0 = kb0 + wave * kGvBPW;
 
+        // Packed weights first, so their latency overlaps the activation
+        // traffic: the 6-byte block 4q+g of row (rg0 + r) * 16 + col.
         uint32_t wd[kGvMaxRG][kGvQuads][2];
 #pragma unroll
         for (int r = 0; r < kGvMaxRG; ++r) {
@@ -620,30 +631,45 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
             }
         }
 
-        // Activation fragments.  All loads are issued unconditionally (row and
-        // block clamped into range) before any is converted, so they overlap;
-        // out-of-range tokens/blocks are zeroed afterwards.
-        floatx4 araw[kGvQuads][4][2];
+        // Activations -> fp16 fragments in LDS.  Unit u = (bl*4 + t)*mp + tok
+        // loads a[tok][32 (wb0+bl) + 4t .. +3] and the 4 elements 16 later.
+        const int units = 48 << mp_log2;
+        for (int base = 0; base < units; base += 64 * kGvAUnits) {
+            floatx4 lo[kGvAUnits], hi[kGvAUnits];
 #pragma unroll
-        for (int q = 0; q < kGvQuads; ++q) {
-            const int blk = min(wb0 + 4 * q + g, nb - 1);
+            for (int i = 0; i < kGvAUnits; ++i) {
+                const int u = min(base + i * 64 + lane, units - 1);
+                const int tok = min(u & (mp - 1), p.M - 1);
+                const int bt = u >> mp_log2;
+                const int blk = min(wb0 + (bt >> 2), nb - 1);
+                const float *src = p.act + (size_t)tok * p.lda + (size_t)blk * 32 + 4 * (bt & 3);
+                lo[i] = *reinterpret_cast<const floatx4 *>(src);
+                hi[i] = *reinterpret_cast<const floatx4 *>(src + 16);
+            }
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float *src = arow + (size_t)blk * 32 + 4 * t;
-                araw[q][t][0] = *reinterpret_cast<const floatx4 *>(src);
-                araw[q][t][1] = *reinterpret_cast<const floatx4 *>(src + 16);
+            for (int i = 0; i < kGvAUnits; ++i) {
+                const int u = base + i * 64 + lane;
+                const int tok = u & (mp - 1), bt = u >> mp_log2;
+                const int bl = bt >> 2, t = bt & 3;
+                if (u < units) {
+                    const bool ok = wb0 + bl < nb;
+                    u32x4 v;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) v[j] = ok ? pack_f16(lo[i][j], hi[i][j]) : 0u;
+                    *reinterpret_cast<u32x4 *>(abuf + ((((bl >> 2) * 4 + t) * 64) + (bl & 3) * 16 + tok) * 16) = v;
+                }
             }
         }
+        // Same-wave LDS accesses complete in order; no barrier is needed
+        // between this wave's writes and its reads.
         u32x4 af[kGvQuads][4];
 #pragma unroll
-        for (int q = 0; q < kGvQuads; ++q) {
-            const bool ok = tok_ok && wb0 + 4 * q + g < nb;
+        for (int q = 0; q < kGvQuads; ++q)
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    af[q][t][j] = ok ? pack_f16(araw[q][t][0][j], araw[q][t][1][j]) : 0u;
-        }
+            for (int t = 0; t < 4; ++t) {
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(abuf + ((q * 4 + t) * 64 + lane) * 16);
+                af[q][t] = col < p.M ? v : u32x4{0u, 0u, 0u, 0u};
+            }
 
 #pragma unroll
         for (int q = 0; q < kGvQuads; ++q) {
@@ -669,12 +695,14 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
         }
     }
 
-    // Cross-wave (split-K) reduction in a fixed order, then store.  16x16
-    // accumulator layout: lane column = lane & 15 (weight row), rows
-    // 4*(lane >> 4) + v (tokens).
+    // Cross-wave (split-K) reduction in a fixed order, in LDS reused from the
+    // activation fragments, then store.  16x16 accumulator layout: lane
+    // column = lane & 15 (weight row), rows 4*(lane >> 4) + v (tokens).
+    __syncthreads();
+    floatx4 *red = reinterpret_cast<floatx4 *>(gsm); // [wave][rg][lane]
 #pragma unroll
     for (int r = 0; r < kGvMaxRG; ++r)
-        if (r < nrg) red[wave][r][lane] = acc[r];
+        if (r < nrg) red[(wave * kGvMaxRG + r) * 64 + lane] = acc[r];
     __syncthreads();
     int bad = 0;
     for (int e = tid; e < nrg * 256; e += kGvWaves * 64) {
@@ -682,7 +710,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
         const int ln = 16 * (tok >> 2) + c, v = tok & 3;
         float s = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kGvWaves; ++w) s += red[w][r][ln][v];
+        for (int w = 0; w < kGvWaves; ++w) s += red[(w * kGvMaxRG + r) * 64 + ln][v];
         s = -s; // the expanded weights carry the opposite sign
         const int n = (rg0 + r) * 16 + c;
         if (tok < p.M && n < p.N) {
@@ -762,12 +790,21 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
 bool gemv_supported(const LinearArgs &a) { return a.M <= kGemvMaxM && fast_layout_ok(a); }
 
 hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
+    static std::once_flag attr_once;
+    static hipError_t attr_err = hipSuccess;
+    std::call_once(attr_once, [] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kGvLds);
+    });
+    if (attr_err != hipSuccess) return attr_err;
     const int groups = (a.N + 15) / 16;
     int nwg = num_cus > 0 ? num_cus : 256;
     const int need = (groups + kGvMaxRG - 1) / kGvMaxRG;
     if (nwg < need) nwg = need;
     if (nwg > groups) nwg = groups;
-    hipLaunchKernelGGL(b1_gemv_kernel, dim3(nwg), dim3(kGvWaves * 64), 0, s, a, groups);
+    int mp_log2 = 0;
+    while ((1 << mp_log2) < a.M) ++mp_log2;
+    hipLaunchKernelGGL(b1_gemv_kernel, dim3(nwg), dim3(kGvWaves * 64), kGvLds, s, a, groups, mp_log2);
     return hipGetLastError();
 }
 

@@ -160,13 +160,14 @@ def test_full_size_properties(torch, b1, shape):
     y3 = b1.linear(a, w2.view(-1), n, mode="auto")
     assert torch.equal(y3, 2.0 * y)
     # complemented sign words: every expanded weight flips sign exactly; the
-    # MFMA's internal rounding is not sign-symmetric bit for bit, so the
-    # negation is checked to 1e-6 of rms(y), far below any sign/index slip
+    # MFMA's internal rounding is not sign-symmetric bit for bit (measured:
+    # a few ulp of the output), so the negation is checked to 1e-5 of
+    # rms(y) -- one wrong sign (|scale * a| ~ 1e-2 rms) is 1000x larger
     wc = w.view(n, k // 32, 6).clone()
     wc[:, :, 2:6] ^= 0xFF
     yc = b1.linear(a, wc.view(-1), n, mode="auto")
     rms = float(y.pow(2).mean().sqrt())
-    assert float((yc + y).abs().max()) <= 1e-6 * rms
+    assert float((yc + y).abs().max()) <= 1e-5 * rms
     # sampled rows vs fp64
     rows = torch.linspace(0, m - 1, 24).long()
     from oracle import b1_oracle as o
