@@ -53,16 +53,21 @@ def time_launches(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall
 
 
-def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto"):
+def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto", sample_clock=False):
     a = synth.device_activations(m, k, 1)
     w = synth.device_packed_weights(n, k, 2)
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
+    sclk = []
+    if sample_clock:   # read the shader clock ~1 s into the warm-up, while the GPU is busy
+        import threading
+        th = threading.Thread(target=lambda: (time.sleep(1.0), sclk.append(observed_sclk_mhz())), daemon=True)
+        th.start()
     ms, wall = time_launches(torch, lambda i: b1.linear(a, w, n, out=y, mode=mode), steps, warmup)
     flop = 2.0 * m * n * k
     return {"shape": [m, k, n], "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12,
             "frac": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "wall_s": wall,
-            "inputs": (a, w)}
+            "sclk": sclk[0] if sclk else None, "inputs": (a, w)}
 
 
 def bench_gemv(torch, b1, synth, m, k, n, steps, warmup):
@@ -101,6 +106,18 @@ def bench_copy(torch, nbytes, steps, warmup):
     return {"bytes": nbytes, "ms": ms, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
 
 
+def observed_sclk_mhz():
+    """Current shader clock from rocm-smi (best effort; None if unavailable)."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True, timeout=20).stdout
+        m = re.search(r"sclk clock level:.*?\((\d+)Mhz\)", out)
+        return int(m.group(1)) if m else None
+    except Exception:
+        return None
+
+
 def cpu_baseline(a_dev, w_dev, n, rows, threads, reps=3):
     """The oracle's AVX2 restatement of src/b1_0_kernel.h:79-239 (ggml row
     split, nth = threads) on the first `rows` rows of the same device inputs
@@ -123,8 +140,10 @@ def cpu_baseline(a_dev, w_dev, n, rows, threads, reps=3):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=1000)
+    # ~1.5 s of GEMM before timing: the shader clock ramps for about a
+    # second under sustained MFMA load before it settles
+    ap.add_argument("--warmup", type=int, default=5000)
     ap.add_argument("--all", action="store_true", help="also time the other config shapes (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["gemm", "gemv", "copy"], default=None,
@@ -148,22 +167,24 @@ def main():
         return
     if args.only == "gemv":
         gm, gk, gn = GEMV
-        v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), args.warmup)
+        v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400))
         print(json.dumps({"gemv": {x: v[x] for x in v}}), flush=True)
         return
     log(f"[bench] GEMM M={m} K={k} N={n} steps={args.steps} warmup={args.warmup}")
-    g = bench_gemm(torch, b1, synth, m, k, n, args.steps, args.warmup)
-    log(f"[bench] GEMM {g['ms']*1e3:.1f} us  {g['tflops']:.1f} TFLOP/s  {100*g['frac']:.1f}% of fp16 MFMA peak")
+    g = bench_gemm(torch, b1, synth, m, k, n, args.steps, args.warmup, sample_clock=True)
+    sclk = g["sclk"]
+    log(f"[bench] GEMM {g['ms']*1e3:.1f} us  {g['tflops']:.1f} TFLOP/s  {100*g['frac']:.1f}% of fp16 MFMA peak"
+        f" (sclk during warm-up: {sclk} MHz)")
     if args.only == "gemm":
         print(json.dumps({"gemm": {x: g[x] for x in g if x != "inputs"}}), flush=True)
         return
 
     gm, gk, gn = GEMV
     log(f"[bench] GEMV M={gm} K={gk} N={gn}")
-    v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), args.warmup)
+    v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400))
     log(f"[bench] GEMV {v['us']:.2f} us/launch (graph)  {v['gbs']:.0f} GB/s packed  "
         f"{100*v['frac']:.1f}% of HBM peak; eager {v['eager_us']:.2f} us/call")
-    v1 = bench_gemv(torch, b1, synth, 1, gk, gn, max(args.steps, 200), args.warmup)
+    v1 = bench_gemv(torch, b1, synth, 1, gk, gn, max(args.steps, 200), min(args.warmup, 400))
     log(f"[bench] GEMV M=1 {v1['us']:.2f} us/call  {v1['gbs']:.0f} GB/s packed")
 
     extra = {}
@@ -172,7 +193,7 @@ def main():
                           ("c3_qkv", (4608, 3072, 9216)), ("c3_out", (4608, 3072, 3072)),
                           ("c4_up", (4608, 3072, 12288)), ("c4_down", (4608, 12288, 3072)),
                           ("c5_linear1", (4608, 3072, 21504)), ("c5_linear2", (4608, 15360, 3072))]:
-            r = bench_gemm(torch, b1, synth, *shp, max(10, args.steps // 2), 3)
+            r = bench_gemm(torch, b1, synth, *shp, max(10, args.steps // 4), 200)
             extra[name] = {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 1),
                            "frac": round(r["frac"], 4)}
             log(f"[bench] {name} {shp}: {r['ms']*1e3:.1f} us {r['tflops']:.1f} TFLOP/s")
@@ -207,7 +228,8 @@ def main():
                    "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(g["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(g["frac"], 4), "traffic": None,
-                     "algorithmic_flop": flop},
+                     "algorithmic_flop": flop, "sclk_mhz_observed": sclk,
+                     "note": "time per step includes the activation fp16 pre-pass kernel"},
         "gemv": {"M": gm, "K": gk, "N": gn, "us_per_call": round(v["us"], 3),
                  "GBps_packed": round(v["gbs"], 1), "frac_hbm": round(v["frac"], 4),
                  "packed_bytes": v["packed_bytes"], "weight_copies": v["weight_copies"],

@@ -375,6 +375,13 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
 // computed.  Activation rows are 256 bytes in LDS with 16-byte chunk c of
 // row r stored at position c ^ (r & 15), so the 16 lanes that one
 // ds_read_b128 phase serves (64 banks) hit 16 different bank groups.
+//
+// The grid is persistent (one work-group per CU, tiles strided by the grid
+// size): the first stage of a work-group's next tile is fetched before the
+// current tile's results are stored, so tile changes do not drain the
+// pipeline.  The MFMA takes the expanded weights as its A operand and the
+// activations as its B operand, so each lane's accumulator holds runs of 4
+// consecutive output columns and the epilogue writes 16-byte vectors.
 
 template <int BM, int BN, int WN, int STAGES>
 struct Gemm2Cfg {
@@ -395,14 +402,12 @@ template <int BM, int BN, int WN, int STAGES>
 __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t *__restrict__ ah,
                                                                  const uint8_t *__restrict__ w, int K, int N,
                                                                  int M, float *__restrict__ out, int64_t ldo,
-                                                                 int32_t *nonfinite, int tiles_n) {
+                                                                 int32_t *nonfinite, int tiles_n, int ntiles,
+                                                                 int vec_store) {
     using C = Gemm2Cfg<BM, BN, WN, STAGES>;
     static_assert(STAGES == 2, "two-slot ring");
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
-    const int t = xcd_tile(blockIdx.x, gridDim.x);
-    const int tm = t / tiles_n, tn = t - tm * tiles_n;
-    const int m0 = tm * BM, n0 = tn * BN;
     // The wave index is made visibly uniform: LDS-DMA destinations go
     // through M0 and must not depend on the lane.
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -411,29 +416,38 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
     const uint32_t rs = (uint32_t)(K / 32) * 6;
     const uint8_t *abase = reinterpret_cast<const uint8_t *>(ah);
 
+    // Tile t -> (m0, n0), contiguous runs of tiles per XCD (xcd_tile maps
+    // the persistent work-group, the loop then strides by the grid).
+    auto tile_origin = [&](int t, int &m0, int &n0) {
+        const int tm = t / tiles_n, tn = t - tm * tiles_n;
+        m0 = tm * BM;
+        n0 = tn * BN;
+    };
+
     // Activation loads: load j of a stage fills LDS bytes [1024 j, +1024)
     // = rows 4j..4j+3; lane L writes position L % 16 of row 4j + L / 16,
     // which holds chunk (L % 16) ^ (row & 15).  Rows past M read row M-1.
     uint32_t aoff[C::LPW];
+    uint32_t boff[C::NTL];
+    auto setup = [&](int m0, int n0) {
 #pragma unroll
-    for (int i = 0; i < C::LPW; ++i) {
-        const int j = wave * C::LPW + i;
-        const int row = 4 * j + (lane >> 4);
-        const int c = (lane & 15) ^ (row & 15);
-        aoff[i] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + (uint32_t)c * 8) * 2;
-    }
+        for (int i = 0; i < C::LPW; ++i) {
+            const int row = 4 * (wave * C::LPW + i) + (lane >> 4);
+            const int c = (lane & 15) ^ (row & 15);
+            aoff[i] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + (uint32_t)c * 8) * 2;
+        }
+        // Weight column of this lane per 32-column sub-tile; columns past N
+        // read row N-1 and are never stored.
+#pragma unroll
+        for (int nt = 0; nt < C::NTL; ++nt)
+            boff[nt] = (uint32_t)min(n0 + wave * WN + nt * 32 + li, N - 1) * rs;
+    };
     auto issue_a = [&](int ks, int slot) {
         uint8_t *sa = smem + slot * C::ASTAGE;
 #pragma unroll
         for (int i = 0; i < C::LPW; ++i)
             dma_lds16(abase + aoff[i] + (uint32_t)ks * C::ROWB, sa + (wave * C::LPW + i) * 1024);
     };
-    // Packed weights: lane column n, 24 bytes (4 blocks) per stage, into
-    // VGPRs.  Columns past N read row N-1 and are never stored.
-    const int ncol = n0 + wave * WN + li;
-    uint32_t boff[C::NTL];
-#pragma unroll
-    for (int nt = 0; nt < C::NTL; ++nt) boff[nt] = (uint32_t)min(ncol + nt * 32, N - 1) * rs;
     auto load_b = [&](int ks, uint32_t (&d)[C::NTL][6]) {
 #pragma unroll
         for (int nt = 0; nt < C::NTL; ++nt) {
@@ -453,12 +467,6 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
             foff[b][h] = li * C::ROWB + (((4 * b + 2 * h + g) ^ (li & 15)) * 16);
 
     floatx16 acc[C::MT][C::NTL];
-#pragma unroll
-    for (int i = 0; i < C::MT; ++i)
-#pragma unroll
-        for (int j = 0; j < C::NTL; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
     // One stage = 8 steps (block b = step/2, half h = step%2).  The fragment
     // reads of step+1 are issued before the MFMAs of step, into a second
@@ -502,56 +510,111 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
                 const half8 bf = __builtin_bit_cast(half8, bd);
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[mt], bf, acc[mt][nt], 0, 0, 0);
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf, cur[mt], acc[mt][nt], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // Pipeline (stage s in slot s % 2): at the top of stage s the wave waits
-    // for its own loads of stage s, then the barrier publishes every wave's
-    // part and retires all reads of slot (s+1) % 2 (stage s-1's), which
-    // stage s+1's loads then refill while stage s is computed.  The loop is
-    // unrolled by two so that slot offsets are compile-time; the stage count
-    // K/128 is even (K % 256 == 0), so the loop has no exit mid-body.
-    uint32_t bq0[C::NTL][6], bq1[C::NTL][6];
-    issue_a(0, 0);
-    load_b(0, bq0);
-    for (int s = 0; s < nstage; s += 2) {
-        wait_vmcnt<0>();
-        lds_barrier();
-        issue_a(s + 1, 1);
-        load_b(s + 1, bq1);
-        compute(0, bq0);
-        wait_vmcnt<0>();
-        lds_barrier();
-        if (s + 2 < nstage) {
-            issue_a(s + 2, 0);
-            load_b(s + 2, bq0);
-        }
-        compute(1, bq1);
-    }
-
-    // Epilogue.  32x32 accumulator layout: lane column li, rows
-    // 8*(v/4) + 4*g + v%4 of each sub-tile; stored negated (see top).
-    int bad = 0;
+    // Epilogue.  Accumulator (n, m) layout of the 32x32 MFMA with weights as
+    // A: lane column li = token m0 + 32 mt + li, rows 8*(v/4) + 4*g + v%4 =
+    // output columns; v = 4q..4q+3 are 4 consecutive columns.  Stored
+    // negated (the expanded weights carry the opposite sign).
+    auto epilogue = [&](int m0, int n0) {
+        int bad = 0;
+        const bool full = vec_store && m0 + BM <= M && n0 + BN <= N;
 #pragma unroll
-    for (int mt = 0; mt < C::MT; ++mt) {
+        for (int mt = 0; mt < C::MT; ++mt) {
+            const int m = m0 + mt * 32 + li;
 #pragma unroll
-        for (int nt = 0; nt < C::NTL; ++nt) {
-            const int n = ncol + nt * 32;
+            for (int nt = 0; nt < C::NTL; ++nt) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = m0 + mt * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-                if (m < M && n < N) {
-                    const float y = -acc[mt][nt][v];
-                    bad += !__builtin_isfinite(y);
-                    out[(size_t)m * ldo + n] = y;
+                for (int q = 0; q < 4; ++q) {
+                    const int n = n0 + wave * WN + nt * 32 + 8 * q + 4 * g;
+                    floatx4 y;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        y[r] = -acc[mt][nt][4 * q + r];
+                        bad += !__builtin_isfinite(y[r]);
+                    }
+                    if (full) {
+                        *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + n) = y;
+                    } else if (m < M) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (n + r < N) out[(size_t)m * ldo + n + r] = y[r];
+                    }
                 }
             }
         }
+        if (!full) {
+            // count only the stored elements on a partial tile
+            bad = 0;
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int m = m0 + mt * 32 + li;
+                        const int n = n0 + wave * WN + nt * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+                        bad += (m < M && n < N) && !__builtin_isfinite(acc[mt][nt][v]);
+                    }
+        }
+        count_nonfinite(nonfinite, bad);
+    };
+
+    int tile = xcd_tile(blockIdx.x, gridDim.x);
+    int m0, n0;
+    tile_origin(tile, m0, n0);
+    setup(m0, n0);
+    uint32_t bq0[C::NTL][6], bq1[C::NTL][6];
+    issue_a(0, 0);
+    load_b(0, bq0);
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+            for (int j = 0; j < C::NTL; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+        // Pipeline (stage s in slot s % 2): at the top of stage s the wave
+        // waits for its own outstanding memory operations, then the barrier
+        // publishes every wave's part of stage s and retires all reads of
+        // slot (s+1) % 2 (stage s-1's), which stage s+1's loads then refill
+        // while stage s is computed.  The loop is unrolled by two so that
+        // slot offsets are compile-time; the stage count K/128 is even
+        // (K % 256 == 0), so the loop has no exit mid-body.
+        for (int s = 0; s < nstage; s += 2) {
+            wait_vmcnt<0>();
+            lds_barrier();
+            issue_a(s + 1, 1);
+            load_b(s + 1, bq1);
+            compute(0, bq0);
+            wait_vmcnt<0>();
+            lds_barrier();
+            if (s + 2 < nstage) {
+                issue_a(s + 2, 0);
+                load_b(s + 2, bq0);
+            }
+            compute(1, bq1);
+        }
+
+        // Slot 0 and bq0 were last read before the final barrier: fetch the
+        // next tile's first stage now, then store this tile.
+        const int cm0 = m0, cn0 = n0;
+        tile += gridDim.x;
+        const bool more = tile < ntiles;
+        if (more) {
+            tile_origin(tile, m0, n0);
+            setup(m0, n0);
+            issue_a(0, 0);
+            load_b(0, bq0);
+        }
+        epilogue(cm0, cn0);
+        if (!more) break;
     }
-    count_nonfinite(nonfinite, bad);
 }
 
 // ----------------------------------------------------------------- gemv --
@@ -758,7 +821,6 @@ using KCfg = Gemm2Cfg<kBM, kBN, kWN, kStages>;
 } // namespace
 
 hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s) {
-    (void)num_cus;
     const size_t need = gemm_workspace_bytes(a);
     if (need == 0 || workspace == nullptr || ws_bytes < need) {
         // Fused-conversion kernel: no workspace needed.
@@ -782,8 +844,11 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
     const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
     hipLaunchKernelGGL(b1_pack_act_kernel, dim3(pgrid), dim3(256), 0, s, a.act, a.lda, ah, a.M, a.K);
     const int tiles_m = (a.M + kBM - 1) / kBM, tiles_n = (a.N + kBN - 1) / kBN;
-    hipLaunchKernelGGL(kernel, dim3(tiles_m * tiles_n), dim3(KCfg::NT), KCfg::LDS, s,
-                       reinterpret_cast<const uint16_t *>(ah), a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, tiles_n);
+    const int ntiles = tiles_m * tiles_n;
+    const int grid = ntiles < num_cus || num_cus <= 0 ? ntiles : num_cus; // persistent
+    const int vec_store = (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && a.ldo % 4 == 0;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, reinterpret_cast<const uint16_t *>(ah), a.w,
+                       a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, tiles_n, ntiles, vec_store);
     return hipGetLastError();
 }
 
