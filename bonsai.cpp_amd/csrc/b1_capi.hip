@@ -193,7 +193,7 @@ size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode) {
     if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
     if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return 0;
     if ((mode == BONSAI_B1_MODE_AUTO || mode == BONSAI_B1_MODE_FAST) && batch <= b1::kGemvMaxM) return 0;
-    return in_dim % 256 == 0 ? (size_t)batch * (size_t)in_dim * 2 : 0;
+    return in_dim % 384 == 0 ? (size_t)batch * (size_t)in_dim * 2 : 0;
 }
 
 int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,

@@ -23,8 +23,8 @@ struct LinearArgs {
 hipError_t launch_exact(const LinearArgs &a, hipStream_t s);
 
 // fp16 MFMA GEMM; requires K % 64 == 0, lda % 4 == 0, act 16-byte aligned.
-// With a workspace of gemm_workspace_bytes(a) bytes (> 0 when K % 256 == 0
-// and the weights are 8-byte aligned) the activations are packed to fp16
+// With a workspace of gemm_workspace_bytes(a) bytes (> 0 when K % 384 == 0)
+// the activations are packed to fp16
 // once and streamed into LDS directly; otherwise the kernel converts them
 // while staging each tile.
 bool gemm_supported(const LinearArgs &a);

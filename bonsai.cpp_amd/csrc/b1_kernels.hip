@@ -82,12 +82,17 @@ __device__ __forceinline__ void lds_barrier() {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// Global -> LDS copy without VGPR staging (global_load_lds_dwordx4).
-// `lds` must be wave-uniform (it goes through M0); lane i lands at
-// lds + i * size.  Kept as plain device functions so that kernel templates
-// using them still instantiate on the host pass.
+// Global -> LDS copies without VGPR staging.  `lds` must be wave-uniform
+// (it goes through M0).  global_load_lds_dwordx4: lane i's 16 bytes land at
+// lds + 16 i.  global_load_lds_dwordx3: lane i's 12 bytes also land at
+// lds + 16 i (a 16-byte lane stride, measured on gfx950), leaving 4 bytes
+// untouched per lane.  Kept as plain device functions so that kernel
+// templates using them still instantiate on the host pass.
 __device__ __forceinline__ void dma_lds16(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma_lds12(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 12, 0, 0);
 }
 
 __device__ __forceinline__ uint32_t dup_lo16(uint32_t d) {
@@ -368,67 +373,80 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
 // Wide-tile GEMM over pre-packed fp16 activations.  Work-group tile BM x BN,
 // NW = BN/WN waves side by side along N (each wave BM x WN; all waves share
 // the activation rows, so no weight column is expanded twice).  K advances
-// in stages of 128 (4 blocks).  Activation stages go global -> LDS directly
-// (global_load_lds_dwordx4, no VGPR staging) into a two-slot ring that
-// fills exactly the first 64 KB of LDS; the 24 packed bytes per weight
-// column and stage go to VGPRs.  Stage s+1 is fetched while stage s is
-// computed.  Activation rows are 256 bytes in LDS with 16-byte chunk c of
-// row r stored at position c ^ (r & 15), so the 16 lanes that one
-// ds_read_b128 phase serves (64 banks) hit 16 different bank groups.
+// in stages of 128 (4 blocks).  Both operands of a stage go global -> LDS
+// directly, with no VGPR staging, into three-slot rings fetched two stages
+// ahead: activations with global_load_lds_dwordx4 (rows of 256 bytes, 16-
+// byte chunk c of row r at position c ^ (r & 15), so the 16 lanes one
+// ds_read_b128 phase serves hit 16 different bank groups of the 64), and
+// the 24 packed bytes per weight column and stage with two
+// global_load_lds_dwordx3 (12 bytes per lane, landing at a 16-byte lane
+// stride).
 //
 // The grid is persistent (one work-group per CU, tiles strided by the grid
-// size): the first stage of a work-group's next tile is fetched before the
-// current tile's results are stored, so tile changes do not drain the
-// pipeline.  The MFMA takes the expanded weights as its A operand and the
-// activations as its B operand, so each lane's accumulator holds runs of 4
-// consecutive output columns and the epilogue writes 16-byte vectors.
+// size, in 4 x 8 tile groups so that the work-groups resident on one XCD
+// share both activation rows and weight columns in its L2): the first two
+// stages of a work-group's next tile are fetched before the current tile's
+// results are stored.  The MFMA takes the expanded weights as its A operand
+// and the activations as its B operand, so each lane's accumulator holds
+// runs of 4 consecutive output columns and the epilogue writes 16-byte
+// vectors.
 
-template <int BM, int BN, int WN, int STAGES>
-struct Gemm2Cfg {
+template <int BM, int BN, int WN>
+struct Gemm3Cfg {
     static constexpr int NW = BN / WN, NT = NW * 64;
     static constexpr int MT = BM / 32, NTL = WN / 32;
-    static constexpr int KC = 128;                   // K per stage (4 blocks)
-    static constexpr int ROWB = KC * 2;              // LDS bytes per row
-    static constexpr int ASTAGE = BM * ROWB;         // activation bytes per slot
-    static constexpr int LPW = ASTAGE / 1024 / NW;   // 1 KB activation loads per wave
-    static constexpr int LDS = STAGES * ASTAGE;
+    static constexpr int STAGES = 3;
+    static constexpr int KC = 128;                    // K per stage (4 blocks)
+    static constexpr int ROWB = KC * 2;               // LDS bytes per activation row
+    static constexpr int ASTAGE = BM * ROWB;          // activation bytes per slot
+    static constexpr int LPW = ASTAGE / 1024 / NW;    // 1 KB activation loads per wave
+    static constexpr int BWAVE = 2 * 1024;            // weight bytes per wave per slot
+    static constexpr int BSTAGE = NW * BWAVE;         // weight bytes per slot
+    static constexpr int BBASE = STAGES * ASTAGE;
+    static constexpr int LDS = STAGES * (ASTAGE + BSTAGE);
+    static constexpr int GROUP_M = 4;                 // tile grouping along M
     static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
-    static_assert(LDS <= 65536, "LDS-DMA destinations stay below 64 KB");
-    static_assert((STAGES - 1) * ASTAGE + (MT - 1) * 32 * ROWB + 128 < 65536,
-                  "fragment offsets fit the ds_read immediate");
+    static_assert(WN == 64, "one weight column per lane of the weight loads");
+    static_assert(LDS <= 160 * 1024, "gfx950 LDS");
 };
 
-template <int BM, int BN, int WN, int STAGES>
+template <int BM, int BN, int WN>
 __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t *__restrict__ ah,
                                                                  const uint8_t *__restrict__ w, int K, int N,
                                                                  int M, float *__restrict__ out, int64_t ldo,
-                                                                 int32_t *nonfinite, int tiles_n, int ntiles,
+                                                                 int32_t *nonfinite, int tiles_m, int tiles_n,
                                                                  int vec_store) {
-    using C = Gemm2Cfg<BM, BN, WN, STAGES>;
-    static_assert(STAGES == 2, "two-slot ring");
+    using C = Gemm3Cfg<BM, BN, WN>;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
     // The wave index is made visibly uniform: LDS-DMA destinations go
     // through M0 and must not depend on the lane.
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 31, g = lane >> 5;
-    const int nstage = K / C::KC;
+    const int nstage = K / C::KC; // a multiple of 3 (K % 384 == 0)
+    const int ntiles = tiles_m * tiles_n;
     const uint32_t rs = (uint32_t)(K / 32) * 6;
     const uint8_t *abase = reinterpret_cast<const uint8_t *>(ah);
 
-    // Tile t -> (m0, n0), contiguous runs of tiles per XCD (xcd_tile maps
-    // the persistent work-group, the loop then strides by the grid).
+    // Tile t -> (m0, n0): groups of GROUP_M tile rows, column-major inside a
+    // group, so a run of consecutive tiles covers GROUP_M x (run/GROUP_M).
     auto tile_origin = [&](int t, int &m0, int &n0) {
-        const int tm = t / tiles_n, tn = t - tm * tiles_n;
-        m0 = tm * BM;
-        n0 = tn * BN;
+        const int group = t / (C::GROUP_M * tiles_n);
+        const int first_m = group * C::GROUP_M;
+        const int gsize = min(C::GROUP_M, tiles_m - first_m);
+        const int tin = t - first_m * tiles_n;
+        m0 = (first_m + tin % gsize) * BM;
+        n0 = (tin / gsize) * BN;
     };
 
     // Activation loads: load j of a stage fills LDS bytes [1024 j, +1024)
-    // = rows 4j..4j+3; lane L writes position L % 16 of row 4j + L / 16,
-    // which holds chunk (L % 16) ^ (row & 15).  Rows past M read row M-1.
+    // of the slot = rows 4j..4j+3; lane L writes position L % 16 of row
+    // 4j + L / 16, which holds chunk (L % 16) ^ (row & 15).  Rows past M
+    // read row M-1.  Weight loads: lane L fetches 12 bytes (blocks 0-1, then
+    // 2-3 of the stage) of column n0 + 64 wave + L; columns past N read
+    // row N-1.  Neither is ever stored.
     uint32_t aoff[C::LPW];
-    uint32_t boff[C::NTL];
+    uint32_t boff;
     auto setup = [&](int m0, int n0) {
 #pragma unroll
         for (int i = 0; i < C::LPW; ++i) {
@@ -436,35 +454,28 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
             const int c = (lane & 15) ^ (row & 15);
             aoff[i] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + (uint32_t)c * 8) * 2;
         }
-        // Weight column of this lane per 32-column sub-tile; columns past N
-        // read row N-1 and are never stored.
-#pragma unroll
-        for (int nt = 0; nt < C::NTL; ++nt)
-            boff[nt] = (uint32_t)min(n0 + wave * WN + nt * 32 + li, N - 1) * rs;
+        boff = (uint32_t)min(n0 + wave * WN + lane, N - 1) * rs;
     };
-    auto issue_a = [&](int ks, int slot) {
-        uint8_t *sa = smem + slot * C::ASTAGE;
+    auto issue = [&](int ks, int slot) {
+        uint8_t *sa = smem + slot * C::ASTAGE + wave * C::LPW * 1024;
+        uint8_t *sw = smem + C::BBASE + slot * C::BSTAGE + wave * C::BWAVE;
 #pragma unroll
-        for (int i = 0; i < C::LPW; ++i)
-            dma_lds16(abase + aoff[i] + (uint32_t)ks * C::ROWB, sa + (wave * C::LPW + i) * 1024);
-    };
-    auto load_b = [&](int ks, uint32_t (&d)[C::NTL][6]) {
-#pragma unroll
-        for (int nt = 0; nt < C::NTL; ++nt) {
-            const uint32_t *src = reinterpret_cast<const uint32_t *>(w + boff[nt] + (uint32_t)ks * 24);
-#pragma unroll
-            for (int q = 0; q < 6; ++q) d[nt][q] = src[q];
-        }
+        for (int i = 0; i < C::LPW; ++i) dma_lds16(abase + aoff[i] + (uint32_t)ks * C::ROWB, sa + i * 1024);
+        dma_lds12(w + boff + (uint32_t)ks * 24, sw);
+        dma_lds12(w + boff + (uint32_t)ks * 24 + 12, sw + 1024);
     };
 
     // Fragment offsets: lane (li, g) reads row li (+32 mt) at chunk
-    // c = 4b + 2h + g, stored at position c ^ (li & 15).
+    // c = 4b + 2h + g, stored at position c ^ (li & 15); its weight column
+    // nt*32 + li sits at a 16-byte stride in each 1 KB half of the wave's
+    // weight area.
     uint32_t foff[4][2];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
             foff[b][h] = li * C::ROWB + (((4 * b + 2 * h + g) ^ (li & 15)) * 16);
+    const uint32_t qoff = C::BBASE + wave * C::BWAVE + li * 16;
 
     floatx16 acc[C::MT][C::NTL];
 
@@ -472,8 +483,9 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
     // reads of step+1 are issued before the MFMAs of step, into a second
     // buffer; a scheduling fence per step keeps the compiler from hoisting
     // every read of the stage.
-    auto compute = [&](int slot, const uint32_t (&d)[C::NTL][6]) {
+    auto compute = [&](int slot) {
         const uint8_t *sb = smem + slot * C::ASTAGE;
+        const uint8_t *sq = smem + slot * C::BSTAGE + qoff;
         auto read_frags = [&](int step, half8 (&af)[C::MT]) {
             const int b = step >> 1, h = step & 1;
 #pragma unroll
@@ -481,7 +493,7 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
                 af[mt] = *reinterpret_cast<const half8 *>(sb + mt * 32 * C::ROWB + foff[b][h]);
         };
         half8 afa[C::MT], afb[C::MT];
-        uint32_t s2[C::NTL], wg[C::NTL];
+        uint32_t d[C::NTL][3], s2[C::NTL], wg[C::NTL];
         read_frags(0, afa);
 #pragma unroll
         for (int step = 0; step < 8; ++step) {
@@ -492,13 +504,16 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
             if (h == 0) {
 #pragma unroll
                 for (int nt = 0; nt < C::NTL; ++nt) {
-                    const int q = (b >> 1) * 3;
                     if ((b & 1) == 0) {
-                        s2[nt] = dup_lo16(d[nt][q]);
-                        wg[nt] = __builtin_amdgcn_alignbit(d[nt][q + 1], d[nt][q], 16) >> (4 * g);
+                        const uint32_t *q = reinterpret_cast<const uint32_t *>(sq + (b >> 1) * 1024 + nt * 512);
+                        d[nt][0] = q[0];
+                        d[nt][1] = q[1];
+                        d[nt][2] = q[2];
+                        s2[nt] = dup_lo16(d[nt][0]);
+                        wg[nt] = __builtin_amdgcn_alignbit(d[nt][1], d[nt][0], 16) >> (4 * g);
                     } else {
-                        s2[nt] = dup_hi16(d[nt][q + 1]);
-                        wg[nt] = d[nt][q + 2] >> (4 * g);
+                        s2[nt] = dup_hi16(d[nt][1]);
+                        wg[nt] = d[nt][2] >> (4 * g);
                     }
                 }
             }
@@ -533,33 +548,22 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
                     const int n = n0 + wave * WN + nt * 32 + 8 * q + 4 * g;
                     floatx4 y;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        y[r] = -acc[mt][nt][4 * q + r];
-                        bad += !__builtin_isfinite(y[r]);
-                    }
+                    for (int r = 0; r < 4; ++r) y[r] = -acc[mt][nt][4 * q + r];
                     if (full) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) bad += !__builtin_isfinite(y[r]);
                         *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + n) = y;
                     } else if (m < M) {
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            if (n + r < N) out[(size_t)m * ldo + n + r] = y[r];
+                        for (int r = 0; r < 4; ++r) {
+                            if (n + r < N) {
+                                bad += !__builtin_isfinite(y[r]);
+                                out[(size_t)m * ldo + n + r] = y[r];
+                            }
+                        }
                     }
                 }
             }
-        }
-        if (!full) {
-            // count only the stored elements on a partial tile
-            bad = 0;
-#pragma unroll
-            for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < C::NTL; ++nt)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int m = m0 + mt * 32 + li;
-                        const int n = n0 + wave * WN + nt * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-                        bad += (m < M && n < N) && !__builtin_isfinite(acc[mt][nt][v]);
-                    }
         }
         count_nonfinite(nonfinite, bad);
     };
@@ -568,9 +572,8 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
     int m0, n0;
     tile_origin(tile, m0, n0);
     setup(m0, n0);
-    uint32_t bq0[C::NTL][6], bq1[C::NTL][6];
-    issue_a(0, 0);
-    load_b(0, bq0);
+    issue(0, 0);
+    issue(1, 1);
     for (;;) {
 #pragma unroll
         for (int i = 0; i < C::MT; ++i)
@@ -579,38 +582,38 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-        // Pipeline (stage s in slot s % 2): at the top of stage s the wave
-        // waits for its own outstanding memory operations, then the barrier
-        // publishes every wave's part of stage s and retires all reads of
-        // slot (s+1) % 2 (stage s-1's), which stage s+1's loads then refill
-        // while stage s is computed.  The loop is unrolled by two so that
-        // slot offsets are compile-time; the stage count K/128 is even
-        // (K % 256 == 0), so the loop has no exit mid-body.
-        for (int s = 0; s < nstage; s += 2) {
-            wait_vmcnt<0>();
-            lds_barrier();
-            issue_a(s + 1, 1);
-            load_b(s + 1, bq1);
-            compute(0, bq0);
-            wait_vmcnt<0>();
-            lds_barrier();
-            if (s + 2 < nstage) {
-                issue_a(s + 2, 0);
-                load_b(s + 2, bq0);
+        // Pipeline (stage s in slot s % 3).  At the top of stage s the wave
+        // waits for its own loads of stage s -- only stage s+1's LPW + 2
+        // loads may still be outstanding (all of them for the first stage of
+        // a tile, which follows the previous tile's stores) -- then the
+        // barrier publishes every wave's part of stage s and retires all
+        // reads of slot (s+2) % 3 (stage s-1's), which stage s+2's loads then
+        // refill.  Unrolled by three so that slots are compile-time; the
+        // stage count is a multiple of three, so the loop has no exit
+        // mid-body.
+        for (int s = 0; s < nstage; s += 3) {
+#pragma unroll
+            for (int u = 0; u < 3; ++u) {
+                if (s + u == 0 || s + u + 1 >= nstage)
+                    wait_vmcnt<0>();
+                else
+                    wait_vmcnt<C::LPW + 2>();
+                lds_barrier();
+                if (s + u + 2 < nstage) issue(s + u + 2, (u + 2) % 3);
+                compute(u);
             }
-            compute(1, bq1);
         }
 
-        // Slot 0 and bq0 were last read before the final barrier: fetch the
-        // next tile's first stage now, then store this tile.
+        // Slots 0 and 1 were last read before the final barrier: fetch the
+        // next tile's first two stages now, then store this tile.
         const int cm0 = m0, cn0 = n0;
         tile += gridDim.x;
         const bool more = tile < ntiles;
         if (more) {
             tile_origin(tile, m0, n0);
             setup(m0, n0);
-            issue_a(0, 0);
-            load_b(0, bq0);
+            issue(0, 0);
+            issue(1, 1);
         }
         epilogue(cm0, cn0);
         if (!more) break;
@@ -802,13 +805,13 @@ static bool fast_layout_ok(const LinearArgs &a) {
 
 bool gemm_supported(const LinearArgs &a) { return fast_layout_ok(a); }
 
-// GEMM over pre-packed activations: K % 256 == 0 (an even number of 4-block
-// stages) and byte offsets into the packed activations and the weights that
-// fit the kernel's 32-bit offsets.
+// GEMM over pre-packed activations: K % 384 == 0 (the stage count K/128 is
+// a multiple of the three ring slots) and byte offsets into the packed
+// activations and the weights that fit the kernel's 32-bit offsets.
 static bool packed_gemm_ok(const LinearArgs &a) {
     const uint64_t act_bytes = (uint64_t)a.M * (uint64_t)a.K * 2;
     const uint64_t w_bytes = (uint64_t)a.N * (uint64_t)(a.K / 32) * 6;
-    return a.K % 256 == 0 && act_bytes < (1ull << 32) && w_bytes < (1ull << 32);
+    return a.K % 384 == 0 && act_bytes < (1ull << 32) && w_bytes < (1ull << 32);
 }
 
 size_t gemm_workspace_bytes(const LinearArgs &a) {
@@ -816,8 +819,8 @@ size_t gemm_workspace_bytes(const LinearArgs &a) {
 }
 
 namespace {
-constexpr int kBM = 128, kBN = 512, kWN = 64, kStages = 2;
-using KCfg = Gemm2Cfg<kBM, kBN, kWN, kStages>;
+constexpr int kBM = 128, kBN = 512, kWN = 64;
+using KCfg = Gemm3Cfg<kBM, kBN, kWN>;
 } // namespace
 
 hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s) {
@@ -831,7 +834,7 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
                            tiles_n);
         return hipGetLastError();
     }
-    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages>;
+    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN>;
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(attr_once, [kernel] {
@@ -848,7 +851,7 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
     const int grid = ntiles < num_cus || num_cus <= 0 ? ntiles : num_cus; // persistent
     const int vec_store = (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && a.ldo % 4 == 0;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, reinterpret_cast<const uint16_t *>(ah), a.w,
-                       a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, tiles_n, ntiles, vec_store);
+                       a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, tiles_m, tiles_n, vec_store);
     return hipGetLastError();
 }
 

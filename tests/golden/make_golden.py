@@ -24,6 +24,7 @@ CASES = {
     "gemv_m8_k3072_n48": (8, 3072, 48, 105, 106),
     "gemm_m160_k192_n72": (160, 192, 72, 107, 108),
     "odd_blocks_m3_k96_n16": (3, 96, 16, 109, 110),
+    "gemm_m200_k384_n600": (200, 384, 600, 111, 112),
 }
 
 
