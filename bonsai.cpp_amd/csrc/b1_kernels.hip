@@ -402,12 +402,17 @@ struct Gemm3Cfg {
     static constexpr int LPW = ASTAGE / 1024 / NW;    // 1 KB activation loads per wave
     static constexpr int BWAVE = 2 * 1024;            // weight bytes per wave per slot
     static constexpr int BSTAGE = NW * BWAVE;         // weight bytes per slot
-    static constexpr int BBASE = STAGES * ASTAGE;
+    // Weight slots take the bottom of LDS and activation slots follow: the
+    // 12-byte weight reads (ds_read_b96) returned wrong data at LDS
+    // addresses at or above 64 KiB on gfx950, while ds_read_b128 and
+    // ds_read_b32 read correctly there (measured on MI355X).
+    static constexpr int ABASE = STAGES * BSTAGE;
     static constexpr int LDS = STAGES * (ASTAGE + BSTAGE);
     static constexpr int GROUP_M = 4;                 // tile grouping along M
     static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
     static_assert(WN == 64, "one weight column per lane of the weight loads");
     static_assert(LDS <= 160 * 1024, "gfx950 LDS");
+    static_assert(ABASE <= 65536, "ds_read_b96 addresses stay below 64 KiB");
 };
 
 template <int BM, int BN, int WN>
@@ -457,8 +462,8 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
         boff = (uint32_t)min(n0 + wave * WN + lane, N - 1) * rs;
     };
     auto issue = [&](int ks, int slot) {
-        uint8_t *sa = smem + slot * C::ASTAGE + wave * C::LPW * 1024;
-        uint8_t *sw = smem + C::BBASE + slot * C::BSTAGE + wave * C::BWAVE;
+        uint8_t *sa = smem + C::ABASE + slot * C::ASTAGE + wave * C::LPW * 1024;
+        uint8_t *sw = smem + slot * C::BSTAGE + wave * C::BWAVE;
 #pragma unroll
         for (int i = 0; i < C::LPW; ++i) dma_lds16(abase + aoff[i] + (uint32_t)ks * C::ROWB, sa + i * 1024);
         dma_lds12(w + boff + (uint32_t)ks * 24, sw);
@@ -475,7 +480,7 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
 #pragma unroll
         for (int h = 0; h < 2; ++h)
             foff[b][h] = li * C::ROWB + (((4 * b + 2 * h + g) ^ (li & 15)) * 16);
-    const uint32_t qoff = C::BBASE + wave * C::BWAVE + li * 16;
+    const uint32_t qoff = wave * C::BWAVE + li * 16;
 
     floatx16 acc[C::MT][C::NTL];
 
@@ -484,7 +489,7 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
     // buffer; a scheduling fence per step keeps the compiler from hoisting
     // every read of the stage.
     auto compute = [&](int slot) {
-        const uint8_t *sb = smem + slot * C::ASTAGE;
+        const uint8_t *sb = smem + C::ABASE + slot * C::ASTAGE;
         const uint8_t *sq = smem + slot * C::BSTAGE + qoff;
         auto read_frags = [&](int step, half8 (&af)[C::MT]) {
             const int b = step >> 1, h = step & 1;
