@@ -12,7 +12,9 @@ from .capi import (  # noqa: F401
     declared_symbols,
     library_path,
     linear,
+    linear_packed_f16,
     linear_raw,
     load,
+    pack_act_f16,
 )
 from . import synth  # noqa: F401

@@ -70,6 +70,12 @@ def load():
     L.bonsai_b1_version.restype = i
     L.bonsai_b1_linear_f32_f32.argtypes = [vp, i, i, vp]
     L.bonsai_b1_linear_f32_f32.restype = None
+    L.bonsai_b1_packed_act_bytes.argtypes = [i, i]
+    L.bonsai_b1_packed_act_bytes.restype = ctypes.c_size_t
+    L.bonsai_b1_pack_act_f16.argtypes = [vp, i64, i, i, vp, vp]
+    L.bonsai_b1_pack_act_f16.restype = i
+    L.bonsai_b1_linear_packed_f16.argtypes = [vp, vp, i, i, i, vp, i64, vp, vp]
+    L.bonsai_b1_linear_packed_f16.restype = i
     _lib = L
     return L
 
@@ -109,6 +115,41 @@ def linear(act, w_packed, out_dim: int, out=None, mode: str = "auto", nonfinite=
                                      out.data_ptr(), out.stride(0), MODES[mode], nf, _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_linear_f32")
+    return out
+
+
+def pack_act_f16(act, packed=None, stream=None):
+    """fp16 K-slot-paired activations of act[M, K] (bonsai_b1_pack_act_f16);
+    returns a uint8 cuda tensor of M*K*2 bytes."""
+    import torch
+    if act.dim() != 2 or act.dtype != torch.float32 or not act.is_cuda or act.stride(1) != 1:
+        raise ValueError("act must be a 2-D fp32 cuda tensor with unit column stride")
+    m, k = act.shape
+    nbytes = load().bonsai_b1_packed_act_bytes(m, k)
+    if packed is None:
+        packed = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=act.device)
+    if packed.numel() < nbytes or not packed.is_contiguous():
+        raise ValueError("packed must hold bonsai_b1_packed_act_bytes(M, K) contiguous bytes")
+    st = load().bonsai_b1_pack_act_f16(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(),
+                                       _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_pack_act_f16")
+    return packed
+
+
+def linear_packed_f16(packed, w_packed, in_dim: int, out_dim: int, batch: int, out=None, nonfinite=None,
+                      stream=None):
+    """out[batch, out_dim] from packed fp16 activations (bonsai_b1_linear_packed_f16)."""
+    import torch
+    if out is None:
+        out = torch.empty((batch, out_dim), dtype=torch.float32, device=packed.device)
+    if out.dim() != 2 or out.shape[0] != batch or out.shape[1] < out_dim or out.stride(1) != 1:
+        raise ValueError("out must be [batch, >=out_dim] fp32 with unit column stride")
+    nf = nonfinite.data_ptr() if nonfinite is not None else None
+    st = load().bonsai_b1_linear_packed_f16(packed.data_ptr(), w_packed.data_ptr(), in_dim, out_dim, batch,
+                                            out.data_ptr(), out.stride(0), nf, _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_linear_packed_f16")
     return out
 
 

@@ -205,6 +205,40 @@ int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
                        workspace_bytes, stream);
 }
 
+size_t bonsai_b1_packed_act_bytes(int batch, int in_dim) {
+    if (batch <= 0 || in_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
+    return (size_t)batch * (size_t)in_dim * 2;
+}
+
+int bonsai_b1_pack_act_f16(const float *act, int64_t lda, int in_dim, int batch, void *packed,
+                           hipStream_t stream) {
+    if (in_dim <= 0 || batch < 0 || in_dim % BONSAI_B1_BLOCK_SIZE || lda < in_dim) return BONSAI_B1_ERR_ARG;
+    if (batch > 0 && (!act || !packed)) return BONSAI_B1_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(packed) & 15u) return BONSAI_B1_ERR_ARG;
+    if (batch > 0 && !b1::pack_supported(act, lda, batch, in_dim)) return BONSAI_B1_ERR_ARG;
+    if (!current_device(nullptr)) return BONSAI_B1_ERR_DEVICE;
+    if (batch == 0) return BONSAI_B1_OK;
+    return b1::launch_pack(act, lda, batch, in_dim, packed, stream) == hipSuccess ? BONSAI_B1_OK
+                                                                                  : BONSAI_B1_ERR_HIP;
+}
+
+int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
+                                float *out, int64_t ldo, int32_t *nonfinite, hipStream_t stream) {
+    if (in_dim <= 0 || out_dim <= 0 || batch < 0 || ldo < out_dim) return BONSAI_B1_ERR_ARG;
+    if (batch > 0 && (!packed_act || !w || !out)) return BONSAI_B1_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(packed_act) & 15u) || (reinterpret_cast<uintptr_t>(w) & 3u) ||
+        (reinterpret_cast<uintptr_t>(out) & 3u))
+        return BONSAI_B1_ERR_ARG;
+    if (in_dim % 384 != 0 || (batch > 0 && !b1::gemm_packed_ok(batch, in_dim, out_dim))) return BONSAI_B1_ERR_ARG;
+    DeviceInfo *dev = current_device(nullptr);
+    if (!dev) return BONSAI_B1_ERR_DEVICE;
+    if (batch == 0) return BONSAI_B1_OK;
+    return b1::launch_gemm_packed(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
+                                  nonfinite, dev->num_cus, stream) == hipSuccess
+               ? BONSAI_B1_OK
+               : BONSAI_B1_ERR_HIP;
+}
+
 void bonsai_b1_release_workspaces(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     for (DeviceInfo &d : g_dev) {

@@ -31,6 +31,17 @@ bool gemm_supported(const LinearArgs &a);
 size_t gemm_workspace_bytes(const LinearArgs &a);
 hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s);
 
+// The two halves of the workspace path.  Packed activations: u32 word
+// (row m, 16 j + d) = fp16(a[m][32 j + d]) | fp16(a[m][32 j + d + 16]) << 16,
+// row stride K/2 words.  pack: K % 32 == 0, lda % 4 == 0, act 16-byte
+// aligned.  gemm_packed: gemm_packed_ok(M, K, N), packed 16-byte aligned,
+// w 4-byte aligned.
+bool pack_supported(const float *act, int64_t lda, int M, int K);
+hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed, hipStream_t s);
+bool gemm_packed_ok(int M, int K, int N);
+hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
+                              int32_t *nonfinite, int num_cus, hipStream_t s);
+
 // Small-M (M <= 16) bandwidth-bound kernel; requires K % 64 == 0,
 // lda % 4 == 0, act 16-byte aligned.
 bool gemv_supported(const LinearArgs &a);

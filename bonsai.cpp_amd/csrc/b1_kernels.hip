@@ -813,20 +813,52 @@ bool gemm_supported(const LinearArgs &a) { return fast_layout_ok(a); }
 // GEMM over pre-packed activations: K % 384 == 0 (the stage count K/128 is
 // a multiple of the three ring slots) and byte offsets into the packed
 // activations and the weights that fit the kernel's 32-bit offsets.
-static bool packed_gemm_ok(const LinearArgs &a) {
-    const uint64_t act_bytes = (uint64_t)a.M * (uint64_t)a.K * 2;
-    const uint64_t w_bytes = (uint64_t)a.N * (uint64_t)(a.K / 32) * 6;
-    return a.K % 384 == 0 && act_bytes < (1ull << 32) && w_bytes < (1ull << 32);
+bool gemm_packed_ok(int M, int K, int N) {
+    const uint64_t act_bytes = (uint64_t)M * (uint64_t)K * 2;
+    const uint64_t w_bytes = (uint64_t)N * (uint64_t)(K / 32) * 6;
+    return M > 0 && K > 0 && N > 0 && K % 384 == 0 && act_bytes < (1ull << 32) && w_bytes < (1ull << 32);
 }
 
 size_t gemm_workspace_bytes(const LinearArgs &a) {
-    return packed_gemm_ok(a) && fast_layout_ok(a) ? (size_t)a.M * a.K * 2 : 0;
+    return gemm_packed_ok(a.M, a.K, a.N) && fast_layout_ok(a) ? (size_t)a.M * a.K * 2 : 0;
+}
+
+bool pack_supported(const float *act, int64_t lda, int M, int K) {
+    return K % 32 == 0 && lda >= K && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(act) & 15u) == 0 &&
+           (uint64_t)M * (uint64_t)(K / 32) * 4 < (1ull << 31);
+}
+
+hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed, hipStream_t s) {
+    const int units = M * (K / 32) * 4;
+    const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
+    hipLaunchKernelGGL(b1_pack_act_kernel, dim3(pgrid), dim3(256), 0, s, act, lda, static_cast<uint32_t *>(packed),
+                       M, K);
+    return hipGetLastError();
 }
 
 namespace {
 constexpr int kBM = 128, kBN = 512, kWN = 64;
 using KCfg = Gemm3Cfg<kBM, kBN, kWN>;
 } // namespace
+
+hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
+                              int32_t *nonfinite, int num_cus, hipStream_t s) {
+    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN>;
+    static std::once_flag attr_once;
+    static hipError_t attr_err = hipSuccess;
+    std::call_once(attr_once, [kernel] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, KCfg::LDS);
+    });
+    if (attr_err != hipSuccess) return attr_err;
+    const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+    const int ntiles = tiles_m * tiles_n;
+    const int grid = ntiles < num_cus || num_cus <= 0 ? ntiles : num_cus; // persistent
+    const int vec_store = (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ldo % 4 == 0;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
+                       K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s) {
     const size_t need = gemm_workspace_bytes(a);
@@ -839,25 +871,9 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
                            tiles_n);
         return hipGetLastError();
     }
-    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN>;
-    static std::once_flag attr_once;
-    static hipError_t attr_err = hipSuccess;
-    std::call_once(attr_once, [kernel] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, KCfg::LDS);
-    });
-    if (attr_err != hipSuccess) return attr_err;
-    uint32_t *ah = static_cast<uint32_t *>(workspace);
-    const int units = a.M * (a.K / 32) * 4;
-    const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
-    hipLaunchKernelGGL(b1_pack_act_kernel, dim3(pgrid), dim3(256), 0, s, a.act, a.lda, ah, a.M, a.K);
-    const int tiles_m = (a.M + kBM - 1) / kBM, tiles_n = (a.N + kBN - 1) / kBN;
-    const int ntiles = tiles_m * tiles_n;
-    const int grid = ntiles < num_cus || num_cus <= 0 ? ntiles : num_cus; // persistent
-    const int vec_store = (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && a.ldo % 4 == 0;
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, reinterpret_cast<const uint16_t *>(ah), a.w,
-                       a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, tiles_m, tiles_n, vec_store);
-    return hipGetLastError();
+    hipError_t e = launch_pack(a.act, a.lda, a.M, a.K, workspace, s);
+    if (e != hipSuccess) return e;
+    return launch_gemm_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, s);
 }
 
 bool gemv_supported(const LinearArgs &a) { return a.M <= kGemvMaxM && fast_layout_ok(a); }

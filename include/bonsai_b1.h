@@ -123,6 +123,36 @@ int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
 void bonsai_b1_release_workspaces(void);
 
 /*
+ * The FAST GEMM in two halves, for a producer of activations that can emit
+ * them in fp16 once (the LayerNorm + modulation feeding each linear,
+ * src/diffuser_graph.cpp:347-352,444-448,479-480) and for linears that
+ * share one input (q/k/v of a block, src/diffuser_graph.cpp:354-361).
+ * Together they compute what bonsai_b1_linear_f32 computes in FAST mode for
+ * in_dim % 384 == 0; the reference's single op b1_linear_f32_f32
+ * (src/b1_0_kernel.h:37) has no such split.
+ *
+ * Packed activations: row m is in_dim/2 little-endian u32 words; word
+ * 16*j + d of the row holds fp16(act[m][32j+d]) in its low half and
+ * fp16(act[m][32j+d+16]) in its high half (round to nearest even), for
+ * block j < in_dim/32 and d < 16.  Total bonsai_b1_packed_act_bytes() bytes.
+ */
+size_t bonsai_b1_packed_act_bytes(int batch, int in_dim);
+
+/* act [batch][lda] fp32 (lda % 4 == 0, 16-byte aligned; in_dim % 32 == 0)
+ * -> packed (16-byte aligned, bonsai_b1_packed_act_bytes bytes).
+ * |act| must stay below 65504 (fp16 range). */
+int bonsai_b1_pack_act_f16(const float *act, int64_t lda, int in_dim,
+                           int batch, void *packed, hipStream_t stream);
+
+/* out[m][n] for packed activations (in_dim % 384 == 0, packed 16-byte
+ * aligned, w 4-byte aligned); same outputs as bonsai_b1_linear_f32 in
+ * FAST/GEMM mode on the activations that were packed.  Never allocates. */
+int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w,
+                                int in_dim, int out_dim, int batch,
+                                float *out, int64_t ldo, int32_t *nonfinite,
+                                hipStream_t stream);
+
+/*
  * Builder-style call; replaces bonsai::b1_linear(ctx, act, w, n_threads, ud)
  * (src/b1_0_kernel.h:290-300): fills ud from w (magic, in_dim, out_dim) and
  * runs the op for `batch` rows of act (the reference's act->ne[1]).

@@ -62,3 +62,34 @@ def test_null_pointers_rejected():
     buf = (ctypes.c_uint8 * 10)()
     assert lib.bonsai_b1_weights_upload(buf, 10, 64, 32, None, ctypes.byref(w)) == capi.ERR_ARG
     assert lib.bonsai_b1_weights_free(None) == capi.ERR_ARG
+
+
+def test_packed_act_bytes():
+    lib = bonsai_b1.load()
+    assert lib.bonsai_b1_packed_act_bytes(4096, 3072) == 4096 * 3072 * 2
+    assert lib.bonsai_b1_packed_act_bytes(0, 3072) == 0
+    assert lib.bonsai_b1_packed_act_bytes(8, 33) == 0
+
+
+@pytest.mark.parametrize("args", [
+    # (packed_ptr, in_dim, out_dim, batch, ldo)
+    (0x10000, 3072 - 32, 64, 8, 64),   # in_dim % 384 != 0
+    (0x10008, 3072, 64, 8, 64),        # packed activations not 16-byte aligned
+    (0x10000, 3072, 64, 8, 32),        # ldo < out_dim
+    (0x10000, 3072, 64, -1, 64),       # negative batch
+])
+def test_linear_packed_rejects_before_device(args):
+    pa, k, n, m, ldo = args
+    lib = bonsai_b1.load()
+    fake = 0x10000
+    assert lib.bonsai_b1_linear_packed_f16(pa, fake, k, n, m, fake, ldo, None, None) == capi.ERR_ARG
+
+
+def test_pack_rejects_before_device():
+    lib = bonsai_b1.load()
+    fake = 0x10000
+    assert lib.bonsai_b1_pack_act_f16(fake, 64, 48, 2, fake, None) == capi.ERR_ARG      # in_dim % 32
+    assert lib.bonsai_b1_pack_act_f16(fake, 66, 64, 2, fake, None) == capi.ERR_ARG      # lda % 4
+    assert lib.bonsai_b1_pack_act_f16(fake + 4, 64, 64, 2, fake, None) == capi.ERR_ARG  # act alignment
+    assert lib.bonsai_b1_pack_act_f16(fake, 64, 64, 2, fake + 8, None) == capi.ERR_ARG  # packed alignment
+    assert lib.bonsai_b1_pack_act_f16(None, 64, 64, 2, fake, None) == capi.ERR_ARG

@@ -320,3 +320,48 @@ def test_graph_replay_matches_eager(torch, b1, mode, m):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, ref), f"replay {i}"
+
+
+# ------------------------------------------- packed-activation entry points --
+
+def test_pack_act_layout_bit_exact(torch, b1, oracle):
+    """bonsai_b1_pack_act_f16: word 16j+d of row m = fp16(a[m][32j+d]) |
+    fp16(a[m][32j+d+16]) << 16, fp16 rounded to nearest even (the oracle's
+    conversion, itself pinned exhaustively against F16C)."""
+    rng = np.random.default_rng(5)
+    m, k = 5, 384
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    # rounding ties and near-ties, fp16 subnormals, signed zero, range edges
+    h = (np.arange(1, 1 + k, dtype=np.uint16) * 7 + 0x3C00).view(np.float16)
+    up = h.astype(np.float32).view(np.uint32) + (1 << 12)  # midpoints between fp16 neighbours
+    a[1] = up.view(np.float32)
+    a[2] = (up + 1).view(np.float32)                       # just above a tie
+    a[3] = rng.uniform(-6e-5, 6e-5, k).astype(np.float32)  # subnormal range
+    a[4, :8] = [0.0, -0.0, 65504.0, -65504.0, 65519.0, 6.1035156e-05, -5.96e-08, 2.98e-08]
+    d = torch.from_numpy(a).cuda()
+    packed = b1.pack_act_f16(d)
+    torch.cuda.synchronize()
+    got = packed.cpu().numpy().view(np.uint32).reshape(m, k // 2)
+    hb = oracle.fp32_to_fp16_bits(a).reshape(m, k // 32, 32).astype(np.uint32)
+    want = (hb[:, :, :16] | (hb[:, :, 16:] << 16)).reshape(m, k // 2)
+    say(f"  pack: {int((got != want).sum())} mismatching words of {got.size}")
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("m,k,n", [(200, 768, 600), (128, 384, 512), (1, 384, 40)])
+def test_linear_packed_matches_fused_entry(torch, b1, m, k, n):
+    """pack + linear_packed gives bit-for-bit what bonsai_b1_linear_f32 gives
+    in GEMM mode (same kernels), including a padded output stride."""
+    from bonsai_b1 import synth
+    a = synth.device_activations(m, k, 41)
+    w = synth.device_packed_weights(n, k, 42)
+    ref = b1.linear(a, w, n, mode="gemm")
+    out = torch.full((m, n + 12), 7.0, device="cuda")
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    packed = b1.pack_act_f16(a)
+    b1.linear_packed_f16(packed, w, k, n, m, out=out[:, :n], nonfinite=nf)
+    torch.cuda.synchronize()
+    say(f"  packed ({m},{k},{n}): max |diff| {float((out[:, :n] - ref).abs().max()):.3e}")
+    assert torch.equal(out[:, :n], ref)
+    assert bool((out[:, n:] == 7.0).all()), "columns past out_dim untouched"
+    assert int(nf.item()) == 0
