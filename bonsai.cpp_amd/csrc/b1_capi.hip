@@ -193,7 +193,7 @@ size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode) {
     if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
     if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return 0;
     if ((mode == BONSAI_B1_MODE_AUTO || mode == BONSAI_B1_MODE_FAST) && batch <= b1::kGemvMaxM) return 0;
-    return in_dim % 384 == 0 ? (size_t)batch * (size_t)in_dim * 2 : 0;
+    return b1::gemm_packed_ok(batch, in_dim, out_dim) ? (size_t)batch * (size_t)in_dim * 2 : 0;
 }
 
 int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
@@ -229,7 +229,7 @@ int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w, int in_di
     if ((reinterpret_cast<uintptr_t>(packed_act) & 15u) || (reinterpret_cast<uintptr_t>(w) & 3u) ||
         (reinterpret_cast<uintptr_t>(out) & 3u))
         return BONSAI_B1_ERR_ARG;
-    if (in_dim % 384 != 0 || (batch > 0 && !b1::gemm_packed_ok(batch, in_dim, out_dim))) return BONSAI_B1_ERR_ARG;
+    if (!b1::gemm_packed_ok(batch > 0 ? batch : 1, in_dim, out_dim)) return BONSAI_B1_ERR_ARG;
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     if (batch == 0) return BONSAI_B1_OK;

@@ -391,11 +391,11 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
 // runs of 4 consecutive output columns and the epilogue writes 16-byte
 // vectors.
 
-template <int BM, int BN, int WN>
-struct Gemm3Cfg {
+template <int BM, int BN, int WN, int STAGES_>
+struct GemmLdsCfg {
     static constexpr int NW = BN / WN, NT = NW * 64;
     static constexpr int MT = BM / 32, NTL = WN / 32;
-    static constexpr int STAGES = 3;
+    static constexpr int STAGES = STAGES_;            // ring slots, fetched STAGES-1 ahead
     static constexpr int KC = 128;                    // K per stage (4 blocks)
     static constexpr int ROWB = KC * 2;               // LDS bytes per activation row
     static constexpr int ASTAGE = BM * ROWB;          // activation bytes per slot
@@ -409,26 +409,34 @@ struct Gemm3Cfg {
     static constexpr int ABASE = STAGES * BSTAGE;
     static constexpr int LDS = STAGES * (ASTAGE + BSTAGE);
     static constexpr int GROUP_M = 4;                 // tile grouping along M
+    static constexpr int EPI_STORES = MT * NTL * 4;   // 16-byte stores per lane, full tile
     static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
     static_assert(WN == 64, "one weight column per lane of the weight loads");
     static_assert(LDS <= 160 * 1024, "gfx950 LDS");
     static_assert(ABASE <= 65536, "ds_read_b96 addresses stay below 64 KiB");
+    // vector memory operations that may be newer than stage s at its top:
+    // the STAGES-2 stages fetched after it, plus at a tile's start the
+    // previous tile's stores
+    static constexpr int AHEAD = (STAGES - 2) * (LPW + 2);
+    static_assert(STAGES == 3, "the three-slot ring is the verified configuration");
+    static_assert(EPI_STORES + AHEAD <= 63, "vmcnt holds 6 bits");
 };
 
-template <int BM, int BN, int WN>
-__global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t *__restrict__ ah,
-                                                                 const uint8_t *__restrict__ w, int K, int N,
-                                                                 int M, float *__restrict__ out, int64_t ldo,
-                                                                 int32_t *nonfinite, int tiles_m, int tiles_n,
-                                                                 int vec_store) {
-    using C = Gemm3Cfg<BM, BN, WN>;
+// Two waves per SIMD (8 waves, one work-group per CU): 256 registers a wave.
+template <int BM, int BN, int WN, int STAGES>
+__global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16_t *__restrict__ ah,
+                                                                    const uint8_t *__restrict__ w, int K, int N,
+                                                                    int M, float *__restrict__ out, int64_t ldo,
+                                                                    int32_t *nonfinite, int tiles_m, int tiles_n,
+                                                                    int vec_store) {
+    using C = GemmLdsCfg<BM, BN, WN, STAGES>;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
     // The wave index is made visibly uniform: LDS-DMA destinations go
     // through M0 and must not depend on the lane.
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 31, g = lane >> 5;
-    const int nstage = K / C::KC; // a multiple of 3 (K % 384 == 0)
+    const int nstage = K / C::KC; // a multiple of STAGES (K % (128 STAGES) == 0)
     const int ntiles = tiles_m * tiles_n;
     const uint32_t rs = (uint32_t)(K / 32) * 6;
     const uint8_t *abase = reinterpret_cast<const uint8_t *>(ah);
@@ -540,7 +548,7 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
     // A: lane column li = token m0 + 32 mt + li, rows 8*(v/4) + 4*g + v%4 =
     // output columns; v = 4q..4q+3 are 4 consecutive columns.  Stored
     // negated (the expanded weights carry the opposite sign).
-    auto epilogue = [&](int m0, int n0) {
+    auto epilogue = [&](int m0, int n0) -> int {
         int bad = 0;
         const bool full = vec_store && m0 + BM <= M && n0 + BN <= N;
 #pragma unroll
@@ -571,14 +579,16 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
             }
         }
         count_nonfinite(nonfinite, bad);
+        return full ? 2 : 1;
     };
 
     int tile = xcd_tile(blockIdx.x, gridDim.x);
     int m0, n0;
     tile_origin(tile, m0, n0);
     setup(m0, n0);
-    issue(0, 0);
-    issue(1, 1);
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t) issue(t, t);
+    int prev_stores = 0; // stores the previous epilogue left: 0 none, 1 scalar, 2 vector
     for (;;) {
 #pragma unroll
         for (int i = 0; i < C::MT; ++i)
@@ -588,39 +598,48 @@ __global__ __launch_bounds__((BN / WN) * 64) void b1_gemm_kernel(const uint16_t 
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
         // Pipeline (stage s in slot s % 3).  At the top of stage s the wave
-        // waits for its own loads of stage s -- only stage s+1's LPW + 2
-        // loads may still be outstanding (all of them for the first stage of
-        // a tile, which follows the previous tile's stores) -- then the
-        // barrier publishes every wave's part of stage s and retires all
-        // reads of slot (s+2) % 3 (stage s-1's), which stage s+2's loads then
-        // refill.  Unrolled by three so that slots are compile-time; the
-        // stage count is a multiple of three, so the loop has no exit
-        // mid-body.
-        for (int s = 0; s < nstage; s += 3) {
+        // waits for its own loads of stage s, then the barrier publishes
+        // every wave's part of stage s and retires all reads of slot
+        // (s+2) % 3 (stage s-1's), which stage s+2's loads then refill.
+        // Vector memory operations retire in issue order and loads and
+        // stores share vmcnt, so "stage s has landed" is "at most the
+        // operations issued after it are outstanding": stage s+1's LPW + 2
+        // loads, plus, in the first two stages of a tile, the previous
+        // tile's 32 vector stores per lane (issued after stages 0 and 1 of
+        // this tile).  Those stores thus drain under two stages of MFMA
+        // work instead of stalling the tile change.  A ragged previous tile
+        // stored a variable count with scalar stores: wait for everything.
+        // Unrolled by three so that slots are compile-time; the stage count
+        // is a multiple of three, so the loop has no exit mid-body.
+        for (int s = 0; s < nstage; s += STAGES) {
 #pragma unroll
-            for (int u = 0; u < 3; ++u) {
-                if (s + u == 0 || s + u + 1 >= nstage)
+            for (int u = 0; u < STAGES; ++u) {
+                if (s + u + 1 >= nstage)
+                    wait_vmcnt<0>();
+                else if (s == 0 && u < STAGES - 1 && prev_stores == 2)
+                    wait_vmcnt<C::EPI_STORES + C::AHEAD>();
+                else if (s == 0 && u == 0 && prev_stores == 1)
                     wait_vmcnt<0>();
                 else
-                    wait_vmcnt<C::LPW + 2>();
+                    wait_vmcnt<C::AHEAD>();
                 lds_barrier();
-                if (s + u + 2 < nstage) issue(s + u + 2, (u + 2) % 3);
+                if (s + u + STAGES - 1 < nstage) issue(s + u + STAGES - 1, (u + STAGES - 1) % STAGES);
                 compute(u);
             }
         }
 
-        // Slots 0 and 1 were last read before the final barrier: fetch the
-        // next tile's first two stages now, then store this tile.
+        // Slots 0..STAGES-2 were last read before the final barrier: fetch
+        // the next tile's first STAGES-1 stages now, then store this tile.
         const int cm0 = m0, cn0 = n0;
         tile += gridDim.x;
         const bool more = tile < ntiles;
         if (more) {
             tile_origin(tile, m0, n0);
             setup(m0, n0);
-            issue(0, 0);
-            issue(1, 1);
+#pragma unroll
+            for (int t = 0; t < STAGES - 1; ++t) issue(t, t);
         }
-        epilogue(cm0, cn0);
+        prev_stores = epilogue(cm0, cn0);
         if (!more) break;
     }
 }
@@ -810,13 +829,21 @@ static bool fast_layout_ok(const LinearArgs &a) {
 
 bool gemm_supported(const LinearArgs &a) { return fast_layout_ok(a); }
 
-// GEMM over pre-packed activations: K % 384 == 0 (the stage count K/128 is
-// a multiple of the three ring slots) and byte offsets into the packed
-// activations and the weights that fit the kernel's 32-bit offsets.
+namespace {
+// The packed GEMM configuration: 128 x 512 tiles of 8 waves, three-slot ring,
+// one work-group per CU.
+constexpr int kBM = 128, kBN = 512, kWN = 64, kStages = 3, kWgPerCu = 1;
+using KCfg = GemmLdsCfg<kBM, kBN, kWN, kStages>;
+} // namespace
+
+// GEMM over pre-packed activations: the stage count K/128 is a multiple of
+// the ring's slot count, and byte offsets into the packed activations and
+// the weights fit the kernel's 32-bit offsets.
 bool gemm_packed_ok(int M, int K, int N) {
     const uint64_t act_bytes = (uint64_t)M * (uint64_t)K * 2;
     const uint64_t w_bytes = (uint64_t)N * (uint64_t)(K / 32) * 6;
-    return M > 0 && K > 0 && N > 0 && K % 384 == 0 && act_bytes < (1ull << 32) && w_bytes < (1ull << 32);
+    return M > 0 && K > 0 && N > 0 && K % (KCfg::KC * kStages) == 0 && act_bytes < (1ull << 32) &&
+           w_bytes < (1ull << 32);
 }
 
 size_t gemm_workspace_bytes(const LinearArgs &a) {
@@ -836,14 +863,9 @@ hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed
     return hipGetLastError();
 }
 
-namespace {
-constexpr int kBM = 128, kBN = 512, kWN = 64;
-using KCfg = Gemm3Cfg<kBM, kBN, kWN>;
-} // namespace
-
 hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
                               int32_t *nonfinite, int num_cus, hipStream_t s) {
-    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN>;
+    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages>;
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(attr_once, [kernel] {
@@ -853,7 +875,8 @@ hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N
     if (attr_err != hipSuccess) return attr_err;
     const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
     const int ntiles = tiles_m * tiles_n;
-    const int grid = ntiles < num_cus || num_cus <= 0 ? ntiles : num_cus; // persistent
+    const int slots = num_cus > 0 ? num_cus * kWgPerCu : ntiles;
+    const int grid = ntiles < slots ? ntiles : slots; // persistent
     const int vec_store = (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ldo % 4 == 0;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
                        K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store);
