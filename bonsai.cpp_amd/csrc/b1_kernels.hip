@@ -24,12 +24,12 @@
 // fp16 dword d (d = 0..15) holds elements (d, d+16).  On the weight side the
 // two sign bits for dword d are then bits d and d+16 of the sign word, which
 // one left shift by (15 - d) lands on bits 15 and 31 — the two fp16 sign bits
-// — so a single v_bfi_b32 against the replicated scale builds the pair.  The
+// — so a single three-input bit op against the replicated scale builds the
+// pair: sign = scale sign XOR (NOT bit), i.e. bit 1 -> +scale and bit 0 ->
+// -scale exactly as in the reference, for negative scales too.  The
 // activation side is written in the same pairing when it is packed to fp16.
 // Any consistent permutation of K inside the MFMA leaves the dot product
-// unchanged.  The bit value 1 lands on the fp16 sign, i.e. the expanded
-// weight is -(reference weight); the MFMA kernels store the negated
-// accumulator so that the output keeps the reference sign.
+// unchanged.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -48,11 +48,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kSignPair = 0x80008000u;
 
-// (x & m) | (y & ~m) in one VALU op.  Written as asm because gfx950 VOP3
-// takes no literal and the compiler otherwise emits shift/and/or triples.
-__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t x, uint32_t y) {
+// Bits of m: ~(x ^ y); other bits: y.  One v_bitop3_b32, whose 8-bit table
+// is indexed by (x_bit << 2) | (m_bit << 1) | y_bit: 0xa6 = {0,1,1,0,0,1,0,1}
+// for indices 0..7.  Written as asm because gfx950 VOP3 takes no literal
+// and the compiler otherwise splits the select.
+__device__ __forceinline__ uint32_t xnor_sel(uint32_t m, uint32_t x, uint32_t y) {
     uint32_t r;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(x), "v"(y));
+    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0xa6" : "=v"(r) : "v"(x), "s"(m), "v"(y));
     return r;
 }
 
@@ -102,9 +104,10 @@ __device__ __forceinline__ uint32_t dup_hi16(uint32_t d) {
     return __builtin_amdgcn_perm(d, d, 0x03020302u);
 }
 
-// Weight dword for fp16 pair slot (bits p and p+16 of `w`, p = 15 - sh).
+// Weight dword for fp16 pair slot (bits p and p+16 of `w`, p = 15 - sh):
+// each half is the fp16 scale with its sign flipped where the bit is 0.
 __device__ __forceinline__ uint32_t wpair(uint32_t w, int sh, uint32_t scale2) {
-    return bfi(kSignPair, w << sh, scale2);
+    return xnor_sel(kSignPair, w << sh, scale2);
 }
 
 __device__ __forceinline__ void count_nonfinite(int32_t *ctr, int bad) {
@@ -335,7 +338,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_fused_kern
             for (int v = 0; v < 16; ++v) {
                 const int m = m0 + wm * WM + mt * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
                 if (m < p.M && n < p.N) {
-                    const float y = -acc[mt][nt][v];
+                    const float y = acc[mt][nt][v];
                     bad += !__builtin_isfinite(y);
                     p.out[(size_t)m * p.ldo + n] = y;
                 }
@@ -469,26 +472,39 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
         }
         boff = (uint32_t)min(n0 + wave * WN + lane, N - 1) * rs;
     };
+    // The stage offset goes into the wave-uniform base, so each load is a
+    // scalar base plus the lane's 32-bit offset (no per-lane 64-bit adds).
     auto issue = [&](int ks, int slot) {
         uint8_t *sa = smem + C::ABASE + slot * C::ASTAGE + wave * C::LPW * 1024;
         uint8_t *sw = smem + slot * C::BSTAGE + wave * C::BWAVE;
+        const uint8_t *ab = abase + (uint32_t)ks * C::ROWB;
+        const uint8_t *wb = w + (uint32_t)ks * 24;
 #pragma unroll
-        for (int i = 0; i < C::LPW; ++i) dma_lds16(abase + aoff[i] + (uint32_t)ks * C::ROWB, sa + i * 1024);
-        dma_lds12(w + boff + (uint32_t)ks * 24, sw);
-        dma_lds12(w + boff + (uint32_t)ks * 24 + 12, sw + 1024);
+        for (int i = 0; i < C::LPW; ++i) dma_lds16(ab + aoff[i], sa + i * 1024);
+        dma_lds12(wb + boff, sw);
+        dma_lds12(wb + 12 + boff, sw + 1024);
     };
 
     // Fragment offsets: lane (li, g) reads row li (+32 mt) at chunk
     // c = 4b + 2h + g, stored at position c ^ (li & 15); its weight column
     // nt*32 + li sits at a 16-byte stride in each 1 KB half of the wave's
     // weight area.
-    uint32_t foff[4][2];
+    // The lane parts of the LDS addresses are kept as LDS pointers, one set
+    // for slots 0-1 and one for slot 2, so that every slot, row-tile and
+    // block offset is a ds_read immediate (< 64 KiB).
+    typedef const __attribute__((address_space(3))) uint8_t lds_u8;
+    lds_u8 *const lbase = (lds_u8 *)smem;
+    lds_u8 *fa01[4][2], *fa2[4][2];
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-            foff[b][h] = li * C::ROWB + (((4 * b + 2 * h + g) ^ (li & 15)) * 16);
-    const uint32_t qoff = wave * C::BWAVE + li * 16;
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t f = li * C::ROWB + (((4 * b + 2 * h + g) ^ (li & 15)) * 16);
+            fa01[b][h] = lbase + C::ABASE + f;
+            fa2[b][h] = lbase + C::ABASE + 2 * C::ASTAGE + f;
+        }
+    lds_u8 *const qa = lbase + wave * C::BWAVE + li * 16;
+    static_assert(C::ASTAGE + (C::MT - 1) * 32 * C::ROWB + 64 < 65536, "fragment immediates");
 
     floatx16 acc[C::MT][C::NTL];
 
@@ -496,18 +512,19 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
     // reads of step+1 are issued before the MFMAs of step, into a second
     // buffer; a scheduling fence per step keeps the compiler from hoisting
     // every read of the stage.
-    auto compute = [&](int slot) {
-        const uint8_t *sb = smem + C::ABASE + slot * C::ASTAGE;
-        const uint8_t *sq = smem + slot * C::BSTAGE + qoff;
+    auto compute = [&](int slot, auto &&after_first_reads) {
+        lds_u8 *sq = qa + slot * C::BSTAGE;
         auto read_frags = [&](int step, half8 (&af)[C::MT]) {
             const int b = step >> 1, h = step & 1;
+            lds_u8 *fb = slot == 2 ? fa2[b][h] : fa01[b][h] + slot * C::ASTAGE;
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt)
-                af[mt] = *reinterpret_cast<const half8 *>(sb + mt * 32 * C::ROWB + foff[b][h]);
+                af[mt] = *reinterpret_cast<const __attribute__((address_space(3))) half8 *>(fb + mt * 32 * C::ROWB);
         };
         half8 afa[C::MT], afb[C::MT];
         uint32_t d[C::NTL][3], s2[C::NTL], wg[C::NTL];
         read_frags(0, afa);
+        after_first_reads();
 #pragma unroll
         for (int step = 0; step < 8; ++step) {
             const int b = step >> 1, h = step & 1;
@@ -518,7 +535,9 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
 #pragma unroll
                 for (int nt = 0; nt < C::NTL; ++nt) {
                     if ((b & 1) == 0) {
-                        const uint32_t *q = reinterpret_cast<const uint32_t *>(sq + (b >> 1) * 1024 + nt * 512);
+                        const __attribute__((address_space(3))) uint32_t *q =
+                            reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(sq + (b >> 1) * 1024 +
+                                                                                                   nt * 512);
                         d[nt][0] = q[0];
                         d[nt][1] = q[1];
                         d[nt][2] = q[2];
@@ -546,11 +565,12 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
 
     // Epilogue.  Accumulator (n, m) layout of the 32x32 MFMA with weights as
     // A: lane column li = token m0 + 32 mt + li, rows 8*(v/4) + 4*g + v%4 =
-    // output columns; v = 4q..4q+3 are 4 consecutive columns.  Stored
-    // negated (the expanded weights carry the opposite sign).
+    // output columns; v = 4q..4q+3 are 4 consecutive columns.  Non-finite
+    // outputs are counted only when the caller passed a counter.
     auto epilogue = [&](int m0, int n0) -> int {
         int bad = 0;
         const bool full = vec_store && m0 + BM <= M && n0 + BN <= N;
+        const bool cnt = nonfinite != nullptr;
 #pragma unroll
         for (int mt = 0; mt < C::MT; ++mt) {
             const int m = m0 + mt * 32 + li;
@@ -561,16 +581,16 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
                     const int n = n0 + wave * WN + nt * 32 + 8 * q + 4 * g;
                     floatx4 y;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) y[r] = -acc[mt][nt][4 * q + r];
+                    for (int r = 0; r < 4; ++r) y[r] = acc[mt][nt][4 * q + r];
                     if (full) {
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) bad += !__builtin_isfinite(y[r]);
+                        for (int r = 0; r < 4; ++r) bad += cnt && !__builtin_isfinite(y[r]);
                         *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + n) = y;
                     } else if (m < M) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             if (n + r < N) {
-                                bad += !__builtin_isfinite(y[r]);
+                                bad += cnt && !__builtin_isfinite(y[r]);
                                 out[(size_t)m * ldo + n + r] = y[r];
                             }
                         }
@@ -623,8 +643,11 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
                 else
                     wait_vmcnt<C::AHEAD>();
                 lds_barrier();
-                if (s + u + STAGES - 1 < nstage) issue(s + u + STAGES - 1, (u + STAGES - 1) % STAGES);
-                compute(u);
+                // the stage's first fragment reads go out before the next
+                // stage's loads, so the loads issue under their latency
+                compute(u, [&] {
+                    if (s + u + STAGES - 1 < nstage) issue(s + u + STAGES - 1, (u + STAGES - 1) % STAGES);
+                });
             }
         }
 
@@ -801,7 +824,6 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
         float s = 0.0f;
 #pragma unroll
         for (int w = 0; w < kGvWaves; ++w) s += red[(w * kGvMaxRG + r) * 64 + ln][v];
-        s = -s; // the expanded weights carry the opposite sign
         const int n = (rg0 + r) * 16 + c;
         if (tok < p.M && n < p.N) {
             bad += !__builtin_isfinite(s);

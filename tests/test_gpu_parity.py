@@ -365,3 +365,28 @@ def test_linear_packed_matches_fused_entry(torch, b1, m, k, n):
     assert torch.equal(out[:, :n], ref)
     assert bool((out[:, n:] == 7.0).all()), "columns past out_dim untouched"
     assert int(nf.item()) == 0
+
+
+@pytest.mark.parametrize("m,k,n", [(8, 768, 96), (160, 768, 600)])
+def test_signed_scales(torch, b1, oracle, m, k, n):
+    """fp16 scales of either sign (and +-0): the reference multiplies the
+    signed scale into +-a (src/b1_0_kernel.h:125-134,253-277), so a negative
+    scale flips every weight of its block.  EXACT is bit-exact vs the
+    scalar oracle, FAST modes within the stated tolerance of fp64."""
+    from bonsai_b1 import synth
+    rng = np.random.default_rng(11)
+    act = rng.standard_normal((m, k)).astype(np.float32)
+    raw = synth.packed_weights(n, k, 12).reshape(n, k // 32, 6).copy()
+    sc = raw[:, :, 0:2].copy().view("<u2")[..., 0]
+    sc |= (rng.integers(0, 2, sc.shape) << 15).astype(np.uint16)     # random sign
+    sc[0, :4] = [0x0000, 0x8000, 0x0000, 0x8000]                      # signed zeros
+    raw[:, :, 0:2] = sc.astype("<u2").view(np.uint8).reshape(n, k // 32, 2)
+    raw = raw.reshape(n, -1)
+    want_scalar, bad = oracle.linear(act, raw, n, variant="scalar")
+    assert bad == 0
+    y = gpu_run(torch, b1, act, raw, n, "exact")
+    assert np.array_equal(y.view(np.uint32), want_scalar.view(np.uint32))
+    ref = oracle.linear_f64(act, raw, n)
+    for mode in (["auto", "gemv", "gemm"] if m <= 16 else ["auto", "gemm"]):
+        y = gpu_run(torch, b1, act, raw, n, mode)
+        assert_fast_close(y, ref, f"signed scales {mode} ({m},{k},{n})")
