@@ -97,6 +97,15 @@ __device__ __forceinline__ void dma_lds12(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 12, 0, 0);
 }
 
+// Raw buffer loads with range checking (offsets at or past num_records read
+// zeros); word 3 of the resource for gfx9-family raw buffers.
+constexpr int kBufferFlags = 0x00020000;
+// 16 bytes per lane from the buffer at byte offset voff, landing at
+// lds + 16 * lane (wave-uniform lds, through M0).
+__device__ __forceinline__ void dma_buf_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds, 16, voff, 0, 0, 0);
+}
+
 __device__ __forceinline__ uint32_t dup_lo16(uint32_t d) {
     return __builtin_amdgcn_perm(d, d, 0x01000100u);
 }
@@ -833,6 +842,201 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
     count_nonfinite(p.nonfinite, bad);
 }
 
+
+// The same kernel with the weights staged through LDS (K % 256 == 0, so rows
+// are 16-byte multiples): coalesced 1 KB buffer loads instead of per-lane
+// 8-byte gathers, which cost one L2 request per row touched.
+constexpr int kGv2RowChunks = kGvChunk * 6 / 16 + 1;          // 37: 36 data + 1 pad
+constexpr int kGv2RowBytes = kGv2RowChunks * 16;              // 592: conflict-free row stride
+constexpr int kGv2RgSlots = 16 * kGv2RowChunks;                                  // 592 per row group
+constexpr int kGv2Insts = (kGvMaxRG * kGv2RgSlots + 64 * kGvWaves - 1) / (64 * kGvWaves); // 7 per wave
+// The weight area holds every slot the kGv2Insts x kGvWaves loads write
+// (1 KB each), not only the kGvMaxRG * 16 rows in use.
+constexpr int kGv2Lds = kGvLds + kGv2Insts * kGvWaves * 1024; // 98304 + 57344
+static_assert(kGv2Insts * kGvWaves * 1024 >= kGvMaxRG * 16 * kGv2RowBytes, "weight rows fit");
+static_assert(kGv2Lds <= 160 * 1024, "gfx950 LDS");
+
+// Weight loads of one wave per pass: slot sl = 64 j + lane of instruction j
+// (j = wave, wave + 8, ...) covers LDS row sl / 37, chunk sl % 37; a fixed
+// count so that vmcnt waits are immediates (unused slots read zeros).
+// Instructions of one wave that cover row groups 0..r (an upper bound over
+// the 8 waves): all of them must have landed before row group r is used.
+__device__ constexpr int gv2_done_before(int r) {
+    const int j_end = ((r + 1) * kGv2RgSlots + 63) / 64; // instructions needed
+    return (j_end + kGvWaves - 1) / kGvWaves;
+}
+
+constexpr int kGvRgPerSync = 2; // row groups made visible per barrier
+
+template <int R>
+__device__ __forceinline__ void gv2_wait_rg() {
+    wait_vmcnt<kGv2Insts - gv2_done_before(R)>();
+}
+
+__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv2_kernel(LinearArgs p, int groups, int mp_log2) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, g = lane >> 4;
+    const int nwg = gridDim.x, bid = blockIdx.x;
+    const int rg0 = (int)(((int64_t)groups * bid) / nwg);
+    const int rg1 = (int)(((int64_t)groups * (bid + 1)) / nwg);
+    const int nrg = rg1 - rg0;
+    const int nb = p.K / 32;
+    const uint32_t rs = (uint32_t)nb * 6;
+    const int mp = 1 << mp_log2; // token slots, power of two >= M
+    uint8_t *abuf = gsm + wave * kGvWaveLds;
+    uint8_t *wbuf = gsm + kGvLds;
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p.w), (short)0, (int)(p.N * rs), kBufferFlags);
+    const int odd = g & 1;
+    const uint32_t sel_word = odd ? 0x07060504u : 0x05040302u;
+    const uint32_t sel_scale = odd ? 0x03020302u : 0x01000100u;
+
+    floatx4 acc[kGvMaxRG];
+#pragma unroll
+    for (int r = 0; r < kGvMaxRG; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb0 = 0; kb0 < nb; kb0 += kGvChunk) {
+        const int wb0 = kb0 + wave * kGvBPW;
+        const int pass_blocks = min(kGvChunk, nb - kb0);
+        const int row_chunks = pass_blocks * 6 / 16;
+
+        // 1. This wave's activation loads, unit u = (bl*4 + t)*mp + tok
+        //    covering a[tok][32 (wb0+bl) + 4t .. +3] and the 4 elements 16
+        //    later; 64 * kGvAUnits units per batch (one batch for M <= 8).
+        const int units = 48 << mp_log2;
+        floatx4 lo[kGvAUnits], hi[kGvAUnits];
+        auto load_units = [&](int base) {
+#pragma unroll
+            for (int i = 0; i < kGvAUnits; ++i) {
+                const int u = min(base + i * 64 + lane, units - 1);
+                const int tok = min(u & (mp - 1), p.M - 1);
+                const int bt = u >> mp_log2;
+                const int blk = min(wb0 + (bt >> 2), nb - 1);
+                const float *src = p.act + (size_t)tok * p.lda + (size_t)blk * 32 + 4 * (bt & 3);
+                lo[i] = *reinterpret_cast<const floatx4 *>(src);
+                hi[i] = *reinterpret_cast<const floatx4 *>(src + 16);
+            }
+        };
+        auto store_units = [&](int base) {
+#pragma unroll
+            for (int i = 0; i < kGvAUnits; ++i) {
+                const int u = base + i * 64 + lane;
+                const int tok = u & (mp - 1), bt = u >> mp_log2;
+                const int bl = bt >> 2, t = bt & 3;
+                if (u < units) {
+                    const bool ok = wb0 + bl < nb;
+                    u32x4 v;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) v[jj] = ok ? pack_f16(lo[i][jj], hi[i][jj]) : 0u;
+                    *reinterpret_cast<u32x4 *>(abuf + ((((bl >> 2) * 4 + t) * 64) + (bl & 3) * 16 + tok) * 16) = v;
+                }
+            }
+        };
+        load_units(0);
+
+        // 2. The work-group's weight rows of this pass, row group by row
+        //    group, as whole 1 KB runs straight into LDS.
+#pragma unroll
+        for (int i = 0; i < kGv2Insts; ++i) {
+            const int j = wave + kGvWaves * i;
+            const int sl = j * 64 + lane;
+            const int row = sl / kGv2RowChunks, ch = sl - row * kGv2RowChunks;
+            const uint32_t voff = (row < nrg * 16 && ch < row_chunks)
+                                      ? (uint32_t)(rg0 * 16 + row) * rs + (uint32_t)kb0 * 6 + (uint32_t)ch * 16
+                                      : 0xFFFFFFF0u;
+            dma_buf_lds16(wrs, wbuf + j * 1024, voff);
+        }
+
+        // 3. Activations -> fp16 fragments in this wave's LDS area; the
+        //    weight loads, issued after the first batch, stay in flight.
+        wait_vmcnt<kGv2Insts>();
+        store_units(0);
+        for (int base = 64 * kGvAUnits; base < units; base += 64 * kGvAUnits) { // M > 8
+            load_units(base);
+            wait_vmcnt<0>();
+            store_units(base);
+        }
+        u32x4 af[kGvQuads][4];
+#pragma unroll
+        for (int q = 0; q < kGvQuads; ++q)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(abuf + ((q * 4 + t) * 64 + lane) * 16);
+                af[q][t] = col < p.M ? v : u32x4{0u, 0u, 0u, 0u};
+            }
+
+        // 4. Row group by row group: once its rows have landed for every
+        //    wave, decode and multiply while later groups still stream.
+#pragma unroll
+        for (int r = 0; r < kGvMaxRG; ++r) {
+            if (r < nrg) {
+                if (r % kGvRgPerSync == 0) {
+                    // row groups r .. r + kGvRgPerSync - 1 have landed
+                    switch (min(r + kGvRgPerSync - 1, kGvMaxRG - 1)) {
+                    case 0: gv2_wait_rg<0>(); break;
+                    case 1: gv2_wait_rg<1>(); break;
+                    case 2: gv2_wait_rg<2>(); break;
+                    case 3: gv2_wait_rg<3>(); break;
+                    case 4: gv2_wait_rg<4>(); break;
+                    default: gv2_wait_rg<5>(); break;
+                    }
+                    lds_barrier();
+                }
+                uint32_t wd[kGvQuads][2];
+#pragma unroll
+                for (int q = 0; q < kGvQuads; ++q) {
+                    const int bl = wave * kGvBPW + 4 * q + g; // block within the pass
+                    const __attribute__((address_space(3))) uint32_t *src =
+                        reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
+                            (__attribute__((address_space(3))) uint8_t *)wbuf + (r * 16 + col) * kGv2RowBytes +
+                            bl * 6 - 2 * odd);
+                    wd[q][0] = src[0];
+                    wd[q][1] = src[1];
+                }
+#pragma unroll
+                for (int q = 0; q < kGvQuads; ++q) {
+                    const uint32_t s2 = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_scale);
+                    const uint32_t w = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_word);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        u32x4 bd;
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj) bd[jj] = wpair(w, 15 - 4 * t - jj, s2);
+                        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(half8, af[q][t]), __builtin_bit_cast(half8, bd), acc[r], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        wait_vmcnt<0>();
+        __syncthreads(); // all reads of wbuf and abuf done before they are reused
+    }
+
+    // Cross-wave (split-K) reduction in a fixed order, in LDS reused from the
+    // activation fragments, then store.  16x16 accumulator layout: lane
+    // column = lane & 15 (weight row), rows 4*(lane >> 4) + v (tokens).
+    floatx4 *red = reinterpret_cast<floatx4 *>(gsm); // [wave][rg][lane]
+#pragma unroll
+    for (int r = 0; r < kGvMaxRG; ++r)
+        if (r < nrg) red[(wave * kGvMaxRG + r) * 64 + lane] = acc[r];
+    __syncthreads();
+    int bad = 0;
+    for (int e = tid; e < nrg * 256; e += kGvWaves * 64) {
+        const int c = e & 15, tok = (e >> 4) & 15, r = e >> 8;
+        const int ln = 16 * (tok >> 2) + c, v = tok & 3;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kGvWaves; ++w) sum += red[(w * kGvMaxRG + r) * 64 + ln][v];
+        const int n = (rg0 + r) * 16 + c;
+        if (tok < p.M && n < p.N) {
+            bad += !__builtin_isfinite(sum);
+            p.out[(size_t)tok * p.ldo + n] = sum;
+        }
+    }
+    count_nonfinite(p.nonfinite, bad);
+}
+
 } // namespace
 
 // ------------------------------------------------------------- launchers --
@@ -929,8 +1133,14 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
     std::call_once(attr_once, [] {
         attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kGvLds);
+        if (attr_err == hipSuccess)
+            attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv2_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGv2Lds);
     });
     if (attr_err != hipSuccess) return attr_err;
+    // Weights staged through LDS when rows are 16-byte multiples and the
+    // weight bytes fit a buffer resource's 31-bit range.
+    const bool staged = a.K % 256 == 0 && (uint64_t)a.N * (uint64_t)(a.K / 32) * 6 < (1ull << 31);
     const int groups = (a.N + 15) / 16;
     int nwg = num_cus > 0 ? num_cus : 256;
     const int need = (groups + kGvMaxRG - 1) / kGvMaxRG;
@@ -938,7 +1148,10 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
     if (nwg > groups) nwg = groups;
     int mp_log2 = 0;
     while ((1 << mp_log2) < a.M) ++mp_log2;
-    hipLaunchKernelGGL(b1_gemv_kernel, dim3(nwg), dim3(kGvWaves * 64), kGvLds, s, a, groups, mp_log2);
+    if (staged)
+        hipLaunchKernelGGL(b1_gemv2_kernel, dim3(nwg), dim3(kGvWaves * 64), kGv2Lds, s, a, groups, mp_log2);
+    else
+        hipLaunchKernelGGL(b1_gemv_kernel, dim3(nwg), dim3(kGvWaves * 64), kGvLds, s, a, groups, mp_log2);
     return hipGetLastError();
 }
 
