@@ -16,5 +16,6 @@ from .capi import (  # noqa: F401
     linear_raw,
     load,
     pack_act_f16,
+    quantize_f32,
 )
 from . import synth  # noqa: F401

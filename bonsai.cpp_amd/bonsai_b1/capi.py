@@ -70,6 +70,8 @@ def load():
     L.bonsai_b1_version.restype = i
     L.bonsai_b1_linear_f32_f32.argtypes = [vp, i, i, vp]
     L.bonsai_b1_linear_f32_f32.restype = None
+    L.bonsai_b1_quantize_f32.argtypes = [vp, i64, i, i, vp, i, vp]
+    L.bonsai_b1_quantize_f32.restype = i
     L.bonsai_b1_packed_act_bytes.argtypes = [i, i]
     L.bonsai_b1_packed_act_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_pack_act_f16.argtypes = [vp, i64, i, i, vp, vp]
@@ -115,6 +117,25 @@ def linear(act, w_packed, out_dim: int, out=None, mode: str = "auto", nonfinite=
                                      out.data_ptr(), out.stride(0), MODES[mode], nf, _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_linear_f32")
+    return out
+
+
+SUM_ORDERS = {"numpy": 0, "sequential": 1}
+
+
+def quantize_f32(w, order: str = "numpy", out=None, stream=None):
+    """Packed B1_0 bytes (uint8 cuda [N, K/32*6]) of fp32 cuda weights w[N, K]
+    (bonsai_b1_quantize_f32)."""
+    import torch
+    if w.dim() != 2 or w.dtype != torch.float32 or not w.is_cuda or w.stride(1) != 1:
+        raise ValueError("w must be a 2-D fp32 cuda tensor with unit column stride")
+    n, k = w.shape
+    if out is None:
+        out = torch.empty((n, k // BLOCK_SIZE * BLOCK_BYTES), dtype=torch.uint8, device=w.device)
+    st = load().bonsai_b1_quantize_f32(w.data_ptr(), w.stride(0), k, n, out.data_ptr(), SUM_ORDERS[order],
+                                       _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_quantize_f32")
     return out
 
 

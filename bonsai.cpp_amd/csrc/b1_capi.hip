@@ -205,6 +205,18 @@ int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
                        workspace_bytes, stream);
 }
 
+int bonsai_b1_quantize_f32(const float *w, int64_t ldw, int in_dim, int out_dim, void *packed, int order,
+                           hipStream_t stream) {
+    if (in_dim <= 0 || out_dim < 0 || in_dim % BONSAI_B1_BLOCK_SIZE || ldw < in_dim) return BONSAI_B1_ERR_ARG;
+    if (order != BONSAI_B1_SUM_NUMPY && order != BONSAI_B1_SUM_SEQUENTIAL) return BONSAI_B1_ERR_ARG;
+    if (out_dim > 0 && (!w || !packed)) return BONSAI_B1_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(w) & 3u) || (reinterpret_cast<uintptr_t>(packed) & 1u)) return BONSAI_B1_ERR_ARG;
+    if (!current_device(nullptr)) return BONSAI_B1_ERR_DEVICE;
+    if (out_dim == 0) return BONSAI_B1_OK;
+    return b1::launch_quantize(w, ldw, in_dim, out_dim, packed, order, stream) == hipSuccess ? BONSAI_B1_OK
+                                                                                            : BONSAI_B1_ERR_HIP;
+}
+
 size_t bonsai_b1_packed_act_bytes(int batch, int in_dim) {
     if (batch <= 0 || in_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
     return (size_t)batch * (size_t)in_dim * 2;

@@ -49,4 +49,8 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s);
 
 constexpr int kGemvMaxM = 16;
 
+// Packed B1_0 writer over device fp32 weights [N][ldw]; order 0 = numpy's
+// np.mean summation, 1 = left to right.
+hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *packed, int order, hipStream_t s);
+
 } // namespace b1

@@ -357,6 +357,59 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_fused_kern
     count_nonfinite(p.nonfinite, bad);
 }
 
+// --------------------------------------------------------- weight writer --
+//
+// fp32 weights [N][ldw] -> packed B1_0, one thread per 32-weight block:
+// scale = fp16(mean |w|) rounded to nearest even, bit i = (w_i >= 0) (so
+// -0 sets the bit and NaN clears it), bytes [scale_lo, scale_hi, sign word
+// LE].  The block sum follows one of the reference's two writers exactly:
+// order 0, numpy's np.mean over 32 float32 values (convert_to_b1_0_packed.py:
+// 21-43: the first element, plus an 8-way pairwise sum of the other 31);
+// order 1, a left-to-right sum (tests/c_ops/test_b1_linear.cpp:129-163).
+
+__global__ __launch_bounds__(256) void b1_quantize_kernel(const float *__restrict__ w, int64_t ldw, int K, int N,
+                                                          uint8_t *__restrict__ out, int order) {
+#pragma clang fp contract(off)
+    const int nb = K / 32;
+    const int64_t total = (int64_t)N * nb;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+        const int64_t n = t / nb;
+        const int b = (int)(t - n * nb);
+        const float *src = w + n * ldw + (int64_t)b * 32;
+        float a[32];
+        uint32_t bits = 0;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const float v = src[i];
+            a[i] = __builtin_fabsf(v);
+            bits |= (v >= 0.0f ? 1u : 0u) << i;
+        }
+        float sum;
+        if (order == 0) {
+            float r[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) r[j] = a[1 + j];
+#pragma unroll
+            for (int i = 8; i < 24; i += 8)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) r[j] += a[1 + i + j];
+            float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+#pragma unroll
+            for (int i = 24; i < 31; ++i) res += a[1 + i];
+            sum = a[0] + res;
+        } else {
+            sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) sum += a[i];
+        }
+        const _Float16 h = (_Float16)(sum / 32.0f);
+        uint16_t *o = reinterpret_cast<uint16_t *>(out + t * 6);
+        o[0] = __builtin_bit_cast(uint16_t, h);
+        o[1] = (uint16_t)(bits & 0xffffu);
+        o[2] = (uint16_t)(bits >> 16);
+    }
+}
+
 // ------------------------------------------------------- pack activations --
 //
 // fp32 activations -> fp16 (RNE) in the K-slot pairing, once per call: u32
@@ -1123,6 +1176,15 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
     hipError_t e = launch_pack(a.act, a.lda, a.M, a.K, workspace, s);
     if (e != hipSuccess) return e;
     return launch_gemm_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, s);
+}
+
+hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *packed, int order, hipStream_t s) {
+    const int64_t total = (int64_t)N * (K / 32);
+    const int64_t want = (total + 255) / 256;
+    const int grid = (int)(want < 65535 ? want : 65535);
+    hipLaunchKernelGGL(b1_quantize_kernel, dim3(grid), dim3(256), 0, s, w, ldw, K, N, static_cast<uint8_t *>(packed),
+                       order);
+    return hipGetLastError();
 }
 
 bool gemv_supported(const LinearArgs &a) { return a.M <= kGemvMaxM && fast_layout_ok(a); }

@@ -195,6 +195,24 @@ int bonsai_b1_weights_upload(const void *host_packed, size_t nbytes,
                              B1Weights *out);
 int bonsai_b1_weights_free(B1Weights *w);
 
+/*
+ * The B1_0 writer on the device; replaces quantize_b1_0 of
+ * convert_to_b1_0_packed.py:21-43 and of tests/c_ops/test_b1_linear.cpp:
+ * 129-163.  w: fp32 [out_dim][ldw] device weights (ldw >= in_dim,
+ * in_dim % 32 == 0); packed: device buffer of out_dim*(in_dim/32)*6 bytes,
+ * 2-byte aligned.  Per 32-weight block: scale = fp16(mean |w|) (round to
+ * nearest even), bit i set when w_i >= 0.  order selects which reference
+ * writer's float32 summation is reproduced bit for bit (they differ by one
+ * fp16 ulp on rare ties).
+ */
+enum {
+    BONSAI_B1_SUM_NUMPY = 0,      /* np.mean, convert_to_b1_0_packed.py */
+    BONSAI_B1_SUM_SEQUENTIAL = 1  /* left to right, the C++ test writer */
+};
+int bonsai_b1_quantize_f32(const float *w, int64_t ldw, int in_dim,
+                           int out_dim, void *packed, int order,
+                           hipStream_t stream);
+
 /* Human-readable text for a status code (static storage). */
 const char *bonsai_b1_status_string(int status);
 

@@ -119,6 +119,32 @@ void b1o_pack(const float *W, int N, int K, uint8_t *P) {
     }
 }
 
+/* tests/c_ops/test_b1_linear.cpp:129-163, the reference's C++ writer: the
+ * same layout, with the block sum taken left to right (it can differ from
+ * the numpy order by one fp16 ulp at a rounding tie). */
+void b1o_pack_seq(const float *W, int N, int K, uint8_t *P) {
+    const int nb = K / B1O_BLOCK_SIZE;
+    for (int n = 0; n < N; n++) {
+        for (int b = 0; b < nb; b++) {
+            const float *blk = W + (size_t)n * K + (size_t)b * B1O_BLOCK_SIZE;
+            float sum = 0.0f;
+            uint32_t bits = 0;
+            for (int i = 0; i < B1O_BLOCK_SIZE; i++) {
+                sum += fabsf(blk[i]);
+                if (blk[i] >= 0.0f) bits |= 1u << i;
+            }
+            uint16_t s = b1o_fp32_to_fp16(sum / 32.0f);
+            uint8_t *o = P + ((size_t)n * nb + b) * B1O_BLOCK_BYTES;
+            o[0] = (uint8_t)(s & 0xff);
+            o[1] = (uint8_t)(s >> 8);
+            o[2] = (uint8_t)(bits & 0xff);
+            o[3] = (uint8_t)((bits >> 8) & 0xff);
+            o[4] = (uint8_t)((bits >> 16) & 0xff);
+            o[5] = (uint8_t)(bits >> 24);
+        }
+    }
+}
+
 static inline uint16_t rd_scale(const uint8_t *b) {
     return (uint16_t)(b[0] | ((uint16_t)b[1] << 8));
 }

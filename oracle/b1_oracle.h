@@ -14,7 +14,9 @@
  *   - ggml row split          src/b1_0_kernel.h:75-77
  *   - fp16 -> fp32            src/b1_0_kernel.h:17-19 (ggml_fp16_to_fp32,
  *                             an exact IEEE conversion)
- *   - packed layout writer    convert_to_b1_0_packed.py:21-43
+ *   - packed layout writer    convert_to_b1_0_packed.py:21-43 (numpy sum
+ *                             order) and tests/c_ops/test_b1_linear.cpp:129-163
+ *                             (sequential sum order)
  *   - packed layout reader    tests/test_weight_parity.py:13-23
  * The reference's abort() on a non-finite output (src/b1_0_kernel.h:194-198,
  * 230-233, 279-282) is reported here as a returned count instead.
@@ -23,6 +25,8 @@
  *   b1o_fp16_to_fp32      exhaustive over all 65536 patterns vs numpy/F16C
  *   b1o_fp32_to_fp16      random + edge values vs numpy astype(float16)
  *   b1o_pack / b1o_unpack round trip bit-exact; pack == numpy quantize_b1_0
+ *   b1o_pack_seq          scale == fp16(np.cumsum(|w|)[-1] / 32) (numpy's
+ *                         cumulative sum is sequential in float32)
  *   b1o_linear_scalar     fp64 brute force, closed forms (ones -> 16.0,
  *                         complement -> negation, one-hot -> +-scale),
  *                         reference cosine gates on the reference's own
@@ -50,6 +54,7 @@ void b1o_fp16_to_fp32_n(const uint16_t *h, float *f, size_t n);
 
 /* Packed layout: W[N][K] fp32 -> P[N][K/32*6] */
 void b1o_pack(const float *W, int N, int K, uint8_t *P);
+void b1o_pack_seq(const float *W, int N, int K, uint8_t *P);
 void b1o_unpack(const uint8_t *P, int N, int K, float *W);
 
 /* One ggml task (ith of nth) of the reference kernel.  act [M][K] fp32

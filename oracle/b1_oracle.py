@@ -131,6 +131,7 @@ def lib():
         L.b1o_fp32_to_fp16.restype = ctypes.c_uint16
         L.b1o_fp16_to_fp32_n.argtypes = [u16p, f32p, ctypes.c_size_t]
         L.b1o_pack.argtypes = [f32p, i, i, u8p]
+        L.b1o_pack_seq.argtypes = [f32p, i, i, u8p]
         L.b1o_unpack.argtypes = [u8p, i, i, f32p]
         for fn in (L.b1o_linear_scalar_task, L.b1o_linear_avx2_task):
             fn.argtypes = [f32p, u8p, f32p, i, i, i, i, i]
@@ -160,11 +161,14 @@ def fp32_to_fp16_bits(f: np.ndarray) -> np.ndarray:
     return np.array([L.b1o_fp32_to_fp16(float(x)) for x in f], dtype=np.uint16)
 
 
-def pack(w: np.ndarray) -> np.ndarray:
+def pack(w: np.ndarray, order: str = "numpy") -> np.ndarray:
+    """B1_0 writer.  order 'numpy': convert_to_b1_0_packed.py's np.mean;
+    'sequential': tests/c_ops/test_b1_linear.cpp's left-to-right sum."""
     w = np.ascontiguousarray(w, dtype=np.float32)
     n, k = w.shape
     out = np.empty((n, k // BLOCK_SIZE * BLOCK_BYTES), dtype=np.uint8)
-    lib().b1o_pack(_p(w, ctypes.c_float), n, k, _p(out, ctypes.c_uint8))
+    fn = {"numpy": lib().b1o_pack, "sequential": lib().b1o_pack_seq}[order]
+    fn(_p(w, ctypes.c_float), n, k, _p(out, ctypes.c_uint8))
     return out
 
 

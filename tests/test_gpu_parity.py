@@ -390,3 +390,28 @@ def test_signed_scales(torch, b1, oracle, m, k, n):
     for mode in (["auto", "gemv", "gemm"] if m <= 16 else ["auto", "gemm"]):
         y = gpu_run(torch, b1, act, raw, n, mode)
         assert_fast_close(y, ref, f"signed scales {mode} ({m},{k},{n})")
+
+
+# ------------------------------------------------------------ B1_0 writer --
+
+@pytest.mark.parametrize("order", ["numpy", "sequential"])
+def test_quantize_matches_reference_writers(torch, b1, oracle, order):
+    """bonsai_b1_quantize_f32 reproduces each reference writer bit for bit:
+    numpy's np.mean order (convert_to_b1_0_packed.py) and the left-to-right
+    order (tests/c_ops/test_b1_linear.cpp), including the rare blocks where
+    the two disagree, signed zeros, ties and a padded row stride."""
+    rng = np.random.default_rng(21)
+    w = rng.standard_normal((1000, 3200)).astype(np.float32)          # orders differ on ~9 blocks
+    w[0, :64] = 0.0
+    w[1, :32] = -0.0
+    w[2, :] = (rng.integers(-3, 4, 3200) * 0.0009765625).astype(np.float32)
+    w[3, :32] = np.float32(1e-40)                                      # subnormal magnitudes
+    big = torch.zeros((1000, 3200 + 32), dtype=torch.float32)
+    big[:, :3200] = torch.from_numpy(w)
+    dw = big.cuda()[:, :3200]
+    got = b1.quantize_f32(dw, order=order)
+    torch.cuda.synchronize()
+    want = oracle.pack(w, order=order)
+    nbad = int((got.cpu().numpy() != want).sum())
+    say(f"  quantize {order}: {nbad} differing bytes")
+    assert nbad == 0

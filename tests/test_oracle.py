@@ -79,6 +79,44 @@ def test_c_pack_equals_numpy_quantize(oracle, dist):
     assert np.array_equal(oracle.pack(w), oracle.quantize_b1_0(w))
 
 
+@pytest.mark.parametrize("dist", ["normal", "wide", "ties", "zeros"])
+def test_c_pack_seq_equals_cumsum(oracle, dist):
+    """Sequential-order writer (tests/c_ops/test_b1_linear.cpp:129-163):
+    scale = fp16(left-to-right float32 sum of |w| / 32); numpy's cumsum over
+    float32 is that left-to-right sum, so it pins the order independently."""
+    rng = np.random.default_rng(8)
+    n, k = 24, 256
+    if dist == "normal":
+        w = rng.standard_normal((n, k)).astype(np.float32)
+    elif dist == "wide":  # magnitudes over many binades: order-sensitive sums
+        w = (rng.standard_normal((n, k)) * 2.0 ** rng.integers(-20, 20, (n, k))).astype(np.float32)
+    elif dist == "ties":
+        w = (rng.integers(-3, 4, (n, k)) * 0.0009765625).astype(np.float32)
+    else:
+        w = np.zeros((n, k), np.float32)
+        w[::2, ::3] = -0.0
+    blocks = np.abs(w).reshape(n, k // 32, 32)
+    seq = np.cumsum(blocks, axis=-1, dtype=np.float32)[..., -1] / np.float32(32)
+    want = oracle.quantize_b1_0(w).reshape(n, k // 32, 6).copy()
+    want[:, :, 0:2] = seq.astype(np.float16).view(np.uint8).reshape(n, k // 32, 2)
+    assert np.array_equal(oracle.pack(w, order="sequential"), want.reshape(n, -1))
+
+
+def test_pack_orders_differ_at_ties(oracle):
+    """The two reference writers disagree by one fp16 ulp on a few blocks in
+    10^5 (fp32 sums of different order straddling an fp16 rounding tie), so
+    the order has to be a parameter of any writer that claims bit parity."""
+    rng = np.random.default_rng(9)
+    w = rng.standard_normal((1000, 3200)).astype(np.float32)
+    a, b = oracle.pack(w), oracle.pack(w, order="sequential")
+    diff = (a != b).reshape(1000, 100, 6)
+    assert diff.any()
+    assert not diff[:, :, 2:].any()                       # sign words never differ
+    sa = a.reshape(1000, 100, 6)[:, :, :2].copy().view("<u2")[..., 0].astype(np.int32)
+    sb = b.reshape(1000, 100, 6)[:, :, :2].copy().view("<u2")[..., 0].astype(np.int32)
+    assert np.abs(sa - sb).max() == 1                     # by one fp16 ulp
+
+
 def test_pack_unpack_roundtrip(oracle):
     """pack(unpack(P)) == P for every block with scale > 0, both readers agree."""
     n, k = 40, 512
