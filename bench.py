@@ -94,6 +94,156 @@ def committed_traffic(name):
     return None
 
 
+def graph_ms(torch, record, reps=3):
+    """One eager pass of record() (a sequence of library calls on the current
+    stream), then the same calls captured into a HIP graph and replayed;
+    returns the GPU time per replay (ms) from events around the replays."""
+    record()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        record()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def bench_mlp(torch, b1, synth):
+    """Flux MLP at 1024x1024 (4608 tokens): up-projection 3072 -> 12288,
+    GELU-tanh, down-projection 12288 -> 3072; each part and the chain, plus
+    the chain with GELU fused into the fp16 packing of the down-projection's
+    input."""
+    m, k, h = 4608, 3072, 12288
+    a = synth.device_activations(m, k, 11)
+    wu = synth.device_packed_weights(h, k, 12)
+    wd = synth.device_packed_weights(k, h, 13)
+    y1 = torch.empty((m, h), device="cuda")
+    g = torch.empty((m, h), device="cuda")
+    y2 = torch.empty((m, k), device="cuda")
+    ws = torch.empty(max(b1.workspace_bytes(m, k, h), b1.workspace_bytes(m, h, k)), dtype=torch.uint8,
+                     device="cuda")
+    packed = torch.empty(m * h * 2, dtype=torch.uint8, device="cuda")
+
+    def up():
+        b1.linear(a, wu, h, out=y1, workspace=ws)
+
+    def gelu():
+        b1.gelu_tanh(y1, out=g)
+
+    def down():
+        b1.linear(g, wd, k, out=y2, workspace=ws)
+
+    def fused():
+        up()
+        b1.gelu_tanh_pack_f16(y1, packed=packed)
+        b1.linear_packed_f16(packed, wd, h, k, m, out=y2)
+
+    r = {name: graph_ms(torch, lambda f=f: [f() for _ in range(4)]) / 4
+         for name, f in (("up", up), ("gelu", gelu), ("down", down))}
+    r["chain"] = graph_ms(torch, lambda: (up(), gelu(), down()))
+    r["chain_fused_gelu"] = graph_ms(torch, fused)
+    flop = 2.0 * m * k * h * 2
+    r["chain_tflops"] = flop / (r["chain"] * 1e-3) / 1e12
+    r["chain_fused_tflops"] = flop / (r["chain_fused_gelu"] * 1e-3) / 1e12
+    r["gelu_GBps"] = m * h * 8 / (r["gelu"] * 1e-3) / 1e9
+    return r
+
+
+def bench_single_stream_step(torch, b1, synth, blocks=38):
+    """One diffusion step's worth of the Flux single-stream block linears,
+    back to back on one stream: per block, linear1 4608 x 3072 -> 21504 and
+    linear2 4608 x 15360 -> 3072, every block with its own resident weights
+    (807 MB packed).  Activations are synthetic stand-ins of the right
+    shapes.  Two dispatches: the fp32 op per linear, and the fp16-packed
+    path (pack + packed GEMM)."""
+    m, k1, n1, k2, n2 = 4608, 3072, 21504, 15360, 3072
+    w1 = [synth.device_packed_weights(n1, k1, 300 + i) for i in range(blocks)]
+    w2 = [synth.device_packed_weights(n2, k2, 400 + i) for i in range(blocks)]
+    a1 = synth.device_activations(m, k1, 14)
+    a2 = synth.device_activations(m, k2, 15)
+    o1 = torch.empty((m, n1), device="cuda")
+    o2 = torch.empty((m, n2), device="cuda")
+    ws = torch.empty(max(b1.workspace_bytes(m, k1, n1), b1.workspace_bytes(m, k2, n2)), dtype=torch.uint8,
+                     device="cuda")
+    p1 = torch.empty(m * k1 * 2, dtype=torch.uint8, device="cuda")
+    p2 = torch.empty(m * k2 * 2, dtype=torch.uint8, device="cuda")
+
+    def step():
+        for i in range(blocks):
+            b1.linear(a1, w1[i], n1, out=o1, workspace=ws)
+            b1.linear(a2, w2[i], n2, out=o2, workspace=ws)
+
+    def step_packed():
+        for i in range(blocks):
+            b1.pack_act_f16(a1, packed=p1)
+            b1.linear_packed_f16(p1, w1[i], k1, n1, m, out=o1)
+            b1.pack_act_f16(a2, packed=p2)
+            b1.linear_packed_f16(p2, w2[i], k2, n2, m, out=o2)
+
+    ms = graph_ms(torch, step, reps=2)
+    flop = 2.0 * m * (k1 * n1 + k2 * n2) * blocks
+    r = {"blocks": blocks, "ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12,
+         "packed_weight_bytes": sum(w.numel() for w in w1 + w2)}
+    r["ms_per_step_packed_path"] = graph_ms(torch, step_packed, reps=2)
+    del w1, w2
+    return r
+
+
+def bench_klein_step(torch, b1, synth):
+    """The 100 B1_0 linears of one reference Flux.2-Klein step at 64x64
+    latents (4096 image + 512 text tokens): 5 double-stream blocks (image and
+    text q/k/v/out 3072 -> 3072, FF-in 3072 -> 18432, FF-out 9216 -> 3072)
+    and 20 single-stream blocks (4608 x 3072 -> 27648, 12288 -> 3072), each
+    with resident weights (690 MB).  q/k/v of a stream share their input:
+    packed once, then three packed GEMMs."""
+    mi, mt, ms_ = 4096, 512, 4608
+    d = []
+    for blk in range(5):
+        per = {}
+        for st in ("img", "txt"):
+            per[st] = {"qkv": [synth.device_packed_weights(3072, 3072, 1000 + 40 * blk + i + (20 if st == "txt" else 0))
+                               for i in range(3)],
+                       "out": synth.device_packed_weights(3072, 3072, 1003 + 40 * blk + (20 if st == "txt" else 0)),
+                       "ff_in": synth.device_packed_weights(18432, 3072, 1004 + 40 * blk + (20 if st == "txt" else 0)),
+                       "ff_out": synth.device_packed_weights(3072, 9216, 1005 + 40 * blk + (20 if st == "txt" else 0))}
+        d.append(per)
+    s = [(synth.device_packed_weights(27648, 3072, 2000 + i), synth.device_packed_weights(3072, 12288, 2100 + i))
+         for i in range(20)]
+    acts = {mm: {kk: synth.device_activations(mm, kk, 16 + kk) for kk in (3072, 9216, 12288)}
+            for mm in (mi, mt, ms_)}
+    outs = {mm: {nn: torch.empty((mm, nn), device="cuda") for nn in (3072, 18432, 27648)} for mm in (mi, mt, ms_)}
+    ws = torch.empty(ms_ * 12288 * 2, dtype=torch.uint8, device="cuda")
+    pk = torch.empty(ms_ * 12288 * 2, dtype=torch.uint8, device="cuda")
+
+    def step():
+        for per in d:
+            for st, mm in (("img", mi), ("txt", mt)):
+                x = acts[mm][3072]
+                b1.pack_act_f16(x, packed=pk)
+                for w in per[st]["qkv"]:
+                    b1.linear_packed_f16(pk, w, 3072, 3072, mm, out=outs[mm][3072])
+                b1.linear(x, per[st]["out"], 3072, out=outs[mm][3072], workspace=ws)
+                b1.linear(x, per[st]["ff_in"], 18432, out=outs[mm][18432], workspace=ws)
+                b1.linear(acts[mm][9216], per[st]["ff_out"], 3072, out=outs[mm][3072], workspace=ws)
+        for w1, w2 in s:
+            b1.linear(acts[ms_][3072], w1, 27648, out=outs[ms_][27648], workspace=ws)
+            b1.linear(acts[ms_][12288], w2, 3072, out=outs[ms_][3072], workspace=ws)
+
+    ms = graph_ms(torch, step, reps=2)
+    flop = (5 * 2 * (mi + mt) * (4 * 3072 * 3072 + 3072 * 18432 + 9216 * 3072)
+            + 20 * 2 * ms_ * (3072 * 27648 + 12288 * 3072))
+    nbytes = sum(w.numel() for per in d for st in per.values() for v in st.values()
+                 for w in (v if isinstance(v, list) else [v])) + sum(a.numel() + b.numel() for a, b in s)
+    return {"linears": 100, "ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
+            "packed_weight_bytes": nbytes}
+
+
 def bench_gemv(torch, b1, synth, m, k, n, steps, warmup):
     """Small-M kernel, weight copies rotated past the MALL.  The launches are
     captured once into a HIP graph (one launch per weight copy) and the graph
@@ -227,6 +377,21 @@ def main():
             extra[name] = {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 1),
                            "frac": round(r["frac"], 4)}
             log(f"[bench] {name} {shp}: {r['ms']*1e3:.1f} us {r['tflops']:.1f} TFLOP/s")
+        mlp = bench_mlp(torch, b1, synth)
+        extra["c4_mlp"] = {x: round(v, 4) for x, v in mlp.items()}
+        log(f"[bench] c4 MLP: up {mlp['up']*1e3:.1f} us, GELU {mlp['gelu']*1e3:.1f} us "
+            f"({mlp['gelu_GBps']:.0f} GB/s), down {mlp['down']*1e3:.1f} us; chain {mlp['chain']*1e3:.1f} us "
+            f"({mlp['chain_tflops']:.0f} TFLOP/s), GELU fused into the pack {mlp['chain_fused_gelu']*1e3:.1f} us")
+        torch.cuda.empty_cache()
+        c5 = bench_single_stream_step(torch, b1, synth)
+        extra["c5_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in c5.items()}
+        log(f"[bench] c5 single-stream step (38 blocks): {c5['ms_per_step']:.2f} ms ({c5['tflops']:.0f} TFLOP/s); "
+            f"packed path {c5['ms_per_step_packed_path']:.2f} ms")
+        torch.cuda.empty_cache()
+        kl = bench_klein_step(torch, b1, synth)
+        extra["klein_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in kl.items()}
+        log(f"[bench] Klein step (100 linears): {kl['ms_per_step']:.2f} ms ({kl['tflops']:.0f} TFLOP/s)")
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:

@@ -10,6 +10,8 @@ from .capi import (  # noqa: F401
     MODES,
     Weights,
     declared_symbols,
+    gelu_tanh,
+    gelu_tanh_pack_f16,
     library_path,
     linear,
     linear_packed_f16,
@@ -17,5 +19,6 @@ from .capi import (  # noqa: F401
     load,
     pack_act_f16,
     quantize_f32,
+    workspace_bytes,
 )
 from . import synth  # noqa: F401

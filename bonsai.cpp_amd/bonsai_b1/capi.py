@@ -58,6 +58,10 @@ def load():
     vp, i, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     L.bonsai_b1_linear_f32.argtypes = [vp, i64, vp, i, i, i, vp, i64, i, vp, vp]
     L.bonsai_b1_linear_f32.restype = i
+    L.bonsai_b1_linear_f32_ws.argtypes = [vp, i64, vp, i, i, i, vp, i64, i, vp, vp, ctypes.c_size_t, vp]
+    L.bonsai_b1_linear_f32_ws.restype = i
+    L.bonsai_b1_workspace_bytes.argtypes = [i, i, i, i]
+    L.bonsai_b1_workspace_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_linear.argtypes = [vp, ctypes.POINTER(B1WeightsC), i, vp,
                                    ctypes.POINTER(B1LinearUserData), i, vp, vp]
     L.bonsai_b1_linear.restype = i
@@ -70,6 +74,10 @@ def load():
     L.bonsai_b1_version.restype = i
     L.bonsai_b1_linear_f32_f32.argtypes = [vp, i, i, vp]
     L.bonsai_b1_linear_f32_f32.restype = None
+    L.bonsai_b1_gelu_tanh_f32.argtypes = [vp, i64, vp, i64, i, i, vp]
+    L.bonsai_b1_gelu_tanh_f32.restype = i
+    L.bonsai_b1_gelu_tanh_pack_f16.argtypes = [vp, i64, i, i, vp, vp]
+    L.bonsai_b1_gelu_tanh_pack_f16.restype = i
     L.bonsai_b1_quantize_f32.argtypes = [vp, i64, i, i, vp, i, vp]
     L.bonsai_b1_quantize_f32.restype = i
     L.bonsai_b1_packed_act_bytes.argtypes = [i, i]
@@ -96,10 +104,17 @@ def linear_raw(act_ptr: int, lda: int, w_ptr: int, in_dim: int, out_dim: int, ba
                                        MODES[mode], nonfinite_ptr or None, stream_handle or None)
 
 
-def linear(act, w_packed, out_dim: int, out=None, mode: str = "auto", nonfinite=None, stream=None):
+def workspace_bytes(batch: int, in_dim: int, out_dim: int, mode: str = "auto") -> int:
+    return int(load().bonsai_b1_workspace_bytes(batch, in_dim, out_dim, MODES[mode]))
+
+
+def linear(act, w_packed, out_dim: int, out=None, mode: str = "auto", nonfinite=None, stream=None,
+           workspace=None):
     """out[M, N] = B1_0 linear of act[M, K] (fp32, cuda, row stride >= K)
     with packed weights w_packed (uint8, cuda, N*(K/32)*6 bytes).
-    Returns `out` (allocated if None).  Stream-ordered; does not sync."""
+    Returns `out` (allocated if None).  Stream-ordered; does not sync.
+    With `workspace` (a cuda tensor) the caller's buffer replaces the
+    library-owned one (bonsai_b1_linear_f32_ws; never allocates)."""
     import torch
     if act.dim() != 2 or act.dtype != torch.float32 or not act.is_cuda or act.stride(1) != 1:
         raise ValueError("act must be a 2-D fp32 cuda tensor with unit column stride")
@@ -113,11 +128,45 @@ def linear(act, w_packed, out_dim: int, out=None, mode: str = "auto", nonfinite=
     if out.dim() != 2 or out.shape[0] != m or out.shape[1] < out_dim or out.stride(1) != 1:
         raise ValueError("out must be [M, >=N] fp32 with unit column stride")
     nf = nonfinite.data_ptr() if nonfinite is not None else None
-    st = load().bonsai_b1_linear_f32(act.data_ptr(), act.stride(0), w_packed.data_ptr(), k, out_dim, m,
-                                     out.data_ptr(), out.stride(0), MODES[mode], nf, _stream_handle(stream))
+    if workspace is not None:
+        st = load().bonsai_b1_linear_f32_ws(act.data_ptr(), act.stride(0), w_packed.data_ptr(), k, out_dim, m,
+                                            out.data_ptr(), out.stride(0), MODES[mode], nf, workspace.data_ptr(),
+                                            workspace.numel() * workspace.element_size(), _stream_handle(stream))
+    else:
+        st = load().bonsai_b1_linear_f32(act.data_ptr(), act.stride(0), w_packed.data_ptr(), k, out_dim, m,
+                                         out.data_ptr(), out.stride(0), MODES[mode], nf, _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_linear_f32")
     return out
+
+
+def gelu_tanh(x, out=None, stream=None):
+    """GELU-tanh of a 2-D fp32 cuda tensor (bonsai_b1_gelu_tanh_f32); out may be x."""
+    import torch
+    if x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda or x.stride(1) != 1:
+        raise ValueError("x must be a 2-D fp32 cuda tensor with unit column stride")
+    if out is None:
+        out = torch.empty_like(x)
+    rows, cols = x.shape
+    st = load().bonsai_b1_gelu_tanh_f32(x.data_ptr(), x.stride(0), out.data_ptr(), out.stride(0), cols, rows,
+                                        _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_gelu_tanh_f32")
+    return out
+
+
+def gelu_tanh_pack_f16(act, packed=None, stream=None):
+    """Packed fp16 activations of gelu_tanh(act) (bonsai_b1_gelu_tanh_pack_f16)."""
+    import torch
+    m, k = act.shape
+    nbytes = load().bonsai_b1_packed_act_bytes(m, k)
+    if packed is None:
+        packed = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=act.device)
+    st = load().bonsai_b1_gelu_tanh_pack_f16(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(),
+                                             _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_gelu_tanh_pack_f16")
+    return packed
 
 
 SUM_ORDERS = {"numpy": 0, "sequential": 1}

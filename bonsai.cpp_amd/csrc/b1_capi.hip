@@ -205,6 +205,28 @@ int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
                        workspace_bytes, stream);
 }
 
+int bonsai_b1_gelu_tanh_f32(const float *x, int64_t ldx, float *y, int64_t ldy, int cols, int rows,
+                            hipStream_t stream) {
+    if (cols < 0 || rows < 0 || cols % 4 || ldx < cols || ldy < cols || ldx % 4 || ldy % 4) return BONSAI_B1_ERR_ARG;
+    if (rows > 0 && cols > 0 && (!x || !y)) return BONSAI_B1_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(y) & 15u)) return BONSAI_B1_ERR_ARG;
+    if (!current_device(nullptr)) return BONSAI_B1_ERR_DEVICE;
+    if (rows == 0 || cols == 0) return BONSAI_B1_OK;
+    return b1::launch_gelu(x, ldx, y, ldy, cols, rows, stream) == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
+}
+
+int bonsai_b1_gelu_tanh_pack_f16(const float *act, int64_t lda, int in_dim, int batch, void *packed,
+                                 hipStream_t stream) {
+    if (in_dim <= 0 || batch < 0 || in_dim % BONSAI_B1_BLOCK_SIZE || lda < in_dim) return BONSAI_B1_ERR_ARG;
+    if (batch > 0 && (!act || !packed)) return BONSAI_B1_ERR_ARG;
+    if (reinterpret_cast<uintptr_t>(packed) & 15u) return BONSAI_B1_ERR_ARG;
+    if (batch > 0 && !b1::pack_supported(act, lda, batch, in_dim)) return BONSAI_B1_ERR_ARG;
+    if (!current_device(nullptr)) return BONSAI_B1_ERR_DEVICE;
+    if (batch == 0) return BONSAI_B1_OK;
+    return b1::launch_gelu_pack(act, lda, batch, in_dim, packed, stream) == hipSuccess ? BONSAI_B1_OK
+                                                                                      : BONSAI_B1_ERR_HIP;
+}
+
 int bonsai_b1_quantize_f32(const float *w, int64_t ldw, int in_dim, int out_dim, void *packed, int order,
                            hipStream_t stream) {
     if (in_dim <= 0 || out_dim < 0 || in_dim % BONSAI_B1_BLOCK_SIZE || ldw < in_dim) return BONSAI_B1_ERR_ARG;

@@ -49,6 +49,11 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s);
 
 constexpr int kGemvMaxM = 16;
 
+// GELU-tanh over [rows][cols] fp32 (cols % 4 == 0, rows 16-byte aligned via
+// ld % 4 == 0); the fused form writes packed fp16 activations (pack rules).
+hipError_t launch_gelu(const float *x, int64_t ldx, float *y, int64_t ldy, int cols, int rows, hipStream_t s);
+hipError_t launch_gelu_pack(const float *act, int64_t lda, int M, int K, void *packed, hipStream_t s);
+
 // Packed B1_0 writer over device fp32 weights [N][ldw]; order 0 = numpy's
 // np.mean summation, 1 = left to right.
 hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *packed, int order, hipStream_t s);

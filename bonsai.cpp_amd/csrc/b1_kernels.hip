@@ -357,6 +357,52 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_fused_kern
     count_nonfinite(p.nonfinite, bad);
 }
 
+// ------------------------------------------------------------- GELU-tanh --
+//
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), elementwise in fp32 with
+// the device library's tanhf.  The plain form writes fp32; the fused form
+// writes the fp16 K-slot-paired activations that the packed GEMM reads, so
+// a GELU between two B1_0 linears costs one read and one half-size write.
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float k0 = 0.7978845608028654f; // sqrt(2 / pi)
+    const float k1 = 0.044715f;
+    const float u = k0 * (x + k1 * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(u));
+}
+
+__global__ __launch_bounds__(256) void b1_gelu_kernel(const float *__restrict__ x, int64_t ldx,
+                                                      float *__restrict__ y, int64_t ldy, int cols, int rows) {
+    const int q = cols / 4; // float4 units per row (cols % 4 == 0)
+    const int64_t units = (int64_t)rows * q;
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+        const int64_t r = u / q;
+        const int c = (int)(u - r * q) * 4;
+        const floatx4 v = *reinterpret_cast<const floatx4 *>(x + r * ldx + c);
+        floatx4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = gelu_tanh(v[j]);
+        *reinterpret_cast<floatx4 *>(y + r * ldy + c) = o;
+    }
+}
+
+__global__ __launch_bounds__(256) void b1_gelu_pack_kernel(const float *__restrict__ act, int64_t lda,
+                                                           uint32_t *__restrict__ ah, int M, int K) {
+    const int nb = K / 32;
+    const int units = M * nb * 4; // (row, block, quad)
+    for (int u = blockIdx.x * 256 + threadIdx.x; u < units; u += gridDim.x * 256) {
+        const int c = u & 3, rb = u >> 2;
+        const int row = rb / nb, blk = rb - row * nb;
+        const float *src = act + (size_t)row * lda + blk * 32 + c * 4;
+        const floatx4 lo = *reinterpret_cast<const floatx4 *>(src);
+        const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + 16);
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = pack_f16(gelu_tanh(lo[j]), gelu_tanh(hi[j]));
+        *reinterpret_cast<u32x4 *>(ah + (size_t)row * (K / 2) + blk * 16 + c * 4) = v;
+    }
+}
+
 // --------------------------------------------------------- weight writer --
 //
 // fp32 weights [N][ldw] -> packed B1_0, one thread per 32-weight block:
@@ -1184,6 +1230,22 @@ hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *pack
     const int grid = (int)(want < 65535 ? want : 65535);
     hipLaunchKernelGGL(b1_quantize_kernel, dim3(grid), dim3(256), 0, s, w, ldw, K, N, static_cast<uint8_t *>(packed),
                        order);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu(const float *x, int64_t ldx, float *y, int64_t ldy, int cols, int rows, hipStream_t s) {
+    const int64_t units = (int64_t)rows * (cols / 4);
+    const int64_t want = (units + 255) / 256;
+    const int grid = (int)(want < 8192 ? want : 8192);
+    hipLaunchKernelGGL(b1_gelu_kernel, dim3(grid), dim3(256), 0, s, x, ldx, y, ldy, cols, rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu_pack(const float *act, int64_t lda, int M, int K, void *packed, hipStream_t s) {
+    const int units = M * (K / 32) * 4;
+    const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
+    hipLaunchKernelGGL(b1_gelu_pack_kernel, dim3(pgrid), dim3(256), 0, s, act, lda,
+                       static_cast<uint32_t *>(packed), M, K);
     return hipGetLastError();
 }
 

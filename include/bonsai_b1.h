@@ -196,6 +196,24 @@ int bonsai_b1_weights_upload(const void *host_packed, size_t nbytes,
 int bonsai_b1_weights_free(B1Weights *w);
 
 /*
+ * GELU with the tanh approximation, 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715
+ * x^3))), between the up- and down-projections of the Flux MLP workload.
+ * Not a reference op: the reference MLP uses SwiGLU
+ * (src/diffuser_graph.cpp:453,456).  fp32 [rows][ldx] -> fp32 [rows][ldy]
+ * (x == y allowed); cols % 4 == 0, ldx and ldy multiples of 4, 16-byte
+ * aligned pointers.
+ */
+int bonsai_b1_gelu_tanh_f32(const float *x, int64_t ldx, float *y,
+                            int64_t ldy, int cols, int rows,
+                            hipStream_t stream);
+
+/* GELU-tanh fused with bonsai_b1_pack_act_f16: packed fp16 activations of
+ * gelu(act), ready for bonsai_b1_linear_packed_f16.  Same requirements as
+ * bonsai_b1_pack_act_f16. */
+int bonsai_b1_gelu_tanh_pack_f16(const float *act, int64_t lda, int in_dim,
+                                 int batch, void *packed, hipStream_t stream);
+
+/*
  * The B1_0 writer on the device; replaces quantize_b1_0 of
  * convert_to_b1_0_packed.py:21-43 and of tests/c_ops/test_b1_linear.cpp:
  * 129-163.  w: fp32 [out_dim][ldw] device weights (ldw >= in_dim,

@@ -415,3 +415,56 @@ def test_quantize_matches_reference_writers(torch, b1, oracle, order):
     nbad = int((got.cpu().numpy() != want).sum())
     say(f"  quantize {order}: {nbad} differing bytes")
     assert nbad == 0
+
+
+# -------------------------------------------------------------- GELU-tanh --
+
+GELU_TOL = 1e-6  # |y - gelu64(x)| <= GELU_TOL * max(1, |x|); the fp32 formula alone is within 1.2e-7
+
+
+def gelu64(x):
+    x = np.asarray(x, np.float64)
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+def gelu_inputs(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    x[0, :12] = [0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0, 100.0, -100.0, 1e4, -1e4, 3e-8, -5.5]
+    return x
+
+
+def test_gelu_tanh_matches_float64(torch, b1):
+    x = gelu_inputs(37, 1028, 3)
+    big = torch.zeros((37, 1032), dtype=torch.float32)
+    big[:, :1028] = torch.from_numpy(x)
+    dx = big.cuda()[:, :1028]
+    y = b1.gelu_tanh(dx)
+    b1.gelu_tanh(dx, out=dx)                                     # in place
+    torch.cuda.synchronize()
+    ref = gelu64(x)
+    for got in (y.cpu().numpy(), dx.cpu().numpy()):
+        err = np.abs(got.astype(np.float64) - ref) / np.maximum(1.0, np.abs(x))
+        say(f"  gelu max scaled err {err.max():.2e}")
+        assert err.max() <= GELU_TOL
+    assert bool((big[:, 1028:] == 0).all()), "padding untouched"
+
+
+def test_gelu_pack_matches_pack_of_gelu(torch, b1, oracle):
+    """gelu_tanh_pack_f16 == the pack_act_f16 layout of fp16(gelu(x)): each
+    fp16 is within half an fp16 ulp (its rounding) plus the fp32 GELU bound
+    GELU_TOL * max(1, |x|) of the float64 GELU.  The second term dominates
+    in the fp16 subnormal range (large negative x, tiny outputs)."""
+    m, k = 6, 768
+    x = gelu_inputs(m, k, 4)
+    packed = b1.gelu_tanh_pack_f16(torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    got = packed.cpu().numpy().view(np.uint32).reshape(m, k // 32, 16)
+    lo = (got & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float64)
+    hi = (got >> 16).astype(np.uint16).view(np.float16).astype(np.float64)
+    vals = np.concatenate([lo, hi], axis=-1).reshape(m, k)     # back to element order
+    ref = gelu64(x)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    err = np.abs(vals - ref) - (0.5 * ulp + GELU_TOL * np.maximum(1.0, np.abs(x)))
+    say(f"  gelu pack worst margin {err.max():.2e}")
+    assert err.max() <= 0
