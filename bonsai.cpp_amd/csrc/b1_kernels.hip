@@ -50,12 +50,12 @@ constexpr uint32_t kSignPair = 0x80008000u;
 
 // Bits of m: ~(x ^ y); other bits: y.  One v_bitop3_b32, whose 8-bit table
 // is indexed by (x_bit << 2) | (m_bit << 1) | y_bit: 0xa6 = {0,1,1,0,0,1,0,1}
-// for indices 0..7.  Written as asm because gfx950 VOP3 takes no literal
-// and the compiler otherwise splits the select.
+// for indices 0..7.  Through the compiler builtin, not inline asm: the
+// compiler must see the VALU write, or it cannot insert the wait states an
+// MFMA reading the result as a source operand needs (an MFMA issued too
+// soon after an asm-hidden write read stale operands here).
 __device__ __forceinline__ uint32_t xnor_sel(uint32_t m, uint32_t x, uint32_t y) {
-    uint32_t r;
-    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0xa6" : "=v"(r) : "v"(x), "s"(m), "v"(y));
-    return r;
+    return __builtin_amdgcn_bitop3_b32(x, m, y, 0xa6);
 }
 
 // (lo, hi) -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32).
@@ -511,7 +511,8 @@ struct GemmLdsCfg {
     static constexpr int ROWB = KC * 2;               // LDS bytes per activation row
     static constexpr int ASTAGE = BM * ROWB;          // activation bytes per slot
     static constexpr int LPW = ASTAGE / 1024 / NW;    // 1 KB activation loads per wave
-    static constexpr int BWAVE = 2 * 1024;            // weight bytes per wave per slot
+    static constexpr int CG = WN / 64;                // 64-column weight load groups per wave
+    static constexpr int BWAVE = CG * 2 * 1024;       // weight bytes per wave per slot
     static constexpr int BSTAGE = NW * BWAVE;         // weight bytes per slot
     // Weight slots take the bottom of LDS and activation slots follow: the
     // 12-byte weight reads (ds_read_b96) returned wrong data at LDS
@@ -522,20 +523,26 @@ struct GemmLdsCfg {
     static constexpr int GROUP_M = 4;                 // tile grouping along M
     static constexpr int EPI_STORES = MT * NTL * 4;   // 16-byte stores per lane, full tile
     static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
-    static_assert(WN == 64, "one weight column per lane of the weight loads");
+    static_assert(WN % 64 == 0, "weight loads cover 64 columns, one per lane");
     static_assert(LDS <= 160 * 1024, "gfx950 LDS");
     static_assert(ABASE <= 65536, "ds_read_b96 addresses stay below 64 KiB");
     // vector memory operations that may be newer than stage s at its top:
     // the STAGES-2 stages fetched after it, plus at a tile's start the
     // previous tile's stores
-    static constexpr int AHEAD = (STAGES - 2) * (LPW + 2);
+    static constexpr int AHEAD = (STAGES - 2) * (LPW + 2 * CG);
+    // The previous tile's stores are counted in vmcnt waits when the count
+    // fits its 6 bits; otherwise a tile starts by draining them.
+    static constexpr bool COUNT_STORES = EPI_STORES + AHEAD <= 63;
+    // 8 waves: 2 per SIMD, 256 registers each.  4 waves (128-column wave
+    // tiles, 256 accumulators): 1 per SIMD with 512.
+    static constexpr int WAVES_PER_SIMD = NW >= 8 ? 2 : 1;
     static_assert(STAGES == 3, "the three-slot ring is the verified configuration");
-    static_assert(EPI_STORES + AHEAD <= 63, "vmcnt holds 6 bits");
+    static_assert(AHEAD <= 63, "vmcnt holds 6 bits");
 };
 
 // Two waves per SIMD (8 waves, one work-group per CU): 256 registers a wave.
 template <int BM, int BN, int WN, int STAGES>
-__global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16_t *__restrict__ ah,
+__global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gemm_kernel(const uint16_t *__restrict__ ah,
                                                                     const uint8_t *__restrict__ w, int K, int N,
                                                                     int M, float *__restrict__ out, int64_t ldo,
                                                                     int32_t *nonfinite, int tiles_m, int tiles_n,
@@ -570,7 +577,7 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
     // 2-3 of the stage) of column n0 + 64 wave + L; columns past N read
     // row N-1.  Neither is ever stored.
     uint32_t aoff[C::LPW];
-    uint32_t boff;
+    uint32_t boff[C::CG];
     auto setup = [&](int m0, int n0) {
 #pragma unroll
         for (int i = 0; i < C::LPW; ++i) {
@@ -578,7 +585,9 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
             const int c = (lane & 15) ^ (row & 15);
             aoff[i] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + (uint32_t)c * 8) * 2;
         }
-        boff = (uint32_t)min(n0 + wave * WN + lane, N - 1) * rs;
+#pragma unroll
+        for (int cg = 0; cg < C::CG; ++cg)
+            boff[cg] = (uint32_t)min(n0 + wave * WN + cg * 64 + lane, N - 1) * rs;
     };
     // The stage offset goes into the wave-uniform base, so each load is a
     // scalar base plus the lane's 32-bit offset (no per-lane 64-bit adds).
@@ -589,8 +598,11 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
         const uint8_t *wb = w + (uint32_t)ks * 24;
 #pragma unroll
         for (int i = 0; i < C::LPW; ++i) dma_lds16(ab + aoff[i], sa + i * 1024);
-        dma_lds12(wb + boff, sw);
-        dma_lds12(wb + 12 + boff, sw + 1024);
+#pragma unroll
+        for (int cg = 0; cg < C::CG; ++cg) {
+            dma_lds12(wb + boff[cg], sw + cg * 2048);
+            dma_lds12(wb + 12 + boff[cg], sw + cg * 2048 + 1024);
+        }
     };
 
     // Fragment offsets: lane (li, g) reads row li (+32 mt) at chunk
@@ -644,8 +656,8 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
                 for (int nt = 0; nt < C::NTL; ++nt) {
                     if ((b & 1) == 0) {
                         const __attribute__((address_space(3))) uint32_t *q =
-                            reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(sq + (b >> 1) * 1024 +
-                                                                                                   nt * 512);
+                            reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
+                                sq + (nt >> 1) * 2048 + (b >> 1) * 1024 + (nt & 1) * 512);
                         d[nt][0] = q[0];
                         d[nt][1] = q[1];
                         d[nt][2] = q[2];
@@ -744,9 +756,9 @@ __global__ __launch_bounds__((BN / WN) * 64, 2) void b1_gemm_kernel(const uint16
             for (int u = 0; u < STAGES; ++u) {
                 if (s + u + 1 >= nstage)
                     wait_vmcnt<0>();
-                else if (s == 0 && u < STAGES - 1 && prev_stores == 2)
-                    wait_vmcnt<C::EPI_STORES + C::AHEAD>();
-                else if (s == 0 && u == 0 && prev_stores == 1)
+                else if (C::COUNT_STORES && s == 0 && u < STAGES - 1 && prev_stores == 2)
+                    wait_vmcnt<(C::COUNT_STORES ? C::EPI_STORES + C::AHEAD : 0)>();
+                else if (s == 0 && u == 0 && prev_stores != 0)
                     wait_vmcnt<0>();
                 else
                     wait_vmcnt<C::AHEAD>();
