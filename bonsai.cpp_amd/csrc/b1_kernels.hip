@@ -514,10 +514,7 @@ struct GemmLdsCfg {
     static constexpr int CG = WN / 64;                // 64-column weight load groups per wave
     static constexpr int BWAVE = CG * 2 * 1024;       // weight bytes per wave per slot
     static constexpr int BSTAGE = NW * BWAVE;         // weight bytes per slot
-    // Weight slots take the bottom of LDS and activation slots follow: the
-    // 12-byte weight reads (ds_read_b96) returned wrong data at LDS
-    // addresses at or above 64 KiB on gfx950, while ds_read_b128 and
-    // ds_read_b32 read correctly there (measured on MI355X).
+    // Weight slots take the bottom of LDS and activation slots follow.
     static constexpr int ABASE = STAGES * BSTAGE;
     static constexpr int LDS = STAGES * (ASTAGE + BSTAGE);
     static constexpr int GROUP_M = 4;                 // tile grouping along M
@@ -525,7 +522,6 @@ struct GemmLdsCfg {
     static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
     static_assert(WN % 64 == 0, "weight loads cover 64 columns, one per lane");
     static_assert(LDS <= 160 * 1024, "gfx950 LDS");
-    static_assert(ABASE <= 65536, "ds_read_b96 addresses stay below 64 KiB");
     // vector memory operations that may be newer than stage s at its top:
     // the STAGES-2 stages fetched after it, plus at a tile's start the
     // previous tile's stores
