@@ -121,6 +121,9 @@ const char *bonsai_b1_status_string(int status) {
     case BONSAI_B1_ERR_HIP: return "HIP runtime error";
     case BONSAI_B1_ERR_NONFINITE: return "non-finite output";
     case BONSAI_B1_ERR_DEVICE: return "no usable gfx950 device";
+    case BONSAI_B1_ERR_NOT_FOUND: return "tensor not found";
+    case BONSAI_B1_ERR_FORMAT: return "malformed file or not a B1_0 tensor";
+    case BONSAI_B1_ERR_IO: return "file could not be opened";
     default: return "unknown status";
     }
 }

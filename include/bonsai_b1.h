@@ -59,7 +59,10 @@ enum {
     BONSAI_B1_ERR_ARG = 1,       /* bad shape, stride, pointer or mode */
     BONSAI_B1_ERR_HIP = 2,       /* a HIP runtime call failed */
     BONSAI_B1_ERR_NONFINITE = 3, /* output held NaN/Inf (reference: abort) */
-    BONSAI_B1_ERR_DEVICE = 4     /* no usable gfx950 device */
+    BONSAI_B1_ERR_DEVICE = 4,    /* no usable gfx950 device */
+    BONSAI_B1_ERR_NOT_FOUND = 5, /* no tensor of that name in the file */
+    BONSAI_B1_ERR_FORMAT = 6,    /* malformed file or not a B1_0 tensor */
+    BONSAI_B1_ERR_IO = 7         /* file could not be opened or mapped */
 };
 
 /* Arithmetic modes.
@@ -230,6 +233,24 @@ enum {
 int bonsai_b1_quantize_f32(const float *w, int64_t ldw, int in_dim,
                            int out_dim, void *packed, int order,
                            hipStream_t stream);
+
+/*
+ * Weight residency from a .safetensors file; replaces load_b1
+ * (src/diffuser.cpp:39-50) over the reader of src/safetensors.h:39-76.
+ * The tensor `name` must be U8 (or I8) [out_dim, in_dim/32*6], as
+ * convert_to_b1_0_packed.py writes it.  The file is mapped read-only, the
+ * tensor bytes uploaded as bonsai_b1_weights_upload does, and the stream
+ * synchronised before the mapping is released.  Errors: ERR_IO (open/map),
+ * ERR_NOT_FOUND, ERR_FORMAT (header, dtype, shape or offsets inconsistent).
+ */
+int bonsai_b1_weights_load_safetensors(const char *path, const char *name,
+                                       hipStream_t stream, B1Weights *out);
+
+/* The same lookup without a device: dimensions of tensor `name` and where
+ * its bytes lie in the file.  Any output pointer may be NULL. */
+int bonsai_b1_safetensors_info(const char *path, const char *name,
+                               int *in_dim, int *out_dim,
+                               uint64_t *data_offset, uint64_t *nbytes);
 
 /* Human-readable text for a status code (static storage). */
 const char *bonsai_b1_status_string(int status);
