@@ -10,6 +10,8 @@ from .capi import (  # noqa: F401
     MODES,
     Weights,
     declared_symbols,
+    device_weights,
+    linear_batch,
     gelu_tanh,
     gelu_tanh_pack_f16,
     library_path,

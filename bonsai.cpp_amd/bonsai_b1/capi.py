@@ -36,6 +36,11 @@ class B1WeightsC(ctypes.Structure):
                 ("nbytes", ctypes.c_size_t), ("device", ctypes.c_int)]
 
 
+class LinearOp(ctypes.Structure):
+    _fields_ = [("act", ctypes.c_void_p), ("lda", ctypes.c_int64), ("w", ctypes.POINTER(B1WeightsC)),
+                ("out", ctypes.c_void_p), ("ldo", ctypes.c_int64), ("batch", ctypes.c_int)]
+
+
 def library_path() -> Path:
     return _LIB
 
@@ -74,6 +79,11 @@ def load():
     L.bonsai_b1_version.restype = i
     L.bonsai_b1_linear_f32_f32.argtypes = [vp, i, i, vp]
     L.bonsai_b1_linear_f32_f32.restype = None
+    L.bonsai_b1_linear_batch.argtypes = [ctypes.POINTER(LinearOp), i, i, vp, vp, ctypes.c_size_t,
+                                         ctypes.POINTER(i), vp]
+    L.bonsai_b1_linear_batch.restype = i
+    L.bonsai_b1_linear_batch_workspace_bytes.argtypes = [ctypes.POINTER(LinearOp), i, i]
+    L.bonsai_b1_linear_batch_workspace_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_gelu_tanh_f32.argtypes = [vp, i64, vp, i64, i, i, vp]
     L.bonsai_b1_gelu_tanh_f32.restype = i
     L.bonsai_b1_gelu_tanh_pack_f16.argtypes = [vp, i64, i, i, vp, vp]
@@ -167,6 +177,38 @@ def gelu_tanh_pack_f16(act, packed=None, stream=None):
     if st != OK:
         raise B1Error(st, "bonsai_b1_gelu_tanh_pack_f16")
     return packed
+
+
+def device_weights(w_packed, in_dim: int, out_dim: int) -> B1WeightsC:
+    """A B1Weights view of packed weights already in a cuda tensor (the
+    tensor must outlive the view)."""
+    c = B1WeightsC()
+    c.data = w_packed.data_ptr()
+    c.in_dim, c.out_dim = in_dim, out_dim
+    c.nbytes = w_packed.numel()
+    c.device = w_packed.device.index or 0
+    return c
+
+
+def linear_batch(ops, mode: str = "auto", nonfinite=None, workspace=None, stream=None):
+    """bonsai_b1_linear_batch over [(act, B1WeightsC, out), ...] (cuda
+    tensors, act/out 2-D fp32 with unit column stride)."""
+    arr = (LinearOp * len(ops))()
+    keep = []
+    for i, (act, w, out) in enumerate(ops):
+        keep.append(w)
+        arr[i].act, arr[i].lda = act.data_ptr(), act.stride(0)
+        arr[i].w = ctypes.pointer(w)
+        arr[i].out, arr[i].ldo = out.data_ptr(), out.stride(0)
+        arr[i].batch = act.shape[0]
+    bad = ctypes.c_int(-1)
+    nf = nonfinite.data_ptr() if nonfinite is not None else None
+    ws = workspace.data_ptr() if workspace is not None else None
+    wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    st = load().bonsai_b1_linear_batch(arr, len(ops), MODES[mode], nf, ws, wsb, ctypes.byref(bad),
+                                       _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, f"bonsai_b1_linear_batch (op {bad.value})")
 
 
 SUM_ORDERS = {"numpy": 0, "sequential": 1}

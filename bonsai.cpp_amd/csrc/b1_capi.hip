@@ -286,6 +286,121 @@ void bonsai_b1_release_workspaces(void) {
     }
 }
 
+// How one op of a batch runs (the same choice linear_impl makes).
+enum class BatchPath { Exact, Gemv, Packed, Fused };
+
+static BatchPath batch_path(const b1::LinearArgs &a, int mode) {
+    if (mode == BONSAI_B1_MODE_EXACT) return BatchPath::Exact;
+    if (b1::gemv_supported(a)) return BatchPath::Gemv;
+    if (b1::gemm_supported(a))
+        return b1::gemm_workspace_bytes(a) > 0 ? BatchPath::Packed : BatchPath::Fused;
+    return BatchPath::Exact;
+}
+
+static b1::LinearArgs batch_args(const bonsai_b1_linear_op &op) {
+    b1::LinearArgs a;
+    a.act = op.act;
+    a.lda = op.lda;
+    a.w = static_cast<const uint8_t *>(op.w->data);
+    a.K = op.w->in_dim;
+    a.N = op.w->out_dim;
+    a.M = op.batch;
+    a.out = op.out;
+    a.ldo = op.ldo;
+    a.nonfinite = nullptr;
+    return a;
+}
+
+static bool batch_op_ok(const bonsai_b1_linear_op &op) {
+    if (!op.w || !op.w->data) return false;
+    return check_args(op.act, op.lda, op.w->data, op.w->in_dim, op.w->out_dim, op.batch, op.out, op.ldo) ==
+           BONSAI_B1_OK;
+}
+
+size_t bonsai_b1_linear_batch_workspace_bytes(const bonsai_b1_linear_op *ops, int n_ops, int mode) {
+    if (!ops || n_ops <= 0 || mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_FAST) return 0;
+    size_t need = 0;
+    for (int i = 0; i < n_ops; ++i) {
+        if (!batch_op_ok(ops[i]) || ops[i].batch == 0) continue;
+        const b1::LinearArgs a = batch_args(ops[i]);
+        if (batch_path(a, mode) == BatchPath::Packed) {
+            const size_t b = b1::gemm_workspace_bytes(a);
+            if (b > need) need = b;
+        }
+    }
+    return need;
+}
+
+int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops, int mode, int32_t *nonfinite,
+                           void *workspace, size_t workspace_bytes, int *bad_op, hipStream_t stream) {
+    if (bad_op) *bad_op = -1;
+    if (n_ops < 0 || (n_ops > 0 && !ops)) return BONSAI_B1_ERR_ARG;
+    if (mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_EXACT) return BONSAI_B1_ERR_ARG;
+    for (int i = 0; i < n_ops; ++i) {
+        if (!batch_op_ok(ops[i])) {
+            if (bad_op) *bad_op = i;
+            return BONSAI_B1_ERR_ARG;
+        }
+    }
+    DeviceInfo *dev = current_device(nullptr);
+    if (!dev) return BONSAI_B1_ERR_DEVICE;
+    const size_t need = bonsai_b1_linear_batch_workspace_bytes(ops, n_ops, mode);
+    if (need > 0) {
+        if (!workspace) {
+            workspace = stream_workspace(dev, stream, need);
+            workspace_bytes = workspace ? need : 0;
+        }
+        if (!workspace || workspace_bytes < need) return BONSAI_B1_ERR_ARG;
+    }
+    // The packed activations in the workspace belong to (act, lda, batch, K).
+    const float *packed_act = nullptr;
+    int64_t packed_lda = 0;
+    int packed_m = 0, packed_k = 0;
+    for (int i = 0; i < n_ops; ++i) {
+        if (ops[i].batch == 0) continue;
+        b1::LinearArgs a = batch_args(ops[i]);
+        a.nonfinite = nonfinite;
+        hipError_t e = hipSuccess;
+        switch (batch_path(a, mode)) {
+        case BatchPath::Exact:
+            e = b1::launch_exact(a, stream);
+            break;
+        case BatchPath::Gemv:
+            e = b1::launch_gemv(a, dev->num_cus, stream);
+            break;
+        case BatchPath::Fused:
+            e = b1::launch_gemm(a, dev->num_cus, nullptr, 0, stream);
+            break;
+        case BatchPath::Packed:
+            if (!(packed_act == a.act && packed_lda == a.lda && packed_m == a.M && packed_k == a.K)) {
+                e = b1::launch_pack(a.act, a.lda, a.M, a.K, workspace, stream);
+                packed_act = a.act;
+                packed_lda = a.lda;
+                packed_m = a.M;
+                packed_k = a.K;
+            }
+            if (e == hipSuccess)
+                e = b1::launch_gemm_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, nonfinite, dev->num_cus,
+                                           stream);
+            break;
+        }
+        if (e != hipSuccess) {
+            if (bad_op) *bad_op = i;
+            return BONSAI_B1_ERR_HIP;
+        }
+        // An output written over the packed activations' source invalidates
+        // the packing.
+        if (packed_act) {
+            const uintptr_t o0 = reinterpret_cast<uintptr_t>(a.out);
+            const uintptr_t o1 = o0 + ((size_t)(a.M - 1) * (size_t)a.ldo + (size_t)a.N) * sizeof(float);
+            const uintptr_t p0 = reinterpret_cast<uintptr_t>(packed_act);
+            const uintptr_t p1 = p0 + ((size_t)(packed_m - 1) * (size_t)packed_lda + (size_t)packed_k) * sizeof(float);
+            if (o0 < p1 && p0 < o1) packed_act = nullptr;
+        }
+    }
+    return BONSAI_B1_OK;
+}
+
 int bonsai_b1_linear(const float *act, const B1Weights *w, int batch,
                      float *out, B1LinearUserData *ud, int mode,
                      int32_t *nonfinite, hipStream_t stream) {

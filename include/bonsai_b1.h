@@ -156,6 +156,35 @@ int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w,
                                 hipStream_t stream);
 
 /*
+ * A sequence of B1_0 linears on one stream: the linear dispatch of a
+ * diffusion step (the b1 lambda at src/diffuser_graph.cpp:277-281 and its
+ * call sites, :354-361,434-457,482,536), run in the order given.  Each op is
+ * what bonsai_b1_linear would run for it.  Consecutive ops that read the
+ * same activations (same act, lda, batch and in_dim -- q/k/v of a block,
+ * :354-361) share one fp16 packing of them, so only the first pays the pack
+ * pass.  workspace: device buffer of bonsai_b1_linear_batch_workspace_bytes
+ * bytes, or NULL for the library's per-stream workspace.  On an invalid op
+ * nothing is launched and *bad_op (if given) receives its index.
+ * No reference counterpart: the reference builds one ggml node per linear.
+ */
+typedef struct bonsai_b1_linear_op {
+    const float *act;    /* fp32 [batch][lda] */
+    int64_t lda;
+    const B1Weights *w;  /* device-resident weights (in_dim, out_dim) */
+    float *out;          /* fp32 [batch][ldo] */
+    int64_t ldo;
+    int batch;
+} bonsai_b1_linear_op;
+
+size_t bonsai_b1_linear_batch_workspace_bytes(const bonsai_b1_linear_op *ops,
+                                              int n_ops, int mode);
+
+int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops,
+                           int mode, int32_t *nonfinite, void *workspace,
+                           size_t workspace_bytes, int *bad_op,
+                           hipStream_t stream);
+
+/*
  * Builder-style call; replaces bonsai::b1_linear(ctx, act, w, n_threads, ud)
  * (src/b1_0_kernel.h:290-300): fills ud from w (magic, in_dim, out_dim) and
  * runs the op for `batch` rows of act (the reference's act->ne[1]).

@@ -93,3 +93,20 @@ def test_pack_rejects_before_device():
     assert lib.bonsai_b1_pack_act_f16(fake + 4, 64, 64, 2, fake, None) == capi.ERR_ARG  # act alignment
     assert lib.bonsai_b1_pack_act_f16(fake, 64, 64, 2, fake + 8, None) == capi.ERR_ARG  # packed alignment
     assert lib.bonsai_b1_pack_act_f16(None, 64, 64, 2, fake, None) == capi.ERR_ARG
+
+
+def test_linear_batch_rejects_before_device():
+    lib = bonsai_b1.load()
+    assert lib.bonsai_b1_linear_batch(None, 1, 0, None, None, 0, None, None) == capi.ERR_ARG
+    w = capi.B1WeightsC()
+    w.data, w.in_dim, w.out_dim = 0x10000, 64, 32
+    bad_w = capi.B1WeightsC()
+    bad_w.data, bad_w.in_dim, bad_w.out_dim = 0x10000, 48, 32      # in_dim % 32 != 0
+    ops = (capi.LinearOp * 2)()
+    for i, ww in enumerate((w, bad_w)):
+        ops[i].act, ops[i].lda, ops[i].w = 0x10000, 64, ctypes.pointer(ww)
+        ops[i].out, ops[i].ldo, ops[i].batch = 0x10000, 32, 4
+    bad = ctypes.c_int(-1)
+    assert lib.bonsai_b1_linear_batch(ops, 2, 0, None, None, 0, ctypes.byref(bad), None) == capi.ERR_ARG
+    assert bad.value == 1
+    assert lib.bonsai_b1_linear_batch(ops, 1, 9, None, None, 0, None, None) == capi.ERR_ARG   # mode

@@ -468,3 +468,52 @@ def test_gelu_pack_matches_pack_of_gelu(torch, b1, oracle):
     err = np.abs(vals - ref) - (0.5 * ulp + GELU_TOL * np.maximum(1.0, np.abs(x)))
     say(f"  gelu pack worst margin {err.max():.2e}")
     assert err.max() <= 0
+
+
+# --------------------------------------------------------- batched dispatch --
+
+@pytest.mark.parametrize("mode", ["auto", "exact"])
+def test_linear_batch_matches_single_calls(torch, b1, mode):
+    """bonsai_b1_linear_batch == the same linears issued one by one (bit for
+    bit: same kernels), over q/k/v sharing one input, a small-M op, a K the
+    packed GEMM does not take (K % 384 != 0), a K % 64 != 0 op, and an op
+    that overwrites a packed input before the next op reads it."""
+    from bonsai_b1 import synth
+    def w(n, k, seed):
+        return synth.device_packed_weights(n, k, seed)
+    x = synth.device_activations(200, 768, 1)
+    y = synth.device_activations(200, 768, 2)
+    z = synth.device_activations(8, 3072, 3)
+    u = synth.device_activations(64, 96, 4)
+    v = synth.device_activations(130, 640, 5)
+    spec = [(x, w(600, 768, 10), 600), (x, w(300, 768, 11), 300), (x, w(40, 768, 12), 40),
+            (y, w(768, 768, 13), 768), (z, w(96, 3072, 14), 96), (u, w(32, 96, 15), 32),
+            (v, w(100, 640, 16), 100)]
+    x_over = x.clone()
+    ops = []
+    outs = [torch.full((a.shape[0], n + 4), 7.0, device="cuda")[:, :n] for a, _, n in spec]
+    for (a, wt, n), o in zip(spec, outs):
+        ops.append((a, b1.device_weights(wt, a.shape[1], n), o))
+    # 7: packed read of x_over (the packing is now of x_over)
+    x_before = torch.empty((200, 40), device="cuda")
+    ops.append((x_over, b1.device_weights(spec[2][1], 768, 40), x_before))
+    # 8: a small-M op (no packing) writes rows 0..7 of x_over
+    w_over = w(768, 3072, 17)
+    ops.append((z, b1.device_weights(w_over, 3072, 768), x_over[:8]))
+    # 9: reads x_over again: the stale packing must not be reused
+    o8 = torch.empty((200, 600), device="cuda")
+    ops.append((x_over, b1.device_weights(spec[0][1], 768, 600), o8))
+    b1.linear_batch(ops, mode=mode)
+    torch.cuda.synchronize()
+    for i, ((a, wt, n), o) in enumerate(zip(spec, outs)):
+        ref = b1.linear(a, wt, n, mode=mode)
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref), f"op {i}"
+    ref_before = b1.linear(x, spec[2][1], 40, mode=mode)
+    new_x = x.clone()
+    b1.linear(z, w_over, 768, out=new_x[:8], mode=mode)
+    ref8 = b1.linear(new_x, spec[0][1], 600, mode=mode)
+    torch.cuda.synchronize()
+    assert torch.equal(x_before, ref_before)
+    assert torch.equal(x_over, new_x)
+    assert torch.equal(o8, ref8)
