@@ -219,29 +219,32 @@ def bench_klein_step(torch, b1, synth):
             for mm in (mi, mt, ms_)}
     outs = {mm: {nn: torch.empty((mm, nn), device="cuda") for nn in (3072, 18432, 27648)} for mm in (mi, mt, ms_)}
     ws = torch.empty(ms_ * 12288 * 2, dtype=torch.uint8, device="cuda")
-    pk = torch.empty(ms_ * 12288 * 2, dtype=torch.uint8, device="cuda")
 
-    def step():
-        for per in d:
-            for st, mm in (("img", mi), ("txt", mt)):
-                x = acts[mm][3072]
-                b1.pack_act_f16(x, packed=pk)
-                for w in per[st]["qkv"]:
-                    b1.linear_packed_f16(pk, w, 3072, 3072, mm, out=outs[mm][3072])
-                b1.linear(x, per[st]["out"], 3072, out=outs[mm][3072], workspace=ws)
-                b1.linear(x, per[st]["ff_in"], 18432, out=outs[mm][18432], workspace=ws)
-                b1.linear(acts[mm][9216], per[st]["ff_out"], 3072, out=outs[mm][3072], workspace=ws)
-        for w1, w2 in s:
-            b1.linear(acts[ms_][3072], w1, 27648, out=outs[ms_][27648], workspace=ws)
-            b1.linear(acts[ms_][12288], w2, 3072, out=outs[ms_][3072], workspace=ws)
+    # the step as one bonsai_b1_linear_batch call, in graph order; q, k and
+    # v of each stream read the same input, so they share one packing
+    # (attention and FF-in inputs are stand-ins of the right shapes)
+    ops = []
+    attn = {mm: synth.device_activations(mm, 3072, 90 + mm) for mm in (mi, mt)}
+    for per in d:
+        for st, mm in (("img", mi), ("txt", mt)):
+            x = acts[mm][3072]
+            for w in per[st]["qkv"]:
+                ops.append((x, b1.device_weights(w, 3072, 3072), outs[mm][3072]))
+            ops.append((attn[mm], b1.device_weights(per[st]["out"], 3072, 3072), outs[mm][3072]))
+            ops.append((x, b1.device_weights(per[st]["ff_in"], 3072, 18432), outs[mm][18432]))
+            ops.append((acts[mm][9216], b1.device_weights(per[st]["ff_out"], 9216, 3072), outs[mm][3072]))
+    for w1, w2 in s:
+        ops.append((acts[ms_][3072], b1.device_weights(w1, 3072, 27648), outs[ms_][27648]))
+        ops.append((acts[ms_][12288], b1.device_weights(w2, 12288, 3072), outs[ms_][3072]))
+    assert len(ops) == 100
 
-    ms = graph_ms(torch, step, reps=2)
+    ms = graph_ms(torch, lambda: b1.linear_batch(ops, workspace=ws), reps=2)
     flop = (5 * 2 * (mi + mt) * (4 * 3072 * 3072 + 3072 * 18432 + 9216 * 3072)
             + 20 * 2 * ms_ * (3072 * 27648 + 12288 * 3072))
     nbytes = sum(w.numel() for per in d for st in per.values() for v in st.values()
                  for w in (v if isinstance(v, list) else [v])) + sum(a.numel() + b.numel() for a, b in s)
-    return {"linears": 100, "ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
-            "packed_weight_bytes": nbytes}
+    return {"linears": len(ops), "ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
+            "packed_weight_bytes": nbytes, "dispatch": "bonsai_b1_linear_batch, one call per step"}
 
 
 def bench_gemv(torch, b1, synth, m, k, n, steps, warmup):
