@@ -681,33 +681,98 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 
     // Epilogue.  Accumulator (n, m) layout of the 32x32 MFMA with weights as
     // A: lane column li = token m0 + 32 mt + li, rows 8*(v/4) + 4*g + v%4 =
-    // output columns; v = 4q..4q+3 are 4 consecutive columns.  Non-finite
-    // outputs are counted only when the caller passed a counter.
+    // output columns; v = 4q..4q+3 are 4 consecutive columns.  Stored as is,
+    // one 16-byte store instruction would cover 32 output rows x 32 bytes.
+    // Full tiles are first rearranged in registers so that each store
+    // instruction covers 8 rows x 128 bytes (whole cache lines):
+    //  1. v_permlane16_swap exchanges lanes 16-31 / 48-63 of column group
+    //     q = 2p with lanes 0-15 / 32-47 of q = 2p+1.  Register set (p, s)
+    //     then holds, in lane (li, g), token 32 mt + 16 s + (li % 16) at
+    //     columns 16p + 8 (li / 16) + 4g + 0..3.
+    //  2. A DPP row rotation by 8 exchanges lane bit 3 with p: register set
+    //     (t, s) holds token 32 mt + 16 s + 8 t + (lane % 8) at columns
+    //     16 ((lane / 8) % 2) + 8 ((lane / 16) % 2) + 4 (lane / 32) + 0..3.
+    // Non-finite outputs are counted only when the caller passed a counter.
     auto epilogue = [&](int m0, int n0) -> int {
         int bad = 0;
         const bool full = vec_store && m0 + BM <= M && n0 + BN <= N;
         const bool cnt = nonfinite != nullptr;
+        if (full) {
+            // the count does not depend on where each value is stored:
+            // take it before the rearrangement, outside the store path
+            if (cnt) {
 #pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt) {
-            const int m = m0 + mt * 32 + li;
+                for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < C::NTL; ++nt) {
+                    for (int nt = 0; nt < C::NTL; ++nt)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int n = n0 + wave * WN + nt * 32 + 8 * q + 4 * g;
-                    floatx4 y;
+                        for (int v = 0; v < 16; ++v) bad += !__builtin_isfinite(acc[mt][nt][v]);
+            }
+            // Buffer stores: the wave's tile origin in the resource, the lane
+            // part in one VGPR and the row offset in an SGPR, so the 32
+            // stores need no per-store address arithmetic.  The host enables
+            // vector stores only when 128 rows span < 2^31 bytes.
+            const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+                out + (size_t)m0 * ldo + n0 + wave * WN, (short)0, (int)(BM * ldo * 4), kBufferFlags);
+            const int lvoff = 4 * ((lane & 7) * (int)ldo + 16 * ((lane >> 3) & 1) + 8 * ((lane >> 4) & 1) +
+                                   4 * (lane >> 5));
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) y[r] = acc[mt][nt][4 * q + r];
-                    if (full) {
+            for (int mt = 0; mt < C::MT; ++mt) {
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) bad += cnt && !__builtin_isfinite(y[r]);
-                        *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + n) = y;
-                    } else if (m < M) {
+                for (int nt = 0; nt < C::NTL; ++nt) {
+                    floatx4 y[2][2]; // [s][t]
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            if (n + r < N) {
-                                bad += cnt && !__builtin_isfinite(y[r]);
-                                out[(size_t)m * ldo + n + r] = y[r];
+                    for (int r = 0; r < 4; ++r) {
+                        uint32_t x[2][2]; // [p][s] after step 1
+#pragma unroll
+                        for (int p = 0; p < 2; ++p) {
+                            // element values are copied out first: a bit cast
+                            // of a vector element reads element 0 in this clang
+                            const float xa = acc[mt][nt][8 * p + r], xb = acc[mt][nt][8 * p + 4 + r];
+                            const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, xa),
+                                                                             __builtin_bit_cast(uint32_t, xb),
+                                                                             false, false);
+                            x[p][0] = sw[0];
+                            x[p][1] = sw[1];
+                        }
+#pragma unroll
+                        for (int s = 0; s < 2; ++s) {
+                            // row_ror:8 reads lane ^ 8; bank mask 0xc writes
+                            // lanes 8-15 of each row, 0x3 lanes 0-7
+                            const int lo = (int)x[0][s], hi = (int)x[1][s];
+                            y[s][0][r] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(lo, hi, 0x128, 0xf, 0xc, false));
+                            y[s][1][r] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(hi, lo, 0x128, 0xf, 0x3, false));
+                        }
+                    }
+#pragma unroll
+                    for (int s = 0; s < 2; ++s)
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) {
+                            const int ro = 4 * ((mt * 32 + 16 * s + 8 * t) * (int)ldo + nt * 32);
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y[s][t]), ors, lvoff, ro,
+                                                                   0);
+                        }
+                    // one accumulator tile at a time keeps the temporaries
+                    // of the rearrangement within the register budget
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt) {
+                const int m = m0 + mt * 32 + li;
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int n = n0 + wave * WN + nt * 32 + 8 * q + 4 * g;
+                        if (m < M) {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                if (n + r < N) {
+                                    bad += cnt && !__builtin_isfinite(acc[mt][nt][4 * q + r]);
+                                    out[(size_t)m * ldo + n + r] = acc[mt][nt][4 * q + r];
+                                }
                             }
                         }
                     }
@@ -1210,7 +1275,7 @@ hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N
     const int ntiles = tiles_m * tiles_n;
     const int slots = num_cus > 0 ? num_cus * kWgPerCu : ntiles;
     const int grid = ntiles < slots ? ntiles : slots; // persistent
-    const int vec_store = (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ldo % 4 == 0;
+    const int vec_store = (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ldo % 4 == 0 && ldo < (int64_t(1) << 22);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
                        K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store);
     return hipGetLastError();
