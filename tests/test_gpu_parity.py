@@ -256,6 +256,29 @@ def test_nonfinite_counter(torch, b1, mode):
     assert int(ctr.item()) == m
 
 
+@pytest.mark.parametrize("m,n", [(256, 1024), (200, 600)])
+def test_nonfinite_counter_wide_tiles(torch, b1, m, n):
+    """The staged GEMM's counter on full 128 x 512 tiles (vector-store path)
+    and on ragged ones: a NaN activation poisons one output row, an Inf fp16
+    scale one output column."""
+    from bonsai_b1 import synth
+    k = 768
+    act = synth.activations(m, k, 5)
+    raw = synth.packed_weights(n, k, 6)
+    ctr = torch.zeros(1, dtype=torch.int32, device="cuda")
+    gpu_run(torch, b1, act, raw, n, "gemm", nonfinite=ctr)
+    assert int(ctr.item()) == 0
+    act[130, 9] = np.nan
+    gpu_run(torch, b1, act, raw, n, "gemm", nonfinite=ctr)
+    assert int(ctr.item()) == n
+    ctr.zero_()
+    act[130, 9] = 0.25
+    r3 = raw.reshape(n, k // 32, 6).copy()
+    r3[517, 3, 0:2] = [0x00, 0x7C]   # +Inf scale for output column 517, block 3
+    gpu_run(torch, b1, act, r3.reshape(n, -1), n, "gemm", nonfinite=ctr)
+    assert int(ctr.item()) == m
+
+
 def test_residency_builder_and_callback(torch, b1, oracle):
     """bonsai_b1_weights_upload + bonsai_b1_linear (b1_linear builder, fills
     the userdata) + the ggml-style callback over stand-in tensors."""
