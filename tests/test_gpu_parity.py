@@ -323,23 +323,26 @@ def test_residency_builder_and_callback(torch, b1, oracle):
     W.free()
 
 
-@pytest.mark.parametrize("mode,m", [("gemv", 8), ("gemm", 256)])
+@pytest.mark.parametrize("mode,m", [("gemv", 8), ("gemm", 256), ("gemm", 4608)])
 def test_graph_replay_matches_eager(torch, b1, mode, m):
-    """Launches captured into a HIP graph (as the benchmark does) give the
-    eager result on every replay, with eager work between replays."""
+    """Launches captured into a HIP graph (as the benchmark does) with the
+    caller's workspace give the eager result on every replay, with eager
+    work between replays; m=4608 runs more than one round of persistent
+    tiles per work-group."""
     from bonsai_b1 import synth
     k, n = 3072, 4096
     a = synth.device_activations(m, k, 31)
     w = synth.device_packed_weights(n, k, 32)
-    ref = b1.linear(a, w, n, mode=mode).clone()
+    ws = torch.empty(max(b1.workspace_bytes(m, k, n, mode), 16), dtype=torch.uint8, device="cuda")
+    ref = b1.linear(a, w, n, mode=mode, workspace=ws).clone()
     y = torch.empty((m, n), device="cuda")
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        b1.linear(a, w, n, out=y, mode=mode)
+        b1.linear(a, w, n, out=y, mode=mode, workspace=ws)
     for i in range(4):
         y.fill_(float(i + 1))
-        b1.linear(a * 0.5, w, n, mode=mode)        # unrelated eager work
+        b1.linear(a * 0.5, w, n, mode=mode, workspace=ws)   # unrelated eager work
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, ref), f"replay {i}"
