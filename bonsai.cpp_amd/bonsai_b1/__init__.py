@@ -12,6 +12,9 @@ from .capi import (  # noqa: F401
     declared_symbols,
     device_weights,
     linear_batch,
+    linear_epi,
+    linear_packed_f16_epi,
+    EPILOGUES,
     gelu_tanh,
     gelu_tanh_pack_f16,
     library_path,

@@ -36,6 +36,14 @@ class B1WeightsC(ctypes.Structure):
                 ("nbytes", ctypes.c_size_t), ("device", ctypes.c_int)]
 
 
+EPILOGUES = {"none": 0, "gate_residual": 1, "swiglu": 2}
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("gate", ctypes.c_void_p), ("residual", ctypes.c_void_p),
+                ("ldr", ctypes.c_int64)]
+
+
 class LinearOp(ctypes.Structure):
     _fields_ = [("act", ctypes.c_void_p), ("lda", ctypes.c_int64), ("w", ctypes.POINTER(B1WeightsC)),
                 ("out", ctypes.c_void_p), ("ldo", ctypes.c_int64), ("batch", ctypes.c_int)]
@@ -96,6 +104,13 @@ def load():
     L.bonsai_b1_pack_act_f16.restype = i
     L.bonsai_b1_linear_packed_f16.argtypes = [vp, vp, i, i, i, vp, i64, vp, vp]
     L.bonsai_b1_linear_packed_f16.restype = i
+    L.bonsai_b1_linear_packed_f16_epi.argtypes = [vp, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), vp, vp]
+    L.bonsai_b1_linear_packed_f16_epi.restype = i
+    L.bonsai_b1_linear_epi_workspace_bytes.argtypes = [i, i, i, i, i]
+    L.bonsai_b1_linear_epi_workspace_bytes.restype = ctypes.c_size_t
+    L.bonsai_b1_linear_epi_f32.argtypes = [vp, i64, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), i, vp, vp,
+                                           ctypes.c_size_t, vp]
+    L.bonsai_b1_linear_epi_f32.restype = i
     _lib = L
     return L
 
@@ -262,6 +277,65 @@ def linear_packed_f16(packed, w_packed, in_dim: int, out_dim: int, batch: int, o
                                             out.data_ptr(), out.stride(0), nf, _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_linear_packed_f16")
+    return out
+
+
+def _epilogue(kind: str, gate, residual, n_out: int, m: int):
+    """The C epilogue struct for `kind`, checking the tensors' shapes."""
+    import torch
+    e = Epilogue(EPILOGUES[kind], None, None, 0)
+    if kind == "gate_residual":
+        if gate is None or residual is None:
+            raise ValueError("gate_residual needs gate [N] and residual [M, >=N]")
+        for t in (gate, residual):
+            if t.dtype != torch.float32 or not t.is_cuda or t.stride(-1) != 1:
+                raise ValueError("gate and residual must be fp32 cuda tensors with unit column stride")
+        if gate.numel() < n_out or residual.dim() != 2 or residual.shape[0] != m or residual.shape[1] < n_out:
+            raise ValueError("gate must have N entries and residual shape [M, >=N]")
+        e.gate, e.residual, e.ldr = gate.data_ptr(), residual.data_ptr(), residual.stride(0)
+    return e
+
+
+def linear_epi(act, w_packed, out_dim: int, epilogue: str, gate=None, residual=None, out=None,
+               mode: str = "auto", nonfinite=None, workspace=None, stream=None):
+    """The linear with a fused epilogue (bonsai_b1_linear_epi_f32):
+    "gate_residual" -> out = residual + gate * y (residual may be out);
+    "swiglu" -> out[:, j] = silu(y[:, j]) * y[:, H + j], H = out_dim / 2."""
+    import torch
+    m, k = act.shape
+    cols = out_dim // 2 if epilogue == "swiglu" else out_dim
+    if out is None:
+        out = torch.empty((m, cols), dtype=torch.float32, device=act.device)
+    if out.dim() != 2 or out.shape[0] != m or out.shape[1] < cols or out.stride(1) != 1:
+        raise ValueError("out must be [M, >=cols] fp32 with unit column stride")
+    e = _epilogue(epilogue, gate, residual, out_dim, m)
+    nf = nonfinite.data_ptr() if nonfinite is not None else None
+    ws, wsb = (workspace.data_ptr(), workspace.numel() * workspace.element_size()) if workspace is not None \
+        else (None, 0)
+    st = load().bonsai_b1_linear_epi_f32(act.data_ptr(), act.stride(0), w_packed.data_ptr(), k, out_dim, m,
+                                         out.data_ptr(), out.stride(0), ctypes.byref(e), MODES[mode], nf, ws, wsb,
+                                         _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_linear_epi_f32")
+    return out
+
+
+def linear_packed_f16_epi(packed, w_packed, in_dim: int, out_dim: int, batch: int, epilogue: str, gate=None,
+                          residual=None, out=None, nonfinite=None, stream=None):
+    """bonsai_b1_linear_packed_f16_epi: the packed GEMM with its epilogue fused."""
+    import torch
+    cols = out_dim // 2 if epilogue == "swiglu" else out_dim
+    if out is None:
+        out = torch.empty((batch, cols), dtype=torch.float32, device=packed.device)
+    if out.dim() != 2 or out.shape[0] != batch or out.shape[1] < cols or out.stride(1) != 1:
+        raise ValueError("out must be [batch, >=cols] fp32 with unit column stride")
+    e = _epilogue(epilogue, gate, residual, out_dim, batch)
+    nf = nonfinite.data_ptr() if nonfinite is not None else None
+    st = load().bonsai_b1_linear_packed_f16_epi(packed.data_ptr(), w_packed.data_ptr(), in_dim, out_dim, batch,
+                                                out.data_ptr(), out.stride(0), ctypes.byref(e), nf,
+                                                _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_linear_packed_f16_epi")
     return out
 
 

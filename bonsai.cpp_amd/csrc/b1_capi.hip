@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <utility>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -274,6 +275,141 @@ int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w, int in_di
                                   nonfinite, dev->num_cus, stream) == hipSuccess
                ? BONSAI_B1_OK
                : BONSAI_B1_ERR_HIP;
+}
+
+// Checks an epilogue against a linear of out_dim outputs (weight rows) and
+// fills the kernels' form.  out's row length is out_dim, or out_dim / 2
+// for SwiGLU.
+static int epi_args(const bonsai_b1_epilogue *epi, int out_dim, int batch, const float *out, int64_t ldo, int *kind,
+                    b1::GemmEpi *g) {
+    *kind = epi ? epi->kind : BONSAI_B1_EPI_NONE;
+    *g = b1::GemmEpi();
+    auto span = [](const float *p, int rows, int64_t ld, int cols) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+        return std::pair<uintptr_t, uintptr_t>(a, a + ((size_t)(rows - 1) * (size_t)ld + (size_t)cols) * 4);
+    };
+    auto overlap = [](std::pair<uintptr_t, uintptr_t> x, std::pair<uintptr_t, uintptr_t> y) {
+        return x.first < y.second && y.first < x.second;
+    };
+    switch (*kind) {
+    case BONSAI_B1_EPI_NONE:
+        return ldo >= out_dim ? BONSAI_B1_OK : BONSAI_B1_ERR_ARG;
+    case BONSAI_B1_EPI_GATE_RESIDUAL: {
+        if (ldo < out_dim || epi->ldr < out_dim) return BONSAI_B1_ERR_ARG;
+        if (batch > 0) {
+            if (!epi->gate || !epi->residual) return BONSAI_B1_ERR_ARG;
+            if ((reinterpret_cast<uintptr_t>(epi->gate) & 3u) || (reinterpret_cast<uintptr_t>(epi->residual) & 3u))
+                return BONSAI_B1_ERR_ARG;
+            const auto o = span(out, batch, ldo, out_dim);
+            // the residual is out itself (read and written element by
+            // element) or lies apart from it; the gate lies apart
+            if (epi->residual == out) {
+                if (epi->ldr != ldo) return BONSAI_B1_ERR_ARG;
+            } else if (overlap(o, span(epi->residual, batch, epi->ldr, out_dim))) {
+                return BONSAI_B1_ERR_ARG;
+            }
+            if (overlap(o, span(epi->gate, 1, out_dim, out_dim))) return BONSAI_B1_ERR_ARG;
+        }
+        g->gate = epi->gate;
+        g->res = epi->residual;
+        g->ldr = epi->ldr;
+        return BONSAI_B1_OK;
+    }
+    case BONSAI_B1_EPI_SWIGLU:
+        if (out_dim % 64 != 0 || ldo < out_dim / 2) return BONSAI_B1_ERR_ARG;
+        g->glu_h = out_dim / 2;
+        return BONSAI_B1_OK;
+    default:
+        return BONSAI_B1_ERR_ARG;
+    }
+}
+
+int bonsai_b1_linear_packed_f16_epi(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
+                                    float *out, int64_t ldo, const bonsai_b1_epilogue *epi, int32_t *nonfinite,
+                                    hipStream_t stream) {
+    if (in_dim <= 0 || out_dim <= 0 || batch < 0) return BONSAI_B1_ERR_ARG;
+    if (batch > 0 && (!packed_act || !w || !out)) return BONSAI_B1_ERR_ARG;
+    if ((reinterpret_cast<uintptr_t>(packed_act) & 15u) || (reinterpret_cast<uintptr_t>(w) & 3u) ||
+        (reinterpret_cast<uintptr_t>(out) & 3u))
+        return BONSAI_B1_ERR_ARG;
+    int kind;
+    b1::GemmEpi g;
+    int st = epi_args(epi, out_dim, batch, out, ldo, &kind, &g);
+    if (st != BONSAI_B1_OK) return st;
+    if (!b1::gemm_packed_ok(batch > 0 ? batch : 1, in_dim, out_dim)) return BONSAI_B1_ERR_ARG;
+    DeviceInfo *dev = current_device(nullptr);
+    if (!dev) return BONSAI_B1_ERR_DEVICE;
+    if (batch == 0) return BONSAI_B1_OK;
+    return b1::launch_gemm_packed_epi(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
+                                      nonfinite, dev->num_cus, kind, g, stream) == hipSuccess
+               ? BONSAI_B1_OK
+               : BONSAI_B1_ERR_HIP;
+}
+
+// Whether a linear runs the packed FAST GEMM (as linear_impl decides).
+static bool packed_path(const b1::LinearArgs &a, int mode) {
+    if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return false;
+    if (mode != BONSAI_B1_MODE_GEMM && b1::gemv_supported(a)) return false;
+    return b1::gemm_supported(a) && b1::gemm_workspace_bytes(a) > 0 && b1::pack_supported(a.act, a.lda, a.M, a.K);
+}
+
+size_t bonsai_b1_linear_epi_workspace_bytes(int batch, int in_dim, int out_dim, int kind, int mode) {
+    if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
+    if (kind == BONSAI_B1_EPI_NONE) return bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode);
+    // either the fp16 packing (fused path) or the linear's output (separate pass)
+    const size_t pack = b1::gemm_packed_ok(batch, in_dim, out_dim) ? (size_t)batch * in_dim * 2 : 0;
+    const size_t y = (size_t)batch * out_dim * 4;
+    return pack > y ? pack : y;
+}
+
+int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int in_dim, int out_dim, int batch,
+                             float *out, int64_t ldo, const bonsai_b1_epilogue *epi, int mode, int32_t *nonfinite,
+                             void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    int kind;
+    b1::GemmEpi g;
+    int st = epi_args(epi, out_dim, batch, out, ldo, &kind, &g);
+    if (st != BONSAI_B1_OK) return st;
+    if (kind == BONSAI_B1_EPI_NONE)
+        return linear_impl(act, lda, w, in_dim, out_dim, batch, out, ldo, mode, nonfinite, workspace ? 1 : 0,
+                           workspace, workspace_bytes, stream);
+    st = check_args(act, lda, w, in_dim, out_dim, batch, out, out_dim);
+    if (st != BONSAI_B1_OK) return st;
+    if (mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_GEMV) return BONSAI_B1_ERR_ARG;
+    DeviceInfo *dev = current_device(nullptr);
+    if (!dev) return BONSAI_B1_ERR_DEVICE;
+    if (batch == 0) return BONSAI_B1_OK;
+    b1::LinearArgs a;
+    a.act = act;
+    a.lda = lda;
+    a.w = static_cast<const uint8_t *>(w);
+    a.K = in_dim;
+    a.N = out_dim;
+    a.M = batch;
+    a.out = out;
+    a.ldo = ldo;
+    a.nonfinite = nonfinite;
+    const bool fused = packed_path(a, mode);
+    const size_t need = fused ? (size_t)batch * in_dim * 2 : (size_t)batch * out_dim * 4;
+    if (!workspace) {
+        workspace = stream_workspace(dev, stream, need);
+        workspace_bytes = workspace ? need : 0;
+    }
+    if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
+        return BONSAI_B1_ERR_ARG;
+    hipError_t e;
+    if (fused) {
+        e = b1::launch_pack(act, lda, batch, in_dim, workspace, stream);
+        if (e == hipSuccess)
+            e = b1::launch_gemm_packed_epi(workspace, a.w, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus,
+                                           kind, g, stream);
+    } else {
+        // the linear into the workspace, then the epilogue pass
+        float *y = static_cast<float *>(workspace);
+        st = linear_impl(act, lda, w, in_dim, out_dim, batch, y, out_dim, mode, nonfinite, 1, nullptr, 0, stream);
+        if (st != BONSAI_B1_OK) return st;
+        e = b1::launch_epi(y, out_dim, batch, out_dim, kind, g, out, ldo, stream);
+    }
+    return e == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
 }
 
 void bonsai_b1_release_workspaces(void) {

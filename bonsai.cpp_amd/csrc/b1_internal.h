@@ -9,6 +9,16 @@
 
 namespace b1 {
 
+// What the packed GEMM's epilogue writes besides the plain product y
+// (kind 1: out = res + gate[n] * y; kind 2: SwiGLU over 2 glu_h weight
+// rows, out[m][j] = silu(y[m][j]) * y[m][glu_h + j]).
+struct GemmEpi {
+    const float *gate = nullptr; // [N]
+    const float *res = nullptr;  // [M][ldr]
+    int64_t ldr = 0;
+    int glu_h = 0;
+};
+
 struct LinearArgs {
     const float *act;   // [M][lda] fp32
     int64_t lda;        // elements
@@ -41,6 +51,16 @@ hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed
 bool gemm_packed_ok(int M, int K, int N);
 hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
                               int32_t *nonfinite, int num_cus, hipStream_t s);
+// The same GEMM with a fused epilogue (kind 0 plain, 1 gate-residual,
+// 2 SwiGLU with N = 2 glu_h, glu_h % 32 == 0, out [M][ldo >= glu_h]).
+hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
+                                  int64_t ldo, int32_t *nonfinite, int num_cus, int kind, const GemmEpi &epi,
+                                  hipStream_t s);
+
+// The epilogue (kind 1 or 2) as a separate pass over y [M][ldy] (N columns
+// of y; kind 2 writes glu_h of them).
+hipError_t launch_epi(const float *y, int64_t ldy, int M, int N, int kind, const GemmEpi &epi, float *out,
+                      int64_t ldo, hipStream_t s);
 
 // Small-M (M <= 16) bandwidth-bound kernel; requires K % 64 == 0,
 // lda % 4 == 0, act 16-byte aligned.

@@ -403,6 +403,45 @@ __global__ __launch_bounds__(256) void b1_gelu_pack_kernel(const float *__restri
     }
 }
 
+// silu(x) = x / (1 + e^-x), in fp32 with the device library's expf.
+__device__ __forceinline__ float silu_f32(float x) {
+#pragma clang fp contract(off)
+    return x / (1.0f + expf(-x));
+}
+
+// r + g y as the reference's two ggml ops (a multiply, then an add), each
+// rounded to fp32: never contracted into one FMA.
+__device__ __forceinline__ float gate_residual(float r, float g, float y) {
+#pragma clang fp contract(off)
+    const float t = g * y;
+    return r + t;
+}
+
+__device__ __forceinline__ float mul_f32(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+
+// ------------------------------------------------------ unfused epilogue --
+//
+// The GEMM epilogues as a separate pass over a linear's output y [M][ldy],
+// for the paths that do not run the packed GEMM; the same fp32 arithmetic
+// as the fused epilogue.  kind 1: out[m][c] = res[m][c] + gate[c] y[m][c];
+// kind 2: out[m][c] = silu(y[m][c]) y[m][H + c]; c < cols.
+
+__global__ __launch_bounds__(256) void b1_epi_kernel(const float *__restrict__ y, int64_t ldy, int M, int cols,
+                                                     int kind, const float *gate, const float *res, int64_t ldr,
+                                                     int H, float *out, int64_t ldo) {
+    const int64_t units = (int64_t)M * cols;
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+        const int64_t m = u / cols;
+        const int c = (int)(u - m * cols);
+        const float v = y[m * ldy + c];
+        out[m * ldo + c] = kind == 1 ? gate_residual(res[m * ldr + c], gate[c], v)
+                                     : mul_f32(silu_f32(v), y[m * ldy + H + c]);
+    }
+}
+
 // --------------------------------------------------------- weight writer --
 //
 // fp32 weights [N][ldw] -> packed B1_0, one thread per 32-weight block:
@@ -537,12 +576,20 @@ struct GemmLdsCfg {
 };
 
 // Two waves per SIMD (8 waves, one work-group per CU): 256 registers a wave.
-template <int BM, int BN, int WN, int STAGES>
+// EPI selects what the epilogue writes (GemmEpi):
+//   0  out = y
+//   1  out = residual + gate[n] * y (fp32 multiply, then add)
+//   2  SwiGLU over a weight matrix of 2H rows, gate rows [0, H) and value
+//      rows [H, 2H): the GEMM runs over the rows in the order gate block b
+//      (32 rows), value block b, ... so that one wave's two 32-column
+//      accumulator tiles hold a gate and its value for the same outputs;
+//      out[m][j] = silu(y[m][j]) * y[m][H + j], H columns.
+template <int BM, int BN, int WN, int STAGES, int EPI>
 __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gemm_kernel(const uint16_t *__restrict__ ah,
                                                                     const uint8_t *__restrict__ w, int K, int N,
                                                                     int M, float *__restrict__ out, int64_t ldo,
                                                                     int32_t *nonfinite, int tiles_m, int tiles_n,
-                                                                    int vec_store) {
+                                                                    int vec_store, GemmEpi epi) {
     using C = GemmLdsCfg<BM, BN, WN, STAGES>;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
@@ -582,8 +629,17 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
             aoff[i] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + (uint32_t)c * 8) * 2;
         }
 #pragma unroll
-        for (int cg = 0; cg < C::CG; ++cg)
-            boff[cg] = (uint32_t)min(n0 + wave * WN + cg * 64 + lane, N - 1) * rs;
+        for (int cg = 0; cg < C::CG; ++cg) {
+            const int c = min(n0 + wave * WN + cg * 64 + lane, N - 1);
+            int row = c;
+            if constexpr (EPI == 2) {
+                // GEMM column c -> weight row: 64-column block b holds gate
+                // rows 32b.. then value rows H + 32b..
+                const int b = c >> 6, within = c & 63;
+                row = within < 32 ? 32 * b + within : epi.glu_h + 32 * b + (within - 32);
+            }
+            boff[cg] = (uint32_t)row * rs;
+        }
     };
     // The stage offset goes into the wave-uniform base, so each load is a
     // scalar base plus the lane's 32-bit offset (no per-lane 64-bit adds).
@@ -695,8 +751,79 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
     // Non-finite outputs are counted only when the caller passed a counter.
     auto epilogue = [&](int m0, int n0) -> int {
         int bad = 0;
-        const bool full = vec_store && m0 + BM <= M && n0 + BN <= N;
         const bool cnt = nonfinite != nullptr;
+        if constexpr (EPI == 2) {
+            // lane (li, g): tile nt=0 holds gates, nt=1 their values, 4
+            // consecutive outputs per register quad
+            const int H = epi.glu_h;
+            const int jb = (n0 >> 1) + wave * 32;
+            const bool fullg = vec_store && m0 + BM <= M && jb + 32 <= H;
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt) {
+                const int m = m0 + mt * 32 + li;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int j = jb + 8 * q + 4 * g;
+                    floatx4 o;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float gt = acc[mt][0][4 * q + r], vl = acc[mt][1][4 * q + r];
+                        o[r] = mul_f32(silu_f32(gt), vl);
+                        if (cnt && m < M && j + r < H) bad += !__builtin_isfinite(gt) + !__builtin_isfinite(vl);
+                    }
+                    if (fullg) {
+                        *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + j) = o;
+                    } else if (m < M) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (j + r < H) out[(size_t)m * ldo + j + r] = o[r];
+                    }
+                }
+            }
+            count_nonfinite(nonfinite, bad);
+            return 1; // a store count the tile-start waits do not model
+        }
+        if constexpr (EPI == 1) {
+            // residual and gate read at the accumulator's own positions:
+            // lane (li, g) holds 4 consecutive columns of token 32 mt + li
+            const bool fullr = vec_store && m0 + BM <= M && n0 + BN <= N;
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt) {
+                const int m = m0 + mt * 32 + li;
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int n = n0 + wave * WN + nt * 32 + 8 * q + 4 * g;
+                        if (fullr) {
+                            const floatx4 rv = *reinterpret_cast<const floatx4 *>(epi.res + (size_t)m * epi.ldr + n);
+                            const floatx4 gw = *reinterpret_cast<const floatx4 *>(epi.gate + n);
+                            floatx4 o;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float yv = acc[mt][nt][4 * q + r];
+                                bad += cnt && !__builtin_isfinite(yv);
+                                o[r] = gate_residual(rv[r], gw[r], yv);
+                            }
+                            *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + n) = o;
+                        } else if (m < M) {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                if (n + r < N) {
+                                    const float yv = acc[mt][nt][4 * q + r];
+                                    bad += cnt && !__builtin_isfinite(yv);
+                                    out[(size_t)m * ldo + n + r] =
+                                        gate_residual(epi.res[(size_t)m * epi.ldr + n + r], epi.gate[n + r], yv);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+            count_nonfinite(nonfinite, bad);
+            return 1; // a store count the tile-start waits do not model
+        }
+        const bool full = vec_store && m0 + BM <= M && n0 + BN <= N;
         if (full) {
             // the count does not depend on where each value is stored:
             // take it before the rearrangement, outside the store path
@@ -714,8 +841,8 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
             // vector stores only when 128 rows span < 2^31 bytes.
             const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
                 out + (size_t)m0 * ldo + n0 + wave * WN, (short)0, (int)(BM * ldo * 4), kBufferFlags);
-            const int lvoff = 4 * ((lane & 7) * (int)ldo + 16 * ((lane >> 3) & 1) + 8 * ((lane >> 4) & 1) +
-                                   4 * (lane >> 5));
+            const int lcol = 16 * ((lane >> 3) & 1) + 8 * ((lane >> 4) & 1) + 4 * (lane >> 5);
+            const int lvoff = 4 * ((lane & 7) * (int)ldo + lcol);
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt) {
 #pragma unroll
@@ -1261,9 +1388,11 @@ hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
-                              int32_t *nonfinite, int num_cus, hipStream_t s) {
-    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages>;
+template <int EPI>
+static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
+                                       int64_t ldo, int32_t *nonfinite, int num_cus, const GemmEpi &epi,
+                                       hipStream_t s) {
+    auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages, EPI>;
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(attr_once, [kernel] {
@@ -1275,10 +1404,29 @@ hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N
     const int ntiles = tiles_m * tiles_n;
     const int slots = num_cus > 0 ? num_cus * kWgPerCu : ntiles;
     const int grid = ntiles < slots ? ntiles : slots; // persistent
-    const int vec_store = (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ldo % 4 == 0 && ldo < (int64_t(1) << 22);
+    auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    int vec_store = al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 22);
+    if (EPI == 1)
+        vec_store = vec_store && al16(epi.res) && al16(epi.gate) && epi.ldr % 4 == 0 && epi.ldr < (int64_t(1) << 22);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
-                       K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store);
+                       K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store, epi);
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
+                              int32_t *nonfinite, int num_cus, hipStream_t s) {
+    return launch_gemm_packed_t<0>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, GemmEpi{}, s);
+}
+
+hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
+                                  int64_t ldo, int32_t *nonfinite, int num_cus, int kind, const GemmEpi &epi,
+                                  hipStream_t s) {
+    switch (kind) {
+    case 0: return launch_gemm_packed_t<0>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
+    case 1: return launch_gemm_packed_t<1>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
+    case 2: return launch_gemm_packed_t<2>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s) {
@@ -1303,6 +1451,17 @@ hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *pack
     const int grid = (int)(want < 65535 ? want : 65535);
     hipLaunchKernelGGL(b1_quantize_kernel, dim3(grid), dim3(256), 0, s, w, ldw, K, N, static_cast<uint8_t *>(packed),
                        order);
+    return hipGetLastError();
+}
+
+hipError_t launch_epi(const float *y, int64_t ldy, int M, int N, int kind, const GemmEpi &epi, float *out,
+                      int64_t ldo, hipStream_t s) {
+    const int cols = kind == 2 ? epi.glu_h : N;
+    const int64_t units = (int64_t)M * cols;
+    const int64_t want = (units + 255) / 256;
+    const int grid = (int)(want < 8192 ? want : 8192);
+    hipLaunchKernelGGL(b1_epi_kernel, dim3(grid), dim3(256), 0, s, y, ldy, M, cols, kind, epi.gate, epi.res, epi.ldr,
+                       epi.glu_h, out, ldo);
     return hipGetLastError();
 }
 

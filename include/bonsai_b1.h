@@ -228,6 +228,52 @@ int bonsai_b1_weights_upload(const void *host_packed, size_t nbytes,
 int bonsai_b1_weights_free(B1Weights *w);
 
 /*
+ * Fused epilogues of the graph around a linear (src/diffuser_graph.cpp):
+ *  - BONSAI_B1_EPI_GATE_RESIDUAL: out = residual + gate[n] * y, the
+ *    modulation-gated residual add after out-projections and FF-out
+ *    (:441-442,459-460,538): h = h + gate * y, an fp32 multiply then an fp32
+ *    add.  residual [batch][ldr] may be out itself (same rows, ldr == ldo).
+ *  - BONSAI_B1_EPI_SWIGLU: the linear's out_dim = 2H outputs are [gate |
+ *    value] (weights rows [0, H) then [H, 2H)); out[m][j] = silu(y[m][j]) *
+ *    y[m][H + j], H columns (ggml_swiglu on FF-in, :453-456, 228).
+ *    H % 32 == 0; silu(x) = x / (1 + exp(-x)) in fp32.
+ * The non-finite counter counts the linear's own outputs y, as the
+ * reference's abort checks them (src/b1_0_kernel.h:194-198).
+ * No reference counterpart: the reference runs these as separate ggml ops.
+ */
+enum {
+    BONSAI_B1_EPI_NONE = 0,
+    BONSAI_B1_EPI_GATE_RESIDUAL = 1,
+    BONSAI_B1_EPI_SWIGLU = 2
+};
+typedef struct bonsai_b1_epilogue {
+    int kind;
+    const float *gate;     /* GATE_RESIDUAL: [out_dim], device */
+    const float *residual; /* GATE_RESIDUAL: [batch][ldr], device */
+    int64_t ldr;
+} bonsai_b1_epilogue;
+
+/* bonsai_b1_linear_packed_f16 with the epilogue fused into the GEMM. */
+int bonsai_b1_linear_packed_f16_epi(const void *packed_act, const void *w,
+                                    int in_dim, int out_dim, int batch,
+                                    float *out, int64_t ldo,
+                                    const bonsai_b1_epilogue *epi,
+                                    int32_t *nonfinite, hipStream_t stream);
+
+/* fp32 activations, any mode.  Where the packed FAST GEMM runs, the
+ * epilogue is fused into it; elsewhere (EXACT, small batch, K % 384 != 0)
+ * the linear writes y into the workspace and a separate pass applies the
+ * same fp32 arithmetic.  workspace: bonsai_b1_linear_epi_workspace_bytes
+ * bytes, or NULL for the library's per-stream workspace. */
+size_t bonsai_b1_linear_epi_workspace_bytes(int batch, int in_dim,
+                                            int out_dim, int kind, int mode);
+int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w,
+                             int in_dim, int out_dim, int batch, float *out,
+                             int64_t ldo, const bonsai_b1_epilogue *epi,
+                             int mode, int32_t *nonfinite, void *workspace,
+                             size_t workspace_bytes, hipStream_t stream);
+
+/*
  * GELU with the tanh approximation, 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715
  * x^3))), between the up- and down-projections of the Flux MLP workload.
  * Not a reference op: the reference MLP uses SwiGLU

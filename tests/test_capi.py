@@ -110,3 +110,46 @@ def test_linear_batch_rejects_before_device():
     assert lib.bonsai_b1_linear_batch(ops, 2, 0, None, None, 0, ctypes.byref(bad), None) == capi.ERR_ARG
     assert bad.value == 1
     assert lib.bonsai_b1_linear_batch(ops, 1, 9, None, None, 0, None, None) == capi.ERR_ARG   # mode
+
+
+def _epi(kind, gate=0, residual=0, ldr=0):
+    return capi.Epilogue(kind, gate or None, residual or None, ldr)
+
+
+@pytest.mark.parametrize("case", [
+    # (epilogue, out_dim, ldo)
+    ("swiglu_odd_h", 96, 48),          # H = 48, not a multiple of 32
+    ("swiglu_ldo", 128, 63),           # ldo < H
+    ("gate_no_res", 64, 64),           # gate-residual without a residual
+    ("gate_ldr", 64, 64),              # ldr < out_dim
+    ("res_overlap", 64, 64),           # residual overlapping out, not equal to it
+    ("res_alias_ld", 64, 64),          # residual == out with another row stride
+    ("kind", 64, 64),                  # unknown kind
+])
+def test_epilogue_rejected_before_device(case):
+    """bonsai_b1_linear_epi_f32 / _packed_f16_epi check the epilogue against
+    the linear's shape and buffers before touching the device."""
+    name, n, ldo = case
+    lib = bonsai_b1.load()
+    out = 0x100000
+    e = {"swiglu_odd_h": _epi(2), "swiglu_ldo": _epi(2),
+         "gate_no_res": _epi(1, gate=0x200000),
+         "gate_ldr": _epi(1, gate=0x200000, residual=0x300000, ldr=32),
+         "res_overlap": _epi(1, gate=0x200000, residual=out + 64, ldr=64),
+         "res_alias_ld": _epi(1, gate=0x200000, residual=out, ldr=128),
+         "kind": _epi(7)}[name]
+    m, k = 32, 384
+    assert lib.bonsai_b1_linear_epi_f32(0x400000, k, 0x500000, k, n, m, out, ldo, ctypes.byref(e), 0, None,
+                                        None, 0, None) == capi.ERR_ARG
+    assert lib.bonsai_b1_linear_packed_f16_epi(0x400000, 0x500000, k, n, m, out, ldo, ctypes.byref(e), None,
+                                               None) == capi.ERR_ARG
+
+
+def test_epilogue_workspace_bytes():
+    """The larger of the fp16 packing (fused path) and the linear's fp32
+    output (separate epilogue pass); none for a plain small-batch linear."""
+    lib = bonsai_b1.load()
+    assert lib.bonsai_b1_linear_epi_workspace_bytes(256, 3072, 6144, 2, 0) == max(256 * 3072 * 2, 256 * 6144 * 4)
+    assert lib.bonsai_b1_linear_epi_workspace_bytes(256, 3072, 1024, 1, 0) == max(256 * 3072 * 2, 256 * 1024 * 4)
+    assert lib.bonsai_b1_linear_epi_workspace_bytes(8, 3072, 1024, 0, 0) == 0
+    assert lib.bonsai_b1_linear_epi_workspace_bytes(8, 3000, 1024, 1, 0) == 0   # in_dim % 32

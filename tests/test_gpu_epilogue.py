@@ -1,0 +1,150 @@
+"""GPU checks of the fused GEMM epilogues (bonsai_b1_linear_epi_f32,
+bonsai_b1_linear_packed_f16_epi) against the same linear without them.
+
+Bars:
+  gate-residual : out = residual + gate * y is one fp32 multiply and one fp32
+                  add per element, so it must equal numpy's float32
+                  residual + gate * y bit for bit, y being the library's own
+                  plain linear output (the fused GEMM computes the same y).
+  SwiGLU        : out = silu(y[:, :H]) * y[:, H:] with silu = x / (1 + e^-x)
+                  in fp32 through the device expf; against the same formula
+                  in float64 on the library's y, |out - ref| <= 1e-6 *
+                  max(|ref|, 1e-30) + 1e-30 per element (expf and the fp32
+                  divide round within a few ulp).  The composition is also
+                  checked against the float64 oracle to the FAST bar.
+Paths: the packed GEMM with the epilogue fused (M > 16, K % 384 == 0), and
+the separate pass after the GEMV (M <= 16), after EXACT mode and after the
+fused-conversion GEMM (K % 384 != 0).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SILU_TOL = 1e-6
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "GPU tests need the MI355X"
+    return t
+
+
+@pytest.fixture(scope="module")
+def b1(torch):
+    import bonsai_b1
+    bonsai_b1.load()
+    return bonsai_b1
+
+
+CASES = [  # (m, k, n, mode): fused packed GEMM, ragged, GEMV pass, EXACT pass, conversion-GEMM pass
+    (256, 768, 1024, "auto"),
+    (200, 768, 640, "auto"),
+    (4608, 3072, 3072, "auto"),
+    (8, 3072, 512, "auto"),
+    (64, 384, 128, "exact"),
+    (200, 640, 576, "gemm"),
+]
+
+
+@pytest.mark.parametrize("m,k,n,mode", CASES)
+def test_gate_residual_bit_exact(torch, b1, m, k, n, mode):
+    from bonsai_b1 import synth
+    say(f"gate-residual ({m},{k},{n}) {mode}")
+    a = synth.device_activations(m, k, 61)
+    w = synth.device_packed_weights(n, k, 62)
+    gate = torch.randn(n, device="cuda")
+    res = torch.randn((m, n + 8), device="cuda")[:, :n]
+    y = b1.linear(a, w, n, mode=mode)
+    out = b1.linear_epi(a, w, n, "gate_residual", gate=gate, residual=res, mode=mode)
+    torch.cuda.synchronize()
+    want = res.cpu().numpy() + gate.cpu().numpy()[None, :] * y.cpu().numpy()   # float32 ops
+    got = out.cpu().numpy()
+    say(f"  mismatching elements: {int((got.view(np.uint32) != want.view(np.uint32)).sum())}")
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # in place: the residual is the output (h = h + gate * y)
+    h = res.clone()
+    b1.linear_epi(a, w, n, "gate_residual", gate=gate, residual=h, out=h, mode=mode)
+    torch.cuda.synchronize()
+    assert np.array_equal(h.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def _swiglu64(y, h):
+    y = y.astype(np.float64)
+    g, v = y[:, :h], y[:, h:2 * h]
+    return g / (1.0 + np.exp(-g)) * v
+
+
+@pytest.mark.parametrize("m,k,n,mode", CASES)
+def test_swiglu_matches_float64(torch, b1, oracle, m, k, n, mode):
+    from bonsai_b1 import synth
+    h = n // 2
+    if h % 32:
+        pytest.skip("H % 32 != 0")
+    say(f"swiglu ({m},{k},{n}) {mode}")
+    a = synth.device_activations(m, k, 63)
+    w = synth.device_packed_weights(n, k, 64)
+    y = b1.linear(a, w, n, mode=mode)
+    out = torch.full((m, h + 4), 7.0, device="cuda")
+    b1.linear_epi(a, w, n, "swiglu", out=out[:, :h], mode=mode)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert bool((got[:, h:] == 7.0).all()), "columns past H untouched"
+    ref = _swiglu64(y.cpu().numpy(), h)
+    err = np.abs(got[:, :h] - ref) / (np.maximum(np.abs(ref), 1e-30))
+    bad = np.abs(got[:, :h] - ref) > SILU_TOL * np.maximum(np.abs(ref), 1e-30) + 1e-30
+    say(f"  max rel err {float(err.max()):.3e}, {int(bad.sum())} beyond the bar")
+    assert not bad.any()
+    if m * n * k <= 3e9:
+        # the whole composition against the float64 oracle, FAST bar
+        yo = oracle.linear_f64(a.cpu().numpy(), w.cpu().numpy().reshape(n, -1), n)
+        ro = _swiglu64(yo, h)
+        den = np.maximum(np.abs(ro), np.sqrt(np.mean(ro * ro)))
+        r = float(np.max(np.abs(got[:, :h] - ro) / den))
+        say(f"  vs oracle rel_to_rms {r:.3e}")
+        assert r <= (1e-2 if mode != "exact" else 1e-5)
+
+
+def test_packed_entry_matches_f32_entry(torch, b1):
+    """bonsai_b1_linear_packed_f16_epi on the packed activations gives what
+    bonsai_b1_linear_epi_f32 gives (same kernels), for both epilogues."""
+    from bonsai_b1 import synth
+    m, k, n = 300, 1152, 1536
+    a = synth.device_activations(m, k, 65)
+    w = synth.device_packed_weights(n, k, 66)
+    gate = torch.randn(n, device="cuda")
+    res = torch.randn((m, n), device="cuda")
+    packed = b1.pack_act_f16(a)
+    for kind, kw in (("gate_residual", {"gate": gate, "residual": res}), ("swiglu", {})):
+        ref = b1.linear_epi(a, w, n, kind, **kw)
+        got = b1.linear_packed_f16_epi(packed, w, k, n, m, kind, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), kind
+
+
+def test_epilogue_counts_linear_outputs(torch, b1):
+    """The non-finite counter counts the linear's outputs y (the values the
+    reference's abort checks), fused or not: a NaN activation row poisons n
+    of them, before SwiGLU halves the columns."""
+    from bonsai_b1 import synth
+    for m, mode in ((256, "auto"), (8, "auto")):
+        k, n = 768, 512
+        act = synth.activations(m, k, 67)
+        act[3, 5] = np.nan
+        a = torch.from_numpy(act).cuda()
+        w = synth.device_packed_weights(n, k, 68)
+        for kind, kw in (("gate_residual", {"gate": torch.ones(n, device="cuda"),
+                                            "residual": torch.zeros((m, n), device="cuda")}),
+                         ("swiglu", {})):
+            ctr = torch.zeros(1, dtype=torch.int32, device="cuda")
+            b1.linear_epi(a, w, n, kind, mode=mode, nonfinite=ctr, **kw)
+            torch.cuda.synchronize()
+            assert int(ctr.item()) == n, (m, kind)
