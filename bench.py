@@ -155,6 +155,40 @@ def bench_mlp(torch, b1, synth):
     return r
 
 
+def bench_ff_epilogues(torch, b1, synth):
+    """The double-block feed-forward of the reference graph at 64x64 latents
+    (src/diffuser_graph.cpp:450-460, 4096 image tokens): FF-in 3072 ->
+    2 x 9216, SwiGLU, FF-out 9216 -> 3072, gate-residual add into h.  Once
+    with the element-wise steps as separate torch passes over the linears'
+    fp32 outputs, once with both fused into the GEMM epilogues."""
+    m, d, hid = 4096, 3072, 9216
+    x = synth.device_activations(m, d, 21)
+    w_in = synth.device_packed_weights(2 * hid, d, 22)
+    w_out = synth.device_packed_weights(d, hid, 23)
+    gate = torch.randn(d, device="cuda")
+    h = torch.randn((m, d), device="cuda")
+    y1 = torch.empty((m, 2 * hid), device="cuda")
+    act = torch.empty((m, hid), device="cuda")
+    y2 = torch.empty((m, d), device="cuda")
+    ws = torch.empty(max(b1.workspace_bytes(m, d, 2 * hid), b1.workspace_bytes(m, hid, d)), dtype=torch.uint8,
+                     device="cuda")
+
+    def separate():
+        b1.linear(x, w_in, 2 * hid, out=y1, workspace=ws)
+        torch.mul(torch.nn.functional.silu(y1[:, :hid]), y1[:, hid:], out=act)
+        b1.linear(act, w_out, d, out=y2, workspace=ws)
+        h.add_(gate * y2)
+
+    def fused():
+        b1.linear_epi(x, w_in, 2 * hid, "swiglu", out=act, workspace=ws)
+        b1.linear_epi(act, w_out, d, "gate_residual", gate=gate, residual=h, out=h, workspace=ws)
+
+    r = {"separate": graph_ms(torch, separate), "fused": graph_ms(torch, fused)}
+    flop = 2.0 * m * d * (2 * hid) + 2.0 * m * hid * d
+    r["fused_tflops"] = flop / (r["fused"] * 1e-3) / 1e12
+    return r
+
+
 def bench_single_stream_step(torch, b1, synth, blocks=38):
     """One diffusion step's worth of the Flux single-stream block linears,
     back to back on one stream: per block, linear1 4608 x 3072 -> 21504 and
@@ -385,6 +419,11 @@ def main():
         log(f"[bench] c4 MLP: up {mlp['up']*1e3:.1f} us, GELU {mlp['gelu']*1e3:.1f} us "
             f"({mlp['gelu_GBps']:.0f} GB/s), down {mlp['down']*1e3:.1f} us; chain {mlp['chain']*1e3:.1f} us "
             f"({mlp['chain_tflops']:.0f} TFLOP/s), GELU fused into the pack {mlp['chain_fused_gelu']*1e3:.1f} us")
+        ff = bench_ff_epilogues(torch, b1, synth)
+        extra["ff_epilogues"] = {x: round(v, 4) for x, v in ff.items()}
+        log(f"[bench] double-block FF (4096 x 3072 -> 2x9216, SwiGLU, -> 3072, gate-residual): separate "
+            f"passes {ff['separate']*1e3:.1f} us, fused epilogues {ff['fused']*1e3:.1f} us "
+            f"({ff['fused_tflops']:.0f} TFLOP/s)")
         torch.cuda.empty_cache()
         c5 = bench_single_stream_step(torch, b1, synth)
         extra["c5_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in c5.items()}
