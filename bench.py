@@ -189,6 +189,23 @@ def bench_ff_epilogues(torch, b1, synth):
     return r
 
 
+def bench_norm_mod(torch, b1, synth):
+    """LayerNorm + modulation of 4096 image tokens x 3072 straight into the
+    packed fp16 activations, against the same values through the separate
+    fp32 producer and the pack pass."""
+    m, d = 4096, 3072
+    x = synth.device_activations(m, d, 31)
+    sc = torch.randn(d, device="cuda") * 0.1
+    sh = torch.randn(d, device="cuda") * 0.1
+    y = torch.empty((m, d), device="cuda")
+    packed = torch.empty(m * d * 2, dtype=torch.uint8, device="cuda")
+    r = {"fused_pack": graph_ms(torch, lambda: [b1.norm_mod(x, sc, sh, packed=packed) for _ in range(8)]) / 8,
+         "fp32_then_pack": graph_ms(torch, lambda: [(b1.norm_mod(x, sc, sh, out=y), b1.pack_act_f16(y, packed=packed))
+                                                    for _ in range(8)]) / 8}
+    r["fused_GBps"] = m * d * 6 / (r["fused_pack"] * 1e-3) / 1e9
+    return r
+
+
 def bench_single_stream_step(torch, b1, synth, blocks=38):
     """One diffusion step's worth of the Flux single-stream block linears,
     back to back on one stream: per block, linear1 4608 x 3072 -> 21504 and
@@ -424,6 +441,10 @@ def main():
         log(f"[bench] double-block FF (4096 x 3072 -> 2x9216, SwiGLU, -> 3072, gate-residual): separate "
             f"passes {ff['separate']*1e3:.1f} us, fused epilogues {ff['fused']*1e3:.1f} us "
             f"({ff['fused_tflops']:.0f} TFLOP/s)")
+        nm = bench_norm_mod(torch, b1, synth)
+        extra["norm_mod"] = {x: round(v, 4) for x, v in nm.items()}
+        log(f"[bench] LayerNorm+modulation 4096x3072 -> packed fp16: {nm['fused_pack']*1e3:.1f} us "
+            f"({nm['fused_GBps']:.0f} GB/s); fp32 then pack {nm['fp32_then_pack']*1e3:.1f} us")
         torch.cuda.empty_cache()
         c5 = bench_single_stream_step(torch, b1, synth)
         extra["c5_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in c5.items()}

@@ -111,6 +111,10 @@ def load():
     L.bonsai_b1_linear_epi_f32.argtypes = [vp, i64, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), i, vp, vp,
                                            ctypes.c_size_t, vp]
     L.bonsai_b1_linear_epi_f32.restype = i
+    L.bonsai_b1_norm_mod_f32.argtypes = [vp, i64, i, i, vp, vp, ctypes.c_float, vp, i64, vp]
+    L.bonsai_b1_norm_mod_f32.restype = i
+    L.bonsai_b1_norm_mod_pack_f16.argtypes = [vp, i64, i, i, vp, vp, ctypes.c_float, vp, vp]
+    L.bonsai_b1_norm_mod_pack_f16.restype = i
     _lib = L
     return L
 
@@ -336,6 +340,29 @@ def linear_packed_f16_epi(packed, w_packed, in_dim: int, out_dim: int, batch: in
                                                 _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_linear_packed_f16_epi")
+    return out
+
+
+def norm_mod(x, scale, shift, eps: float = 1e-6, out=None, packed=None, stream=None):
+    """LayerNorm (no affine) + modulation x_n * (scale + 1) + shift over the
+    rows of x [rows, H]: fp32 into `out`, or, with packed=True or a uint8
+    tensor, the packed fp16 activations (bonsai_b1_norm_mod_pack_f16)."""
+    import torch
+    rows, h = x.shape
+    if packed is not None:
+        if packed is True:
+            packed = torch.empty(rows * h * 2, dtype=torch.uint8, device=x.device)
+        st = load().bonsai_b1_norm_mod_pack_f16(x.data_ptr(), x.stride(0), h, rows, scale.data_ptr(),
+                                                shift.data_ptr(), eps, packed.data_ptr(), _stream_handle(stream))
+        if st != OK:
+            raise B1Error(st, "bonsai_b1_norm_mod_pack_f16")
+        return packed
+    if out is None:
+        out = torch.empty((rows, h), dtype=torch.float32, device=x.device)
+    st = load().bonsai_b1_norm_mod_f32(x.data_ptr(), x.stride(0), h, rows, scale.data_ptr(), shift.data_ptr(), eps,
+                                       out.data_ptr(), out.stride(0), _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_norm_mod_f32")
     return out
 
 

@@ -231,6 +231,39 @@ int bonsai_b1_gelu_tanh_pack_f16(const float *act, int64_t lda, int in_dim, int 
                                                                                       : BONSAI_B1_ERR_HIP;
 }
 
+static int norm_mod_args(const float *x, int64_t ldx, int H, int rows, const float *scale, const float *shift,
+                         const void *dst) {
+    auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (H <= 0 || rows < 0 || H % BONSAI_B1_BLOCK_SIZE || ldx < H || ldx % 4) return BONSAI_B1_ERR_ARG;
+    if (rows > 0 && (!x || !scale || !shift || !dst)) return BONSAI_B1_ERR_ARG;
+    if (!al16(x) || !al16(scale) || !al16(shift) || !al16(dst)) return BONSAI_B1_ERR_ARG;
+    if ((uint64_t)rows * (uint64_t)H >= (1ull << 40)) return BONSAI_B1_ERR_ARG;
+    return BONSAI_B1_OK;
+}
+
+int bonsai_b1_norm_mod_f32(const float *x, int64_t ldx, int H, int rows, const float *scale, const float *shift,
+                           float eps, float *y, int64_t ldy, hipStream_t stream) {
+    int st = norm_mod_args(x, ldx, H, rows, scale, shift, y);
+    if (st != BONSAI_B1_OK) return st;
+    if (ldy < H || ldy % 4) return BONSAI_B1_ERR_ARG;
+    if (!current_device(nullptr)) return BONSAI_B1_ERR_DEVICE;
+    if (rows == 0) return BONSAI_B1_OK;
+    return b1::launch_norm_mod(x, ldx, H, rows, scale, shift, eps, y, ldy, nullptr, stream) == hipSuccess
+               ? BONSAI_B1_OK
+               : BONSAI_B1_ERR_HIP;
+}
+
+int bonsai_b1_norm_mod_pack_f16(const float *x, int64_t ldx, int H, int rows, const float *scale,
+                                const float *shift, float eps, void *packed, hipStream_t stream) {
+    int st = norm_mod_args(x, ldx, H, rows, scale, shift, packed);
+    if (st != BONSAI_B1_OK) return st;
+    if (!current_device(nullptr)) return BONSAI_B1_ERR_DEVICE;
+    if (rows == 0) return BONSAI_B1_OK;
+    return b1::launch_norm_mod(x, ldx, H, rows, scale, shift, eps, nullptr, 0, packed, stream) == hipSuccess
+               ? BONSAI_B1_OK
+               : BONSAI_B1_ERR_HIP;
+}
+
 int bonsai_b1_quantize_f32(const float *w, int64_t ldw, int in_dim, int out_dim, void *packed, int order,
                            hipStream_t stream) {
     if (in_dim <= 0 || out_dim < 0 || in_dim % BONSAI_B1_BLOCK_SIZE || ldw < in_dim) return BONSAI_B1_ERR_ARG;

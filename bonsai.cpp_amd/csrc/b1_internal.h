@@ -62,6 +62,13 @@ hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, i
 hipError_t launch_epi(const float *y, int64_t ldy, int M, int N, int kind, const GemmEpi &epi, float *out,
                       int64_t ldo, hipStream_t s);
 
+// LayerNorm (no affine, eps inside the square root) + modulation
+// x_n * (scale + 1) + shift over rows of H (H % 32 == 0, 16-byte aligned
+// rows and vectors); writes fp32 y [rows][ldy] or, with packed != nullptr,
+// the packed fp16 activations.
+hipError_t launch_norm_mod(const float *x, int64_t ldx, int H, int rows, const float *scale, const float *shift,
+                           float eps, float *y, int64_t ldy, void *packed, hipStream_t s);
+
 // Small-M (M <= 16) bandwidth-bound kernel; requires K % 64 == 0,
 // lda % 4 == 0, act 16-byte aligned.
 bool gemv_supported(const LinearArgs &a);

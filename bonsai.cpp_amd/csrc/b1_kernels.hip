@@ -422,6 +422,92 @@ __device__ __forceinline__ float mul_f32(float a, float b) {
     return a * b;
 }
 
+// ------------------------------------------- LayerNorm + modulation (A) --
+//
+// The producer of the linears' activations in the reference graph
+// (src/diffuser_graph.cpp:347-352, 444-448, 479-480):
+//   x_n = ggml_norm(x, eps):  (x - mean) / sqrt(var + eps) over a row,
+//   out = x_n * (scale[j] + 1) + shift[j],
+// each step an fp32 op (no FMA).  mean and var are accumulated in double
+// (the ggml CPU norm's ggml_float sums), mean = sum / H rounded to fp32,
+// var = sum((x - mean)^2) / H with each square an fp32 product.  One wave
+// per row; the row is read three times (sum, squares, output), from L2 after
+// the first.  The output is fp32 [rows][ldy], or fp16 in the K-slot pairing
+// the packed GEMM reads (word 16 blk + d = out[32 blk + d] | out[32 blk + d
+// + 16] << 16).
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float norm_mod(float x, float mean, float rstd, float sc, float sh) {
+#pragma clang fp contract(off)
+    const float n = (x - mean) * rstd;
+    return n * (sc + 1.0f) + sh;
+}
+
+__global__ __launch_bounds__(256) void b1_norm_mod_kernel(const float *__restrict__ x, int64_t ldx, int H, int rows,
+                                                          const float *__restrict__ scale,
+                                                          const float *__restrict__ shift, float eps,
+                                                          float *__restrict__ y, int64_t ldy,
+                                                          uint32_t *__restrict__ packed) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return; // whole wave
+    const float *xr = x + (size_t)row * ldx;
+    const int units = H / 32 * 4; // (block, quad): elements 32 blk + 4 t .. +3 and 16 later
+    double s = 0.0;
+    for (int u = lane; u < units; u += 64) {
+        const float *p = xr + (u >> 2) * 32 + (u & 3) * 4;
+        const floatx4 lo = *reinterpret_cast<const floatx4 *>(p);
+        const floatx4 hi = *reinterpret_cast<const floatx4 *>(p + 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s += (double)lo[j] + (double)hi[j];
+    }
+    const float mean = (float)(wave_sum_f64(s) / H);
+    double s2 = 0.0;
+    for (int u = lane; u < units; u += 64) {
+        const float *p = xr + (u >> 2) * 32 + (u & 3) * 4;
+        const floatx4 lo = *reinterpret_cast<const floatx4 *>(p);
+        const floatx4 hi = *reinterpret_cast<const floatx4 *>(p + 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float a = lo[j] - mean, b = hi[j] - mean;
+            s2 += (double)(a * a);
+            s2 += (double)(b * b);
+        }
+    }
+    const float var = (float)(wave_sum_f64(s2) / H);
+    const float rstd = 1.0f / sqrtf(var + eps);
+    for (int u = lane; u < units; u += 64) {
+        const int c = (u >> 2) * 32 + (u & 3) * 4;
+        const floatx4 lo = *reinterpret_cast<const floatx4 *>(xr + c);
+        const floatx4 hi = *reinterpret_cast<const floatx4 *>(xr + c + 16);
+        const floatx4 sl = *reinterpret_cast<const floatx4 *>(scale + c);
+        const floatx4 sh = *reinterpret_cast<const floatx4 *>(scale + c + 16);
+        const floatx4 tl = *reinterpret_cast<const floatx4 *>(shift + c);
+        const floatx4 th = *reinterpret_cast<const floatx4 *>(shift + c + 16);
+        floatx4 ol, oh;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ol[j] = norm_mod(lo[j], mean, rstd, sl[j], tl[j]);
+            oh[j] = norm_mod(hi[j], mean, rstd, sh[j], th[j]);
+        }
+        if (packed) {
+            u32x4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = pack_f16(ol[j], oh[j]);
+            *reinterpret_cast<u32x4 *>(packed + (size_t)row * (H / 2) + (u >> 2) * 16 + (u & 3) * 4) = v;
+        } else {
+            *reinterpret_cast<floatx4 *>(y + (size_t)row * ldy + c) = ol;
+            *reinterpret_cast<floatx4 *>(y + (size_t)row * ldy + c + 16) = oh;
+        }
+    }
+}
+
 // ------------------------------------------------------ unfused epilogue --
 //
 // The GEMM epilogues as a separate pass over a linear's output y [M][ldy],
@@ -1451,6 +1537,13 @@ hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *pack
     const int grid = (int)(want < 65535 ? want : 65535);
     hipLaunchKernelGGL(b1_quantize_kernel, dim3(grid), dim3(256), 0, s, w, ldw, K, N, static_cast<uint8_t *>(packed),
                        order);
+    return hipGetLastError();
+}
+
+hipError_t launch_norm_mod(const float *x, int64_t ldx, int H, int rows, const float *scale, const float *shift,
+                           float eps, float *y, int64_t ldy, void *packed, hipStream_t s) {
+    hipLaunchKernelGGL(b1_norm_mod_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, ldx, H, rows, scale, shift, eps,
+                       y, ldy, static_cast<uint32_t *>(packed));
     return hipGetLastError();
 }
 

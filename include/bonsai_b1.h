@@ -274,6 +274,25 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w,
                              size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * The producer of the linears' activations: LayerNorm without affine
+ * (ggml_norm, eps inside the square root) and the modulation
+ * x_n * (scale + 1) + shift, as the reference graph computes before each
+ * block's first linears (src/diffuser_graph.cpp:347-352, 444-448,
+ * 479-480).  Per row of H: mean and variance accumulated in double (the
+ * ggml CPU norm's accumulators), every other step an fp32 op.  The _pack
+ * form writes the packed fp16 activations bonsai_b1_linear_packed_f16
+ * reads, so the linear that follows runs without its own pack pass.
+ * H % 32 == 0; x, scale, shift, y 16-byte aligned; ldx, ldy % 4 == 0.
+ * No reference counterpart as one op (three ggml ops and a conversion).
+ */
+int bonsai_b1_norm_mod_f32(const float *x, int64_t ldx, int H, int rows,
+                           const float *scale, const float *shift, float eps,
+                           float *y, int64_t ldy, hipStream_t stream);
+int bonsai_b1_norm_mod_pack_f16(const float *x, int64_t ldx, int H, int rows,
+                                const float *scale, const float *shift,
+                                float eps, void *packed, hipStream_t stream);
+
+/*
  * GELU with the tanh approximation, 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715
  * x^3))), between the up- and down-projections of the Flux MLP workload.
  * Not a reference op: the reference MLP uses SwiGLU

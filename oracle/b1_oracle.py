@@ -12,6 +12,12 @@ Two layers:
     dequant_unrounded  tests/c_ops/test_b1_linear.py:21-34 (fp32 mean, no
                        fp16 rounding -- the reference tests' own expectation)
     avx2_lane_model    lane-by-lane numpy model of src/b1_0_kernel.h:116-192
+    norm_mod           ggml_norm + modulation of src/diffuser_graph.cpp:347-352
+                       (ggml itself is not vendored: the definition is the
+                       published LayerNorm, with the ggml CPU norm's double
+                       accumulators; pinned by closed forms in the tests)
+    swiglu_f64         silu(gate) * value over [gate | value]
+                       (tests/ops/test_all_ops.py:29-45 of the reference)
 * ctypes bindings of the C restatement in b1_oracle.c (scalar spec path,
   AVX2 path with the reference tiling, fp64 brute force, pack/unpack,
   fp16 conversions).  Build it with `make -C oracle`.
@@ -108,6 +114,47 @@ def avx2_lane_model(act: np.ndarray, raw: np.ndarray, n: int) -> np.ndarray:
 
 
 # ------------------------------------------------------------- C oracle ---
+
+def norm_mod(x: np.ndarray, scale: np.ndarray, shift: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """Per row of x [rows, H] (src/diffuser_graph.cpp:347-352):
+    mean = fp32(sum_f64(x) / H); v = fp32(x - mean);
+    var = fp32(sum_f64(fp32(v * v)) / H); rstd = fp32(1 / fp32(sqrt(fp32(var + eps))));
+    n = fp32(v * rstd); out = fp32(fp32(n * fp32(scale + 1)) + shift)."""
+    x = np.asarray(x, np.float32)
+    f = np.float32
+    h = x.shape[1]
+    mean = (x.astype(np.float64).sum(axis=1) / h).astype(np.float32)[:, None]
+    v = (x - mean).astype(np.float32)
+    var = ((v * v).astype(np.float32).astype(np.float64).sum(axis=1) / h).astype(np.float32)[:, None]
+    rstd = (f(1.0) / np.sqrt((var + f(eps)).astype(np.float32))).astype(np.float32)
+    n = (v * rstd).astype(np.float32)
+    t = (np.asarray(scale, np.float32) + f(1.0)).astype(np.float32)[None, :]
+    return ((n * t).astype(np.float32) + np.asarray(shift, np.float32)[None, :]).astype(np.float32)
+
+
+def norm_mod_f64(x: np.ndarray, scale: np.ndarray, shift: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """The same LayerNorm + modulation in float64 throughout."""
+    x = np.asarray(x, np.float64)
+    mean = x.mean(axis=1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=1, keepdims=True)
+    return (x - mean) / np.sqrt(var + eps) * (np.asarray(scale, np.float64) + 1.0) + np.asarray(shift, np.float64)
+
+
+def pack_act_words(a: np.ndarray) -> np.ndarray:
+    """fp32 [rows, K] -> the packed fp16 activations as u32 [rows, K/2]:
+    word 16 j + d = fp16(a[32 j + d]) | fp16(a[32 j + d + 16]) << 16 (RNE)."""
+    rows, k = a.shape
+    hb = fp32_to_fp16_bits(np.ascontiguousarray(a, np.float32)).reshape(rows, k // 32, 32).astype(np.uint32)
+    return (hb[:, :, :16] | (hb[:, :, 16:] << 16)).reshape(rows, k // 2)
+
+
+def swiglu_f64(y: np.ndarray) -> np.ndarray:
+    """[gate | value] -> silu(gate) * value in float64."""
+    y = np.asarray(y, np.float64)
+    h = y.shape[1] // 2
+    g = y[:, :h]
+    return g / (1.0 + np.exp(-g)) * y[:, h:2 * h]
+
 
 def build() -> None:
     """Compile the C restatement into oracle/_build/ (gcc, a few seconds)."""

@@ -153,3 +153,15 @@ def test_epilogue_workspace_bytes():
     assert lib.bonsai_b1_linear_epi_workspace_bytes(256, 3072, 1024, 1, 0) == max(256 * 3072 * 2, 256 * 1024 * 4)
     assert lib.bonsai_b1_linear_epi_workspace_bytes(8, 3072, 1024, 0, 0) == 0
     assert lib.bonsai_b1_linear_epi_workspace_bytes(8, 3000, 1024, 1, 0) == 0   # in_dim % 32
+
+
+def test_norm_mod_rejects_before_device():
+    lib = bonsai_b1.load()
+    f = 0x100000
+    ok = (f, 3072, 3072, 4, f + 0x10000, f + 0x20000, ctypes.c_float(1e-6))
+    assert lib.bonsai_b1_norm_mod_f32(f, 3072, 3000, 4, f, f, ctypes.c_float(1e-6), f, 3072, None) == capi.ERR_ARG  # H % 32
+    assert lib.bonsai_b1_norm_mod_f32(f, 3070, 3072, 4, f, f, ctypes.c_float(1e-6), f, 3072, None) == capi.ERR_ARG  # ldx < H
+    assert lib.bonsai_b1_norm_mod_f32(f + 4, 3072, 3072, 4, f, f, ctypes.c_float(1e-6), f, 3072, None) == capi.ERR_ARG
+    assert lib.bonsai_b1_norm_mod_f32(*ok, f + 0x30000, 3071, None) == capi.ERR_ARG      # ldy < H
+    assert lib.bonsai_b1_norm_mod_pack_f16(*ok, f + 8, None) == capi.ERR_ARG             # packed alignment
+    assert lib.bonsai_b1_norm_mod_pack_f16(f, 3072, 3072, 4, None, f, ctypes.c_float(1e-6), f, None) == capi.ERR_ARG

@@ -15,6 +15,8 @@ Bars:
 Paths: the packed GEMM with the epilogue fused (M > 16, K % 384 == 0), and
 the separate pass after the GEMV (M <= 16), after EXACT mode and after the
 fused-conversion GEMM (K % 384 != 0).
+The activation producer (LayerNorm + modulation, fp32 or packed fp16) is
+checked bit for bit against the oracle's restatement.
 """
 import sys
 
@@ -148,3 +150,38 @@ def test_epilogue_counts_linear_outputs(torch, b1):
             b1.linear_epi(a, w, n, kind, mode=mode, nonfinite=ctr, **kw)
             torch.cuda.synchronize()
             assert int(ctr.item()) == n, (m, kind)
+
+
+# ---------------------------------------------- LayerNorm + modulation (A) --
+
+@pytest.mark.parametrize("rows,h", [(4096, 3072), (37, 3072), (5, 12288), (3, 96)])
+def test_norm_mod_matches_oracle(torch, b1, oracle, rows, h):
+    """bonsai_b1_norm_mod_f32 against the oracle's restatement of ggml_norm
+    + modulation, bit for bit; the _pack form against the oracle's fp16 pack
+    of the same values; and a linear fed by the packed form equals the
+    linear of the fp32 form (the pack pass it replaces)."""
+    rng = np.random.default_rng(81)
+    x = (rng.standard_normal((rows, h)) * 2 + 0.5).astype(np.float32)
+    x[0, :] = 1.75                       # constant row: var = 0, out = shift
+    sc = (rng.standard_normal(h) * 0.2).astype(np.float32)
+    sh = (rng.standard_normal(h) * 0.2).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    scd, shd = torch.from_numpy(sc).cuda(), torch.from_numpy(sh).cuda()
+    y = b1.norm_mod(xd, scd, shd, eps=1e-6)
+    packed = b1.norm_mod(xd, scd, shd, eps=1e-6, packed=True)
+    torch.cuda.synchronize()
+    want = oracle.norm_mod(x, sc, sh, eps=1e-6)
+    got = y.cpu().numpy()
+    nbad = int((got.view(np.uint32) != want.view(np.uint32)).sum())
+    say(f"  norm_mod ({rows},{h}): {nbad} mismatching, max |diff| {float(np.abs(got - want).max()):.3e}")
+    assert nbad == 0
+    words = packed.cpu().numpy().view(np.uint32).reshape(rows, h // 2)
+    assert np.array_equal(words, oracle.pack_act_words(want))
+    if h % 384 == 0 and rows > 16:
+        from bonsai_b1 import synth
+        n = 512
+        w = synth.device_packed_weights(n, h, 82)
+        a = b1.linear(y, w, n, mode="gemm")
+        c = b1.linear_packed_f16(packed, w, h, n, rows)
+        torch.cuda.synchronize()
+        assert torch.equal(a, c)

@@ -341,3 +341,59 @@ def test_golden_fixtures_reproduce(oracle):
         assert np.array_equal(sc, c["y_scalar"]), name
         assert np.array_equal(av, c["y_avx2"]), name
         assert np.allclose(oracle.linear_f64(c["act"], c["w"], n), c["y_f64"], rtol=0, atol=1e-9), name
+
+
+# ------------------------------------------- LayerNorm + modulation, SwiGLU ----
+
+def test_norm_mod_closed_forms(oracle):
+    """oracle.norm_mod (ggml_norm + x_n * (scale + 1) + shift,
+    src/diffuser_graph.cpp:347-352) against what the mathematics fixes:
+    float64 LayerNorm within fp32 rounding; a constant row normalises to
+    exactly 0, so the output is exactly `shift`; scale = -1 gives exactly
+    `shift`; scale = shift = 0 leaves rows of mean 0 and variance
+    1 - eps / (var + eps) up to rounding; an affine change a x + b of a row
+    (a > 0) leaves the normalised row unchanged up to rounding."""
+    rng = np.random.default_rng(71)
+    h = 3072
+    x = (rng.standard_normal((6, h)) * 3 + 1.5).astype(np.float32)
+    sc = rng.standard_normal(h).astype(np.float32) * 0.1
+    sh = rng.standard_normal(h).astype(np.float32) * 0.1
+    y = oracle.norm_mod(x, sc, sh)
+    ref = oracle.norm_mod_f64(x, sc, sh)
+    assert np.max(np.abs(y - ref)) < 5e-6
+    xc = np.full((2, h), 3.25, np.float32)
+    assert np.array_equal(oracle.norm_mod(xc, sc, sh), np.broadcast_to(sh, (2, h)))
+    assert np.array_equal(oracle.norm_mod(x, np.full(h, -1, np.float32), sh), np.broadcast_to(sh, x.shape))
+    z = np.zeros(h, np.float32)
+    n0 = oracle.norm_mod(x, z, z).astype(np.float64)
+    assert np.all(np.abs(n0.mean(axis=1)) < 1e-6)
+    assert np.all(np.abs(n0.var(axis=1) - 1) < 1e-5)
+    n1 = oracle.norm_mod((x * np.float32(4.0) + np.float32(-7.0)).astype(np.float32), z, z)
+    assert np.max(np.abs(n1 - n0)) < 2e-5
+    # a plausible mistake: eps outside the square root
+    wrong = (x - x.mean(1, keepdims=True)) / (np.sqrt(x.var(1, keepdims=True)) + 1e-2)
+    assert np.max(np.abs(oracle.norm_mod(x, z, z, eps=1e-2) - wrong)) > 1e-4
+
+
+def test_pack_act_words_layout(oracle):
+    """Word 16 j + d of a row holds elements 32 j + d (low half) and
+    32 j + d + 16 (high half), each fp16 RNE (numpy astype(float16))."""
+    a = np.arange(2 * 64, dtype=np.float32).reshape(2, 64) / 8
+    w = oracle.pack_act_words(a)
+    h = a.astype(np.float16).view(np.uint16).astype(np.uint32)
+    assert w.shape == (2, 32)
+    assert w[1, 16 + 3] == h[1, 32 + 3] | (h[1, 32 + 3 + 16] << 16)
+    assert w[0, 0] == h[0, 0] | (h[0, 16] << 16)
+
+
+def test_swiglu_f64_definition(oracle):
+    """[gate | value] -> silu(gate) * value (the reference's own statement,
+    tests/ops/test_all_ops.py:29-45): silu(0) = 0, silu(x) -> x for large x,
+    and the halves are not swapped (value 0 gives 0 whatever the gate)."""
+    y = np.array([[0.0, 20.0, -20.0, 1.0, 5.0, 2.0, 3.0, 0.0]])
+    out = oracle.swiglu_f64(y)
+    assert out.shape == (1, 4)
+    assert out[0, 0] == 0.0
+    assert abs(out[0, 1] - 20.0 * 2.0) < 1e-6
+    assert abs(out[0, 2]) < 1e-6
+    assert out[0, 3] == 0.0
