@@ -448,6 +448,36 @@ __device__ __forceinline__ float norm_mod(float x, float mean, float rstd, float
     return n * (sc + 1.0f) + sh;
 }
 
+// Output of one (block, quad) unit: the 4 + 4 values of elements c..c+3
+// and c+16..c+19, as fp32 or as 4 packed fp16 words.
+__device__ __forceinline__ void norm_mod_store(const floatx4 &lo, const floatx4 &hi, int c, int u, int row, int H,
+                                               float mean, float rstd, const float *__restrict__ scale,
+                                               const float *__restrict__ shift, float *__restrict__ y, int64_t ldy,
+                                               uint32_t *__restrict__ packed) {
+    const floatx4 sl = *reinterpret_cast<const floatx4 *>(scale + c);
+    const floatx4 sh = *reinterpret_cast<const floatx4 *>(scale + c + 16);
+    const floatx4 tl = *reinterpret_cast<const floatx4 *>(shift + c);
+    const floatx4 th = *reinterpret_cast<const floatx4 *>(shift + c + 16);
+    floatx4 ol, oh;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        ol[j] = norm_mod(lo[j], mean, rstd, sl[j], tl[j]);
+        oh[j] = norm_mod(hi[j], mean, rstd, sh[j], th[j]);
+    }
+    if (packed) {
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = pack_f16(ol[j], oh[j]);
+        *reinterpret_cast<u32x4 *>(packed + (size_t)row * (H / 2) + (u >> 2) * 16 + (u & 3) * 4) = v;
+    } else {
+        *reinterpret_cast<floatx4 *>(y + (size_t)row * ldy + c) = ol;
+        *reinterpret_cast<floatx4 *>(y + (size_t)row * ldy + c + 16) = oh;
+    }
+}
+
+// U > 0: the row is held in registers (H <= 512 U), read once with all its
+// loads in flight.  U == 0: any H, the row read three times.
+template <int U>
 __global__ __launch_bounds__(256) void b1_norm_mod_kernel(const float *__restrict__ x, int64_t ldx, int H, int rows,
                                                           const float *__restrict__ scale,
                                                           const float *__restrict__ shift, float eps,
@@ -459,51 +489,70 @@ __global__ __launch_bounds__(256) void b1_norm_mod_kernel(const float *__restric
     if (row >= rows) return; // whole wave
     const float *xr = x + (size_t)row * ldx;
     const int units = H / 32 * 4; // (block, quad): elements 32 blk + 4 t .. +3 and 16 later
-    double s = 0.0;
-    for (int u = lane; u < units; u += 64) {
-        const float *p = xr + (u >> 2) * 32 + (u & 3) * 4;
-        const floatx4 lo = *reinterpret_cast<const floatx4 *>(p);
-        const floatx4 hi = *reinterpret_cast<const floatx4 *>(p + 16);
+    auto col = [](int u) { return (u >> 2) * 32 + (u & 3) * 4; };
+    if constexpr (U > 0) {
+        floatx4 lo[U], hi[U];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s += (double)lo[j] + (double)hi[j];
-    }
-    const float mean = (float)(wave_sum_f64(s) / H);
-    double s2 = 0.0;
-    for (int u = lane; u < units; u += 64) {
-        const float *p = xr + (u >> 2) * 32 + (u & 3) * 4;
-        const floatx4 lo = *reinterpret_cast<const floatx4 *>(p);
-        const floatx4 hi = *reinterpret_cast<const floatx4 *>(p + 16);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float a = lo[j] - mean, b = hi[j] - mean;
-            s2 += (double)(a * a);
-            s2 += (double)(b * b);
+        for (int i = 0; i < U; ++i) {
+            const int u = lane + 64 * i;
+            if (u < units) {
+                lo[i] = *reinterpret_cast<const floatx4 *>(xr + col(u));
+                hi[i] = *reinterpret_cast<const floatx4 *>(xr + col(u) + 16);
+            } else {
+                lo[i] = hi[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
         }
-    }
-    const float var = (float)(wave_sum_f64(s2) / H);
-    const float rstd = 1.0f / sqrtf(var + eps);
-    for (int u = lane; u < units; u += 64) {
-        const int c = (u >> 2) * 32 + (u & 3) * 4;
-        const floatx4 lo = *reinterpret_cast<const floatx4 *>(xr + c);
-        const floatx4 hi = *reinterpret_cast<const floatx4 *>(xr + c + 16);
-        const floatx4 sl = *reinterpret_cast<const floatx4 *>(scale + c);
-        const floatx4 sh = *reinterpret_cast<const floatx4 *>(scale + c + 16);
-        const floatx4 tl = *reinterpret_cast<const floatx4 *>(shift + c);
-        const floatx4 th = *reinterpret_cast<const floatx4 *>(shift + c + 16);
-        floatx4 ol, oh;
+        double s = 0.0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            ol[j] = norm_mod(lo[j], mean, rstd, sl[j], tl[j]);
-            oh[j] = norm_mod(hi[j], mean, rstd, sh[j], th[j]);
+        for (int i = 0; i < U; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s += (double)lo[i][j] + (double)hi[i][j];
+        const float mean = (float)(wave_sum_f64(s) / H);
+        double s2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            if (lane + 64 * i < units) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float a = lo[i][j] - mean, b = hi[i][j] - mean;
+                    s2 += (double)(a * a);
+                    s2 += (double)(b * b);
+                }
+            }
         }
-        if (packed) {
-            u32x4 v;
+        const float var = (float)(wave_sum_f64(s2) / H);
+        const float rstd = 1.0f / sqrtf(var + eps);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = pack_f16(ol[j], oh[j]);
-            *reinterpret_cast<u32x4 *>(packed + (size_t)row * (H / 2) + (u >> 2) * 16 + (u & 3) * 4) = v;
-        } else {
-            *reinterpret_cast<floatx4 *>(y + (size_t)row * ldy + c) = ol;
-            *reinterpret_cast<floatx4 *>(y + (size_t)row * ldy + c + 16) = oh;
+        for (int i = 0; i < U; ++i) {
+            const int u = lane + 64 * i;
+            if (u < units) norm_mod_store(lo[i], hi[i], col(u), u, row, H, mean, rstd, scale, shift, y, ldy, packed);
+        }
+    } else {
+        double s = 0.0;
+        for (int u = lane; u < units; u += 64) {
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(xr + col(u));
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(xr + col(u) + 16);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s += (double)lo[j] + (double)hi[j];
+        }
+        const float mean = (float)(wave_sum_f64(s) / H);
+        double s2 = 0.0;
+        for (int u = lane; u < units; u += 64) {
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(xr + col(u));
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(xr + col(u) + 16);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float a = lo[j] - mean, b = hi[j] - mean;
+                s2 += (double)(a * a);
+                s2 += (double)(b * b);
+            }
+        }
+        const float var = (float)(wave_sum_f64(s2) / H);
+        const float rstd = 1.0f / sqrtf(var + eps);
+        for (int u = lane; u < units; u += 64) {
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(xr + col(u));
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(xr + col(u) + 16);
+            norm_mod_store(lo, hi, col(u), u, row, H, mean, rstd, scale, shift, y, ldy, packed);
         }
     }
 }
@@ -1542,8 +1591,15 @@ hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *pack
 
 hipError_t launch_norm_mod(const float *x, int64_t ldx, int H, int rows, const float *scale, const float *shift,
                            float eps, float *y, int64_t ldy, void *packed, hipStream_t s) {
-    hipLaunchKernelGGL(b1_norm_mod_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, ldx, H, rows, scale, shift, eps,
-                       y, ldy, static_cast<uint32_t *>(packed));
+    const dim3 grid((rows + 3) / 4);
+    uint32_t *pk = static_cast<uint32_t *>(packed);
+    if (H <= 512 * 6)
+        hipLaunchKernelGGL(b1_norm_mod_kernel<6>, grid, dim3(256), 0, s, x, ldx, H, rows, scale, shift, eps, y, ldy, pk);
+    else if (H <= 512 * 24)
+        hipLaunchKernelGGL(b1_norm_mod_kernel<24>, grid, dim3(256), 0, s, x, ldx, H, rows, scale, shift, eps, y, ldy,
+                           pk);
+    else
+        hipLaunchKernelGGL(b1_norm_mod_kernel<0>, grid, dim3(256), 0, s, x, ldx, H, rows, scale, shift, eps, y, ldy, pk);
     return hipGetLastError();
 }
 
