@@ -251,51 +251,62 @@ def bench_klein_step(torch, b1, synth):
     latents (4096 image + 512 text tokens): 5 double-stream blocks (image and
     text q/k/v/out 3072 -> 3072, FF-in 3072 -> 18432, FF-out 9216 -> 3072)
     and 20 single-stream blocks (4608 x 3072 -> 27648, 12288 -> 3072), each
-    with resident weights (690 MB).  q/k/v of a stream share their input:
-    packed once, then three packed GEMMs."""
+    with resident weights (690 MB), as one bonsai_b1_linear_batch call per
+    step.  q, k and v of a stream read the same input; their weights are
+    stored back to back (as bonsai_b1_weights_concat lays them out) and
+    their outputs are adjacent column ranges, so the batch runs them as one
+    GEMM over 9216 rows.  The same step with q/k/v writing separate outputs
+    (three GEMMs sharing one packing) is timed beside it."""
     mi, mt, ms_ = 4096, 512, 4608
     d = []
     for blk in range(5):
         per = {}
         for st in ("img", "txt"):
-            per[st] = {"qkv": [synth.device_packed_weights(3072, 3072, 1000 + 40 * blk + i + (20 if st == "txt" else 0))
-                               for i in range(3)],
-                       "out": synth.device_packed_weights(3072, 3072, 1003 + 40 * blk + (20 if st == "txt" else 0)),
-                       "ff_in": synth.device_packed_weights(18432, 3072, 1004 + 40 * blk + (20 if st == "txt" else 0)),
-                       "ff_out": synth.device_packed_weights(3072, 9216, 1005 + 40 * blk + (20 if st == "txt" else 0))}
+            base = 1000 + 40 * blk + (20 if st == "txt" else 0)
+            qkv = torch.cat([synth.device_packed_weights(3072, 3072, base + i).reshape(-1) for i in range(3)])
+            per[st] = {"qkv": qkv,
+                       "out": synth.device_packed_weights(3072, 3072, base + 3),
+                       "ff_in": synth.device_packed_weights(18432, 3072, base + 4),
+                       "ff_out": synth.device_packed_weights(3072, 9216, base + 5)}
         d.append(per)
     s = [(synth.device_packed_weights(27648, 3072, 2000 + i), synth.device_packed_weights(3072, 12288, 2100 + i))
          for i in range(20)]
     acts = {mm: {kk: synth.device_activations(mm, kk, 16 + kk) for kk in (3072, 9216, 12288)}
             for mm in (mi, mt, ms_)}
-    outs = {mm: {nn: torch.empty((mm, nn), device="cuda") for nn in (3072, 18432, 27648)} for mm in (mi, mt, ms_)}
+    outs = {mm: {nn: torch.empty((mm, nn), device="cuda") for nn in (3072, 9216, 18432, 27648)} for mm in (mi, mt, ms_)}
     ws = torch.empty(ms_ * 12288 * 2, dtype=torch.uint8, device="cuda")
+    rs = 3072 // 32 * 6
 
-    # the step as one bonsai_b1_linear_batch call, in graph order; q, k and
-    # v of each stream read the same input, so they share one packing
-    # (attention and FF-in inputs are stand-ins of the right shapes)
-    ops = []
-    attn = {mm: synth.device_activations(mm, 3072, 90 + mm) for mm in (mi, mt)}
-    for per in d:
-        for st, mm in (("img", mi), ("txt", mt)):
-            x = acts[mm][3072]
-            for w in per[st]["qkv"]:
-                ops.append((x, b1.device_weights(w, 3072, 3072), outs[mm][3072]))
-            ops.append((attn[mm], b1.device_weights(per[st]["out"], 3072, 3072), outs[mm][3072]))
-            ops.append((x, b1.device_weights(per[st]["ff_in"], 3072, 18432), outs[mm][18432]))
-            ops.append((acts[mm][9216], b1.device_weights(per[st]["ff_out"], 9216, 3072), outs[mm][3072]))
-    for w1, w2 in s:
-        ops.append((acts[ms_][3072], b1.device_weights(w1, 3072, 27648), outs[ms_][27648]))
-        ops.append((acts[ms_][12288], b1.device_weights(w2, 12288, 3072), outs[ms_][3072]))
-    assert len(ops) == 100
+    def step_ops(fuse_qkv):
+        # graph order; attention and FF-in inputs are stand-ins of the right shapes
+        ops = []
+        attn = {mm: acts[mm][3072] for mm in (mi, mt)}
+        for per in d:
+            for st, mm in (("img", mi), ("txt", mt)):
+                x = acts[mm][3072]
+                for i in range(3):
+                    wv = b1.device_weights(per[st]["qkv"][i * 3072 * rs:(i + 1) * 3072 * rs], 3072, 3072)
+                    o = outs[mm][9216][:, i * 3072:(i + 1) * 3072] if fuse_qkv else outs[mm][3072]
+                    ops.append((x, wv, o))
+                ops.append((attn[mm], b1.device_weights(per[st]["out"], 3072, 3072), outs[mm][3072]))
+                ops.append((x, b1.device_weights(per[st]["ff_in"], 3072, 18432), outs[mm][18432]))
+                ops.append((acts[mm][9216], b1.device_weights(per[st]["ff_out"], 9216, 3072), outs[mm][3072]))
+        for w1, w2 in s:
+            ops.append((acts[ms_][3072], b1.device_weights(w1, 3072, 27648), outs[ms_][27648]))
+            ops.append((acts[ms_][12288], b1.device_weights(w2, 12288, 3072), outs[ms_][3072]))
+        assert len(ops) == 100
+        return ops
 
-    ms = graph_ms(torch, lambda: b1.linear_batch(ops, workspace=ws), reps=2)
+    ops_f, ops_s = step_ops(True), step_ops(False)
+    ms = graph_ms(torch, lambda: b1.linear_batch(ops_f, workspace=ws), reps=2)
+    ms_sep = graph_ms(torch, lambda: b1.linear_batch(ops_s, workspace=ws), reps=2)
     flop = (5 * 2 * (mi + mt) * (4 * 3072 * 3072 + 3072 * 18432 + 9216 * 3072)
             + 20 * 2 * ms_ * (3072 * 27648 + 12288 * 3072))
-    nbytes = sum(w.numel() for per in d for st in per.values() for v in st.values()
-                 for w in (v if isinstance(v, list) else [v])) + sum(a.numel() + b.numel() for a, b in s)
-    return {"linears": len(ops), "ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
-            "packed_weight_bytes": nbytes, "dispatch": "bonsai_b1_linear_batch, one call per step"}
+    nbytes = sum(v.numel() for per in d for st in per.values() for v in st.values()) + \
+        sum(a.numel() + b.numel() for a, b in s)
+    return {"linears": 100, "ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
+            "ms_per_step_separate_qkv": ms_sep, "packed_weight_bytes": nbytes,
+            "dispatch": "bonsai_b1_linear_batch, one call per step; q/k/v as one GEMM over concatenated weights"}
 
 
 def bench_gemv(torch, b1, synth, m, k, n, steps, warmup):
@@ -453,7 +464,8 @@ def main():
         torch.cuda.empty_cache()
         kl = bench_klein_step(torch, b1, synth)
         extra["klein_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in kl.items()}
-        log(f"[bench] Klein step (100 linears): {kl['ms_per_step']:.2f} ms ({kl['tflops']:.0f} TFLOP/s)")
+        log(f"[bench] Klein step (100 linears): {kl['ms_per_step']:.2f} ms ({kl['tflops']:.0f} TFLOP/s); "
+            f"q/k/v as three GEMMs {kl['ms_per_step_separate_qkv']:.2f} ms")
         torch.cuda.empty_cache()
 
     cpu = None

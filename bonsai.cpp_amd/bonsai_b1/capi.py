@@ -111,6 +111,8 @@ def load():
     L.bonsai_b1_linear_epi_f32.argtypes = [vp, i64, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), i, vp, vp,
                                            ctypes.c_size_t, vp]
     L.bonsai_b1_linear_epi_f32.restype = i
+    L.bonsai_b1_weights_concat.argtypes = [ctypes.POINTER(B1WeightsC), i, vp, ctypes.POINTER(B1WeightsC)]
+    L.bonsai_b1_weights_concat.restype = i
     L.bonsai_b1_norm_mod_f32.argtypes = [vp, i64, i, i, vp, vp, ctypes.c_float, vp, i64, vp]
     L.bonsai_b1_norm_mod_f32.restype = i
     L.bonsai_b1_norm_mod_pack_f16.argtypes = [vp, i64, i, i, vp, vp, ctypes.c_float, vp, vp]

@@ -540,7 +540,38 @@ int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops, int mode, 
         case BatchPath::Fused:
             e = b1::launch_gemm(a, dev->num_cus, nullptr, 0, stream);
             break;
-        case BatchPath::Packed:
+        case BatchPath::Packed: {
+            // Consecutive ops on this input whose weights follow each other
+            // in memory and whose outputs are adjacent column ranges of one
+            // row stride are one GEMM over the concatenated rows (q/k/v with
+            // concatenated weights, src/diffuser_graph.cpp:354-361), unless an
+            // output overlaps the input they all read.
+            int last = i;
+            int n_sum = a.N;
+            while (last + 1 < n_ops) {
+                const bonsai_b1_linear_op &p = ops[last], &q = ops[last + 1];
+                // the packed size from the dimensions (nbytes is not trusted)
+                const size_t p_bytes =
+                    (size_t)p.w->out_dim * (size_t)(p.w->in_dim / BONSAI_B1_BLOCK_SIZE) * BONSAI_B1_BLOCK_BYTES;
+                if (q.batch != a.M || q.act != a.act || q.lda != a.lda || q.w->in_dim != a.K || q.ldo != a.ldo ||
+                    q.w->data != static_cast<const uint8_t *>(p.w->data) + p_bytes ||
+                    q.out != p.out + p.w->out_dim || n_sum + (int64_t)q.w->out_dim > INT32_MAX)
+                    break;
+                b1::LinearArgs qa = batch_args(q);
+                if (batch_path(qa, mode) != BatchPath::Packed) break;
+                n_sum += q.w->out_dim;
+                ++last;
+            }
+            if (last > i) {
+                const uintptr_t o0 = reinterpret_cast<uintptr_t>(a.out);
+                const uintptr_t o1 = o0 + ((size_t)(a.M - 1) * (size_t)a.ldo + (size_t)n_sum) * sizeof(float);
+                const uintptr_t i0 = reinterpret_cast<uintptr_t>(a.act);
+                const uintptr_t i1 = i0 + ((size_t)(a.M - 1) * (size_t)a.lda + (size_t)a.K) * sizeof(float);
+                if (o0 < i1 && i0 < o1) {
+                    last = i;
+                    n_sum = a.N;
+                }
+            }
             if (!(packed_act == a.act && packed_lda == a.lda && packed_m == a.M && packed_k == a.K)) {
                 e = b1::launch_pack(a.act, a.lda, a.M, a.K, workspace, stream);
                 packed_act = a.act;
@@ -549,9 +580,12 @@ int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops, int mode, 
                 packed_k = a.K;
             }
             if (e == hipSuccess)
-                e = b1::launch_gemm_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, nonfinite, dev->num_cus,
+                e = b1::launch_gemm_packed(workspace, a.w, a.K, n_sum, a.M, a.out, a.ldo, nonfinite, dev->num_cus,
                                            stream);
+            a.N = n_sum; // the outputs written, for the overlap check below
+            i = last;
             break;
+        }
         }
         if (e != hipSuccess) {
             if (bad_op) *bad_op = i;
@@ -653,6 +687,42 @@ int bonsai_b1_weights_upload(const void *host_packed, size_t nbytes,
     out->in_dim = in_dim;
     out->out_dim = out_dim;
     out->nbytes = nbytes;
+    out->device = dev;
+    return BONSAI_B1_OK;
+}
+
+int bonsai_b1_weights_concat(const B1Weights *parts, int n_parts, hipStream_t stream, B1Weights *out) {
+    if (!parts || n_parts <= 0 || !out) return BONSAI_B1_ERR_ARG;
+    const int k = parts[0].in_dim;
+    size_t total = 0;
+    int64_t rows = 0;
+    for (int i = 0; i < n_parts; ++i) {
+        const B1Weights &p = parts[i];
+        if (!p.data || p.in_dim != k || p.out_dim <= 0 ||
+            p.nbytes != (size_t)p.out_dim * (size_t)(k / BONSAI_B1_BLOCK_SIZE) * BONSAI_B1_BLOCK_BYTES)
+            return BONSAI_B1_ERR_ARG;
+        total += p.nbytes;
+        rows += p.out_dim;
+    }
+    if (k <= 0 || k % BONSAI_B1_BLOCK_SIZE || rows > INT32_MAX) return BONSAI_B1_ERR_ARG;
+    int dev = 0;
+    if (!current_device(&dev)) return BONSAI_B1_ERR_DEVICE;
+    void *d = nullptr;
+    if (hipMalloc(&d, total) != hipSuccess) return BONSAI_B1_ERR_HIP;
+    size_t off = 0;
+    for (int i = 0; i < n_parts; ++i) {
+        if (hipMemcpyAsync(static_cast<uint8_t *>(d) + off, parts[i].data, parts[i].nbytes, hipMemcpyDeviceToDevice,
+                           stream) != hipSuccess) {
+            (void)hipStreamSynchronize(stream);
+            (void)hipFree(d);
+            return BONSAI_B1_ERR_HIP;
+        }
+        off += parts[i].nbytes;
+    }
+    out->data = d;
+    out->in_dim = k;
+    out->out_dim = (int)rows;
+    out->nbytes = total;
     out->device = dev;
     return BONSAI_B1_OK;
 }

@@ -162,7 +162,9 @@ int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w,
  * what bonsai_b1_linear would run for it.  Consecutive ops that read the
  * same activations (same act, lda, batch and in_dim -- q/k/v of a block,
  * :354-361) share one fp16 packing of them, so only the first pays the pack
- * pass.  workspace: device buffer of bonsai_b1_linear_batch_workspace_bytes
+ * pass; when their weights are also adjacent row ranges of one buffer
+ * (bonsai_b1_weights_concat) and their outputs adjacent column ranges with
+ * one row stride, they run as a single GEMM over the concatenated rows.  workspace: device buffer of bonsai_b1_linear_batch_workspace_bytes
  * bytes, or NULL for the library's per-stream workspace.  On an invalid op
  * nothing is launched and *bad_op (if given) receives its index.
  * No reference counterpart: the reference builds one ggml node per linear.
@@ -226,6 +228,19 @@ int bonsai_b1_weights_upload(const void *host_packed, size_t nbytes,
                              int in_dim, int out_dim, hipStream_t stream,
                              B1Weights *out);
 int bonsai_b1_weights_free(B1Weights *w);
+
+/*
+ * One device copy of several weight tensors of the same in_dim, rows back
+ * to back (out_dim = sum of the parts'): the N-concatenated weights of
+ * q, k and v (src/diffuser_graph.cpp:354-361) for one GEMM.  A part's rows
+ * stay a contiguous range, so a B1Weights {data + offset, in_dim, rows}
+ * names it; bonsai_b1_linear_batch runs consecutive ops over such adjacent
+ * ranges, with adjacent output columns, as one GEMM.  Free only the
+ * returned whole.  No reference counterpart (the reference keeps q, k, v
+ * separate).
+ */
+int bonsai_b1_weights_concat(const B1Weights *parts, int n_parts,
+                             hipStream_t stream, B1Weights *out);
 
 /*
  * Fused epilogues of the graph around a linear (src/diffuser_graph.cpp):

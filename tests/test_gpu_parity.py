@@ -543,3 +543,58 @@ def test_linear_batch_matches_single_calls(torch, b1, mode):
     assert torch.equal(x_before, ref_before)
     assert torch.equal(x_over, new_x)
     assert torch.equal(o8, ref8)
+
+
+def test_linear_batch_fuses_concatenated_qkv(torch, b1):
+    """q/k/v with weights as adjacent row ranges of one buffer and outputs as
+    adjacent column ranges of one tensor run as one GEMM over the
+    concatenated rows (bit for bit the three linears, which compute every
+    output column the same way); bonsai_b1_weights_concat builds that buffer
+    from separate device weights.  An op whose output overwrites the shared
+    input is not fused."""
+    import ctypes
+    from bonsai_b1 import capi, synth
+    m, k, n = 512, 3072, 1024
+    x = synth.device_activations(m, k, 91)
+    parts = [synth.device_packed_weights(n, k, 92 + i) for i in range(3)]
+    lib = b1.load()
+    cs = (capi.B1WeightsC * 3)(*[b1.device_weights(p, k, n) for p in parts])
+    cat = capi.B1WeightsC()
+    assert lib.bonsai_b1_weights_concat(cs, 3, None, ctypes.byref(cat)) == capi.OK
+    torch.cuda.synchronize()
+    assert cat.out_dim == 3 * n and cat.nbytes == 3 * parts[0].numel()
+    catd = torch.empty(cat.nbytes, dtype=torch.uint8, device="cuda")
+    import glob
+    import os
+    hip = ctypes.CDLL(sorted(glob.glob(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so*")))[0])
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(catd.data_ptr(), cat.data, cat.nbytes, 3) == 0     # device to device
+    assert torch.equal(catd, torch.cat([p.reshape(-1) for p in parts]))
+    rs = (k // 32) * 6
+    views = [capi.B1WeightsC(cat.data + i * n * rs, k, n, n * rs, cat.device) for i in range(3)]
+    qkv = torch.full((m, 3 * n + 4), 7.0, device="cuda")
+    ops = [(x, views[i], qkv[:, i * n:(i + 1) * n]) for i in range(3)]
+    b1.linear_batch(ops)
+    torch.cuda.synchronize()
+    for i in range(3):
+        ref = b1.linear(x, parts[i], n)
+        torch.cuda.synchronize()
+        assert torch.equal(qkv[:, i * n:(i + 1) * n], ref), i
+    assert bool((qkv[:, 3 * n:] == 7.0).all())
+    # the first output overwrites the input the others read: run in order
+    xx = torch.empty((m, 3 * n), device="cuda")
+    xx[:, :k] = x
+    a_in = xx[:, :k]
+    ops2 = [(a_in, views[0], xx[:, :n]), (a_in, views[1], xx[:, n:2 * n]), (a_in, views[2], xx[:, 2 * n:3 * n])]
+    b1.linear_batch(ops2)
+    x0 = x.clone()
+    y0 = b1.linear(x0, parts[0], n)
+    x1 = x0.clone()
+    x1[:, :n] = y0
+    y1 = b1.linear(x1, parts[1], n)
+    x2 = x1.clone()
+    x2[:, n:2 * n] = y1
+    y2 = b1.linear(x2, parts[2], n)
+    torch.cuda.synchronize()
+    assert torch.equal(xx[:, :n], y0) and torch.equal(xx[:, n:2 * n], y1) and torch.equal(xx[:, 2 * n:], y2)
+    assert lib.bonsai_b1_weights_free(ctypes.byref(cat)) == capi.OK
