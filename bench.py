@@ -499,7 +499,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(kern_tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": committed_traffic(TRAFFIC_PROFILE),
-                     "kernel": "b1_gemm_kernel<128,512,64>", "kernel_us": round(kern_ms * 1e3, 2),
+                     "kernel": "b1_gemm_kernel<128,512,64,3,0>", "kernel_us": round(kern_ms * 1e3, 2),
                      "algorithmic_flop": flop, "sclk_mhz_observed": sclk,
                      "step_minus_kernel_us": round(pack_ms * 1e3, 2),
                      "traffic_source": f"profiles/{TRAFFIC_PROFILE}.md",

@@ -279,7 +279,10 @@ int bonsai_b1_linear_packed_f16_epi(const void *packed_act, const void *w,
  * epilogue is fused into it; elsewhere (EXACT, small batch, K % 384 != 0)
  * the linear writes y into the workspace and a separate pass applies the
  * same fp32 arithmetic.  workspace: bonsai_b1_linear_epi_workspace_bytes
- * bytes, or NULL for the library's per-stream workspace. */
+ * bytes, or NULL for the library's per-stream workspace (which is never
+ * allocated while the stream is being captured: a capture needs a large
+ * enough library workspace from an earlier call, or the caller's, or the
+ * call returns BONSAI_B1_ERR_ARG). */
 size_t bonsai_b1_linear_epi_workspace_bytes(int batch, int in_dim,
                                             int out_dim, int kind, int mode);
 int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w,
