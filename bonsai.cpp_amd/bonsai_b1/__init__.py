@@ -13,6 +13,7 @@ from .capi import (  # noqa: F401
     device_weights,
     linear_batch,
     linear_epi,
+    linear_epi_workspace_bytes,
     norm_mod,
     linear_packed_f16_epi,
     EPILOGUES,

@@ -302,6 +302,11 @@ def _epilogue(kind: str, gate, residual, n_out: int, m: int):
     return e
 
 
+def linear_epi_workspace_bytes(batch: int, in_dim: int, out_dim: int, epilogue: str, mode: str = "auto") -> int:
+    return int(load().bonsai_b1_linear_epi_workspace_bytes(batch, in_dim, out_dim, EPILOGUES[epilogue],
+                                                            MODES[mode]))
+
+
 def linear_epi(act, w_packed, out_dim: int, epilogue: str, gate=None, residual=None, out=None,
                mode: str = "auto", nonfinite=None, workspace=None, stream=None):
     """The linear with a fused epilogue (bonsai_b1_linear_epi_f32):

@@ -185,3 +185,57 @@ def test_norm_mod_matches_oracle(torch, b1, oracle, rows, h):
         c = b1.linear_packed_f16(packed, w, h, n, rows)
         torch.cuda.synchronize()
         assert torch.equal(a, c)
+
+
+def test_epilogue_graph_replay(torch, b1):
+    """The fused SwiGLU and gate-residual linears captured in a HIP graph with
+    the caller's workspace give the eager result on every replay (the
+    gate-residual writes a fresh output each time: out != residual)."""
+    from bonsai_b1 import synth
+    m, k, n = 512, 3072, 2048
+    a = synth.device_activations(m, k, 71)
+    w = synth.device_packed_weights(n, k, 72)
+    gate = torch.randn(n, device="cuda")
+    res = torch.randn((m, n), device="cuda")
+    ws = torch.empty(max(b1.linear_epi_workspace_bytes(m, k, n, "swiglu"),
+                         b1.linear_epi_workspace_bytes(m, k, n, "gate_residual")), dtype=torch.uint8, device="cuda")
+    ref_g = b1.linear_epi(a, w, n, "swiglu", workspace=ws).clone()
+    ref_r = b1.linear_epi(a, w, n, "gate_residual", gate=gate, residual=res, workspace=ws).clone()
+    og = torch.empty((m, n // 2), device="cuda")
+    orr = torch.empty((m, n), device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        b1.linear_epi(a, w, n, "swiglu", out=og, workspace=ws)
+        b1.linear_epi(a, w, n, "gate_residual", gate=gate, residual=res, out=orr, workspace=ws)
+    for i in range(3):
+        og.fill_(float(i))
+        orr.fill_(float(i))
+        b1.linear(a * 0.25, w, n)       # unrelated eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(og, ref_g) and torch.equal(orr, ref_r), f"replay {i}"
+
+
+def test_two_streams_own_workspaces(torch, b1):
+    """Calls on two streams with library-owned workspaces run concurrently
+    without sharing a packing buffer: each stream's results equal the
+    serial ones."""
+    from bonsai_b1 import synth
+    m, k, n = 1024, 3072, 4096
+    a1 = synth.device_activations(m, k, 73)
+    a2 = synth.device_activations(m, k, 74)
+    w = synth.device_packed_weights(n, k, 75)
+    r1 = b1.linear(a1, w, n)
+    r2 = b1.linear(a2, w, n)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    o1 = torch.empty((m, n), device="cuda")
+    o2 = torch.empty((m, n), device="cuda")
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            b1.linear(a1, w, n, out=o1)
+        with torch.cuda.stream(s2):
+            b1.linear(a2, w, n, out=o2)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, r1) and torch.equal(o2, r2)
