@@ -49,6 +49,10 @@ class LinearOp(ctypes.Structure):
                 ("out", ctypes.c_void_p), ("ldo", ctypes.c_int64), ("batch", ctypes.c_int)]
 
 
+class LinearOpEpi(ctypes.Structure):
+    _fields_ = [("op", LinearOp), ("epi", Epilogue)]
+
+
 def library_path() -> Path:
     return _LIB
 
@@ -111,6 +115,11 @@ def load():
     L.bonsai_b1_linear_epi_f32.argtypes = [vp, i64, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), i, vp, vp,
                                            ctypes.c_size_t, vp]
     L.bonsai_b1_linear_epi_f32.restype = i
+    L.bonsai_b1_linear_batch_epi.argtypes = [ctypes.POINTER(LinearOpEpi), i, i, vp, vp, ctypes.c_size_t,
+                                             ctypes.POINTER(i), vp]
+    L.bonsai_b1_linear_batch_epi.restype = i
+    L.bonsai_b1_linear_batch_epi_workspace_bytes.argtypes = [ctypes.POINTER(LinearOpEpi), i, i]
+    L.bonsai_b1_linear_batch_epi_workspace_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_weights_concat.argtypes = [ctypes.POINTER(B1WeightsC), i, vp, ctypes.POINTER(B1WeightsC)]
     L.bonsai_b1_weights_concat.restype = i
     L.bonsai_b1_norm_mod_f32.argtypes = [vp, i64, i, i, vp, vp, ctypes.c_float, vp, i64, vp]
@@ -213,21 +222,32 @@ def device_weights(w_packed, in_dim: int, out_dim: int) -> B1WeightsC:
 
 def linear_batch(ops, mode: str = "auto", nonfinite=None, workspace=None, stream=None):
     """bonsai_b1_linear_batch over [(act, B1WeightsC, out), ...] (cuda
-    tensors, act/out 2-D fp32 with unit column stride)."""
-    arr = (LinearOp * len(ops))()
+    tensors, act/out 2-D fp32 with unit column stride).  An op may carry a
+    fourth item, its epilogue: "swiglu", or ("gate_residual", gate,
+    residual); then bonsai_b1_linear_batch_epi runs the list."""
+    with_epi = any(len(op) > 3 for op in ops)
+    arr = ((LinearOpEpi if with_epi else LinearOp) * len(ops))()
     keep = []
-    for i, (act, w, out) in enumerate(ops):
+    for i, op in enumerate(ops):
+        act, w, out = op[:3]
         keep.append(w)
-        arr[i].act, arr[i].lda = act.data_ptr(), act.stride(0)
-        arr[i].w = ctypes.pointer(w)
-        arr[i].out, arr[i].ldo = out.data_ptr(), out.stride(0)
-        arr[i].batch = act.shape[0]
+        o = arr[i].op if with_epi else arr[i]
+        o.act, o.lda = act.data_ptr(), act.stride(0)
+        o.w = ctypes.pointer(w)
+        o.out, o.ldo = out.data_ptr(), out.stride(0)
+        o.batch = act.shape[0]
+        if with_epi:
+            spec = op[3] if len(op) > 3 else "none"
+            if isinstance(spec, str):
+                arr[i].epi = _epilogue(spec, None, None, w.out_dim, act.shape[0])
+            else:
+                arr[i].epi = _epilogue(spec[0], spec[1], spec[2], w.out_dim, act.shape[0])
     bad = ctypes.c_int(-1)
     nf = nonfinite.data_ptr() if nonfinite is not None else None
     ws = workspace.data_ptr() if workspace is not None else None
     wsb = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    st = load().bonsai_b1_linear_batch(arr, len(ops), MODES[mode], nf, ws, wsb, ctypes.byref(bad),
-                                       _stream_handle(stream))
+    fn = load().bonsai_b1_linear_batch_epi if with_epi else load().bonsai_b1_linear_batch
+    st = fn(arr, len(ops), MODES[mode], nf, ws, wsb, ctypes.byref(bad), _stream_handle(stream))
     if st != OK:
         raise B1Error(st, f"bonsai_b1_linear_batch (op {bad.value})")
 

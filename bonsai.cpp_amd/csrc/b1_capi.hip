@@ -3,6 +3,7 @@
 // ggml-style custom-op callback.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 #include <utility>
 #include <stdio.h>
@@ -480,80 +481,128 @@ static b1::LinearArgs batch_args(const bonsai_b1_linear_op &op) {
     return a;
 }
 
-static bool batch_op_ok(const bonsai_b1_linear_op &op) {
+// The op's own arguments; out's row stride is checked against out_dim
+// columns, or out_dim / 2 after SwiGLU (epi_args checks that case).
+static bool batch_op_ok(const bonsai_b1_linear_op &op, const bonsai_b1_epilogue *epi = nullptr) {
     if (!op.w || !op.w->data) return false;
-    return check_args(op.act, op.lda, op.w->data, op.w->in_dim, op.w->out_dim, op.batch, op.out, op.ldo) ==
+    const int64_t ldo = (epi && epi->kind == BONSAI_B1_EPI_SWIGLU) ? op.w->out_dim : op.ldo;
+    return check_args(op.act, op.lda, op.w->data, op.w->in_dim, op.w->out_dim, op.batch, op.out, ldo) ==
            BONSAI_B1_OK;
 }
 
-size_t bonsai_b1_linear_batch_workspace_bytes(const bonsai_b1_linear_op *ops, int n_ops, int mode) {
-    if (!ops || n_ops <= 0 || mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_FAST) return 0;
-    size_t need = 0;
+extern "C++" {
+
+// One op of a batch and its epilogue (nullptr: none).
+struct BatchOp {
+    const bonsai_b1_linear_op *op;
+    const bonsai_b1_epilogue *epi;
+};
+
+static int epi_kind(const bonsai_b1_epilogue *e) { return e ? e->kind : BONSAI_B1_EPI_NONE; }
+
+// Workspace areas of a batch: the largest fp16 packing among its packed-GEMM
+// ops, and the largest fp32 linear output among its ops whose epilogue runs
+// as a separate pass (the other paths).  Layout: [pack][y].
+template <class OpAt>
+static void batch_areas(int n_ops, int mode, OpAt at, size_t *pack, size_t *ybytes) {
+    *pack = 0;
+    *ybytes = 0;
     for (int i = 0; i < n_ops; ++i) {
-        if (!batch_op_ok(ops[i]) || ops[i].batch == 0) continue;
-        const b1::LinearArgs a = batch_args(ops[i]);
+        const BatchOp b = at(i);
+        if (!batch_op_ok(*b.op, b.epi) || b.op->batch == 0) continue;
+        const b1::LinearArgs a = batch_args(*b.op);
         if (batch_path(a, mode) == BatchPath::Packed) {
-            const size_t b = b1::gemm_workspace_bytes(a);
-            if (b > need) need = b;
+            *pack = std::max(*pack, b1::gemm_workspace_bytes(a));
+        } else if (epi_kind(b.epi) != BONSAI_B1_EPI_NONE) {
+            *ybytes = std::max(*ybytes, (size_t)a.M * (size_t)a.N * sizeof(float));
         }
     }
-    return need;
 }
 
-int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops, int mode, int32_t *nonfinite,
-                           void *workspace, size_t workspace_bytes, int *bad_op, hipStream_t stream) {
+static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+template <class OpAt>
+static size_t batch_need(int n_ops, int mode, OpAt at) {
+    size_t pack, y;
+    batch_areas(n_ops, mode, at, &pack, &y);
+    return y ? round256(pack) + y : pack;
+}
+
+template <class OpAt>
+static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, size_t workspace_bytes, int *bad_op,
+                     hipStream_t stream, OpAt at) {
     if (bad_op) *bad_op = -1;
-    if (n_ops < 0 || (n_ops > 0 && !ops)) return BONSAI_B1_ERR_ARG;
+    if (n_ops < 0) return BONSAI_B1_ERR_ARG;
     if (mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_EXACT) return BONSAI_B1_ERR_ARG;
     for (int i = 0; i < n_ops; ++i) {
-        if (!batch_op_ok(ops[i])) {
+        const BatchOp b = at(i);
+        int kind;
+        b1::GemmEpi g;
+        if (!batch_op_ok(*b.op, b.epi) ||
+            epi_args(b.epi, b.op->w->out_dim, b.op->batch, b.op->out, b.op->ldo, &kind, &g) != BONSAI_B1_OK) {
             if (bad_op) *bad_op = i;
             return BONSAI_B1_ERR_ARG;
         }
     }
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
-    const size_t need = bonsai_b1_linear_batch_workspace_bytes(ops, n_ops, mode);
+    size_t pack_area, y_area;
+    batch_areas(n_ops, mode, at, &pack_area, &y_area);
+    const size_t need = y_area ? round256(pack_area) + y_area : pack_area;
     if (need > 0) {
         if (!workspace) {
             workspace = stream_workspace(dev, stream, need);
             workspace_bytes = workspace ? need : 0;
         }
-        if (!workspace || workspace_bytes < need) return BONSAI_B1_ERR_ARG;
+        if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
+            return BONSAI_B1_ERR_ARG;
     }
+    float *ybuf = y_area ? reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + round256(pack_area)) : nullptr;
     // The packed activations in the workspace belong to (act, lda, batch, K).
     const float *packed_act = nullptr;
     int64_t packed_lda = 0;
     int packed_m = 0, packed_k = 0;
     for (int i = 0; i < n_ops; ++i) {
-        if (ops[i].batch == 0) continue;
-        b1::LinearArgs a = batch_args(ops[i]);
+        const BatchOp bo = at(i);
+        if (bo.op->batch == 0) continue;
+        b1::LinearArgs a = batch_args(*bo.op);
         a.nonfinite = nonfinite;
+        int kind;
+        b1::GemmEpi g;
+        (void)epi_args(bo.epi, a.N, a.M, a.out, a.ldo, &kind, &g);
+        int out_cols = kind == BONSAI_B1_EPI_SWIGLU ? a.N / 2 : a.N;
+        const BatchPath path = batch_path(a, mode);
         hipError_t e = hipSuccess;
-        switch (batch_path(a, mode)) {
-        case BatchPath::Exact:
-            e = b1::launch_exact(a, stream);
-            break;
-        case BatchPath::Gemv:
-            e = b1::launch_gemv(a, dev->num_cus, stream);
-            break;
-        case BatchPath::Fused:
-            e = b1::launch_gemm(a, dev->num_cus, nullptr, 0, stream);
-            break;
-        case BatchPath::Packed: {
-            // Consecutive ops on this input whose weights follow each other
-            // in memory and whose outputs are adjacent column ranges of one
-            // row stride are one GEMM over the concatenated rows (q/k/v with
-            // concatenated weights, src/diffuser_graph.cpp:354-361), unless an
-            // output overlaps the input they all read.
+        if (path != BatchPath::Packed) {
+            // the linear, into the workspace first when an epilogue follows
+            b1::LinearArgs la = a;
+            if (kind != BONSAI_B1_EPI_NONE) {
+                la.out = ybuf;
+                la.ldo = a.N;
+            }
+            switch (path) {
+            case BatchPath::Exact: e = b1::launch_exact(la, stream); break;
+            case BatchPath::Gemv: e = b1::launch_gemv(la, dev->num_cus, stream); break;
+            default: e = b1::launch_gemm(la, dev->num_cus, nullptr, 0, stream); break;
+            }
+            if (e == hipSuccess && kind != BONSAI_B1_EPI_NONE)
+                e = b1::launch_epi(ybuf, a.N, a.M, a.N, kind, g, a.out, a.ldo, stream);
+        } else {
+            // Consecutive plain ops on this input whose weights follow each
+            // other in memory and whose outputs are adjacent column ranges of
+            // one row stride are one GEMM over the concatenated rows (q/k/v
+            // with concatenated weights, src/diffuser_graph.cpp:354-361),
+            // unless an output overlaps the input they all read.
             int last = i;
             int n_sum = a.N;
-            while (last + 1 < n_ops) {
-                const bonsai_b1_linear_op &p = ops[last], &q = ops[last + 1];
+            while (kind == BONSAI_B1_EPI_NONE && last + 1 < n_ops) {
+                const BatchOp pb = at(last), qb = at(last + 1);
+                const bonsai_b1_linear_op &p = *pb.op, &q = *qb.op;
                 // the packed size from the dimensions (nbytes is not trusted)
                 const size_t p_bytes =
                     (size_t)p.w->out_dim * (size_t)(p.w->in_dim / BONSAI_B1_BLOCK_SIZE) * BONSAI_B1_BLOCK_BYTES;
-                if (q.batch != a.M || q.act != a.act || q.lda != a.lda || q.w->in_dim != a.K || q.ldo != a.ldo ||
+                if (epi_kind(qb.epi) != BONSAI_B1_EPI_NONE || q.batch != a.M || q.act != a.act || q.lda != a.lda ||
+                    q.w->in_dim != a.K || q.ldo != a.ldo ||
                     q.w->data != static_cast<const uint8_t *>(p.w->data) + p_bytes ||
                     q.out != p.out + p.w->out_dim || n_sum + (int64_t)q.w->out_dim > INT32_MAX)
                     break;
@@ -580,12 +629,10 @@ int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops, int mode, 
                 packed_k = a.K;
             }
             if (e == hipSuccess)
-                e = b1::launch_gemm_packed(workspace, a.w, a.K, n_sum, a.M, a.out, a.ldo, nonfinite, dev->num_cus,
-                                           stream);
-            a.N = n_sum; // the outputs written, for the overlap check below
+                e = b1::launch_gemm_packed_epi(workspace, a.w, a.K, n_sum, a.M, a.out, a.ldo, nonfinite,
+                                               dev->num_cus, kind, g, stream);
+            if (last > i) out_cols = n_sum;
             i = last;
-            break;
-        }
         }
         if (e != hipSuccess) {
             if (bad_op) *bad_op = i;
@@ -595,13 +642,39 @@ int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops, int mode, 
         // the packing.
         if (packed_act) {
             const uintptr_t o0 = reinterpret_cast<uintptr_t>(a.out);
-            const uintptr_t o1 = o0 + ((size_t)(a.M - 1) * (size_t)a.ldo + (size_t)a.N) * sizeof(float);
+            const uintptr_t o1 = o0 + ((size_t)(a.M - 1) * (size_t)a.ldo + (size_t)out_cols) * sizeof(float);
             const uintptr_t p0 = reinterpret_cast<uintptr_t>(packed_act);
             const uintptr_t p1 = p0 + ((size_t)(packed_m - 1) * (size_t)packed_lda + (size_t)packed_k) * sizeof(float);
             if (o0 < p1 && p0 < o1) packed_act = nullptr;
         }
     }
     return BONSAI_B1_OK;
+}
+
+} // extern "C++"
+
+size_t bonsai_b1_linear_batch_workspace_bytes(const bonsai_b1_linear_op *ops, int n_ops, int mode) {
+    if (!ops || n_ops <= 0 || mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_FAST) return 0;
+    return batch_need(n_ops, mode, [&](int i) { return BatchOp{&ops[i], nullptr}; });
+}
+
+int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops, int mode, int32_t *nonfinite,
+                           void *workspace, size_t workspace_bytes, int *bad_op, hipStream_t stream) {
+    if (n_ops > 0 && !ops) return BONSAI_B1_ERR_ARG;
+    return batch_run(n_ops, mode, nonfinite, workspace, workspace_bytes, bad_op, stream,
+                     [&](int i) { return BatchOp{&ops[i], nullptr}; });
+}
+
+size_t bonsai_b1_linear_batch_epi_workspace_bytes(const bonsai_b1_linear_op_epi *ops, int n_ops, int mode) {
+    if (!ops || n_ops <= 0 || mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_EXACT) return 0;
+    return batch_need(n_ops, mode, [&](int i) { return BatchOp{&ops[i].op, &ops[i].epi}; });
+}
+
+int bonsai_b1_linear_batch_epi(const bonsai_b1_linear_op_epi *ops, int n_ops, int mode, int32_t *nonfinite,
+                               void *workspace, size_t workspace_bytes, int *bad_op, hipStream_t stream) {
+    if (n_ops > 0 && !ops) return BONSAI_B1_ERR_ARG;
+    return batch_run(n_ops, mode, nonfinite, workspace, workspace_bytes, bad_op, stream,
+                     [&](int i) { return BatchOp{&ops[i].op, &ops[i].epi}; });
 }
 
 int bonsai_b1_linear(const float *act, const B1Weights *w, int batch,

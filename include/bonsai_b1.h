@@ -187,6 +187,23 @@ int bonsai_b1_linear_batch(const bonsai_b1_linear_op *ops, int n_ops,
                            hipStream_t stream);
 
 /*
+ * bonsai_b1_linear_batch with an epilogue per op (bonsai_b1_epilogue,
+ * declared below): a step's linears and the element-wise ops the graph puts
+ * right after them (SwiGLU after FF-in, the gated residual add after
+ * out-projections and FF-out) in one call.  Ops with an epilogue are not
+ * merged into N-concatenated GEMMs; an epilogue that cannot be fused (EXACT
+ * mode, small batch, K % 384 != 0) runs as a separate pass over the
+ * linear's output in the workspace.
+ */
+struct bonsai_b1_epilogue;
+typedef struct bonsai_b1_linear_op_epi bonsai_b1_linear_op_epi;
+size_t bonsai_b1_linear_batch_epi_workspace_bytes(const bonsai_b1_linear_op_epi *ops, int n_ops, int mode);
+int bonsai_b1_linear_batch_epi(const bonsai_b1_linear_op_epi *ops, int n_ops,
+                               int mode, int32_t *nonfinite, void *workspace,
+                               size_t workspace_bytes, int *bad_op,
+                               hipStream_t stream);
+
+/*
  * Builder-style call; replaces bonsai::b1_linear(ctx, act, w, n_threads, ud)
  * (src/b1_0_kernel.h:290-300): fills ud from w (magic, in_dim, out_dim) and
  * runs the op for `batch` rows of act (the reference's act->ne[1]).
@@ -267,6 +284,12 @@ typedef struct bonsai_b1_epilogue {
     const float *residual; /* GATE_RESIDUAL: [batch][ldr], device */
     int64_t ldr;
 } bonsai_b1_epilogue;
+
+/* An op of bonsai_b1_linear_batch_epi: the linear and its epilogue. */
+struct bonsai_b1_linear_op_epi {
+    bonsai_b1_linear_op op;
+    bonsai_b1_epilogue epi;
+};
 
 /* bonsai_b1_linear_packed_f16 with the epilogue fused into the GEMM. */
 int bonsai_b1_linear_packed_f16_epi(const void *packed_act, const void *w,

@@ -165,3 +165,22 @@ def test_norm_mod_rejects_before_device():
     assert lib.bonsai_b1_norm_mod_f32(*ok, f + 0x30000, 3071, None) == capi.ERR_ARG      # ldy < H
     assert lib.bonsai_b1_norm_mod_pack_f16(*ok, f + 8, None) == capi.ERR_ARG             # packed alignment
     assert lib.bonsai_b1_norm_mod_pack_f16(f, 3072, 3072, 4, None, f, ctypes.c_float(1e-6), f, None) == capi.ERR_ARG
+
+
+def test_batch_epi_rejects_before_device():
+    """bonsai_b1_linear_batch_epi checks every op's epilogue before touching
+    the device: a SwiGLU op whose weights have an odd number of 32-row
+    pairs is named by bad_op."""
+    lib = bonsai_b1.load()
+    w = capi.B1WeightsC()
+    w.data, w.in_dim, w.out_dim = 0x10000, 64, 64
+    bad_w = capi.B1WeightsC()
+    bad_w.data, bad_w.in_dim, bad_w.out_dim = 0x10000, 64, 96     # 2H = 96: H % 32 != 0
+    ops = (capi.LinearOpEpi * 2)()
+    for i, ww in enumerate((w, bad_w)):
+        ops[i].op.act, ops[i].op.lda, ops[i].op.w = 0x10000, 64, ctypes.pointer(ww)
+        ops[i].op.out, ops[i].op.ldo, ops[i].op.batch = 0x100000, 64, 4
+        ops[i].epi.kind = capi.EPILOGUES["swiglu"]
+    bad = ctypes.c_int(-1)
+    assert lib.bonsai_b1_linear_batch_epi(ops, 2, 0, None, None, 0, ctypes.byref(bad), None) == capi.ERR_ARG
+    assert bad.value == 1

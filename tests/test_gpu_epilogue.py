@@ -239,3 +239,41 @@ def test_two_streams_own_workspaces(torch, b1):
             b1.linear(a2, w, n, out=o2)
         torch.cuda.synchronize()
         assert torch.equal(o1, r1) and torch.equal(o2, r2)
+
+
+@pytest.mark.parametrize("mode", ["auto", "exact"])
+def test_batch_with_epilogues_matches_single_calls(torch, b1, mode):
+    """bonsai_b1_linear_batch_epi == the same ops one by one through
+    bonsai_b1_linear_epi_f32 (bit for bit: same kernels): a double-block
+    feed-forward (FF-in + SwiGLU, FF-out + in-place gate-residual), a plain
+    op, and small-batch ops whose epilogues run as a separate pass."""
+    from bonsai_b1 import synth
+    m, d, hid = 256, 768, 1536
+    x = synth.device_activations(m, d, 101)
+    w_in = synth.device_packed_weights(2 * hid, d, 102)
+    w_out = synth.device_packed_weights(d, hid, 103)
+    w_p = synth.device_packed_weights(640, d, 104)
+    gate = torch.randn(d, device="cuda")
+    h0 = torch.randn((m, d), device="cuda")
+    xs = synth.device_activations(8, d, 105)
+    hs0 = torch.randn((8, d), device="cuda")
+    dw = b1.device_weights
+    act, h, plain = torch.empty((m, hid), device="cuda"), h0.clone(), torch.empty((m, 640), device="cuda")
+    acts, hs = torch.empty((8, hid), device="cuda"), hs0.clone()
+    ops = [(x, dw(w_in, d, 2 * hid), act, "swiglu"),
+           (act, dw(w_out, hid, d), h, ("gate_residual", gate, h)),
+           (x, dw(w_p, d, 640), plain),
+           (xs, dw(w_in, d, 2 * hid), acts, "swiglu"),
+           (acts, dw(w_out, hid, d), hs, ("gate_residual", gate, hs))]
+    b1.linear_batch(ops, mode=mode)
+    r_act = b1.linear_epi(x, w_in, 2 * hid, "swiglu", mode=mode)
+    r_h = h0.clone()
+    b1.linear_epi(r_act, w_out, d, "gate_residual", gate=gate, residual=r_h, out=r_h, mode=mode)
+    r_plain = b1.linear(x, w_p, 640, mode=mode)
+    r_acts = b1.linear_epi(xs, w_in, 2 * hid, "swiglu", mode=mode)
+    r_hs = hs0.clone()
+    b1.linear_epi(r_acts, w_out, d, "gate_residual", gate=gate, residual=r_hs, out=r_hs, mode=mode)
+    torch.cuda.synchronize()
+    for got, ref, name in ((act, r_act, "ff_in"), (h, r_h, "ff_out"), (plain, r_plain, "plain"),
+                           (acts, r_acts, "ff_in small"), (hs, r_hs, "ff_out small")):
+        assert torch.equal(got, ref), name
