@@ -100,6 +100,11 @@ __device__ __forceinline__ void dma_lds12(const void *src, void *lds) {
 // Raw buffer loads with range checking (offsets at or past num_records read
 // zeros); word 3 of the resource for gfx9-family raw buffers.
 constexpr int kBufferFlags = 0x00020000;
+// Cache policy of the GEMM's output stores: non-temporal.  The fp32 output
+// is written once and is far larger than L2, so streaming it keeps L2 for
+// the operand tiles other work-groups re-read (measured 268.6 -> 264.0 us at
+// M=4096 K=3072 N=12288).
+constexpr int kStoreNT = 2;
 // 16 bytes per lane from the buffer at byte offset voff, landing at
 // lds + 16 * lane (wave-uniform lds, through M0).
 __device__ __forceinline__ void dma_buf_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff) {
@@ -1012,7 +1017,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                         for (int t = 0; t < 2; ++t) {
                             const int ro = 4 * ((mt * 32 + 16 * s + 8 * t) * (int)ldo + nt * 32);
                             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y[s][t]), ors, lvoff, ro,
-                                                                   0);
+                                                                   kStoreNT);
                         }
                     // one accumulator tile at a time keeps the temporaries
                     // of the rearrangement within the register budget
