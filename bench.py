@@ -337,6 +337,69 @@ def bench_klein_step(torch, b1, synth):
             "dispatch": "bonsai_b1_linear_batch, one call per step; q/k/v as one GEMM over concatenated weights"}
 
 
+def bench_weights_load(torch, b1, blocks=38):
+    """Weight residency for the C5 model's B1_0 tensors (38 blocks x
+    [21504, 576] + [3072, 2880] packed bytes, 807 MB) from one .safetensors
+    file in the page cache: bonsai_b1_safetensors_load (file mapped and
+    parsed once, pinned staging) against one bonsai_b1_weights_upload per
+    tensor straight from the mapping (pageable memory).  Each is timed from
+    the call to the weights being resident; best of two."""
+    import ctypes
+    import mmap
+    import shutil
+    import tempfile
+    import numpy as np
+    from safetensors.numpy import save_file
+    rng = np.random.default_rng(7)
+    shapes = [(21504, 576), (3072, 2880)]
+    tensors = {f"single_transformer_blocks.{i}.{nm}.weight": rng.integers(0, 256, shp, dtype=np.uint8)
+               for i in range(blocks) for nm, shp in zip(("proj_mlp", "proj_out"), shapes)}
+    nbytes = sum(t.nbytes for t in tensors.values())
+    d = tempfile.mkdtemp(prefix="b1w")
+    try:
+        path = f"{d}/c5.safetensors"
+        save_file(tensors, path)
+        del tensors
+        names = None
+        r = {"tensors": 2 * blocks, "bytes": nbytes, "pinned_s": None, "pageable_s": None}
+        with b1.SafetensorsFile(path) as f:
+            names = f.names()
+            spans = [f.find(nm) for nm in names]
+            for _ in range(2):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                ws = f.load(names)
+                dt = time.perf_counter() - t0
+                for w in ws:
+                    b1.weights_free(w)
+                r["pinned_s"] = dt if r["pinned_s"] is None else min(r["pinned_s"], dt)
+        lib = b1.load()
+        st = torch.cuda.current_stream()
+        with open(path, "rb") as fh, mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ) as mm:
+            base = np.frombuffer(mm, dtype=np.uint8)
+            ptr = base.ctypes.data
+            for _ in range(2):
+                ws = []
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for (k, n, off, nb) in spans:
+                    w = b1.capi.B1WeightsC()
+                    assert lib.bonsai_b1_weights_upload(ptr + off, nb, k, n, ctypes.c_void_p(st.cuda_stream),
+                                                        ctypes.byref(w)) == 0
+                    ws.append(w)
+                st.synchronize()
+                dt = time.perf_counter() - t0
+                for w in ws:
+                    b1.weights_free(w)
+                r["pageable_s"] = dt if r["pageable_s"] is None else min(r["pageable_s"], dt)
+            del base
+        r["pinned_GBps"] = nbytes / r["pinned_s"] / 1e9
+        r["pageable_GBps"] = nbytes / r["pageable_s"] / 1e9
+        return r
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def bench_gemv(torch, b1, synth, m, k, n, steps, warmup):
     """Small-M kernel, weight copies rotated past the MALL.  The launches are
     captured once into a HIP graph (one launch per weight copy) and the graph
@@ -512,6 +575,12 @@ def main():
         log(f"[bench] c5 single-stream step (38 blocks): {c5['ms_per_step']:.2f} ms ({c5['tflops']:.0f} TFLOP/s) "
             f"from fp32 activations; {c5['ms_per_step_packed_inputs']:.2f} ms "
             f"({c5['tflops_packed_inputs']:.0f} TFLOP/s) over producer-packed fp16 inputs")
+        torch.cuda.empty_cache()
+        wl = bench_weights_load(torch, b1)
+        extra["weights_load"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in wl.items()}
+        log(f"[bench] weight residency, C5 model ({wl['tensors']} tensors, {wl['bytes'] / 1e6:.0f} MB) from "
+            f".safetensors: pinned pipeline {wl['pinned_s'] * 1e3:.0f} ms ({wl['pinned_GBps']:.1f} GB/s), "
+            f"per-tensor upload from the mapping {wl['pageable_s'] * 1e3:.0f} ms ({wl['pageable_GBps']:.1f} GB/s)")
         torch.cuda.empty_cache()
         kl = bench_klein_step(torch, b1, synth)
         extra["klein_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in kl.items()}

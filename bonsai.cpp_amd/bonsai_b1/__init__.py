@@ -8,7 +8,9 @@ device is not gfx950, calls raise.
 from .capi import (  # noqa: F401
     B1Error,
     MODES,
+    SafetensorsFile,
     Weights,
+    weights_free,
     declared_symbols,
     device_weights,
     linear_batch,

@@ -126,6 +126,20 @@ def load():
     L.bonsai_b1_norm_mod_f32.restype = i
     L.bonsai_b1_norm_mod_pack_f16.argtypes = [vp, i64, i, i, vp, vp, ctypes.c_float, vp, vp]
     L.bonsai_b1_norm_mod_pack_f16.restype = i
+    L.bonsai_b1_safetensors_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(vp)]
+    L.bonsai_b1_safetensors_open.restype = i
+    L.bonsai_b1_safetensors_close.argtypes = [vp]
+    L.bonsai_b1_safetensors_close.restype = None
+    L.bonsai_b1_safetensors_count.argtypes = [vp]
+    L.bonsai_b1_safetensors_count.restype = i
+    L.bonsai_b1_safetensors_name.argtypes = [vp, i]
+    L.bonsai_b1_safetensors_name.restype = ctypes.c_char_p
+    L.bonsai_b1_safetensors_find.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(i), ctypes.POINTER(i),
+                                             ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]
+    L.bonsai_b1_safetensors_find.restype = i
+    L.bonsai_b1_safetensors_load.argtypes = [vp, ctypes.POINTER(ctypes.c_char_p), i, vp,
+                                             ctypes.POINTER(B1WeightsC)]
+    L.bonsai_b1_safetensors_load.restype = i
     _lib = L
     return L
 
@@ -391,6 +405,70 @@ def norm_mod(x, scale, shift, eps: float = 1e-6, out=None, packed=None, stream=N
     if st != OK:
         raise B1Error(st, "bonsai_b1_norm_mod_f32")
     return out
+
+
+class SafetensorsFile:
+    """An open .safetensors file (bonsai_b1_safetensors_open): mapped and its
+    header parsed once, like bonsai::SafetensorsFile (src/safetensors.h:
+    27-90).  load() makes B1_0 tensors device-resident through the pinned
+    staging pipeline (bonsai_b1_safetensors_load)."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        st = load().bonsai_b1_safetensors_open(str(path).encode(), ctypes.byref(h))
+        if st != OK:
+            raise B1Error(st, "bonsai_b1_safetensors_open")
+        self._h = h
+
+    def names(self):
+        L = load()
+        return [L.bonsai_b1_safetensors_name(self._h, i).decode()
+                for i in range(L.bonsai_b1_safetensors_count(self._h))]
+
+    def find(self, name: str):
+        """(in_dim, out_dim, data_offset, nbytes) of B1_0 tensor `name`."""
+        k, n = ctypes.c_int(), ctypes.c_int()
+        off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+        st = load().bonsai_b1_safetensors_find(self._h, name.encode(), ctypes.byref(k), ctypes.byref(n),
+                                               ctypes.byref(off), ctypes.byref(nb))
+        if st != OK:
+            raise B1Error(st, "bonsai_b1_safetensors_find")
+        return k.value, n.value, off.value, nb.value
+
+    def load(self, names, stream=None):
+        """B1WeightsC for each name (free each with weights_free).  stream:
+        a torch stream, a raw handle (int), or None for the current one."""
+        arr = (ctypes.c_char_p * max(1, len(names)))(*[n.encode() for n in names])
+        out = (B1WeightsC * max(1, len(names)))()
+        sh = ctypes.c_void_p(stream) if isinstance(stream, int) else _stream_handle(stream)
+        st = load().bonsai_b1_safetensors_load(self._h, arr, len(names), sh, out)
+        if st != OK:
+            raise B1Error(st, "bonsai_b1_safetensors_load")
+        return [out[i] for i in range(len(names))]
+
+    def close(self):
+        if self._h:
+            load().bonsai_b1_safetensors_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def weights_free(w):
+    """bonsai_b1_weights_free on a B1WeightsC."""
+    st = load().bonsai_b1_weights_free(ctypes.byref(w))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_weights_free")
 
 
 class Weights:

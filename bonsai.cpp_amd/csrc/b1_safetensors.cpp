@@ -15,7 +15,10 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <string>
+#include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include <hip/hip_runtime_api.h>
@@ -83,6 +86,35 @@ class Header {
                 *found = true;
             } else if (!skip()) {
                 return false;
+            }
+            ws();
+            if (eat(',')) continue;
+            if (eat('}')) return true;
+            return false;
+        }
+    }
+
+    // Every top-level entry but "__metadata__", in header order.  Returns
+    // false on malformed JSON or a repeated name.
+    bool index(std::vector<std::pair<std::string, Entry>> *out) {
+        ws();
+        if (!eat('{')) return false;
+        ws();
+        if (peek() == '}') return ++i_, true;
+        std::unordered_map<std::string, int> seen;
+        for (;;) {
+            std::string key;
+            ws();
+            if (!str(&key)) return false;
+            ws();
+            if (!eat(':')) return false;
+            ws();
+            if (key == "__metadata__") {
+                if (!skip()) return false;
+            } else {
+                Entry e;
+                if (!entry(&e) || !seen.emplace(key, 0).second) return false;
+                out->emplace_back(std::move(key), std::move(e));
             }
             ws();
             if (eat(',')) continue;
@@ -263,73 +295,247 @@ class Header {
     }
 };
 
-// Locates a B1_0 tensor: file bytes [*data, *data + *nbytes) with its dims.
-int locate(const Mapped &m, const char *name, const uint8_t **data, uint64_t *nbytes, int64_t *rows,
-           int64_t *cols) {
-    if (m.n < 8) return BONSAI_B1_ERR_FORMAT;
-    uint64_t hlen = 0;
-    for (int k = 7; k >= 0; --k) hlen = (hlen << 8) | m.p[k];
-    if (hlen == 0 || hlen > m.n - 8) return BONSAI_B1_ERR_FORMAT;
-    Header h(reinterpret_cast<const char *>(m.p + 8), (size_t)hlen);
-    Entry e;
-    bool found = false;
-    if (!h.find(name, &e, &found)) return BONSAI_B1_ERR_FORMAT;
-    if (!found) return BONSAI_B1_ERR_NOT_FOUND;
+// A B1_0 tensor is U8 (or I8) [rows, cols], cols a whole number of 6-byte
+// blocks, its byte range inside the data section (data_len bytes) and
+// consistent with the shape.
+int b1_check(const Entry &e, uint64_t data_len, int64_t *rows, int64_t *cols) {
     if (!e.has_offsets || e.shape.size() != 2 || e.end < e.begin) return BONSAI_B1_ERR_FORMAT;
-    const uint64_t data_start = 8 + hlen;
-    if (e.end > m.n - data_start) return BONSAI_B1_ERR_FORMAT;
+    if (e.end > data_len) return BONSAI_B1_ERR_FORMAT;
     if (e.dtype != "U8" && e.dtype != "I8") return BONSAI_B1_ERR_FORMAT;
     const int64_t r = e.shape[0], c = e.shape[1];
     if (r <= 0 || c <= 0 || c % BONSAI_B1_BLOCK_BYTES) return BONSAI_B1_ERR_FORMAT;
     if ((uint64_t)r > (e.end - e.begin) / (uint64_t)c || (uint64_t)r * (uint64_t)c != e.end - e.begin)
         return BONSAI_B1_ERR_FORMAT;
     if (r > INT32_MAX || c / BONSAI_B1_BLOCK_BYTES * BONSAI_B1_BLOCK_SIZE > INT32_MAX) return BONSAI_B1_ERR_FORMAT;
-    *data = m.p + data_start + e.begin;
-    *nbytes = e.end - e.begin;
     *rows = r;
     *cols = c;
     return BONSAI_B1_OK;
 }
 
+// Pinned host buffers the tensor bytes pass through on their way to the
+// device: the mapped file is pageable memory, which the runtime would copy
+// through a staging buffer of its own with the host waiting on each piece.
+// Here host threads fill one buffer while the DMA engine drains the others.
+constexpr size_t kStageMax = 16u << 20; // bytes per buffer
+constexpr int kStageBufs = 3;
+constexpr size_t kCopySlice = 4u << 20; // bytes per host copy thread
+
+struct Stager {
+    void *buf[kStageBufs] = {};
+    hipEvent_t ev[kStageBufs] = {};
+    size_t bytes = 0;
+    int device = -1;
+
+    void release() {
+        for (int i = 0; i < kStageBufs; ++i) {
+            if (buf[i]) (void)hipHostFree(buf[i]);
+            if (ev[i]) (void)hipEventDestroy(ev[i]);
+            buf[i] = nullptr;
+            ev[i] = nullptr;
+        }
+        bytes = 0;
+        device = -1;
+    }
+    // Buffers of at least `want` bytes (capped) with events on `dev`.
+    bool ensure(size_t want, int dev) {
+        want = std::min(kStageMax, (want + 65535) & ~(size_t)65535);
+        if (device == dev && bytes >= want) return true;
+        release();
+        for (int i = 0; i < kStageBufs; ++i) {
+            if (hipHostMalloc(&buf[i], want, hipHostMallocDefault) != hipSuccess ||
+                hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) != hipSuccess) {
+                release();
+                return false;
+            }
+        }
+        bytes = want;
+        device = dev;
+        return true;
+    }
+};
+
+// Host copy of n bytes, split over a few threads for large pieces (one
+// thread copying out of the page cache does not keep up with the DMA).
+void copy_host(void *dst, const uint8_t *src, size_t n) {
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const size_t parts = std::min<size_t>(std::min<size_t>(4, hw), (n + kCopySlice - 1) / kCopySlice);
+    if (parts <= 1) {
+        memcpy(dst, src, n);
+        return;
+    }
+    std::vector<std::thread> th;
+    const size_t step = (n + parts - 1) / parts;
+    for (size_t p = 1; p < parts; ++p) {
+        const size_t o = p * step;
+        if (o < n) th.emplace_back([=] { memcpy(static_cast<uint8_t *>(dst) + o, src + o, std::min(step, n - o)); });
+    }
+    memcpy(dst, src, std::min(step, n));
+    for (auto &t : th) t.join();
+}
+
 } // namespace
+
+// An open .safetensors file: the file mapped once and its header parsed
+// once, as SafetensorsFile (src/safetensors.h:27-90) holds it.
+struct bonsai_b1_safetensors {
+    Mapped m;
+    uint64_t data_start = 0;
+    std::vector<std::pair<std::string, Entry>> entries; // header order
+    std::unordered_map<std::string, size_t> by_name;
+    Stager stage;
+    ~bonsai_b1_safetensors() { stage.release(); }
+
+    int open(const char *path) {
+        if (!m.open(path)) return BONSAI_B1_ERR_IO;
+        if (m.n < 8) return BONSAI_B1_ERR_FORMAT;
+        uint64_t hlen = 0;
+        for (int k = 7; k >= 0; --k) hlen = (hlen << 8) | m.p[k];
+        if (hlen == 0 || hlen > m.n - 8) return BONSAI_B1_ERR_FORMAT;
+        Header h(reinterpret_cast<const char *>(m.p + 8), (size_t)hlen);
+        if (!h.index(&entries)) return BONSAI_B1_ERR_FORMAT;
+        data_start = 8 + hlen;
+        for (size_t i = 0; i < entries.size(); ++i) by_name.emplace(entries[i].first, i);
+        return BONSAI_B1_OK;
+    }
+    // A B1_0 tensor's bytes in the mapping and its dims.
+    int find(const char *name, const uint8_t **data, uint64_t *nbytes, int64_t *rows, int64_t *cols) const {
+        const auto it = by_name.find(name);
+        if (it == by_name.end()) return BONSAI_B1_ERR_NOT_FOUND;
+        const Entry &e = entries[it->second].second;
+        const int st = b1_check(e, m.n - data_start, rows, cols);
+        if (st != BONSAI_B1_OK) return st;
+        *data = m.p + data_start + e.begin;
+        *nbytes = e.end - e.begin;
+        return BONSAI_B1_OK;
+    }
+};
+
 
 extern "C" {
 
-int bonsai_b1_safetensors_info(const char *path, const char *name, int *in_dim, int *out_dim,
+int bonsai_b1_safetensors_open(const char *path, bonsai_b1_safetensors **out) {
+    if (!path || !out) return BONSAI_B1_ERR_ARG;
+    *out = nullptr;
+    bonsai_b1_safetensors *f = new (std::nothrow) bonsai_b1_safetensors();
+    if (!f) return BONSAI_B1_ERR_IO;
+    const int st = f->open(path);
+    if (st != BONSAI_B1_OK) {
+        delete f;
+        return st;
+    }
+    *out = f;
+    return BONSAI_B1_OK;
+}
+
+void bonsai_b1_safetensors_close(bonsai_b1_safetensors *f) { delete f; }
+
+int bonsai_b1_safetensors_count(const bonsai_b1_safetensors *f) { return f ? (int)f->entries.size() : -1; }
+
+const char *bonsai_b1_safetensors_name(const bonsai_b1_safetensors *f, int i) {
+    if (!f || i < 0 || (size_t)i >= f->entries.size()) return nullptr;
+    return f->entries[(size_t)i].first.c_str();
+}
+
+int bonsai_b1_safetensors_find(const bonsai_b1_safetensors *f, const char *name, int *in_dim, int *out_dim,
                                uint64_t *data_offset, uint64_t *nbytes) {
-    if (!path || !name) return BONSAI_B1_ERR_ARG;
-    Mapped m;
-    if (!m.open(path)) return BONSAI_B1_ERR_IO;
+    if (!f || !name) return BONSAI_B1_ERR_ARG;
     const uint8_t *data = nullptr;
     uint64_t nb = 0;
     int64_t rows = 0, cols = 0;
-    const int st = locate(m, name, &data, &nb, &rows, &cols);
+    const int st = f->find(name, &data, &nb, &rows, &cols);
     if (st != BONSAI_B1_OK) return st;
     if (in_dim) *in_dim = (int)(cols / BONSAI_B1_BLOCK_BYTES * BONSAI_B1_BLOCK_SIZE);
     if (out_dim) *out_dim = (int)rows;
-    if (data_offset) *data_offset = (uint64_t)(data - m.p);
+    if (data_offset) *data_offset = (uint64_t)(data - f->m.p);
     if (nbytes) *nbytes = nb;
     return BONSAI_B1_OK;
 }
 
+int bonsai_b1_safetensors_load(bonsai_b1_safetensors *f, const char *const *names, int n, hipStream_t stream,
+                               B1Weights *out) {
+    if (!f || n < 0 || (n > 0 && (!names || !out))) return BONSAI_B1_ERR_ARG;
+    for (int i = 0; i < n; ++i) out[i] = B1Weights{};
+    if (n == 0) return BONSAI_B1_OK;
+    // Every name is resolved before anything is allocated.
+    struct Job {
+        const uint8_t *src;
+        uint64_t nb;
+        int in_dim, out_dim;
+    };
+    std::vector<Job> jobs((size_t)n);
+    uint64_t largest = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!names[i]) return BONSAI_B1_ERR_ARG;
+        int64_t rows = 0, cols = 0;
+        const int st = f->find(names[i], &jobs[(size_t)i].src, &jobs[(size_t)i].nb, &rows, &cols);
+        if (st != BONSAI_B1_OK) return st;
+        jobs[(size_t)i].in_dim = (int)(cols / BONSAI_B1_BLOCK_BYTES * BONSAI_B1_BLOCK_SIZE);
+        jobs[(size_t)i].out_dim = (int)rows;
+        largest = std::max(largest, jobs[(size_t)i].nb);
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return BONSAI_B1_ERR_DEVICE;
+    if (!f->stage.ensure((size_t)largest, dev)) return BONSAI_B1_ERR_HIP;
+    int status = BONSAI_B1_OK;
+    for (int i = 0; i < n && status == BONSAI_B1_OK; ++i) {
+        void *d = nullptr;
+        if (hipMalloc(&d, (size_t)jobs[(size_t)i].nb) != hipSuccess) {
+            status = BONSAI_B1_ERR_HIP;
+            break;
+        }
+        out[i] = B1Weights{d, jobs[(size_t)i].in_dim, jobs[(size_t)i].out_dim, (size_t)jobs[(size_t)i].nb, dev};
+    }
+    // Chunks go round the staging buffers: a buffer is refilled once the
+    // copy that last read it has completed.
+    Stager &sg = f->stage;
+    bool pending[kStageBufs] = {};
+    int slot = 0;
+    for (int i = 0; i < n && status == BONSAI_B1_OK; ++i) {
+        const Job &j = jobs[(size_t)i];
+        uint8_t *dst = static_cast<uint8_t *>(out[i].data);
+        for (uint64_t off = 0; off < j.nb; off += sg.bytes) {
+            const size_t len = (size_t)std::min<uint64_t>(sg.bytes, j.nb - off);
+            if (pending[slot] && hipEventSynchronize(sg.ev[slot]) != hipSuccess) {
+                status = BONSAI_B1_ERR_HIP;
+                break;
+            }
+            copy_host(sg.buf[slot], j.src + off, len);
+            if (hipMemcpyAsync(dst + off, sg.buf[slot], len, hipMemcpyHostToDevice, stream) != hipSuccess ||
+                hipEventRecord(sg.ev[slot], stream) != hipSuccess) {
+                status = BONSAI_B1_ERR_HIP;
+                break;
+            }
+            pending[slot] = true;
+            slot = (slot + 1) % kStageBufs;
+        }
+    }
+    // The staging buffers are free, and the weights resident, once the
+    // stream has passed the last copy.
+    if (hipStreamSynchronize(stream) != hipSuccess && status == BONSAI_B1_OK) status = BONSAI_B1_ERR_HIP;
+    if (status != BONSAI_B1_OK) {
+        for (int i = 0; i < n; ++i) {
+            (void)bonsai_b1_weights_free(&out[i]);
+            out[i] = B1Weights{};
+        }
+    }
+    return status;
+}
+
+int bonsai_b1_safetensors_info(const char *path, const char *name, int *in_dim, int *out_dim,
+                               uint64_t *data_offset, uint64_t *nbytes) {
+    if (!path || !name) return BONSAI_B1_ERR_ARG;
+    bonsai_b1_safetensors f;
+    const int st = f.open(path);
+    if (st != BONSAI_B1_OK) return st;
+    return bonsai_b1_safetensors_find(&f, name, in_dim, out_dim, data_offset, nbytes);
+}
+
 int bonsai_b1_weights_load_safetensors(const char *path, const char *name, hipStream_t stream, B1Weights *out) {
     if (!path || !name || !out) return BONSAI_B1_ERR_ARG;
-    Mapped m;
-    if (!m.open(path)) return BONSAI_B1_ERR_IO;
-    const uint8_t *data = nullptr;
-    uint64_t nb = 0;
-    int64_t rows = 0, cols = 0;
-    int st = locate(m, name, &data, &nb, &rows, &cols);
+    bonsai_b1_safetensors f;
+    const int st = f.open(path);
     if (st != BONSAI_B1_OK) return st;
-    st = bonsai_b1_weights_upload(data, (size_t)nb, (int)(cols / BONSAI_B1_BLOCK_BYTES * BONSAI_B1_BLOCK_SIZE),
-                                  (int)rows, stream, out);
-    if (st != BONSAI_B1_OK) return st;
-    // The copy reads the mapping: finish it before the file is unmapped.
-    if (hipStreamSynchronize(stream) != hipSuccess) {
-        (void)bonsai_b1_weights_free(out);
-        return BONSAI_B1_ERR_HIP;
-    }
-    return BONSAI_B1_OK;
+    return bonsai_b1_safetensors_load(&f, &name, 1, stream, out);
 }
 
 } // extern "C"

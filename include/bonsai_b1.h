@@ -373,10 +373,11 @@ int bonsai_b1_quantize_f32(const float *w, int64_t ldw, int in_dim,
  * Weight residency from a .safetensors file; replaces load_b1
  * (src/diffuser.cpp:39-50) over the reader of src/safetensors.h:39-76.
  * The tensor `name` must be U8 (or I8) [out_dim, in_dim/32*6], as
- * convert_to_b1_0_packed.py writes it.  The file is mapped read-only, the
- * tensor bytes uploaded as bonsai_b1_weights_upload does, and the stream
- * synchronised before the mapping is released.  Errors: ERR_IO (open/map),
- * ERR_NOT_FOUND, ERR_FORMAT (header, dtype, shape or offsets inconsistent).
+ * convert_to_b1_0_packed.py writes it.  One tensor through
+ * bonsai_b1_safetensors_open / _load / _close: the file is mapped
+ * read-only and the call returns once the copy has completed.  Errors:
+ * ERR_IO (open/map), ERR_NOT_FOUND, ERR_FORMAT (header, dtype, shape or
+ * offsets inconsistent).  For many tensors of one file, open it once.
  */
 int bonsai_b1_weights_load_safetensors(const char *path, const char *name,
                                        hipStream_t stream, B1Weights *out);
@@ -386,6 +387,40 @@ int bonsai_b1_weights_load_safetensors(const char *path, const char *name,
 int bonsai_b1_safetensors_info(const char *path, const char *name,
                                int *in_dim, int *out_dim,
                                uint64_t *data_offset, uint64_t *nbytes);
+
+/*
+ * An open .safetensors file, for loading a whole model: the file is mapped
+ * once and its header parsed once, as bonsai::SafetensorsFile
+ * (src/safetensors.h:27-90: open, find, tensors()) holds it, instead of
+ * once per tensor.  open: ERR_IO (open/map), ERR_FORMAT (header).  count
+ * and name enumerate every tensor of the header (B1_0 or not) in header
+ * order; name returns NULL past the end, and the string lives as long as
+ * the handle.  find is bonsai_b1_safetensors_info on the open file.  A
+ * handle may be used from one thread at a time.
+ */
+typedef struct bonsai_b1_safetensors bonsai_b1_safetensors;
+int bonsai_b1_safetensors_open(const char *path, bonsai_b1_safetensors **out);
+void bonsai_b1_safetensors_close(bonsai_b1_safetensors *f);
+int bonsai_b1_safetensors_count(const bonsai_b1_safetensors *f);
+const char *bonsai_b1_safetensors_name(const bonsai_b1_safetensors *f, int i);
+int bonsai_b1_safetensors_find(const bonsai_b1_safetensors *f,
+                               const char *name, int *in_dim, int *out_dim,
+                               uint64_t *data_offset, uint64_t *nbytes);
+
+/*
+ * Weight residency for n B1_0 tensors of an open file, on the current
+ * device; replaces load_b1 (src/diffuser.cpp:39-50) applied tensor by
+ * tensor.  Every name is checked before anything is allocated (errors as
+ * bonsai_b1_safetensors_find).  Each tensor gets its own device allocation
+ * (free with bonsai_b1_weights_free).  The bytes pass through pinned host
+ * buffers held by the handle (up to 3 x 16 MB, allocated on first use):
+ * host threads copy a piece out of the mapping while the DMA engine moves
+ * the previous pieces on `stream`.  Returns once every copy has completed;
+ * on any error nothing stays allocated and out[] is zeroed.
+ */
+int bonsai_b1_safetensors_load(bonsai_b1_safetensors *f,
+                               const char *const *names, int n,
+                               hipStream_t stream, B1Weights *out);
 
 /* Human-readable text for a status code (static storage). */
 const char *bonsai_b1_status_string(int status);
