@@ -251,6 +251,43 @@ def bench_single_stream_step(torch, b1, synth, blocks=38):
     return r
 
 
+def bench_c5_block_chain(torch, b1, synth, blocks=38):
+    """The C5 single-stream blocks as a chain of this library's kernels,
+    attention aside (src/diffuser_graph.cpp:477-538 in shape): per block,
+    LayerNorm + modulation written as packed fp16, linear1 3072 -> 21504,
+    the packed linear2 input built in place by two producers (the q columns
+    standing in for the attention output, columns 0-3071; GELU-tanh of the
+    MLP part, columns 3072-15359), and linear2 15360 -> 3072 with the
+    gate-residual epilogue updating the residual stream in place.  Block
+    i + 1 reads what block i wrote."""
+    m, h, n1, k2 = 4608, 3072, 21504, 15360
+    w1 = [synth.device_packed_weights(n1, h, 500 + i) for i in range(blocks)]
+    w2 = [synth.device_packed_weights(h, k2, 600 + i) for i in range(blocks)]
+    g = torch.Generator(device="cuda").manual_seed(5)
+    scale = [0.1 * torch.randn(h, device="cuda", generator=g) for _ in range(blocks)]
+    shift = [0.1 * torch.randn(h, device="cuda", generator=g) for _ in range(blocks)]
+    gate = [0.05 * torch.randn(h, device="cuda", generator=g) for _ in range(blocks)]
+    x = synth.device_activations(m, h, 17)
+    p1 = torch.empty(m * h * 2, dtype=torch.uint8, device="cuda")
+    y1 = torch.empty((m, n1), device="cuda")
+    p2 = torch.empty(m * k2 * 2, dtype=torch.uint8, device="cuda")
+
+    def step():
+        for i in range(blocks):
+            b1.norm_mod(x, scale[i], shift[i], packed=p1)
+            b1.linear_packed_f16(p1, w1[i], h, n1, m, out=y1)
+            b1.pack_act_f16(y1[:, :h], packed=p2, ldp=k2)
+            b1.gelu_tanh_pack_f16(y1[:, 3 * h:], packed=p2[h * 2:], ldp=k2)
+            b1.linear_packed_f16_epi(p2, w2[i], k2, h, m, "gate_residual", gate=gate[i], residual=x, out=x)
+
+    ms = graph_ms(torch, step, reps=2)
+    flop = 2.0 * m * (h * n1 + k2 * h) * blocks
+    finite = bool(torch.isfinite(x).all())
+    del w1, w2
+    return {"blocks": blocks, "ms_per_step": ms, "gemm_tflops": flop / (ms * 1e-3) / 1e12,
+            "kernels_per_block": 5, "residual_finite": finite}
+
+
 def bench_klein_step(torch, b1, synth):
     """The 100 B1_0 linears of one reference Flux.2-Klein step at 64x64
     latents (4096 image + 512 text tokens): 5 double-stream blocks (image and
@@ -575,6 +612,12 @@ def main():
         log(f"[bench] c5 single-stream step (38 blocks): {c5['ms_per_step']:.2f} ms ({c5['tflops']:.0f} TFLOP/s) "
             f"from fp32 activations; {c5['ms_per_step_packed_inputs']:.2f} ms "
             f"({c5['tflops_packed_inputs']:.0f} TFLOP/s) over producer-packed fp16 inputs")
+        torch.cuda.empty_cache()
+        ch = bench_c5_block_chain(torch, b1, synth)
+        extra["c5_block_chain"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in ch.items()}
+        log(f"[bench] c5 block chain (38 single-stream blocks, attention aside: norm+mod -> packed, linear1, "
+            f"packed [q | GELU(MLP)], linear2 + gate-residual): {ch['ms_per_step']:.2f} ms "
+            f"({ch['gemm_tflops']:.0f} TFLOP/s of GEMM work)")
         torch.cuda.empty_cache()
         wl = bench_weights_load(torch, b1)
         extra["weights_load"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in wl.items()}

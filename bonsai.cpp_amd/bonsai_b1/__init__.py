@@ -28,6 +28,7 @@ from .capi import (  # noqa: F401
     load,
     pack_act_f16,
     quantize_f32,
+    swiglu_pack_f16,
     workspace_bytes,
 )
 from . import synth  # noqa: F401

@@ -100,12 +100,20 @@ def load():
     L.bonsai_b1_gelu_tanh_f32.restype = i
     L.bonsai_b1_gelu_tanh_pack_f16.argtypes = [vp, i64, i, i, vp, vp]
     L.bonsai_b1_gelu_tanh_pack_f16.restype = i
+    L.bonsai_b1_gelu_tanh_pack_f16_ld.argtypes = [vp, i64, i, i, vp, i64, vp]
+    L.bonsai_b1_gelu_tanh_pack_f16_ld.restype = i
+    L.bonsai_b1_swiglu_pack_f16.argtypes = [vp, i64, i, i, vp, vp]
+    L.bonsai_b1_swiglu_pack_f16.restype = i
+    L.bonsai_b1_swiglu_pack_f16_ld.argtypes = [vp, i64, i, i, vp, i64, vp]
+    L.bonsai_b1_swiglu_pack_f16_ld.restype = i
     L.bonsai_b1_quantize_f32.argtypes = [vp, i64, i, i, vp, i, vp]
     L.bonsai_b1_quantize_f32.restype = i
     L.bonsai_b1_packed_act_bytes.argtypes = [i, i]
     L.bonsai_b1_packed_act_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_pack_act_f16.argtypes = [vp, i64, i, i, vp, vp]
     L.bonsai_b1_pack_act_f16.restype = i
+    L.bonsai_b1_pack_act_f16_ld.argtypes = [vp, i64, i, i, vp, i64, vp]
+    L.bonsai_b1_pack_act_f16_ld.restype = i
     L.bonsai_b1_linear_packed_f16.argtypes = [vp, vp, i, i, i, vp, i64, vp, vp]
     L.bonsai_b1_linear_packed_f16.restype = i
     L.bonsai_b1_linear_packed_f16_epi.argtypes = [vp, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), vp, vp]
@@ -209,17 +217,59 @@ def gelu_tanh(x, out=None, stream=None):
     return out
 
 
-def gelu_tanh_pack_f16(act, packed=None, stream=None):
-    """Packed fp16 activations of gelu_tanh(act) (bonsai_b1_gelu_tanh_pack_f16)."""
+def _packed_target(act, packed, ldp):
+    """The packed buffer of a producer: new when None; with ldp (packed row
+    length in fp16 elements) a view starting at the target column range."""
     import torch
     m, k = act.shape
-    nbytes = load().bonsai_b1_packed_act_bytes(m, k)
-    if packed is None:
-        packed = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=act.device)
-    st = load().bonsai_b1_gelu_tanh_pack_f16(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(),
-                                             _stream_handle(stream))
+    if ldp is None:
+        nbytes = load().bonsai_b1_packed_act_bytes(m, k)
+        if packed is None:
+            packed = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=act.device)
+        if packed.numel() < nbytes or not packed.is_contiguous():
+            raise ValueError("packed must hold bonsai_b1_packed_act_bytes(M, K) contiguous bytes")
+    elif packed is None or packed.numel() < ((m - 1) * ldp + k) * 2 or not packed.is_contiguous():
+        raise ValueError("packed must be a contiguous view holding (M-1)*ldp + K fp16 elements")
+    return packed
+
+
+def gelu_tanh_pack_f16(act, packed=None, stream=None, ldp=None):
+    """Packed fp16 activations of gelu_tanh(act) (bonsai_b1_gelu_tanh_pack_f16;
+    with ldp, bonsai_b1_gelu_tanh_pack_f16_ld into a column range)."""
+    m, k = act.shape
+    packed = _packed_target(act, packed, ldp)
+    if ldp is None:
+        st = load().bonsai_b1_gelu_tanh_pack_f16(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(),
+                                                 _stream_handle(stream))
+    else:
+        st = load().bonsai_b1_gelu_tanh_pack_f16_ld(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(), ldp,
+                                                    _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_gelu_tanh_pack_f16")
+    return packed
+
+
+def swiglu_pack_f16(act, packed=None, stream=None, ldp=None):
+    """Packed fp16 activations of SwiGLU over act [M, 2H] (gates first):
+    silu(a[:, :H]) * a[:, H:] (bonsai_b1_swiglu_pack_f16; with ldp,
+    bonsai_b1_swiglu_pack_f16_ld into the column range `packed` starts at)."""
+    import torch
+    m, k2 = act.shape
+    if k2 % 2:
+        raise ValueError("act must hold 2H columns")
+    h = k2 // 2
+    if ldp is None:
+        if packed is None:
+            packed = torch.empty(max(m * h * 2, 16), dtype=torch.uint8, device=act.device)
+        st = load().bonsai_b1_swiglu_pack_f16(act.data_ptr(), act.stride(0), h, m, packed.data_ptr(),
+                                              _stream_handle(stream))
+    else:
+        if packed is None or packed.numel() < ((m - 1) * ldp + h) * 2:
+            raise ValueError("packed must be a view holding (M-1)*ldp + H fp16 elements")
+        st = load().bonsai_b1_swiglu_pack_f16_ld(act.data_ptr(), act.stride(0), h, m, packed.data_ptr(), ldp,
+                                                 _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_swiglu_pack_f16")
     return packed
 
 
@@ -285,20 +335,22 @@ def quantize_f32(w, order: str = "numpy", out=None, stream=None):
     return out
 
 
-def pack_act_f16(act, packed=None, stream=None):
+def pack_act_f16(act, packed=None, stream=None, ldp=None):
     """fp16 K-slot-paired activations of act[M, K] (bonsai_b1_pack_act_f16);
-    returns a uint8 cuda tensor of M*K*2 bytes."""
+    returns a uint8 cuda tensor of M*K*2 bytes.  With ldp (packed row length
+    in fp16 elements), bonsai_b1_pack_act_f16_ld into the column range that
+    the `packed` view starts at."""
     import torch
     if act.dim() != 2 or act.dtype != torch.float32 or not act.is_cuda or act.stride(1) != 1:
         raise ValueError("act must be a 2-D fp32 cuda tensor with unit column stride")
     m, k = act.shape
-    nbytes = load().bonsai_b1_packed_act_bytes(m, k)
-    if packed is None:
-        packed = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=act.device)
-    if packed.numel() < nbytes or not packed.is_contiguous():
-        raise ValueError("packed must hold bonsai_b1_packed_act_bytes(M, K) contiguous bytes")
-    st = load().bonsai_b1_pack_act_f16(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(),
-                                       _stream_handle(stream))
+    packed = _packed_target(act, packed, ldp)
+    if ldp is None:
+        st = load().bonsai_b1_pack_act_f16(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(),
+                                           _stream_handle(stream))
+    else:
+        st = load().bonsai_b1_pack_act_f16_ld(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(), ldp,
+                                              _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_pack_act_f16")
     return packed

@@ -220,16 +220,46 @@ int bonsai_b1_gelu_tanh_f32(const float *x, int64_t ldx, float *y, int64_t ldy, 
     return b1::launch_gelu(x, ldx, y, ldy, cols, rows, stream) == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
 }
 
-int bonsai_b1_gelu_tanh_pack_f16(const float *act, int64_t lda, int in_dim, int batch, void *packed,
-                                 hipStream_t stream) {
+// Arguments of the packing producers: packed rows of ldp fp16 elements
+// (ldp >= in_dim, 16-byte row alignment), packed 16-byte aligned.
+static int pack_args(const float *act, int64_t lda, int in_dim, int batch, const void *packed, int64_t ldp) {
     if (in_dim <= 0 || batch < 0 || in_dim % BONSAI_B1_BLOCK_SIZE || lda < in_dim) return BONSAI_B1_ERR_ARG;
+    if (ldp < in_dim || ldp % 8) return BONSAI_B1_ERR_ARG;
     if (batch > 0 && (!act || !packed)) return BONSAI_B1_ERR_ARG;
     if (reinterpret_cast<uintptr_t>(packed) & 15u) return BONSAI_B1_ERR_ARG;
     if (batch > 0 && !b1::pack_supported(act, lda, batch, in_dim)) return BONSAI_B1_ERR_ARG;
     if (!current_device(nullptr)) return BONSAI_B1_ERR_DEVICE;
-    if (batch == 0) return BONSAI_B1_OK;
-    return b1::launch_gelu_pack(act, lda, batch, in_dim, packed, stream) == hipSuccess ? BONSAI_B1_OK
-                                                                                      : BONSAI_B1_ERR_HIP;
+    return BONSAI_B1_OK;
+}
+
+int bonsai_b1_gelu_tanh_pack_f16_ld(const float *act, int64_t lda, int in_dim, int batch, void *packed,
+                                    int64_t ldp, hipStream_t stream) {
+    const int st = pack_args(act, lda, in_dim, batch, packed, ldp);
+    if (st != BONSAI_B1_OK || batch == 0) return st;
+    return b1::launch_gelu_pack(act, lda, batch, in_dim, packed, ldp, stream) == hipSuccess ? BONSAI_B1_OK
+                                                                                           : BONSAI_B1_ERR_HIP;
+}
+
+int bonsai_b1_gelu_tanh_pack_f16(const float *act, int64_t lda, int in_dim, int batch, void *packed,
+                                 hipStream_t stream) {
+    return bonsai_b1_gelu_tanh_pack_f16_ld(act, lda, in_dim, batch, packed, in_dim, stream);
+}
+
+int bonsai_b1_swiglu_pack_f16_ld(const float *act, int64_t lda, int hidden, int batch, void *packed, int64_t ldp,
+                                 hipStream_t stream) {
+    if (hidden <= 0 || hidden % BONSAI_B1_BLOCK_SIZE || hidden > INT32_MAX / 2) return BONSAI_B1_ERR_ARG;
+    if (ldp < hidden || ldp % 8) return BONSAI_B1_ERR_ARG;
+    // the input as a pack of its 2 hidden columns would be checked; the
+    // output row stride is checked above
+    const int st = pack_args(act, lda, 2 * hidden, batch, packed, 2 * hidden);
+    if (st != BONSAI_B1_OK || batch == 0) return st;
+    return b1::launch_swiglu_pack(act, lda, batch, hidden, packed, ldp, stream) == hipSuccess ? BONSAI_B1_OK
+                                                                                             : BONSAI_B1_ERR_HIP;
+}
+
+int bonsai_b1_swiglu_pack_f16(const float *act, int64_t lda, int hidden, int batch, void *packed,
+                              hipStream_t stream) {
+    return bonsai_b1_swiglu_pack_f16_ld(act, lda, hidden, batch, packed, hidden, stream);
 }
 
 static int norm_mod_args(const float *x, int64_t ldx, int H, int rows, const float *scale, const float *shift,
@@ -282,16 +312,17 @@ size_t bonsai_b1_packed_act_bytes(int batch, int in_dim) {
     return (size_t)batch * (size_t)in_dim * 2;
 }
 
+int bonsai_b1_pack_act_f16_ld(const float *act, int64_t lda, int in_dim, int batch, void *packed, int64_t ldp,
+                              hipStream_t stream) {
+    const int st = pack_args(act, lda, in_dim, batch, packed, ldp);
+    if (st != BONSAI_B1_OK || batch == 0) return st;
+    return b1::launch_pack(act, lda, batch, in_dim, packed, ldp, stream) == hipSuccess ? BONSAI_B1_OK
+                                                                                      : BONSAI_B1_ERR_HIP;
+}
+
 int bonsai_b1_pack_act_f16(const float *act, int64_t lda, int in_dim, int batch, void *packed,
                            hipStream_t stream) {
-    if (in_dim <= 0 || batch < 0 || in_dim % BONSAI_B1_BLOCK_SIZE || lda < in_dim) return BONSAI_B1_ERR_ARG;
-    if (batch > 0 && (!act || !packed)) return BONSAI_B1_ERR_ARG;
-    if (reinterpret_cast<uintptr_t>(packed) & 15u) return BONSAI_B1_ERR_ARG;
-    if (batch > 0 && !b1::pack_supported(act, lda, batch, in_dim)) return BONSAI_B1_ERR_ARG;
-    if (!current_device(nullptr)) return BONSAI_B1_ERR_DEVICE;
-    if (batch == 0) return BONSAI_B1_OK;
-    return b1::launch_pack(act, lda, batch, in_dim, packed, stream) == hipSuccess ? BONSAI_B1_OK
-                                                                                  : BONSAI_B1_ERR_HIP;
+    return bonsai_b1_pack_act_f16_ld(act, lda, in_dim, batch, packed, in_dim, stream);
 }
 
 int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
@@ -432,7 +463,7 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
         return BONSAI_B1_ERR_ARG;
     hipError_t e;
     if (fused) {
-        e = b1::launch_pack(act, lda, batch, in_dim, workspace, stream);
+        e = b1::launch_pack(act, lda, batch, in_dim, workspace, in_dim, stream);
         if (e == hipSuccess)
             e = b1::launch_gemm_packed_epi(workspace, a.w, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus,
                                            kind, g, stream);
@@ -622,7 +653,7 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
                 }
             }
             if (!(packed_act == a.act && packed_lda == a.lda && packed_m == a.M && packed_k == a.K)) {
-                e = b1::launch_pack(a.act, a.lda, a.M, a.K, workspace, stream);
+                e = b1::launch_pack(a.act, a.lda, a.M, a.K, workspace, a.K, stream);
                 packed_act = a.act;
                 packed_lda = a.lda;
                 packed_m = a.M;

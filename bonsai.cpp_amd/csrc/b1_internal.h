@@ -43,11 +43,12 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
 
 // The two halves of the workspace path.  Packed activations: u32 word
 // (row m, 16 j + d) = fp16(a[m][32 j + d]) | fp16(a[m][32 j + d + 16]) << 16,
-// row stride K/2 words.  pack: K % 32 == 0, lda % 4 == 0, act 16-byte
-// aligned.  gemm_packed: gemm_packed_ok(M, K, N), packed 16-byte aligned,
-// w 4-byte aligned.
+// row stride ldp/2 words (ldp >= K fp16 elements, ldp % 8 == 0; the GEMM
+// reads ldp == K).  pack: K % 32 == 0, lda % 4 == 0, act 16-byte aligned.
+// gemm_packed: gemm_packed_ok(M, K, N), packed 16-byte aligned, w 4-byte
+// aligned.
 bool pack_supported(const float *act, int64_t lda, int M, int K);
-hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed, hipStream_t s);
+hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed, int64_t ldp, hipStream_t s);
 bool gemm_packed_ok(int M, int K, int N);
 hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
                               int32_t *nonfinite, int num_cus, hipStream_t s);
@@ -79,7 +80,12 @@ constexpr int kGemvMaxM = 16;
 // GELU-tanh over [rows][cols] fp32 (cols % 4 == 0, rows 16-byte aligned via
 // ld % 4 == 0); the fused form writes packed fp16 activations (pack rules).
 hipError_t launch_gelu(const float *x, int64_t ldx, float *y, int64_t ldy, int cols, int rows, hipStream_t s);
-hipError_t launch_gelu_pack(const float *act, int64_t lda, int M, int K, void *packed, hipStream_t s);
+hipError_t launch_gelu_pack(const float *act, int64_t lda, int M, int K, void *packed, int64_t ldp,
+                            hipStream_t s);
+// SwiGLU over act [M][2H] (gate half first) into packed fp16 [M][H] at row
+// stride ldp (pack rules with K = 2H for the input).
+hipError_t launch_swiglu_pack(const float *act, int64_t lda, int M, int H, void *packed, int64_t ldp,
+                              hipStream_t s);
 
 // Packed B1_0 writer over device fp32 weights [N][ldw]; order 0 = numpy's
 // np.mean summation, 1 = left to right.

@@ -392,7 +392,7 @@ __global__ __launch_bounds__(256) void b1_gelu_kernel(const float *__restrict__ 
 }
 
 __global__ __launch_bounds__(256) void b1_gelu_pack_kernel(const float *__restrict__ act, int64_t lda,
-                                                           uint32_t *__restrict__ ah, int M, int K) {
+                                                           uint32_t *__restrict__ ah, int64_t ldw, int M, int K) {
     const int nb = K / 32;
     const int units = M * nb * 4; // (row, block, quad)
     for (int u = blockIdx.x * 256 + threadIdx.x; u < units; u += gridDim.x * 256) {
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(256) void b1_gelu_pack_kernel(const float *__restri
         u32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = pack_f16(gelu_tanh(lo[j]), gelu_tanh(hi[j]));
-        *reinterpret_cast<u32x4 *>(ah + (size_t)row * (K / 2) + blk * 16 + c * 4) = v;
+        *reinterpret_cast<u32x4 *>(ah + (size_t)row * ldw + blk * 16 + c * 4) = v;
     }
 }
 
@@ -425,6 +425,30 @@ __device__ __forceinline__ float gate_residual(float r, float g, float y) {
 __device__ __forceinline__ float mul_f32(float a, float b) {
 #pragma clang fp contract(off)
     return a * b;
+}
+
+// SwiGLU (ggml_swiglu: silu of the first half of a row times its second
+// half) fused with the fp16 packing, written at a packed row stride of ldw
+// words: act [M][lda] holds 2H columns, the packed output H.
+__global__ __launch_bounds__(256) void b1_swiglu_pack_kernel(const float *__restrict__ act, int64_t lda,
+                                                             uint32_t *__restrict__ ah, int64_t ldw, int M, int H) {
+    const int nb = H / 32;
+    const int units = M * nb * 4; // (row, block, quad)
+    for (int u = blockIdx.x * 256 + threadIdx.x; u < units; u += gridDim.x * 256) {
+        const int c = u & 3, rb = u >> 2;
+        const int row = rb / nb, blk = rb - row * nb;
+        const float *g = act + (size_t)row * lda + blk * 32 + c * 4;
+        const float *v = g + H;
+        const floatx4 glo = *reinterpret_cast<const floatx4 *>(g);
+        const floatx4 ghi = *reinterpret_cast<const floatx4 *>(g + 16);
+        const floatx4 vlo = *reinterpret_cast<const floatx4 *>(v);
+        const floatx4 vhi = *reinterpret_cast<const floatx4 *>(v + 16);
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            o[j] = pack_f16(mul_f32(silu_f32(glo[j]), vlo[j]), mul_f32(silu_f32(ghi[j]), vhi[j]));
+        *reinterpret_cast<u32x4 *>(ah + (size_t)row * ldw + blk * 16 + c * 4) = o;
+    }
 }
 
 // ------------------------------------------- LayerNorm + modulation (A) --
@@ -642,7 +666,7 @@ __global__ __launch_bounds__(256) void b1_quantize_kernel(const float *__restric
 // The GEMM then streams this straight into LDS with no per-tile conversion.
 
 __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restrict__ act, int64_t lda,
-                                                          uint32_t *__restrict__ ah, int M, int K) {
+                                                          uint32_t *__restrict__ ah, int64_t ldw, int M, int K) {
     const int nb = K / 32;
     const int units = M * nb * 4; // (row, block, quad)
     for (int u = blockIdx.x * 256 + threadIdx.x; u < units; u += gridDim.x * 256) {
@@ -654,7 +678,7 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
         u32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = pack_f16(lo[j], hi[j]);
-        *reinterpret_cast<u32x4 *>(ah + (size_t)row * (K / 2) + blk * 16 + c * 4) = v;
+        *reinterpret_cast<u32x4 *>(ah + (size_t)row * ldw + blk * 16 + c * 4) = v;
     }
 }
 
@@ -1520,11 +1544,11 @@ bool pack_supported(const float *act, int64_t lda, int M, int K) {
            (uint64_t)M * (uint64_t)(K / 32) * 4 < (1ull << 31);
 }
 
-hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed, hipStream_t s) {
+hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed, int64_t ldp, hipStream_t s) {
     const int units = M * (K / 32) * 4;
     const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
     hipLaunchKernelGGL(b1_pack_act_kernel, dim3(pgrid), dim3(256), 0, s, act, lda, static_cast<uint32_t *>(packed),
-                       M, K);
+                       ldp / 2, M, K);
     return hipGetLastError();
 }
 
@@ -1580,7 +1604,7 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
                            tiles_n);
         return hipGetLastError();
     }
-    hipError_t e = launch_pack(a.act, a.lda, a.M, a.K, workspace, s);
+    hipError_t e = launch_pack(a.act, a.lda, a.M, a.K, workspace, a.K, s);
     if (e != hipSuccess) return e;
     return launch_gemm_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, s);
 }
@@ -1627,11 +1651,21 @@ hipError_t launch_gelu(const float *x, int64_t ldx, float *y, int64_t ldy, int c
     return hipGetLastError();
 }
 
-hipError_t launch_gelu_pack(const float *act, int64_t lda, int M, int K, void *packed, hipStream_t s) {
+hipError_t launch_gelu_pack(const float *act, int64_t lda, int M, int K, void *packed, int64_t ldp,
+                            hipStream_t s) {
     const int units = M * (K / 32) * 4;
     const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
     hipLaunchKernelGGL(b1_gelu_pack_kernel, dim3(pgrid), dim3(256), 0, s, act, lda,
-                       static_cast<uint32_t *>(packed), M, K);
+                       static_cast<uint32_t *>(packed), ldp / 2, M, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_pack(const float *act, int64_t lda, int M, int H, void *packed, int64_t ldp,
+                              hipStream_t s) {
+    const int units = M * (H / 32) * 4;
+    const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
+    hipLaunchKernelGGL(b1_swiglu_pack_kernel, dim3(pgrid), dim3(256), 0, s, act, lda,
+                       static_cast<uint32_t *>(packed), ldp / 2, M, H);
     return hipGetLastError();
 }
 

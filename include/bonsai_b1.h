@@ -147,6 +147,18 @@ size_t bonsai_b1_packed_act_bytes(int batch, int in_dim);
 int bonsai_b1_pack_act_f16(const float *act, int64_t lda, int in_dim,
                            int batch, void *packed, hipStream_t stream);
 
+/* The same into a column range of wider packed activations: packed rows of
+ * ldp fp16 elements (ldp >= in_dim, ldp % 8 == 0), `packed` pointing at
+ * the range's first column (a multiple of 32, so 64-byte aligned within
+ * the row).  Producers of adjacent ranges build the packed input of a GEMM
+ * over concatenated activations, such as the single-stream block's
+ * linear2 over [attention output | GELU(MLP)] (src/diffuser_graph.cpp:
+ * 533-536), without an fp32 concatenation.  No reference counterpart
+ * (ggml_concat there). */
+int bonsai_b1_pack_act_f16_ld(const float *act, int64_t lda, int in_dim,
+                              int batch, void *packed, int64_t ldp,
+                              hipStream_t stream);
+
 /* out[m][n] for packed activations (in_dim % 384 == 0, packed 16-byte
  * aligned, w 4-byte aligned); same outputs as bonsai_b1_linear_f32 in
  * FAST/GEMM mode on the activations that were packed.  Never allocates. */
@@ -350,6 +362,25 @@ int bonsai_b1_gelu_tanh_f32(const float *x, int64_t ldx, float *y,
  * bonsai_b1_pack_act_f16. */
 int bonsai_b1_gelu_tanh_pack_f16(const float *act, int64_t lda, int in_dim,
                                  int batch, void *packed, hipStream_t stream);
+/* ... into a column range of wider packed activations, as
+ * bonsai_b1_pack_act_f16_ld. */
+int bonsai_b1_gelu_tanh_pack_f16_ld(const float *act, int64_t lda,
+                                    int in_dim, int batch, void *packed,
+                                    int64_t ldp, hipStream_t stream);
+
+/* SwiGLU fused with the packing: replaces ggml_swiglu (mlp_act,
+ * src/diffuser_graph.cpp:227-229) feeding a B1_0 linear.  act [batch][lda]
+ * holds 2*hidden columns per row, gates first; the packed output holds
+ * hidden columns, silu(a[m][j]) * a[m][hidden + j] in fp32 (no
+ * contraction) rounded to fp16, the same values as the SwiGLU epilogue of
+ * bonsai_b1_linear_packed_f16_epi.  hidden % 32 == 0; the input as for
+ * bonsai_b1_pack_act_f16 over 2*hidden columns; ldp and `packed` as for
+ * bonsai_b1_pack_act_f16_ld (the plain form writes rows of hidden). */
+int bonsai_b1_swiglu_pack_f16(const float *act, int64_t lda, int hidden,
+                              int batch, void *packed, hipStream_t stream);
+int bonsai_b1_swiglu_pack_f16_ld(const float *act, int64_t lda, int hidden,
+                                 int batch, void *packed, int64_t ldp,
+                                 hipStream_t stream);
 
 /*
  * The B1_0 writer on the device; replaces quantize_b1_0 of

@@ -184,3 +184,21 @@ def test_batch_epi_rejects_before_device():
     bad = ctypes.c_int(-1)
     assert lib.bonsai_b1_linear_batch_epi(ops, 2, 0, None, None, 0, ctypes.byref(bad), None) == capi.ERR_ARG
     assert bad.value == 1
+
+
+def test_strided_producers_reject_before_device():
+    """The column-range producers check the packed row stride and the
+    SwiGLU width before any launch (no device here)."""
+    lib = bonsai_b1.load()
+    f = 0x100000
+    for fn in (lib.bonsai_b1_pack_act_f16_ld, lib.bonsai_b1_gelu_tanh_pack_f16_ld):
+        assert fn(f, 3072, 3072, 4, f, 3000, None) == capi.ERR_ARG     # ldp < in_dim
+        assert fn(f, 3072, 3072, 4, f, 15364, None) == capi.ERR_ARG    # rows not 16-byte aligned
+        assert fn(f, 3072, 3072, 4, f + 8, 15360, None) == capi.ERR_ARG
+        assert fn(None, 3072, 3072, 4, f, 15360, None) == capi.ERR_ARG
+    sw = lib.bonsai_b1_swiglu_pack_f16_ld
+    assert sw(f, 6144, 3000, 4, f, 3072, None) == capi.ERR_ARG          # hidden % 32
+    assert sw(f, 6000, 3072, 4, f, 3072, None) == capi.ERR_ARG          # lda < 2 hidden
+    assert sw(f, 6144, 3072, 4, f, 3064, None) == capi.ERR_ARG          # ldp < hidden
+    assert sw(f, 6144, 3072, 4, f, 3076, None) == capi.ERR_ARG          # ldp % 8
+    assert lib.bonsai_b1_swiglu_pack_f16(f, 6144, 3072, 4, None, None) == capi.ERR_ARG
