@@ -17,7 +17,12 @@ Two layers:
                        published LayerNorm, with the ggml CPU norm's double
                        accumulators; pinned by closed forms in the tests)
     swiglu_f64         silu(gate) * value over [gate | value]
-                       (tests/ops/test_all_ops.py:29-45 of the reference)
+                       (tests/ops/test_all_ops.py:29-45 of the reference;
+                       pinned by closed forms and torch's silu)
+    gelu_tanh_f64      0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), the
+                       GELU-tanh between the C4 linears (a configuration
+                       choice, not a reference op; pinned by torch's
+                       gelu(approximate="tanh") and by erf-GELU closeness)
 * ctypes bindings of the C restatement in b1_oracle.c (scalar spec path,
   AVX2 path with the reference tiling, fp64 brute force, pack/unpack,
   fp16 conversions).  Build it with `make -C oracle`.
@@ -146,6 +151,12 @@ def pack_act_words(a: np.ndarray) -> np.ndarray:
     rows, k = a.shape
     hb = fp32_to_fp16_bits(np.ascontiguousarray(a, np.float32)).reshape(rows, k // 32, 32).astype(np.uint32)
     return (hb[:, :, :16] | (hb[:, :, 16:] << 16)).reshape(rows, k // 2)
+
+
+def gelu_tanh_f64(x: np.ndarray) -> np.ndarray:
+    """GELU with the tanh approximation, in float64."""
+    x = np.asarray(x, np.float64)
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
 
 
 def swiglu_f64(y: np.ndarray) -> np.ndarray:

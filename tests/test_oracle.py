@@ -397,3 +397,34 @@ def test_swiglu_f64_definition(oracle):
     assert abs(out[0, 1] - 20.0 * 2.0) < 1e-6
     assert abs(out[0, 2]) < 1e-6
     assert out[0, 3] == 0.0
+
+
+def test_swiglu_f64_against_torch(oracle):
+    """swiglu_f64 against an independent implementation: torch's silu in
+    float64 on the gate half times the value half."""
+    import torch
+    rng = np.random.default_rng(11)
+    y = rng.standard_normal((7, 64)) * 4
+    want = (torch.nn.functional.silu(torch.from_numpy(y[:, :32])) * torch.from_numpy(y[:, 32:])).numpy()
+    assert np.allclose(oracle.swiglu_f64(y), want, rtol=1e-14, atol=1e-300)
+
+
+def test_gelu_tanh_f64_pinned(oracle):
+    """gelu_tanh_f64 against torch's gelu(approximate="tanh") in float64,
+    and within the tanh approximation's known distance (< 5e-4 absolute on
+    this range) of the exact erf GELU; closed forms at 0 and the tails.  A
+    wrong constant (0.0447 for 0.044715, or sqrt(pi/2) for sqrt(2/pi))
+    fails the first check."""
+    import torch
+    from scipy.special import erf
+    x = np.linspace(-8, 8, 4001)
+    got = oracle.gelu_tanh_f64(x)
+    want = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    assert np.allclose(got, want, rtol=1e-13, atol=1e-15)
+    exact = 0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))
+    assert np.max(np.abs(got - exact)) < 5e-4
+    assert oracle.gelu_tanh_f64(np.array([0.0]))[0] == 0.0
+    assert abs(oracle.gelu_tanh_f64(np.array([30.0]))[0] - 30.0) < 1e-12
+    assert abs(oracle.gelu_tanh_f64(np.array([-30.0]))[0]) < 1e-12
+    bad = 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.0447 * x ** 3)))
+    assert not np.allclose(bad, want, rtol=1e-13, atol=1e-15)
