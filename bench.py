@@ -437,27 +437,36 @@ def bench_weights_load(torch, b1, blocks=38):
         shutil.rmtree(d, ignore_errors=True)
 
 
-def bench_gemv(torch, b1, synth, m, k, n, steps, warmup):
+def bench_gemv(torch, b1, synth, m, k, n, steps, warmup, packed_input=False):
     """Small-M kernel, weight copies rotated past the MALL.  The launches are
     captured once into a HIP graph (one launch per weight copy) and the graph
     is replayed, so the GPU runs the kernels back to back with no host in the
-    loop; the per-launch time is the event time over the replays / launches."""
+    loop; the per-launch time is the event time over the replays / launches.
+    packed_input: the activations arrive in the packed fp16 layout (from a
+    producer) and bonsai_b1_linear_packed_f16 runs the same kernel without
+    the conversion."""
     nbytes = n * (k // 32) * 6
     copies = max(2, (2 * MALL_BYTES) // nbytes + 1)      # rotate > 2x the MALL
     ws = [synth.device_packed_weights(n, k, 100 + c) for c in range(copies)]
     a = synth.device_activations(m, k, 3)
+    pa = b1.pack_act_f16(a) if packed_input else None
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
-    b1.linear(a, ws[0], n, out=y, mode="gemv")          # load the code object
+
+    def call(c):
+        if packed_input:
+            b1.linear_packed_f16(pa, ws[c], k, n, m, out=y)
+        else:
+            b1.linear(a, ws[c], n, out=y, mode="gemv")
+    call(0)                                              # load the code object
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for c in range(copies):
-            b1.linear(a, ws[c], n, out=y, mode="gemv")
+            call(c)
     reps = max(1, steps // copies)
     ms, wall = time_launches(torch, lambda i: graph.replay(), reps, max(1, warmup // copies))
     ms /= copies
-    eager_ms, _ = time_launches(torch, lambda i: b1.linear(a, ws[i % copies], n, out=y, mode="gemv"),
-                                steps, warmup)
+    eager_ms, _ = time_launches(torch, lambda i: call(i % copies), steps, warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"shape": [m, k, n], "ms": ms, "us": ms * 1e3, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
             "packed_bytes": nbytes, "weight_copies": copies, "launches": reps * copies,
@@ -581,6 +590,9 @@ def main():
         f"{100*v['frac']:.1f}% of HBM peak; eager {v['eager_us']:.2f} us/call")
     v1 = bench_gemv(torch, b1, synth, 1, gk, gn, max(args.steps, 200), min(args.warmup, 400))
     log(f"[bench] GEMV M=1 {v1['us']:.2f} us/call  {v1['gbs']:.0f} GB/s packed")
+    vp = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400), packed_input=True)
+    log(f"[bench] GEMV M={gm} over packed fp16 activations {vp['us']:.2f} us/launch  {vp['gbs']:.0f} GB/s "
+        f"({100 * vp['frac']:.1f}% of HBM peak)")
 
     extra = {}
     if args.all:
@@ -675,7 +687,9 @@ def main():
                  "packed_bytes": v["packed_bytes"], "weight_copies": v["weight_copies"],
                  "timing": "hip graph of back-to-back launches, one per weight copy",
                  "eager_us_per_call": round(v["eager_us"], 3),
-                 "M1_us_per_call": round(v1["us"], 3), "M1_GBps_packed": round(v1["gbs"], 1)},
+                 "M1_us_per_call": round(v1["us"], 3), "M1_GBps_packed": round(v1["gbs"], 1),
+                 "packed_input_us_per_call": round(vp["us"], 3), "packed_input_GBps": round(vp["gbs"], 1),
+                 "packed_input_frac_hbm": round(vp["frac"], 4)},
         "cpu_baseline": cpu,
     }
     if extra:

@@ -336,10 +336,14 @@ int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w, int in_di
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     if (batch == 0) return BONSAI_B1_OK;
-    return b1::launch_gemm_packed(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
-                                  nonfinite, dev->num_cus, stream) == hipSuccess
-               ? BONSAI_B1_OK
-               : BONSAI_B1_ERR_HIP;
+    // a few tokens: the bandwidth-bound small-M kernel, not a 128-row tile
+    const hipError_t e =
+        b1::gemv_packed_ok(batch, in_dim, out_dim)
+            ? b1::launch_gemv_packed(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
+                                     nonfinite, dev->num_cus, stream)
+            : b1::launch_gemm_packed(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
+                                     nonfinite, dev->num_cus, stream);
+    return e == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
 }
 
 // Checks an epilogue against a linear of out_dim outputs (weight rows) and

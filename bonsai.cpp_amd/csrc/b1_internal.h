@@ -77,6 +77,12 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s);
 
 constexpr int kGemvMaxM = 16;
 
+// The small-M kernel over packed fp16 activations (the layout launch_pack
+// writes, row stride K): M <= 16, gemm_packed_ok(M, K, N), K % 256 == 0.
+bool gemv_packed_ok(int M, int K, int N);
+hipError_t launch_gemv_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
+                              int32_t *nonfinite, int num_cus, hipStream_t s);
+
 // GELU-tanh over [rows][cols] fp32 (cols % 4 == 0, rows 16-byte aligned via
 // ld % 4 == 0); the fused form writes packed fp16 activations (pack rules).
 hipError_t launch_gelu(const float *x, int64_t ldx, float *y, int64_t ldy, int cols, int rows, hipStream_t s);

@@ -1336,6 +1336,11 @@ __device__ __forceinline__ void gv2_wait_rg() {
     wait_vmcnt<kGv2Insts - gv2_done_before(R)>();
 }
 
+// PACKED: p.act points at packed fp16 activations ([M][K] in the K-slot
+// pairing, row stride K), which go global -> LDS straight into the fragment
+// layout (no conversion); token slots past M read row M - 1 and are zeroed
+// at the fragment read like the fp32 path's.
+template <bool PACKED>
 __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv2_kernel(LinearArgs p, int groups, int mp_log2) {
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1367,7 +1372,9 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv2_kernel(LinearArgs p, i
         // 1. This wave's activation loads, unit u = (bl*4 + t)*mp + tok
         //    covering a[tok][32 (wb0+bl) + 4t .. +3] and the 4 elements 16
         //    later; 64 * kGvAUnits units per batch (one batch for M <= 8).
-        const int units = 48 << mp_log2;
+        //    Packed: fragment (q, t) is one 1 KB load, lane (g, tok) reading
+        //    the 16 bytes of dwords 4t..4t+3 of block 4q + g of row tok.
+        const int units = PACKED ? 0 : 48 << mp_log2;
         floatx4 lo[kGvAUnits], hi[kGvAUnits];
         auto load_units = [&](int base) {
 #pragma unroll
@@ -1396,7 +1403,22 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv2_kernel(LinearArgs p, i
                 }
             }
         };
-        load_units(0);
+        if constexpr (PACKED) {
+            const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(p.act), (short)0, (int)((uint32_t)p.M * (uint32_t)p.K * 2u), kBufferFlags);
+            const uint32_t trow = (uint32_t)min(lane & 15, p.M - 1) * (uint32_t)p.K * 2u;
+#pragma unroll
+            for (int q = 0; q < kGvQuads; ++q) {
+                const int blk = wb0 + 4 * q + (lane >> 4);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t voff = blk < nb ? trow + (uint32_t)blk * 64u + (uint32_t)t * 16u : 0xFFFFFFF0u;
+                    dma_buf_lds16(ars, abuf + (q * 4 + t) * 1024, voff);
+                }
+            }
+        } else {
+            load_units(0);
+        }
 
         // 2. The work-group's weight rows of this pass, row group by row
         //    group, as whole 1 KB runs straight into LDS.
@@ -1414,11 +1436,13 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv2_kernel(LinearArgs p, i
         // 3. Activations -> fp16 fragments in this wave's LDS area; the
         //    weight loads, issued after the first batch, stay in flight.
         wait_vmcnt<kGv2Insts>();
-        store_units(0);
-        for (int base = 64 * kGvAUnits; base < units; base += 64 * kGvAUnits) { // M > 8
-            load_units(base);
-            wait_vmcnt<0>();
-            store_units(base);
+        if constexpr (!PACKED) {
+            store_units(0);
+            for (int base = 64 * kGvAUnits; base < units; base += 64 * kGvAUnits) { // M > 8
+                load_units(base);
+                wait_vmcnt<0>();
+                store_units(base);
+            }
         }
         u32x4 af[kGvQuads][4];
 #pragma unroll
@@ -1671,20 +1695,29 @@ hipError_t launch_swiglu_pack(const float *act, int64_t lda, int M, int H, void 
 
 bool gemv_supported(const LinearArgs &a) { return a.M <= kGemvMaxM && fast_layout_ok(a); }
 
-hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
+static hipError_t gemv_attrs() {
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(attr_once, [] {
         attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kGvLds);
         if (attr_err == hipSuccess)
-            attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv2_kernel),
+            attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv2_kernel<false>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGv2Lds);
+        if (attr_err == hipSuccess)
+            attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv2_kernel<true>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kGv2Lds);
     });
-    if (attr_err != hipSuccess) return attr_err;
-    // Weights staged through LDS when rows are 16-byte multiples and the
-    // weight bytes fit a buffer resource's 31-bit range.
-    const bool staged = a.K % 256 == 0 && (uint64_t)a.N * (uint64_t)(a.K / 32) * 6 < (1ull << 31);
+    return attr_err;
+}
+
+// Weights staged through LDS when rows are 16-byte multiples and the weight
+// bytes fit a buffer resource's 31-bit range.
+static bool gemv_staged(int K, int N) {
+    return K % 256 == 0 && (uint64_t)N * (uint64_t)(K / 32) * 6 < (1ull << 31);
+}
+
+static void gemv_grid(const LinearArgs &a, int num_cus, int *nwg_out, int *groups_out, int *mp_log2_out) {
     const int groups = (a.N + 15) / 16;
     int nwg = num_cus > 0 ? num_cus : 256;
     const int need = (groups + kGvMaxRG - 1) / kGvMaxRG;
@@ -1692,10 +1725,36 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
     if (nwg > groups) nwg = groups;
     int mp_log2 = 0;
     while ((1 << mp_log2) < a.M) ++mp_log2;
-    if (staged)
-        hipLaunchKernelGGL(b1_gemv2_kernel, dim3(nwg), dim3(kGvWaves * 64), kGv2Lds, s, a, groups, mp_log2);
+    *nwg_out = nwg;
+    *groups_out = groups;
+    *mp_log2_out = mp_log2;
+}
+
+hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
+    const hipError_t attr_err = gemv_attrs();
+    if (attr_err != hipSuccess) return attr_err;
+    int nwg, groups, mp_log2;
+    gemv_grid(a, num_cus, &nwg, &groups, &mp_log2);
+    if (gemv_staged(a.K, a.N))
+        hipLaunchKernelGGL(b1_gemv2_kernel<false>, dim3(nwg), dim3(kGvWaves * 64), kGv2Lds, s, a, groups, mp_log2);
     else
         hipLaunchKernelGGL(b1_gemv_kernel, dim3(nwg), dim3(kGvWaves * 64), kGvLds, s, a, groups, mp_log2);
+    return hipGetLastError();
+}
+
+bool gemv_packed_ok(int M, int K, int N) {
+    return M >= 1 && M <= kGemvMaxM && gemm_packed_ok(M, K, N) && gemv_staged(K, N) &&
+           (uint64_t)M * (uint64_t)K * 2 < (1ull << 31);
+}
+
+hipError_t launch_gemv_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
+                              int32_t *nonfinite, int num_cus, hipStream_t s) {
+    const hipError_t attr_err = gemv_attrs();
+    if (attr_err != hipSuccess) return attr_err;
+    const LinearArgs a{static_cast<const float *>(packed), K, w, K, N, M, out, ldo, nonfinite};
+    int nwg, groups, mp_log2;
+    gemv_grid(a, num_cus, &nwg, &groups, &mp_log2);
+    hipLaunchKernelGGL(b1_gemv2_kernel<true>, dim3(nwg), dim3(kGvWaves * 64), kGv2Lds, s, a, groups, mp_log2);
     return hipGetLastError();
 }
 

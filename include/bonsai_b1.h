@@ -161,7 +161,8 @@ int bonsai_b1_pack_act_f16_ld(const float *act, int64_t lda, int in_dim,
 
 /* out[m][n] for packed activations (in_dim % 384 == 0, packed 16-byte
  * aligned, w 4-byte aligned); same outputs as bonsai_b1_linear_f32 in
- * FAST/GEMM mode on the activations that were packed.  Never allocates. */
+ * FAST/GEMM mode on the activations that were packed, or, for batch <= 16
+ * with in_dim % 256 == 0, as its small-M (GEMV) mode.  Never allocates. */
 int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w,
                                 int in_dim, int out_dim, int batch,
                                 float *out, int64_t ldo, int32_t *nonfinite,

@@ -393,6 +393,29 @@ def test_linear_packed_matches_fused_entry(torch, b1, m, k, n):
     assert int(nf.item()) == 0
 
 
+@pytest.mark.parametrize("m,k,n,mode", [(1, 3072, 18432, "gemv"), (8, 3072, 18432, "gemv"), (16, 3072, 1000, "gemv"),
+                                         (5, 768, 48, "gemv"), (3, 1536, 4000, "gemv"), (8, 1152, 500, "gemm")])
+def test_linear_packed_small_m(torch, b1, m, k, n, mode):
+    """Packed activations with M <= 16 run the small-M kernel (fragments
+    loaded straight from the packing) and give bit for bit what the fp32
+    entry's small-M kernel gives; K % 256 != 0 stays on the GEMM tile and
+    matches GEMM mode."""
+    from bonsai_b1 import synth
+    say(f"packed small-M ({m},{k},{n}) vs {mode}")
+    a = synth.device_activations(m, k, 43)
+    w = synth.device_packed_weights(n, k, 44)
+    ref = b1.linear(a, w, n, mode=mode)
+    out = torch.full((m, n + 12), 7.0, device="cuda")
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    packed = b1.pack_act_f16(a)
+    b1.linear_packed_f16(packed, w, k, n, m, out=out[:, :n], nonfinite=nf)
+    torch.cuda.synchronize()
+    say(f"  max |diff| {float((out[:, :n] - ref).abs().max()):.3e}")
+    assert torch.equal(out[:, :n], ref)
+    assert bool((out[:, n:] == 7.0).all()), "columns past out_dim untouched"
+    assert int(nf.item()) == 0
+
+
 @pytest.mark.parametrize("m,k,n", [(8, 768, 96), (160, 768, 600)])
 def test_signed_scales(torch, b1, oracle, m, k, n):
     """fp16 scales of either sign (and +-0): the reference multiplies the
