@@ -359,17 +359,21 @@ struct Stager {
 void copy_host(void *dst, const uint8_t *src, size_t n) {
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
     const size_t parts = std::min<size_t>(std::min<size_t>(4, hw), (n + kCopySlice - 1) / kCopySlice);
-    if (parts <= 1) {
-        memcpy(dst, src, n);
-        return;
-    }
+    uint8_t *d = static_cast<uint8_t *>(dst);
+    const size_t step = parts > 1 ? (n + parts - 1) / parts : n;
     std::vector<std::thread> th;
-    const size_t step = (n + parts - 1) / parts;
-    for (size_t p = 1; p < parts; ++p) {
-        const size_t o = p * step;
-        if (o < n) th.emplace_back([=] { memcpy(static_cast<uint8_t *>(dst) + o, src + o, std::min(step, n - o)); });
+    try {
+        th.reserve(parts);
+        for (size_t p = 1; p < parts && p * step < n; ++p) {
+            const size_t o = p * step;
+            th.emplace_back([=] { memcpy(d + o, src + o, std::min(step, n - o)); });
+        }
+    } catch (...) {
+        // fewer threads than pieces: the pieces without one are copied here
     }
-    memcpy(dst, src, std::min(step, n));
+    const size_t rest = std::min(n, step * (th.size() + 1)); // first piece no thread took
+    memcpy(d, src, std::min(step, n));
+    if (rest < n) memcpy(d + rest, src + rest, n - rest);
     for (auto &t : th) t.join();
 }
 
