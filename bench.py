@@ -340,6 +340,9 @@ def bench_klein_step(torch, b1, synth):
         return ops
 
     ops_f, ops_s = step_ops(True), step_ops(False)
+    need = max(b1.linear_batch_workspace_bytes(ops_f), b1.linear_batch_workspace_bytes(ops_s))
+    if need > ws.numel():
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
     ms = graph_ms(torch, lambda: b1.linear_batch(ops_f, workspace=ws), reps=2)
     ms_sep = graph_ms(torch, lambda: b1.linear_batch(ops_s, workspace=ws), reps=2)
     # the same GEMMs over inputs already in the packed fp16 layout (as fused

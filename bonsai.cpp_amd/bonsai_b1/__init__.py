@@ -14,6 +14,7 @@ from .capi import (  # noqa: F401
     declared_symbols,
     device_weights,
     linear_batch,
+    linear_batch_workspace_bytes,
     linear_epi,
     linear_epi_workspace_bytes,
     norm_mod,

@@ -284,11 +284,7 @@ def device_weights(w_packed, in_dim: int, out_dim: int) -> B1WeightsC:
     return c
 
 
-def linear_batch(ops, mode: str = "auto", nonfinite=None, workspace=None, stream=None):
-    """bonsai_b1_linear_batch over [(act, B1WeightsC, out), ...] (cuda
-    tensors, act/out 2-D fp32 with unit column stride).  An op may carry a
-    fourth item, its epilogue: "swiglu", or ("gate_residual", gate,
-    residual); then bonsai_b1_linear_batch_epi runs the list."""
+def _batch_ops(ops):
     with_epi = any(len(op) > 3 for op in ops)
     arr = ((LinearOpEpi if with_epi else LinearOp) * len(ops))()
     keep = []
@@ -306,6 +302,24 @@ def linear_batch(ops, mode: str = "auto", nonfinite=None, workspace=None, stream
                 arr[i].epi = _epilogue(spec, None, None, w.out_dim, act.shape[0])
             else:
                 arr[i].epi = _epilogue(spec[0], spec[1], spec[2], w.out_dim, act.shape[0])
+    return arr, with_epi, keep
+
+
+def linear_batch_workspace_bytes(ops, mode: str = "auto") -> int:
+    """Workspace bytes a linear_batch call over `ops` uses on the current
+    device (bonsai_b1_linear_batch[_epi]_workspace_bytes)."""
+    arr, with_epi, _ = _batch_ops(ops)
+    fn = load().bonsai_b1_linear_batch_epi_workspace_bytes if with_epi else \
+        load().bonsai_b1_linear_batch_workspace_bytes
+    return int(fn(arr, len(ops), MODES[mode]))
+
+
+def linear_batch(ops, mode: str = "auto", nonfinite=None, workspace=None, stream=None):
+    """bonsai_b1_linear_batch over [(act, B1WeightsC, out), ...] (cuda
+    tensors, act/out 2-D fp32 with unit column stride).  An op may carry a
+    fourth item, its epilogue: "swiglu", or ("gate_residual", gate,
+    residual); then bonsai_b1_linear_batch_epi runs the list."""
+    arr, with_epi, keep = _batch_ops(ops)
     bad = ctypes.c_int(-1)
     nf = nonfinite.data_ptr() if nonfinite is not None else None
     ws = workspace.data_ptr() if workspace is not None else None

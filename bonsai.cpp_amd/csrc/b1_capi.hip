@@ -154,7 +154,7 @@ static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim,
     a.nonfinite = nonfinite;
 
     auto gemm = [&]() {
-        const size_t need = b1::gemm_workspace_bytes(a);
+        const size_t need = b1::gemm_workspace_bytes_total(a, dev->num_cus);
         if (need > 0 && ws_mode == 0) {
             ws = stream_workspace(dev, stream, need);
             ws_bytes = ws ? need : 0;
@@ -198,7 +198,13 @@ size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode) {
     if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
     if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return 0;
     if ((mode == BONSAI_B1_MODE_AUTO || mode == BONSAI_B1_MODE_FAST) && batch <= b1::kGemvMaxM) return 0;
-    return b1::gemm_packed_ok(batch, in_dim, out_dim) ? (size_t)batch * (size_t)in_dim * 2 : 0;
+    if (!b1::gemm_packed_ok(batch, in_dim, out_dim)) return 0;
+    // the packing, then (on a device where the shape splits along K) the
+    // split-K partials
+    const size_t pack = (size_t)batch * (size_t)in_dim * 2;
+    const DeviceInfo *dev = current_device(nullptr);
+    const int splits = dev ? b1::gemm_splits(batch, in_dim, out_dim, dev->num_cus) : 1;
+    return splits > 1 ? ((pack + 255) & ~(size_t)255) + b1::gemm_split_bytes(batch, out_dim, splits) : pack;
 }
 
 int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
@@ -535,32 +541,88 @@ struct BatchOp {
 
 static int epi_kind(const bonsai_b1_epilogue *e) { return e ? e->kind : BONSAI_B1_EPI_NONE; }
 
-// Workspace areas of a batch: the largest fp16 packing among its packed-GEMM
-// ops, and the largest fp32 linear output among its ops whose epilogue runs
-// as a separate pass (the other paths).  Layout: [pack][y].
+static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// The ops from i on that run as one GEMM with op i, on the packed path:
+// consecutive plain ops on the same input whose weights follow each other in
+// memory and whose outputs are adjacent column ranges of one row stride (q/k/v
+// with concatenated weights, src/diffuser_graph.cpp:354-361), split along K
+// as op i alone would be, unless an output overlaps the input they all read.
+// Returns the last op of the run; *n_sum is its output width.
 template <class OpAt>
-static void batch_areas(int n_ops, int mode, OpAt at, size_t *pack, size_t *ybytes) {
-    *pack = 0;
-    *ybytes = 0;
+static int fuse_span(int n_ops, int mode, int num_cus, OpAt at, int i, int *n_sum) {
+    const BatchOp bi = at(i);
+    const b1::LinearArgs a = batch_args(*bi.op);
+    const int splits = b1::gemm_splits(a.M, a.K, a.N, num_cus);
+    int last = i;
+    *n_sum = a.N;
+    while (epi_kind(bi.epi) == BONSAI_B1_EPI_NONE && last + 1 < n_ops) {
+        const BatchOp pb = at(last), qb = at(last + 1);
+        const bonsai_b1_linear_op &p = *pb.op, &q = *qb.op;
+        // the packed size from the dimensions (nbytes is not trusted)
+        const size_t p_bytes =
+            (size_t)p.w->out_dim * (size_t)(p.w->in_dim / BONSAI_B1_BLOCK_SIZE) * BONSAI_B1_BLOCK_BYTES;
+        if (epi_kind(qb.epi) != BONSAI_B1_EPI_NONE || q.batch != a.M || q.act != a.act || q.lda != a.lda ||
+            q.w->in_dim != a.K || q.ldo != a.ldo || q.w->data != static_cast<const uint8_t *>(p.w->data) + p_bytes ||
+            q.out != p.out + p.w->out_dim || *n_sum + (int64_t)q.w->out_dim > INT32_MAX)
+            break;
+        const b1::LinearArgs qa = batch_args(q);
+        if (batch_path(qa, mode) != BatchPath::Packed || b1::gemm_splits(qa.M, qa.K, qa.N, num_cus) != splits) break;
+        *n_sum += q.w->out_dim;
+        ++last;
+    }
+    if (last > i) {
+        const uintptr_t o0 = reinterpret_cast<uintptr_t>(a.out);
+        const uintptr_t o1 = o0 + ((size_t)(a.M - 1) * (size_t)a.ldo + (size_t)*n_sum) * sizeof(float);
+        const uintptr_t i0 = reinterpret_cast<uintptr_t>(a.act);
+        const uintptr_t i1 = i0 + ((size_t)(a.M - 1) * (size_t)a.lda + (size_t)a.K) * sizeof(float);
+        if (o0 < i1 && i0 < o1) {
+            last = i;
+            *n_sum = a.N;
+        }
+    }
+    return last;
+}
+
+// Workspace areas of a batch, laid out [pack][split][y], each 256-byte
+// aligned: the largest fp16 packing among its packed-GEMM ops, the largest
+// split-K partial area among its plain packed GEMMs (fused runs included),
+// and the largest fp32 linear output among its ops whose epilogue runs as a
+// separate pass (the other paths).
+struct BatchAreas {
+    size_t pack = 0, split = 0, y = 0;
+    size_t split_off() const { return round256(pack); }
+    size_t y_off() const { return split_off() + round256(split); }
+    size_t need() const { return y ? y_off() + y : split ? split_off() + split : pack; }
+};
+
+template <class OpAt>
+static BatchAreas batch_areas(int n_ops, int mode, int num_cus, OpAt at) {
+    BatchAreas r;
     for (int i = 0; i < n_ops; ++i) {
         const BatchOp b = at(i);
         if (!batch_op_ok(*b.op, b.epi) || b.op->batch == 0) continue;
         const b1::LinearArgs a = batch_args(*b.op);
         if (batch_path(a, mode) == BatchPath::Packed) {
-            *pack = std::max(*pack, b1::gemm_workspace_bytes(a));
+            r.pack = std::max(r.pack, b1::gemm_workspace_bytes(a));
+            if (epi_kind(b.epi) == BONSAI_B1_EPI_NONE) {
+                int n_sum;
+                const int last = fuse_span(n_ops, mode, num_cus, at, i, &n_sum);
+                r.split = std::max(r.split,
+                                   b1::gemm_split_bytes(a.M, n_sum, b1::gemm_splits(a.M, a.K, a.N, num_cus)));
+                i = last;
+            }
         } else if (epi_kind(b.epi) != BONSAI_B1_EPI_NONE) {
-            *ybytes = std::max(*ybytes, (size_t)a.M * (size_t)a.N * sizeof(float));
+            r.y = std::max(r.y, (size_t)a.M * (size_t)a.N * sizeof(float));
         }
     }
+    return r;
 }
-
-static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 template <class OpAt>
 static size_t batch_need(int n_ops, int mode, OpAt at) {
-    size_t pack, y;
-    batch_areas(n_ops, mode, at, &pack, &y);
-    return y ? round256(pack) + y : pack;
+    const DeviceInfo *dev = current_device(nullptr);
+    return batch_areas(n_ops, mode, dev ? dev->num_cus : 0, at).need();
 }
 
 template <class OpAt>
@@ -581,18 +643,20 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
     }
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
-    size_t pack_area, y_area;
-    batch_areas(n_ops, mode, at, &pack_area, &y_area);
-    const size_t need = y_area ? round256(pack_area) + y_area : pack_area;
-    if (need > 0) {
+    BatchAreas areas = batch_areas(n_ops, mode, dev->num_cus, at);
+    if (areas.need() > 0) {
         if (!workspace) {
-            workspace = stream_workspace(dev, stream, need);
-            workspace_bytes = workspace ? need : 0;
+            workspace = stream_workspace(dev, stream, areas.need());
+            workspace_bytes = workspace ? areas.need() : 0;
         }
-        if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
+        // a workspace without room for the split-K partials runs every GEMM
+        // unsplit (the same outputs up to the order of the K summation)
+        if (workspace && workspace_bytes < areas.need()) areas.split = 0;
+        if (!workspace || workspace_bytes < areas.need() || (reinterpret_cast<uintptr_t>(workspace) & 15u))
             return BONSAI_B1_ERR_ARG;
     }
-    float *ybuf = y_area ? reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + round256(pack_area)) : nullptr;
+    float *ybuf = areas.y ? reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + areas.y_off()) : nullptr;
+    void *split_area = areas.split ? static_cast<uint8_t *>(workspace) + areas.split_off() : nullptr;
     // The packed activations in the workspace belong to (act, lda, batch, K).
     const float *packed_act = nullptr;
     int64_t packed_lda = 0;
@@ -623,39 +687,8 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
             if (e == hipSuccess && kind != BONSAI_B1_EPI_NONE)
                 e = b1::launch_epi(ybuf, a.N, a.M, a.N, kind, g, a.out, a.ldo, stream);
         } else {
-            // Consecutive plain ops on this input whose weights follow each
-            // other in memory and whose outputs are adjacent column ranges of
-            // one row stride are one GEMM over the concatenated rows (q/k/v
-            // with concatenated weights, src/diffuser_graph.cpp:354-361),
-            // unless an output overlaps the input they all read.
-            int last = i;
-            int n_sum = a.N;
-            while (kind == BONSAI_B1_EPI_NONE && last + 1 < n_ops) {
-                const BatchOp pb = at(last), qb = at(last + 1);
-                const bonsai_b1_linear_op &p = *pb.op, &q = *qb.op;
-                // the packed size from the dimensions (nbytes is not trusted)
-                const size_t p_bytes =
-                    (size_t)p.w->out_dim * (size_t)(p.w->in_dim / BONSAI_B1_BLOCK_SIZE) * BONSAI_B1_BLOCK_BYTES;
-                if (epi_kind(qb.epi) != BONSAI_B1_EPI_NONE || q.batch != a.M || q.act != a.act || q.lda != a.lda ||
-                    q.w->in_dim != a.K || q.ldo != a.ldo ||
-                    q.w->data != static_cast<const uint8_t *>(p.w->data) + p_bytes ||
-                    q.out != p.out + p.w->out_dim || n_sum + (int64_t)q.w->out_dim > INT32_MAX)
-                    break;
-                b1::LinearArgs qa = batch_args(q);
-                if (batch_path(qa, mode) != BatchPath::Packed) break;
-                n_sum += q.w->out_dim;
-                ++last;
-            }
-            if (last > i) {
-                const uintptr_t o0 = reinterpret_cast<uintptr_t>(a.out);
-                const uintptr_t o1 = o0 + ((size_t)(a.M - 1) * (size_t)a.ldo + (size_t)n_sum) * sizeof(float);
-                const uintptr_t i0 = reinterpret_cast<uintptr_t>(a.act);
-                const uintptr_t i1 = i0 + ((size_t)(a.M - 1) * (size_t)a.lda + (size_t)a.K) * sizeof(float);
-                if (o0 < i1 && i0 < o1) {
-                    last = i;
-                    n_sum = a.N;
-                }
-            }
+            int n_sum;
+            const int last = fuse_span(n_ops, mode, dev->num_cus, at, i, &n_sum);
             if (!(packed_act == a.act && packed_lda == a.lda && packed_m == a.M && packed_k == a.K)) {
                 e = b1::launch_pack(a.act, a.lda, a.M, a.K, workspace, a.K, stream);
                 packed_act = a.act;
@@ -663,9 +696,15 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
                 packed_m = a.M;
                 packed_k = a.K;
             }
-            if (e == hipSuccess)
-                e = b1::launch_gemm_packed_epi(workspace, a.w, a.K, n_sum, a.M, a.out, a.ldo, nonfinite,
-                                               dev->num_cus, kind, g, stream);
+            const int splits = kind == BONSAI_B1_EPI_NONE ? b1::gemm_splits(a.M, a.K, a.N, dev->num_cus) : 1;
+            if (e == hipSuccess) {
+                if (splits > 1 && split_area && areas.split >= b1::gemm_split_bytes(a.M, n_sum, splits))
+                    e = b1::launch_gemm_packed_split(workspace, a.w, a.K, n_sum, a.M, a.out, a.ldo, nonfinite,
+                                                     dev->num_cus, splits, split_area, stream);
+                else
+                    e = b1::launch_gemm_packed_epi(workspace, a.w, a.K, n_sum, a.M, a.out, a.ldo, nonfinite,
+                                                   dev->num_cus, kind, g, stream);
+            }
             if (last > i) out_cols = n_sum;
             i = last;
         }

@@ -39,7 +39,17 @@ hipError_t launch_exact(const LinearArgs &a, hipStream_t s);
 // while staging each tile.
 bool gemm_supported(const LinearArgs &a);
 size_t gemm_workspace_bytes(const LinearArgs &a);
+// With room for the split-K partials after the packing (256-byte aligned),
+// launch_gemm splits K when gemm_splits says so.
+size_t gemm_workspace_bytes_total(const LinearArgs &a, int num_cus);
 hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s);
+
+// Split-K for plain GEMMs whose tiles would leave most CUs idle: the number
+// of K ranges (1 = none; a function of the shape and CU count only, so
+// every caller splits a given shape the same way) and the fp32 partial
+// area it needs (splits x M x N rounded up to 4 columns).
+int gemm_splits(int M, int K, int N, int num_cus);
+size_t gemm_split_bytes(int M, int N, int splits);
 
 // The two halves of the workspace path.  Packed activations: u32 word
 // (row m, 16 j + d) = fp16(a[m][32 j + d]) | fp16(a[m][32 j + d + 16]) << 16,
@@ -52,6 +62,12 @@ hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed
 bool gemm_packed_ok(int M, int K, int N);
 hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
                               int32_t *nonfinite, int num_cus, hipStream_t s);
+// The same split into `splits` K ranges (a divisor of K / 384) with the
+// partials in `partials` (gemm_split_bytes, 16-byte aligned), summed in
+// order by a second kernel.
+hipError_t launch_gemm_packed_split(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
+                                    int64_t ldo, int32_t *nonfinite, int num_cus, int splits, void *partials,
+                                    hipStream_t s);
 // The same GEMM with a fused epilogue (kind 0 plain, 1 gate-residual,
 // 2 SwiGLU with N = 2 glu_h, glu_h % 32 == 0, out [M][ldo >= glu_h]).
 hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, int N, int M, float *out,

@@ -100,11 +100,12 @@ __device__ __forceinline__ void dma_lds12(const void *src, void *lds) {
 // Raw buffer loads with range checking (offsets at or past num_records read
 // zeros); word 3 of the resource for gfx9-family raw buffers.
 constexpr int kBufferFlags = 0x00020000;
-// Cache policy of the GEMM's output stores: non-temporal.  The fp32 output
-// is written once and is far larger than L2, so streaming it keeps L2 for
-// the operand tiles other work-groups re-read (measured 268.6 -> 264.0 us at
+// Cache policy of the GEMM's full-tile output stores: the default.  Each
+// 16-byte store covers 32 rows x 32 bytes, a quarter of each 128-byte line,
+// and L2 merges the four quarters before the line goes to memory; the
+// non-temporal policy sends each quarter on its own (355 vs ~267 us at
 // M=4096 K=3072 N=12288).
-constexpr int kStoreNT = 2;
+constexpr int kStoreNT = 0;
 // 16 bytes per lane from the buffer at byte offset voff, landing at
 // lds + 16 * lane (wave-uniform lds, through M0).
 __device__ __forceinline__ void dma_buf_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff) {
@@ -753,7 +754,8 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                                                                     const uint8_t *__restrict__ w, int K, int N,
                                                                     int M, float *__restrict__ out, int64_t ldo,
                                                                     int32_t *nonfinite, int tiles_m, int tiles_n,
-                                                                    int vec_store, GemmEpi epi) {
+                                                                    int vec_store, GemmEpi epi, int ksplit,
+                                                                    int64_t pstride) {
     using C = GemmLdsCfg<BM, BN, WN, STAGES>;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
@@ -761,8 +763,13 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
     // through M0 and must not depend on the lane.
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 31, g = lane >> 5;
-    const int nstage = K / C::KC; // a multiple of STAGES (K % (128 STAGES) == 0)
+    // Work unit u: K range `split` = u / (tiles_m tiles_n) of ksplit equal
+    // ranges, output tile u % (tiles_m tiles_n).  With ksplit > 1 a unit's
+    // plain product goes to partial slice `split` (out + split * pstride),
+    // which a separate pass sums.
+    const int nstage = K / C::KC / ksplit; // stages per unit, a multiple of STAGES
     const int ntiles = tiles_m * tiles_n;
+    const int nunits = ntiles * ksplit;
     const uint32_t rs = (uint32_t)(K / 32) * 6;
     const uint8_t *abase = reinterpret_cast<const uint8_t *>(ah);
 
@@ -901,19 +908,11 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 
     // Epilogue.  Accumulator (n, m) layout of the 32x32 MFMA with weights as
     // A: lane column li = token m0 + 32 mt + li, rows 8*(v/4) + 4*g + v%4 =
-    // output columns; v = 4q..4q+3 are 4 consecutive columns.  Stored as is,
-    // one 16-byte store instruction would cover 32 output rows x 32 bytes.
-    // Full tiles are first rearranged in registers so that each store
-    // instruction covers 8 rows x 128 bytes (whole cache lines):
-    //  1. v_permlane16_swap exchanges lanes 16-31 / 48-63 of column group
-    //     q = 2p with lanes 0-15 / 32-47 of q = 2p+1.  Register set (p, s)
-    //     then holds, in lane (li, g), token 32 mt + 16 s + (li % 16) at
-    //     columns 16p + 8 (li / 16) + 4g + 0..3.
-    //  2. A DPP row rotation by 8 exchanges lane bit 3 with p: register set
-    //     (t, s) holds token 32 mt + 16 s + 8 t + (lane % 8) at columns
-    //     16 ((lane / 8) % 2) + 8 ((lane / 16) % 2) + 4 (lane / 32) + 0..3.
-    // Non-finite outputs are counted only when the caller passed a counter.
-    auto epilogue = [&](int m0, int n0) -> int {
+    // output columns; v = 4q..4q+3 are 4 consecutive columns, stored as one
+    // 16-byte vector (one store instruction covers 32 output rows x 32
+    // bytes).  Non-finite outputs are counted only when the caller passed a
+    // counter.
+    auto epilogue = [&](int m0, int n0, float *__restrict__ out) -> int {
         int bad = 0;
         const bool cnt = nonfinite != nullptr;
         if constexpr (EPI == 2) {
@@ -989,8 +988,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
         }
         const bool full = vec_store && m0 + BM <= M && n0 + BN <= N;
         if (full) {
-            // the count does not depend on where each value is stored:
-            // take it before the rearrangement, outside the store path
+            // the count, outside the store path
             if (cnt) {
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt)
@@ -999,55 +997,31 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 #pragma unroll
                         for (int v = 0; v < 16; ++v) bad += !__builtin_isfinite(acc[mt][nt][v]);
             }
-            // Buffer stores: the wave's tile origin in the resource, the lane
-            // part in one VGPR and the row offset in an SGPR, so the 32
-            // stores need no per-store address arithmetic.  The host enables
+            // Buffer stores of the accumulator layout: the wave's tile origin
+            // in the resource, the lane part in one VGPR and the (mt, nt, q)
+            // offset in an SGPR, so the 32 stores need no per-store address
+            // arithmetic.  Each covers 32 rows x 32 bytes.  The host enables
             // vector stores only when 128 rows span < 2^31 bytes.
             const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
                 out + (size_t)m0 * ldo + n0 + wave * WN, (short)0, (int)(BM * ldo * 4), kBufferFlags);
-            const int lcol = 16 * ((lane >> 3) & 1) + 8 * ((lane >> 4) & 1) + 4 * (lane >> 5);
-            const int lvoff = 4 * ((lane & 7) * (int)ldo + lcol);
+            const int lvoff = 4 * (li * (int)ldo + 4 * g);
 #pragma unroll
-            for (int mt = 0; mt < C::MT; ++mt) {
+            for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
-                for (int nt = 0; nt < C::NTL; ++nt) {
-                    floatx4 y[2][2]; // [s][t]
+                for (int nt = 0; nt < C::NTL; ++nt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        uint32_t x[2][2]; // [p][s] after step 1
+                    for (int q = 0; q < 4; ++q) {
+                        // element values are copied out first: a bit cast of
+                        // a vector element reads element 0 in this clang
+                        u32x4 v;
 #pragma unroll
-                        for (int p = 0; p < 2; ++p) {
-                            // element values are copied out first: a bit cast
-                            // of a vector element reads element 0 in this clang
-                            const float xa = acc[mt][nt][8 * p + r], xb = acc[mt][nt][8 * p + 4 + r];
-                            const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, xa),
-                                                                             __builtin_bit_cast(uint32_t, xb),
-                                                                             false, false);
-                            x[p][0] = sw[0];
-                            x[p][1] = sw[1];
+                        for (int r = 0; r < 4; ++r) {
+                            const float x = acc[mt][nt][4 * q + r];
+                            v[r] = __builtin_bit_cast(uint32_t, x);
                         }
-#pragma unroll
-                        for (int s = 0; s < 2; ++s) {
-                            // row_ror:8 reads lane ^ 8; bank mask 0xc writes
-                            // lanes 8-15 of each row, 0x3 lanes 0-7
-                            const int lo = (int)x[0][s], hi = (int)x[1][s];
-                            y[s][0][r] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(lo, hi, 0x128, 0xf, 0xc, false));
-                            y[s][1][r] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(hi, lo, 0x128, 0xf, 0x3, false));
-                        }
+                        const int ro = 4 * (mt * 32 * (int)ldo + nt * 32 + 8 * q);
+                        __builtin_amdgcn_raw_buffer_store_b128(v, ors, lvoff, ro, kStoreNT);
                     }
-#pragma unroll
-                    for (int s = 0; s < 2; ++s)
-#pragma unroll
-                        for (int t = 0; t < 2; ++t) {
-                            const int ro = 4 * ((mt * 32 + 16 * s + 8 * t) * (int)ldo + nt * 32);
-                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y[s][t]), ors, lvoff, ro,
-                                                                   kStoreNT);
-                        }
-                    // one accumulator tile at a time keeps the temporaries
-                    // of the rearrangement within the register budget
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
         } else {
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt) {
@@ -1074,12 +1048,19 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
         return full ? 2 : 1;
     };
 
-    int tile = xcd_tile(blockIdx.x, gridDim.x);
-    int m0, n0;
-    tile_origin(tile, m0, n0);
+    int unit = xcd_tile(blockIdx.x, gridDim.x);
+    int m0, n0, kst0;   // tile origin; first global stage of the unit's K range
+    float *uout;        // where the unit's epilogue writes
+    auto unit_origin = [&](int u) {
+        const int split = u / ntiles;
+        tile_origin(u - split * ntiles, m0, n0);
+        kst0 = split * nstage;
+        uout = out + (size_t)split * (size_t)pstride;
+    };
+    unit_origin(unit);
     setup(m0, n0);
 #pragma unroll
-    for (int t = 0; t < STAGES - 1; ++t) issue(t, t);
+    for (int t = 0; t < STAGES - 1; ++t) issue(kst0 + t, t);
     int prev_stores = 0; // stores the previous epilogue left: 0 none, 1 scalar, 2 vector
     for (;;) {
 #pragma unroll
@@ -1118,7 +1099,8 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                 // the stage's first fragment reads go out before the next
                 // stage's loads, so the loads issue under their latency
                 compute(u, [&] {
-                    if (s + u + STAGES - 1 < nstage) issue(s + u + STAGES - 1, (u + STAGES - 1) % STAGES);
+                    if (s + u + STAGES - 1 < nstage)
+                        issue(kst0 + s + u + STAGES - 1, (u + STAGES - 1) % STAGES);
                 });
             }
         }
@@ -1126,17 +1108,54 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
         // Slots 0..STAGES-2 were last read before the final barrier: fetch
         // the next tile's first STAGES-1 stages now, then store this tile.
         const int cm0 = m0, cn0 = n0;
-        tile += gridDim.x;
-        const bool more = tile < ntiles;
+        float *const cout = uout;
+        unit += gridDim.x;
+        const bool more = unit < nunits;
         if (more) {
-            tile_origin(tile, m0, n0);
+            unit_origin(unit);
             setup(m0, n0);
 #pragma unroll
-            for (int t = 0; t < STAGES - 1; ++t) issue(t, t);
+            for (int t = 0; t < STAGES - 1; ++t) issue(kst0 + t, t);
         }
-        prev_stores = epilogue(cm0, cn0);
+        prev_stores = epilogue(cm0, cn0, cout);
         if (!more) break;
     }
+}
+
+// Split-K reduction: out[m][n] = sum over s = 0..S-1, in that order, of
+// part[s][m][n] (slices pstride apart, rows ldp apart, ldp % 4 == 0), with
+// the non-finite count of the sums.
+__global__ __launch_bounds__(256) void b1_splitk_reduce_kernel(const float *__restrict__ part, int64_t ldp,
+                                                               int64_t pstride, int S, int M, int N,
+                                                               float *__restrict__ out, int64_t ldo,
+                                                               int32_t *nonfinite, int vec) {
+    const int q = (N + 3) / 4; // 4-column units per row
+    const int64_t units = (int64_t)M * q;
+    int bad = 0;
+    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+        const int m = (int)(u / q), c = (int)(u - (int64_t)m * q) * 4;
+        const float *src = part + (size_t)m * ldp + c;
+        floatx4 sum = *reinterpret_cast<const floatx4 *>(src);
+        for (int sp = 1; sp < S; ++sp) {
+            const floatx4 v = *reinterpret_cast<const floatx4 *>(src + (size_t)sp * pstride);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sum[r] += v[r];
+        }
+        float *dst = out + (size_t)m * ldo + c;
+        if (vec && c + 4 <= N) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bad += nonfinite && !__builtin_isfinite(sum[r]);
+            *reinterpret_cast<floatx4 *>(dst) = sum;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (c + r < N) {
+                    bad += nonfinite && !__builtin_isfinite(sum[r]);
+                    dst[r] = sum[r];
+                }
+        }
+    }
+    count_nonfinite(nonfinite, bad);
 }
 
 // ----------------------------------------------------------------- gemv --
@@ -1576,10 +1595,41 @@ hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed
     return hipGetLastError();
 }
 
+// Split-K: how many K ranges to split a plain GEMM into, 1 for none.  A
+// split pays only when the 128 x 512 tiles leave most CUs idle (fewer than
+// half busy): it multiplies the work units by S, then a separate pass sums
+// S fp32 partial products.  Model, in microseconds: a 384-K unit of a tile
+// takes ~10.9; the partials cost their write and read at ~5 TB/s plus ~3
+// for the extra launch.  S divides K / 384, at most 16.
+int gemm_splits(int M, int K, int N, int num_cus) {
+    if (num_cus <= 0 || !gemm_packed_ok(M, K, N) || N % 4) return 1;
+    const int tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+    const int slots = num_cus * kWgPerCu;
+    if (2 * tiles > slots) return 1;
+    const int units = K / (KCfg::KC * kStages);
+    int best = 1;
+    double best_us = 0;
+    for (int sp = 1; sp <= 16 && sp <= units; ++sp) {
+        if (units % sp) continue;
+        const double rounds = (double)((tiles * sp + slots - 1) / slots);
+        double us = rounds * (units / sp) * 10.9;
+        if (sp > 1) us += 2.0 * sp * (double)M * N * 4 / 5e6 + 3.0;
+        if (sp == 1 || us < best_us) {
+            best = sp;
+            best_us = us;
+        }
+    }
+    return best;
+}
+
+size_t gemm_split_bytes(int M, int N, int splits) {
+    return splits > 1 ? (size_t)splits * (size_t)M * (size_t)((N + 3) & ~3) * sizeof(float) : 0;
+}
+
 template <int EPI>
 static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
                                        int64_t ldo, int32_t *nonfinite, int num_cus, const GemmEpi &epi,
-                                       hipStream_t s) {
+                                       hipStream_t s, int ksplit = 1, float *partials = nullptr) {
     auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages, EPI>;
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
@@ -1589,21 +1639,45 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
     });
     if (attr_err != hipSuccess) return attr_err;
     const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-    const int ntiles = tiles_m * tiles_n;
-    const int slots = num_cus > 0 ? num_cus * kWgPerCu : ntiles;
-    const int grid = ntiles < slots ? ntiles : slots; // persistent
+    const bool split = EPI == 0 && ksplit > 1 && partials != nullptr;
+    const int units = tiles_m * tiles_n * (split ? ksplit : 1);
+    const int slots = num_cus > 0 ? num_cus * kWgPerCu : units;
+    const int grid = units < slots ? units : slots; // persistent
     auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (split) {
+        // the units' plain products into the partial slices, then their sum
+        const int64_t ldp = (N + 3) & ~3;
+        const int64_t pstride = (int64_t)M * ldp;
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed),
+                           w, K, N, M, partials, ldp, nullptr, tiles_m, tiles_n,
+                           (int)(al16(partials) && ldp < (int64_t(1) << 22)), epi, ksplit, pstride);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t q = (int64_t)M * ((N + 3) / 4);
+        const int64_t want = (q + 255) / 256, cap = (int64_t)(num_cus > 0 ? num_cus : 256) * 8;
+        const int rgrid = (int)(want < cap ? want : cap);
+        hipLaunchKernelGGL(b1_splitk_reduce_kernel, dim3(rgrid), dim3(256), 0, s, partials, ldp, pstride, ksplit, M,
+                           N, out, ldo, nonfinite, (int)(al16(out) && ldo % 4 == 0));
+        return hipGetLastError();
+    }
     int vec_store = al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 22);
     if (EPI == 1)
         vec_store = vec_store && al16(epi.res) && al16(epi.gate) && epi.ldr % 4 == 0 && epi.ldr < (int64_t(1) << 22);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
-                       K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store, epi);
+                       K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store, epi, 1, (int64_t)0);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
                               int32_t *nonfinite, int num_cus, hipStream_t s) {
     return launch_gemm_packed_t<0>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, GemmEpi{}, s);
+}
+
+hipError_t launch_gemm_packed_split(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
+                                    int64_t ldo, int32_t *nonfinite, int num_cus, int splits, void *partials,
+                                    hipStream_t s) {
+    return launch_gemm_packed_t<0>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, GemmEpi{}, s, splits,
+                                   static_cast<float *>(partials));
 }
 
 hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
@@ -1630,7 +1704,20 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
     }
     hipError_t e = launch_pack(a.act, a.lda, a.M, a.K, workspace, a.K, s);
     if (e != hipSuccess) return e;
+    // the split-K partials after the packing, when the workspace holds them
+    const int splits = gemm_splits(a.M, a.K, a.N, num_cus);
+    const size_t pack_area = (need + 255) & ~(size_t)255;
+    if (splits > 1 && ws_bytes >= pack_area + gemm_split_bytes(a.M, a.N, splits))
+        return launch_gemm_packed_split(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, splits,
+                                        static_cast<uint8_t *>(workspace) + pack_area, s);
     return launch_gemm_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, s);
+}
+
+size_t gemm_workspace_bytes_total(const LinearArgs &a, int num_cus) {
+    const size_t pack = gemm_workspace_bytes(a);
+    if (pack == 0) return 0;
+    const int splits = gemm_splits(a.M, a.K, a.N, num_cus);
+    return splits > 1 ? ((pack + 255) & ~(size_t)255) + gemm_split_bytes(a.M, a.N, splits) : pack;
 }
 
 hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *packed, int order, hipStream_t s) {

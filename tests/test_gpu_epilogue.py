@@ -47,6 +47,14 @@ def b1(torch):
     return bonsai_b1
 
 
+def plain_linear(torch, b1, a, w, n, mode):
+    """The linear without an epilogue, as the fused-epilogue GEMM computes
+    it: a workspace that holds the packing only keeps the GEMM unsplit along
+    K (a split sums the K ranges in another order)."""
+    ws = torch.empty(a.shape[0] * a.shape[1] * 2 + 16, dtype=torch.uint8, device="cuda")
+    return b1.linear(a, w, n, mode=mode, workspace=ws)
+
+
 CASES = [  # (m, k, n, mode): fused packed GEMM, ragged, GEMV pass, EXACT pass, conversion-GEMM pass
     (256, 768, 1024, "auto"),
     (200, 768, 640, "auto"),
@@ -65,7 +73,7 @@ def test_gate_residual_bit_exact(torch, b1, m, k, n, mode):
     w = synth.device_packed_weights(n, k, 62)
     gate = torch.randn(n, device="cuda")
     res = torch.randn((m, n + 8), device="cuda")[:, :n]
-    y = b1.linear(a, w, n, mode=mode)
+    y = plain_linear(torch, b1, a, w, n, mode)
     out = b1.linear_epi(a, w, n, "gate_residual", gate=gate, residual=res, mode=mode)
     torch.cuda.synchronize()
     want = res.cpu().numpy() + gate.cpu().numpy()[None, :] * y.cpu().numpy()   # float32 ops
@@ -94,7 +102,7 @@ def test_swiglu_matches_float64(torch, b1, oracle, m, k, n, mode):
     say(f"swiglu ({m},{k},{n}) {mode}")
     a = synth.device_activations(m, k, 63)
     w = synth.device_packed_weights(n, k, 64)
-    y = b1.linear(a, w, n, mode=mode)
+    y = plain_linear(torch, b1, a, w, n, mode)
     out = torch.full((m, h + 4), 7.0, device="cuda")
     b1.linear_epi(a, w, n, "swiglu", out=out[:, :h], mode=mode)
     torch.cuda.synchronize()
@@ -181,7 +189,7 @@ def test_norm_mod_matches_oracle(torch, b1, oracle, rows, h):
         from bonsai_b1 import synth
         n = 512
         w = synth.device_packed_weights(n, h, 82)
-        a = b1.linear(y, w, n, mode="gemm")
+        a = plain_linear(torch, b1, y, w, n, "gemm")
         c = b1.linear_packed_f16(packed, w, h, n, rows)
         torch.cuda.synchronize()
         assert torch.equal(a, c)

@@ -374,14 +374,23 @@ def test_pack_act_layout_bit_exact(torch, b1, oracle):
     assert np.array_equal(got, want)
 
 
+def unsplit_linear(torch, b1, a, w, n, mode):
+    """The fp32 entry with a workspace that holds the packing only, so the
+    GEMM runs unsplit along K (the packed entry, which takes no workspace,
+    never splits)."""
+    ws = torch.empty(a.shape[0] * a.shape[1] * 2 + 16, dtype=torch.uint8, device="cuda")
+    return b1.linear(a, w, n, mode=mode, workspace=ws)
+
+
 @pytest.mark.parametrize("m,k,n", [(200, 768, 600), (128, 384, 512), (1, 384, 40)])
 def test_linear_packed_matches_fused_entry(torch, b1, m, k, n):
     """pack + linear_packed gives bit-for-bit what bonsai_b1_linear_f32 gives
-    in GEMM mode (same kernels), including a padded output stride."""
+    in GEMM mode unsplit along K (same kernels), including a padded output
+    stride."""
     from bonsai_b1 import synth
     a = synth.device_activations(m, k, 41)
     w = synth.device_packed_weights(n, k, 42)
-    ref = b1.linear(a, w, n, mode="gemm")
+    ref = unsplit_linear(torch, b1, a, w, n, "gemm")
     out = torch.full((m, n + 12), 7.0, device="cuda")
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     packed = b1.pack_act_f16(a)
@@ -404,7 +413,7 @@ def test_linear_packed_small_m(torch, b1, m, k, n, mode):
     say(f"packed small-M ({m},{k},{n}) vs {mode}")
     a = synth.device_activations(m, k, 43)
     w = synth.device_packed_weights(n, k, 44)
-    ref = b1.linear(a, w, n, mode=mode)
+    ref = unsplit_linear(torch, b1, a, w, n, mode)
     out = torch.full((m, n + 12), 7.0, device="cuda")
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     packed = b1.pack_act_f16(a)
@@ -621,3 +630,64 @@ def test_linear_batch_fuses_concatenated_qkv(torch, b1):
     torch.cuda.synchronize()
     assert torch.equal(xx[:, :n], y0) and torch.equal(xx[:, n:2 * n], y1) and torch.equal(xx[:, 2 * n:], y2)
     assert lib.bonsai_b1_weights_free(ctypes.byref(cat)) == capi.OK
+
+
+# ---------------------------------------------------------------- split-K --
+
+SPLIT_CASES = [  # (m, k, n): shapes whose 128 x 512 tiles leave most CUs idle
+    (256, 3072, 3072),    # C1: 12 tiles
+    (512, 9216, 3072),    # Klein text stream FF-out: 24 tiles, long K
+    (512, 3072, 9216),    # Klein text stream q/k/v
+    (37, 15360, 384),     # one tile
+    (200, 768, 600),
+    (1000, 1152, 2100),
+]
+
+
+@pytest.mark.parametrize("m,k,n", SPLIT_CASES)
+def test_split_k(torch, b1, m, k, n):
+    """GEMMs split along K (work units of a tile and a K range, fp32 partial
+    products summed in a fixed order by a second kernel): against the same
+    GEMM unsplit, the difference is the summation order alone (<= 1e-5 of
+    the output rms); against EXACT, the FAST bar; two runs are bit for bit
+    the same; a padded, non-multiple-of-4 output stride is written only in
+    its columns."""
+    from bonsai_b1 import synth
+    say(f"split-K ({m},{k},{n})")
+    a = synth.device_activations(m, k, 45)
+    w = synth.device_packed_weights(n, k, 46)
+    y = b1.linear(a, w, n, mode="gemm")
+    y2 = b1.linear(a, w, n, mode="gemm")
+    yu = unsplit_linear(torch, b1, a, w, n, "gemm")
+    ye = b1.linear(a, w, n, mode="exact")
+    out = torch.full((m, n + 3), 7.0, device="cuda")
+    b1.linear(a, w, n, out=out[:, :n], mode="gemm")
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2), "split-K is deterministic"
+    rms = float(yu.pow(2).mean().sqrt())
+    d = float((y - yu).abs().max())
+    say(f"  split vs unsplit max |diff| {d:.3e} (rms {rms:.3e}); identical: {bool(torch.equal(y, yu))}")
+    assert d <= 1e-5 * rms
+    assert_fast_close(y.cpu().numpy(), ye.cpu().numpy(), f"split-K {(m, k, n)} vs exact")
+    assert torch.equal(out[:, :n], y)
+    assert bool((out[:, n:] == 7.0).all()), "columns past out_dim untouched"
+
+
+def test_split_k_counts_nonfinite(torch, b1):
+    """The non-finite count comes from the summed outputs (the partials are
+    not counted): an infinite activation makes its row's outputs non-finite
+    in the split GEMM as in the unsplit one."""
+    from bonsai_b1 import synth
+    m, k, n = 256, 3072, 3072
+    a = synth.device_activations(m, k, 47)
+    a[5, 100] = float("inf")
+    w = synth.device_packed_weights(n, k, 48)
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    y = b1.linear(a, w, n, mode="gemm", nonfinite=nf)
+    nfu = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = torch.empty(m * k * 2 + 16, dtype=torch.uint8, device="cuda")
+    yu = b1.linear(a, w, n, mode="gemm", nonfinite=nfu, workspace=ws)
+    torch.cuda.synchronize()
+    bad = int((~torch.isfinite(y)).sum())
+    say(f"  non-finite outputs {bad}, counted {int(nf.item())} split / {int(nfu.item())} unsplit")
+    assert bad == n and int(nf.item()) == bad and int(nfu.item()) == int((~torch.isfinite(yu)).sum())

@@ -56,7 +56,10 @@ def test_strided_producers_build_concatenated_input(torch, b1, m, k1, k2):
         # the GEMM over the built input equals the linear over the fp32 concatenation
         w = synth.device_packed_weights(384, k, 73)
         y = b1.linear_packed_f16(buf, w, k, 384, m)
-        yr = b1.linear(torch.cat([a1, b1.gelu_tanh(a2.contiguous())], 1), w, 384)
+        cat = torch.cat([a1, b1.gelu_tanh(a2.contiguous())], 1)
+        # the fp32 entry unsplit along K, as the packed entry (no workspace) runs
+        ws = torch.empty(m * k * 2 + 16, dtype=torch.uint8, device="cuda")
+        yr = b1.linear(cat, w, 384, workspace=ws)
         torch.cuda.synchronize()
         assert torch.equal(y, yr)
 
