@@ -691,3 +691,45 @@ def test_split_k_counts_nonfinite(torch, b1):
     bad = int((~torch.isfinite(y)).sum())
     say(f"  non-finite outputs {bad}, counted {int(nf.item())} split / {int(nfu.item())} unsplit")
     assert bad == n and int(nf.item()) == bad and int(nfu.item()) == int((~torch.isfinite(yu)).sum())
+
+
+@pytest.mark.parametrize("m,k,n,splits", [(256, 3072, 3072, 8), (200, 768, 600, 2)])
+def test_split_k_equals_per_range_composition(torch, b1, m, k, n, splits):
+    """Bit for bit, on every one of several launches: the split GEMM equals
+    the sum, in range order, of unsplit GEMMs over the K ranges (sliced
+    activations and weights).  Regression test for an epilogue that
+    rearranged accumulators across lanes before storing and intermittently
+    stored stale values of one accumulator register in four lanes."""
+    from bonsai_b1 import synth
+    a = synth.device_activations(m, k, 45)
+    w = synth.device_packed_weights(n, k, 46)
+    wr = w.view(n, k // 32, 6)
+    kr = k // splits
+    ref = None
+    for s in range(splits):
+        ws_ = wr[:, s * kr // 32:(s + 1) * kr // 32, :].contiguous().view(-1)
+        part = unsplit_linear(torch, b1, a[:, s * kr:(s + 1) * kr].contiguous(), ws_, n, "gemm")
+        ref = part if ref is None else ref + part
+    for run in range(6):
+        y = b1.linear(a, w, n, mode="gemm")
+        torch.cuda.synchronize()
+        nbad = int((y != ref).sum())
+        say(f"  run {run}: {nbad} elements differ")
+        assert nbad == 0
+
+
+@pytest.mark.parametrize("m,k,n", [(200, 384, 600), (256, 768, 1024)])
+def test_one_tile_per_work_group_repeats(torch, b1, m, k, n):
+    """Unsplit GEMMs with one output tile per work-group (the epilogue right
+    after the last MFMAs, nothing in between): every launch gives the same
+    bits and stays within the FAST bar of EXACT."""
+    from bonsai_b1 import synth
+    a = synth.device_activations(m, k, 49)
+    w = synth.device_packed_weights(n, k, 50)
+    ye = b1.linear(a, w, n, mode="exact")
+    first = unsplit_linear(torch, b1, a, w, n, "gemm")
+    for run in range(8):
+        y = unsplit_linear(torch, b1, a, w, n, "gemm")
+        torch.cuda.synchronize()
+        assert torch.equal(y, first), f"launch {run}"
+    assert_fast_close(first.cpu().numpy(), ye.cpu().numpy(), f"one tile per WG {(m, k, n)}")
