@@ -118,7 +118,8 @@ def bench_mlp(torch, b1, synth):
     """Flux MLP at 1024x1024 (4608 tokens): up-projection 3072 -> 12288,
     GELU-tanh, down-projection 12288 -> 3072; each part and the chain, plus
     the chain with GELU fused into the fp16 packing of the down-projection's
-    input."""
+    input, and with GELU in the up-projection's epilogue writing that
+    packing directly."""
     m, k, h = 4608, 3072, 12288
     a = synth.device_activations(m, k, 11)
     wu = synth.device_packed_weights(h, k, 12)
@@ -148,9 +149,20 @@ def bench_mlp(torch, b1, synth):
          for name, f in (("up", up), ("gelu", gelu), ("down", down))}
     r["chain"] = graph_ms(torch, lambda: (up(), gelu(), down()))
     r["chain_fused_gelu"] = graph_ms(torch, fused)
+    pa = torch.empty(m * k * 2, dtype=torch.uint8, device="cuda")
+
+    def epilogue():
+        # GELU in the up-projection's epilogue, written as the packed input
+        # of the down-projection
+        b1.pack_act_f16(a, packed=pa)
+        b1.linear_packed_f16_to_packed(pa, wu, k, h, m, 0, "gelu_tanh", packed_out=packed)
+        b1.linear_packed_f16(packed, wd, h, k, m, out=y2)
+
+    r["chain_epilogue_gelu"] = graph_ms(torch, epilogue)
     flop = 2.0 * m * k * h * 2
     r["chain_tflops"] = flop / (r["chain"] * 1e-3) / 1e12
     r["chain_fused_tflops"] = flop / (r["chain_fused_gelu"] * 1e-3) / 1e12
+    r["chain_epilogue_tflops"] = flop / (r["chain_epilogue_gelu"] * 1e-3) / 1e12
     r["gelu_GBps"] = m * h * 8 / (r["gelu"] * 1e-3) / 1e9
     return r
 
@@ -160,7 +172,8 @@ def bench_ff_epilogues(torch, b1, synth):
     (src/diffuser_graph.cpp:450-460, 4096 image tokens): FF-in 3072 ->
     2 x 9216, SwiGLU, FF-out 9216 -> 3072, gate-residual add into h.  Once
     with the element-wise steps as separate torch passes over the linears'
-    fp32 outputs, once with both fused into the GEMM epilogues."""
+    fp32 outputs, once with both fused into the GEMM epilogues, and once
+    with FF-in's SwiGLU epilogue writing FF-out's packed fp16 input."""
     m, d, hid = 4096, 3072, 9216
     x = synth.device_activations(m, d, 21)
     w_in = synth.device_packed_weights(2 * hid, d, 22)
@@ -183,9 +196,20 @@ def bench_ff_epilogues(torch, b1, synth):
         b1.linear_epi(x, w_in, 2 * hid, "swiglu", out=act, workspace=ws)
         b1.linear_epi(act, w_out, d, "gate_residual", gate=gate, residual=h, out=h, workspace=ws)
 
-    r = {"separate": graph_ms(torch, separate), "fused": graph_ms(torch, fused)}
+    px = torch.empty(m * d * 2, dtype=torch.uint8, device="cuda")
+    pk = torch.empty(m * hid * 2, dtype=torch.uint8, device="cuda")
+
+    def packed_out():
+        # SwiGLU in FF-in's epilogue written as FF-out's packed input
+        b1.pack_act_f16(x, packed=px)
+        b1.linear_packed_f16_to_packed(px, w_in, d, 2 * hid, m, 0, "swiglu", packed_out=pk)
+        b1.linear_packed_f16_epi(pk, w_out, hid, d, m, "gate_residual", gate=gate, residual=h, out=h)
+
+    r = {"separate": graph_ms(torch, separate), "fused": graph_ms(torch, fused),
+         "fused_packed_out": graph_ms(torch, packed_out)}
     flop = 2.0 * m * d * (2 * hid) + 2.0 * m * hid * d
     r["fused_tflops"] = flop / (r["fused"] * 1e-3) / 1e12
+    r["fused_packed_out_tflops"] = flop / (r["fused_packed_out"] * 1e-3) / 1e12
     return r
 
 
@@ -259,7 +283,8 @@ def bench_c5_block_chain(torch, b1, synth, blocks=38):
     standing in for the attention output, columns 0-3071; GELU-tanh of the
     MLP part, columns 3072-15359), and linear2 15360 -> 3072 with the
     gate-residual epilogue updating the residual stream in place.  Block
-    i + 1 reads what block i wrote."""
+    i + 1 reads what block i wrote.  Timed again with GELU(MLP) written by
+    linear1's epilogue into linear2's packed input (4 kernels per block)."""
     m, h, n1, k2 = 4608, 3072, 21504, 15360
     w1 = [synth.device_packed_weights(n1, h, 500 + i) for i in range(blocks)]
     w2 = [synth.device_packed_weights(h, k2, 600 + i) for i in range(blocks)]
@@ -280,12 +305,25 @@ def bench_c5_block_chain(torch, b1, synth, blocks=38):
             b1.gelu_tanh_pack_f16(y1[:, 3 * h:], packed=p2[h * 2:], ldp=k2)
             b1.linear_packed_f16_epi(p2, w2[i], k2, h, m, "gate_residual", gate=gate[i], residual=x, out=x)
 
+    def step_epilogue():
+        # linear1's epilogue: q/k/v as fp32, GELU(MLP) straight into
+        # columns 3072-15359 of linear2's packed input
+        for i in range(blocks):
+            b1.norm_mod(x, scale[i], shift[i], packed=p1)
+            b1.linear_packed_f16_to_packed(p1, w1[i], h, n1, m, 3 * h, "gelu_tanh", out=y1[:, :3 * h],
+                                           packed_out=p2[h * 2:], ldp=k2)
+            b1.pack_act_f16(y1[:, :h], packed=p2, ldp=k2)
+            b1.linear_packed_f16_epi(p2, w2[i], k2, h, m, "gate_residual", gate=gate[i], residual=x, out=x)
+
     ms = graph_ms(torch, step, reps=2)
-    flop = 2.0 * m * (h * n1 + k2 * h) * blocks
     finite = bool(torch.isfinite(x).all())
+    ms_epi = graph_ms(torch, step_epilogue, reps=2)
+    finite = finite and bool(torch.isfinite(x).all())
+    flop = 2.0 * m * (h * n1 + k2 * h) * blocks
     del w1, w2
     return {"blocks": blocks, "ms_per_step": ms, "gemm_tflops": flop / (ms * 1e-3) / 1e12,
-            "kernels_per_block": 5, "residual_finite": finite}
+            "kernels_per_block": 5, "ms_per_step_epilogue": ms_epi,
+            "gemm_tflops_epilogue": flop / (ms_epi * 1e-3) / 1e12, "residual_finite": finite}
 
 
 def bench_klein_step(torch, b1, synth):
@@ -611,12 +649,15 @@ def main():
         extra["c4_mlp"] = {x: round(v, 4) for x, v in mlp.items()}
         log(f"[bench] c4 MLP: up {mlp['up']*1e3:.1f} us, GELU {mlp['gelu']*1e3:.1f} us "
             f"({mlp['gelu_GBps']:.0f} GB/s), down {mlp['down']*1e3:.1f} us; chain {mlp['chain']*1e3:.1f} us "
-            f"({mlp['chain_tflops']:.0f} TFLOP/s), GELU fused into the pack {mlp['chain_fused_gelu']*1e3:.1f} us")
+            f"({mlp['chain_tflops']:.0f} TFLOP/s), GELU fused into the pack {mlp['chain_fused_gelu']*1e3:.1f} us, "
+            f"GELU in the up-projection's epilogue {mlp['chain_epilogue_gelu']*1e3:.1f} us "
+            f"({mlp['chain_epilogue_tflops']:.0f} TFLOP/s)")
         ff = bench_ff_epilogues(torch, b1, synth)
         extra["ff_epilogues"] = {x: round(v, 4) for x, v in ff.items()}
         log(f"[bench] double-block FF (4096 x 3072 -> 2x9216, SwiGLU, -> 3072, gate-residual): separate "
             f"passes {ff['separate']*1e3:.1f} us, fused epilogues {ff['fused']*1e3:.1f} us "
-            f"({ff['fused_tflops']:.0f} TFLOP/s)")
+            f"({ff['fused_tflops']:.0f} TFLOP/s); SwiGLU epilogue writing FF-out's packed input "
+            f"{ff['fused_packed_out']*1e3:.1f} us ({ff['fused_packed_out_tflops']:.0f} TFLOP/s)")
         nm = bench_norm_mod(torch, b1, synth)
         extra["norm_mod"] = {x: round(v, 4) for x, v in nm.items()}
         log(f"[bench] LayerNorm+modulation 4096x3072 -> packed fp16: {nm['fused_pack']*1e3:.1f} us "
@@ -632,7 +673,8 @@ def main():
         extra["c5_block_chain"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in ch.items()}
         log(f"[bench] c5 block chain (38 single-stream blocks, attention aside: norm+mod -> packed, linear1, "
             f"packed [q | GELU(MLP)], linear2 + gate-residual): {ch['ms_per_step']:.2f} ms "
-            f"({ch['gemm_tflops']:.0f} TFLOP/s of GEMM work)")
+            f"({ch['gemm_tflops']:.0f} TFLOP/s of GEMM work); GELU(MLP) from linear1's epilogue "
+            f"{ch['ms_per_step_epilogue']:.2f} ms ({ch['gemm_tflops_epilogue']:.0f} TFLOP/s)")
         torch.cuda.empty_cache()
         wl = bench_weights_load(torch, b1)
         extra["weights_load"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in wl.items()}

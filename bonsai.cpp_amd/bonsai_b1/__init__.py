@@ -19,6 +19,8 @@ from .capi import (  # noqa: F401
     linear_epi_workspace_bytes,
     norm_mod,
     linear_packed_f16_epi,
+    linear_packed_f16_to_packed,
+    ACTS,
     EPILOGUES,
     gelu_tanh,
     gelu_tanh_pack_f16,

@@ -37,6 +37,7 @@ class B1WeightsC(ctypes.Structure):
 
 
 EPILOGUES = {"none": 0, "gate_residual": 1, "swiglu": 2}
+ACTS = {"none": 0, "gelu_tanh": 1, "swiglu": 2}
 
 
 class Epilogue(ctypes.Structure):
@@ -118,6 +119,8 @@ def load():
     L.bonsai_b1_linear_packed_f16.restype = i
     L.bonsai_b1_linear_packed_f16_epi.argtypes = [vp, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), vp, vp]
     L.bonsai_b1_linear_packed_f16_epi.restype = i
+    L.bonsai_b1_linear_packed_f16_to_packed.argtypes = [vp, vp, i, i, i, vp, i64, i, i, vp, i64, vp, vp]
+    L.bonsai_b1_linear_packed_f16_to_packed.restype = i
     L.bonsai_b1_linear_epi_workspace_bytes.argtypes = [i, i, i, i, i]
     L.bonsai_b1_linear_epi_workspace_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_linear_epi_f32.argtypes = [vp, i64, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), i, vp, vp,
@@ -448,6 +451,39 @@ def linear_packed_f16_epi(packed, w_packed, in_dim: int, out_dim: int, batch: in
     if st != OK:
         raise B1Error(st, "bonsai_b1_linear_packed_f16_epi")
     return out
+
+
+def linear_packed_f16_to_packed(packed, w_packed, in_dim: int, out_dim: int, batch: int, split: int,
+                                act: str = "none", out=None, packed_out=None, ldp=None, nonfinite=None,
+                                stream=None):
+    """bonsai_b1_linear_packed_f16_to_packed: y columns [0, split) as fp32
+    into out [batch, >=split]; columns [split, out_dim) through `act`
+    ("none", "gelu_tanh", or "swiglu" over [gate | value]) into packed fp16
+    activations: a new [batch, cols] packing when packed_out is None,
+    otherwise packed_out (contiguous; with ldp, a view starting at the
+    target column range of rows of ldp fp16 elements).  Returns (out,
+    packed_out); out is None when split == 0."""
+    import torch
+    cols = (out_dim - split) // 2 if act == "swiglu" else out_dim - split
+    if out is None and split > 0:
+        out = torch.empty((batch, split), dtype=torch.float32, device=packed.device)
+    if out is not None and (out.dim() != 2 or out.shape[0] != batch or out.shape[1] < split or out.stride(1) != 1):
+        raise ValueError("out must be [batch, >=split] fp32 with unit column stride")
+    if ldp is None:
+        ldp = cols
+        if packed_out is None and cols > 0:
+            packed_out = torch.empty(max(batch * cols * 2, 16), dtype=torch.uint8, device=packed.device)
+    if cols > 0 and (packed_out is None or not packed_out.is_contiguous()
+                     or packed_out.numel() * packed_out.element_size() < ((batch - 1) * ldp + cols) * 2):
+        raise ValueError("packed_out must be a contiguous view holding (batch-1)*ldp + cols fp16 elements")
+    nf = nonfinite.data_ptr() if nonfinite is not None else None
+    st = load().bonsai_b1_linear_packed_f16_to_packed(
+        packed.data_ptr(), w_packed.data_ptr(), in_dim, out_dim, batch,
+        out.data_ptr() if out is not None else None, out.stride(0) if out is not None else 0, split, ACTS[act],
+        packed_out.data_ptr() if packed_out is not None else None, ldp, nf, _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_linear_packed_f16_to_packed")
+    return out, packed_out
 
 
 def norm_mod(x, scale, shift, eps: float = 1e-6, out=None, packed=None, stream=None):

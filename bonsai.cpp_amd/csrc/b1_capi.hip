@@ -421,6 +421,57 @@ int bonsai_b1_linear_packed_f16_epi(const void *packed_act, const void *w, int i
                : BONSAI_B1_ERR_HIP;
 }
 
+int bonsai_b1_linear_packed_f16_to_packed(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
+                                          float *out, int64_t ldo, int split, int act, void *packed_out,
+                                          int64_t ldp, int32_t *nonfinite, hipStream_t stream) {
+    if (in_dim <= 0 || out_dim <= 0 || batch < 0) return BONSAI_B1_ERR_ARG;
+    if (split < 0 || split > out_dim || split % BONSAI_B1_BLOCK_SIZE || out_dim % BONSAI_B1_BLOCK_SIZE)
+        return BONSAI_B1_ERR_ARG;
+    if (act != BONSAI_B1_ACT_NONE && act != BONSAI_B1_ACT_GELU_TANH && act != BONSAI_B1_ACT_SWIGLU)
+        return BONSAI_B1_ERR_ARG;
+    const bool glu = act == BONSAI_B1_ACT_SWIGLU;
+    if (glu && (split % 64 || (out_dim - split) % 64)) return BONSAI_B1_ERR_ARG;
+    // packed columns written: SwiGLU halves its [gate | value] columns
+    const int pcols = glu ? (out_dim - split) / 2 : out_dim - split;
+    auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!al16(packed_act) || (reinterpret_cast<uintptr_t>(w) & 3u)) return BONSAI_B1_ERR_ARG;
+    if (split > 0 && (!al16(out) || ldo < split || ldo % 4)) return BONSAI_B1_ERR_ARG;
+    if (pcols > 0 && (!al16(packed_out) || ldp < pcols || ldp % 8)) return BONSAI_B1_ERR_ARG;
+    if (!b1::gemm_packed_ok(batch > 0 ? batch : 1, in_dim, out_dim)) return BONSAI_B1_ERR_ARG;
+    if (batch > 0) {
+        if (!packed_act || !w || (split > 0 && !out) || (pcols > 0 && !packed_out)) return BONSAI_B1_ERR_ARG;
+        // the outputs lie apart from the activations the GEMM still reads
+        // and from each other
+        auto span = [](const void *p, int rows, int64_t ld_bytes, int64_t row_bytes) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+            return std::pair<uintptr_t, uintptr_t>(a, a + (size_t)(rows - 1) * (size_t)ld_bytes + (size_t)row_bytes);
+        };
+        auto overlap = [](std::pair<uintptr_t, uintptr_t> x, std::pair<uintptr_t, uintptr_t> y) {
+            return x.first < y.second && y.first < x.second;
+        };
+        const auto in = span(packed_act, batch, (int64_t)in_dim * 2, (int64_t)in_dim * 2);
+        if (split > 0 && overlap(in, span(out, batch, ldo * 4, (int64_t)split * 4))) return BONSAI_B1_ERR_ARG;
+        if (pcols > 0) {
+            const auto po = span(packed_out, batch, ldp * 2, (int64_t)pcols * 2);
+            if (overlap(in, po)) return BONSAI_B1_ERR_ARG;
+            if (split > 0 && overlap(po, span(out, batch, ldo * 4, (int64_t)split * 4))) return BONSAI_B1_ERR_ARG;
+        }
+    }
+    DeviceInfo *dev = current_device(nullptr);
+    if (!dev) return BONSAI_B1_ERR_DEVICE;
+    if (batch == 0) return BONSAI_B1_OK;
+    b1::GemmEpi g;
+    g.pk = static_cast<uint32_t *>(packed_out);
+    g.ldpw = ldp / 2;
+    g.split = split;
+    g.act = act;
+    g.glu_h = glu ? pcols : 0;
+    return b1::launch_gemm_packed_epi(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
+                                      nonfinite, dev->num_cus, 3, g, stream) == hipSuccess
+               ? BONSAI_B1_OK
+               : BONSAI_B1_ERR_HIP;
+}
+
 // Whether a linear runs the packed FAST GEMM (as linear_impl decides).
 static bool packed_path(const b1::LinearArgs &a, int mode) {
     if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return false;

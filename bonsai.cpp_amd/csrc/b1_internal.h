@@ -11,12 +11,18 @@ namespace b1 {
 
 // What the packed GEMM's epilogue writes besides the plain product y
 // (kind 1: out = res + gate[n] * y; kind 2: SwiGLU over 2 glu_h weight
-// rows, out[m][j] = silu(y[m][j]) * y[m][glu_h + j]).
+// rows, out[m][j] = silu(y[m][j]) * y[m][glu_h + j]; kind 3: columns
+// [0, split) of y to out as fp32, columns split + j as act(y) into packed
+// fp16 activations, column j of pk's rows of ldpw dwords, act 1 = GELU-tanh).
 struct GemmEpi {
     const float *gate = nullptr; // [N]
     const float *res = nullptr;  // [M][ldr]
     int64_t ldr = 0;
     int glu_h = 0;
+    uint32_t *pk = nullptr; // kind 3: packed fp16 pairs, 16-byte aligned
+    int64_t ldpw = 0;       // its row stride in dwords (a multiple of 4)
+    int split = 0;          // a multiple of 32
+    int act = 0;            // 0 none, 1 GELU-tanh
 };
 
 struct LinearArgs {
@@ -69,7 +75,9 @@ hipError_t launch_gemm_packed_split(const void *packed, const uint8_t *w, int K,
                                     int64_t ldo, int32_t *nonfinite, int num_cus, int splits, void *partials,
                                     hipStream_t s);
 // The same GEMM with a fused epilogue (kind 0 plain, 1 gate-residual,
-// 2 SwiGLU with N = 2 glu_h, glu_h % 32 == 0, out [M][ldo >= glu_h]).
+// 2 SwiGLU with N = 2 glu_h, glu_h % 32 == 0, out [M][ldo >= glu_h],
+// 3 fp32 / packed fp16 columns with N % 32 == 0; with split > 0, out 16-byte
+// aligned and ldo % 4 == 0).
 hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
                                   int64_t ldo, int32_t *nonfinite, int num_cus, int kind, const GemmEpi &epi,
                                   hipStream_t s);

@@ -365,16 +365,24 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_fused_kern
 
 // ------------------------------------------------------------- GELU-tanh --
 //
-// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), elementwise in fp32 with
-// the device library's tanhf.  The plain form writes fp32; the fused form
-// writes the fp16 K-slot-paired activations that the packed GEMM reads, so
-// a GELU between two B1_0 linears costs one read and one half-size write.
-
+// 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), elementwise in
+// fp32.  The plain form writes fp32; the fused forms write the fp16
+// K-slot-paired activations that the packed GEMM reads, so a GELU between
+// two B1_0 linears costs one read and one half-size write (or, in the
+// GEMM's epilogue, nothing beyond the GEMM's own half-size output).
+//
+// Evaluated as x / (1 + e^(-2u)), the same function (1 + tanh(u) =
+// 2 / (1 + e^(-2u))), with e^(-2u) = 2^(x (c1 + c2 x^2)), c1 = -2
+// sqrt(2/pi) / ln 2 and c2 = 0.044715 c1: one hardware exp2 and one
+// reciprocal instead of a library tanh, which matters in the GEMM epilogue
+// where no MFMA work overlaps it.  Within 3e-7 max(1, |x|) of the float64
+// function (1-ulp exp2 and reciprocal included).  Large negative x: the
+// exponential overflows to inf and the result is -0; NaN stays NaN.
 __device__ __forceinline__ float gelu_tanh(float x) {
-    const float k0 = 0.7978845608028654f; // sqrt(2 / pi)
-    const float k1 = 0.044715f;
-    const float u = k0 * (x + k1 * x * x * x);
-    return 0.5f * x * (1.0f + tanhf(u));
+    const float c1 = -2.30220819f;  // -2 sqrt(2/pi) log2(e)
+    const float c2 = -0.102943242f; // 0.044715 c1
+    const float t = x * __builtin_fmaf(c2, x * x, c1);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 __global__ __launch_bounds__(256) void b1_gelu_kernel(const float *__restrict__ x, int64_t ldx,
@@ -809,6 +817,13 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                 const int b = c >> 6, within = c & 63;
                 row = within < 32 ? 32 * b + within : epi.glu_h + 32 * b + (within - 32);
             }
+            if constexpr (EPI == 3) {
+                // the same order over the SwiGLU columns [split, N)
+                if (epi.act == 2 && c >= epi.split) {
+                    const int b = (c - epi.split) >> 6, within = (c - epi.split) & 63;
+                    row = epi.split + (within < 32 ? 32 * b + within : epi.glu_h + 32 * b + (within - 32));
+                }
+            }
             boff[cg] = (uint32_t)row * rs;
         }
     };
@@ -978,6 +993,87 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                                     out[(size_t)m * ldo + n + r] =
                                         gate_residual(epi.res[(size_t)m * epi.ldr + n + r], epi.gate[n + r], yv);
                                 }
+                            }
+                        }
+                    }
+                }
+            }
+            count_nonfinite(nonfinite, bad);
+            return 1; // a store count the tile-start waits do not model
+        }
+        if constexpr (EPI == 3) {
+            // Columns below split: 16-byte fp32 stores.  From split on, the
+            // packed fp16 activations of the next linear: a packed block's
+            // dword d holds columns (d, d + 16) of its 32, and lane (li, g)
+            // holds columns 8q + 4g + r of each 32-column tile, so
+            // registers 4q + r and 4q + 8 + r (q < 2) form dword 8q + 4g +
+            // r and 4 consecutive dwords are one 16-byte store.  split and
+            // N are multiples of 32 (64 for SwiGLU), so a tile (a wave's 64
+            // columns for SwiGLU) is wholly one kind.
+            static_assert(C::NTL == 2, "SwiGLU pairs one gate and one value tile per wave");
+            const int wb = n0 + wave * WN; // wave-uniform
+            if (epi.act == 2 && wb >= epi.split) {
+                // tile 0 holds the gates, tile 1 their values, of the 32
+                // outputs of packed block (wb - split) / 64
+                if (wb < N) {
+                    uint32_t *const pb = epi.pk + ((wb - epi.split) >> 6) * 16 + 4 * g;
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt) {
+                        const int m = m0 + mt * 32 + li;
+                        if (m >= M) continue;
+#pragma unroll
+                        for (int q = 0; q < 2; ++q) {
+                            u32x4 v;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float g0 = acc[mt][0][4 * q + r], v0 = acc[mt][1][4 * q + r];
+                                const float g1 = acc[mt][0][4 * q + 8 + r], v1 = acc[mt][1][4 * q + 8 + r];
+                                if (cnt)
+                                    bad += !__builtin_isfinite(g0) + !__builtin_isfinite(v0) +
+                                           !__builtin_isfinite(g1) + !__builtin_isfinite(v1);
+                                v[r] = pack_f16(mul_f32(silu_f32(g0), v0), mul_f32(silu_f32(g1), v1));
+                            }
+                            *reinterpret_cast<u32x4 *>(pb + (size_t)m * epi.ldpw + 8 * q) = v;
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt) {
+                    const int cb = wb + nt * 32; // wave-uniform
+                    if (cb >= N) continue;
+                    if (cb >= epi.split) {
+                        uint32_t *const pb = epi.pk + ((cb - epi.split) >> 5) * 16 + 4 * g;
+#pragma unroll
+                        for (int mt = 0; mt < C::MT; ++mt) {
+                            const int m = m0 + mt * 32 + li;
+                            if (m >= M) continue;
+#pragma unroll
+                            for (int q = 0; q < 2; ++q) {
+                                u32x4 v;
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) {
+                                    const float y0 = acc[mt][nt][4 * q + r], y1 = acc[mt][nt][4 * q + 8 + r];
+                                    if (cnt) bad += !__builtin_isfinite(y0) + !__builtin_isfinite(y1);
+                                    v[r] = epi.act ? pack_f16(gelu_tanh(y0), gelu_tanh(y1)) : pack_f16(y0, y1);
+                                }
+                                *reinterpret_cast<u32x4 *>(pb + (size_t)m * epi.ldpw + 8 * q) = v;
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int mt = 0; mt < C::MT; ++mt) {
+                            const int m = m0 + mt * 32 + li;
+                            if (m >= M) continue;
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                floatx4 o;
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) {
+                                    o[r] = acc[mt][nt][4 * q + r];
+                                    if (cnt) bad += !__builtin_isfinite(o[r]);
+                                }
+                                *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + cb + 8 * q + 4 * g) = o;
                             }
                         }
                     }
@@ -1687,6 +1783,7 @@ hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, i
     case 0: return launch_gemm_packed_t<0>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
     case 1: return launch_gemm_packed_t<1>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
     case 2: return launch_gemm_packed_t<2>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
+    case 3: return launch_gemm_packed_t<3>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -311,6 +311,43 @@ int bonsai_b1_linear_packed_f16_epi(const void *packed_act, const void *w,
                                     const bonsai_b1_epilogue *epi,
                                     int32_t *nonfinite, hipStream_t stream);
 
+/*
+ * bonsai_b1_linear_packed_f16 whose output feeds the next B1_0 linear
+ * directly: columns [0, split) of y are stored as fp32 in out (row stride
+ * ldo), and columns [split, out_dim) pass through `act` and are stored as
+ * packed fp16 activations in packed_out (row stride ldp fp16 elements, the
+ * layout of bonsai_b1_pack_act_f16_ld):
+ *  - BONSAI_B1_ACT_NONE / _GELU_TANH: column split + j -> packed column j;
+ *  - BONSAI_B1_ACT_SWIGLU: columns [split, out_dim) are [gate | value] of
+ *    H = (out_dim - split) / 2 each (weight rows split.. then split + H..),
+ *    packed column j = silu(y[split + j]) * y[split + H + j].
+ * The results equal bonsai_b1_linear_packed_f16 followed by
+ * bonsai_b1_pack_act_f16_ld, bonsai_b1_gelu_tanh_pack_f16_ld or
+ * bonsai_b1_swiglu_pack_f16_ld over those columns, bit for bit, without
+ * the fp32 round trip.  It fuses the reference single block's linear1
+ * (src/diffuser_graph.cpp:482-488: q/k/v columns to attention, MLP columns
+ * through mlp_act = ggml_swiglu, :227-229, into the second half of
+ * ggml_concat's input to to_out, :531-534) and the double block's FF-in
+ * (:450-456).  The non-finite counter counts y.
+ * split and out_dim multiples of 32 (64 for SwiGLU, both split and
+ * out_dim - split); in_dim % 384 == 0; split > 0: out 16-byte aligned,
+ * ldo >= split, ldo % 4 == 0; packed columns: packed_out 16-byte aligned,
+ * ldp >= their count, ldp % 8 == 0; the outputs apart from packed_act and
+ * from each other.  Always the 128-row GEMM tile, also for a few rows.
+ * No reference counterpart as one op (the reference runs separate ggml ops).
+ */
+enum {
+    BONSAI_B1_ACT_NONE = 0,
+    BONSAI_B1_ACT_GELU_TANH = 1,
+    BONSAI_B1_ACT_SWIGLU = 2
+};
+int bonsai_b1_linear_packed_f16_to_packed(const void *packed_act, const void *w,
+                                          int in_dim, int out_dim, int batch,
+                                          float *out, int64_t ldo, int split,
+                                          int act, void *packed_out,
+                                          int64_t ldp, int32_t *nonfinite,
+                                          hipStream_t stream);
+
 /* fp32 activations, any mode.  Where the packed FAST GEMM runs, the
  * epilogue is fused into it; elsewhere (EXACT, small batch, K % 384 != 0)
  * the linear writes y into the workspace and a separate pass applies the

@@ -202,3 +202,42 @@ def test_strided_producers_reject_before_device():
     assert sw(f, 6144, 3072, 4, f, 3064, None) == capi.ERR_ARG          # ldp < hidden
     assert sw(f, 6144, 3072, 4, f, 3076, None) == capi.ERR_ARG          # ldp % 8
     assert lib.bonsai_b1_swiglu_pack_f16(f, 6144, 3072, 4, None, None) == capi.ERR_ARG
+
+
+def test_packed_output_linear_rejects_before_device():
+    """bonsai_b1_linear_packed_f16_to_packed checks split, act, strides,
+    alignment and overlap before any launch (no device here)."""
+    lib = bonsai_b1.load()
+    fn = lib.bonsai_b1_linear_packed_f16_to_packed
+    a, w, o, p = 0x1000000, 0x2000000, 0x40000000, 0x80000000  # far apart
+    M, K, N = 64, 3072, 21504
+    ok = (a, w, K, N, M, o, 9216, 9216, 1, p, 15360, None, None)
+
+    def call(**kw):
+        args = list(ok)
+        names = ["act_p", "w", "k", "n", "m", "out", "ldo", "split", "act", "pk", "ldp", "nf", "s"]
+        for key, val in kw.items():
+            args[names.index(key)] = val
+        return fn(*args)
+
+    assert call() == capi.ERR_DEVICE                     # valid: fails only at the device
+    assert call(split=100) == capi.ERR_ARG               # split % 32
+    assert call(split=N + 32) == capi.ERR_ARG
+    assert call(act=3) == capi.ERR_ARG
+    assert call(act=2, split=9248) == capi.ERR_ARG       # SwiGLU split % 64
+    assert call(act=2, n=21536) == capi.ERR_ARG          # SwiGLU columns % 64
+    assert call(ldp=15364) == capi.ERR_ARG               # ldp % 8
+    assert call(ldp=12000) == capi.ERR_ARG               # ldp < packed columns
+    assert call(act=2, ldp=6136) == capi.ERR_ARG         # SwiGLU: ldp < (N - split) / 2
+    assert call(act=2, ldp=6144) == capi.ERR_DEVICE
+    assert call(ldo=9000) == capi.ERR_ARG                # ldo < split
+    assert call(ldo=9218) == capi.ERR_ARG                # ldo % 4
+    assert call(out=o + 4) == capi.ERR_ARG               # out not 16-byte aligned
+    assert call(pk=p + 8) == capi.ERR_ARG                # packed_out not 16-byte aligned
+    assert call(out=None) == capi.ERR_ARG
+    assert call(pk=None) == capi.ERR_ARG
+    assert call(split=N, ldo=N, pk=None) == capi.ERR_DEVICE   # no packed columns
+    assert call(split=0, out=None, ldp=N) == capi.ERR_DEVICE   # no fp32 columns
+    assert call(pk=a + 64) == capi.ERR_ARG               # packed_out overlaps the input
+    assert call(out=p) == capi.ERR_ARG                   # the outputs overlap
+    assert call(k=3000) == capi.ERR_ARG                  # in_dim % 384
