@@ -405,6 +405,22 @@ def bench_klein_step(torch, b1, synth):
         for pa, wt, kk, nn, o in gemms:
             b1.linear_packed_f16(pa, wt, kk, nn, o.shape[0], out=o)
     ms_packed = graph_ms(torch, step_packed, reps=2)
+
+    # the same, with the MLP activations produced by the GEMMs that precede
+    # them: FF-in and the single blocks' linear1 write SwiGLU of their MLP
+    # columns straight into the packed input of FF-out / to_out (linear1's
+    # q/k/v columns as fp32), as bonsai_b1_linear_packed_f16_to_packed does
+    def step_packed_epilogue():
+        for pa, wt, kk, nn, o in gemms:
+            mm = o.shape[0]
+            if nn == 18432:
+                b1.linear_packed_f16_to_packed(pa, wt, kk, nn, mm, 0, "swiglu", packed_out=packed[(mm, 9216)])
+            elif nn == 27648:
+                b1.linear_packed_f16_to_packed(pa, wt, kk, nn, mm, 9216, "swiglu", out=outs[mm][9216],
+                                               packed_out=packed[(mm, 12288)][3072 * 2:], ldp=12288)
+            else:
+                b1.linear_packed_f16(pa, wt, kk, nn, mm, out=o)
+    ms_epi = graph_ms(torch, step_packed_epilogue, reps=2)
     flop = (5 * 2 * (mi + mt) * (4 * 3072 * 3072 + 3072 * 18432 + 9216 * 3072)
             + 20 * 2 * ms_ * (3072 * 27648 + 12288 * 3072))
     nbytes = sum(v.numel() for per in d for st in per.values() for v in st.values()) + \
@@ -412,6 +428,7 @@ def bench_klein_step(torch, b1, synth):
     return {"linears": 100, "ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
             "ms_per_step_separate_qkv": ms_sep, "packed_weight_bytes": nbytes,
             "ms_per_step_packed_inputs": ms_packed, "tflops_packed_inputs": flop / (ms_packed * 1e-3) / 1e12,
+            "ms_per_step_swiglu_epilogues": ms_epi, "tflops_swiglu_epilogues": flop / (ms_epi * 1e-3) / 1e12,
             "dispatch": "bonsai_b1_linear_batch, one call per step; q/k/v as one GEMM over concatenated weights"}
 
 
@@ -686,7 +703,9 @@ def main():
         extra["klein_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in kl.items()}
         log(f"[bench] Klein step (100 linears): {kl['ms_per_step']:.2f} ms ({kl['tflops']:.0f} TFLOP/s); "
             f"q/k/v as three GEMMs {kl['ms_per_step_separate_qkv']:.2f} ms; over producer-packed fp16 inputs "
-            f"{kl['ms_per_step_packed_inputs']:.2f} ms ({kl['tflops_packed_inputs']:.0f} TFLOP/s)")
+            f"{kl['ms_per_step_packed_inputs']:.2f} ms ({kl['tflops_packed_inputs']:.0f} TFLOP/s); with FF-in and "
+            f"linear1 writing SwiGLU as the next packed input {kl['ms_per_step_swiglu_epilogues']:.2f} ms "
+            f"({kl['tflops_swiglu_epilogues']:.0f} TFLOP/s)")
         torch.cuda.empty_cache()
 
     cpu = None
