@@ -599,7 +599,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5000)
     ap.add_argument("--all", action="store_true", help="also time the other config shapes (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["gemm", "gemv", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "gemv", "copy", "c5chain"], default=None,
                     help="run one leg only (profiler runs); prints that leg's numbers")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -617,6 +617,10 @@ def main():
     if args.only == "copy":
         c = bench_copy(torch, 256 << 20, args.steps, args.warmup)
         print(json.dumps({"copy": c}), flush=True)
+        return
+    if args.only == "c5chain":
+        ch = bench_c5_block_chain(torch, b1, synth)
+        print(json.dumps({"c5_block_chain": ch}), flush=True)
         return
     if args.only == "gemv":
         gm, gk, gn = GEMV

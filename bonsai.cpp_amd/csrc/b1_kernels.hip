@@ -965,6 +965,48 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
             // residual and gate read at the accumulator's own positions:
             // lane (li, g) holds 4 consecutive columns of token 32 mt + li
             const bool fullr = vec_store && m0 + BM <= M && n0 + BN <= N;
+            if (fullr) {
+                // The residual may be `out` itself, so the compiler keeps
+                // every load behind the stores before it in program order.
+                // The gate is loaded once and each 32-row group's residual
+                // before any of its stores: 5 memory round trips a tile
+                // instead of 32 (each element is still read before it is
+                // written, which the in-place form needs).
+                floatx4 gw[C::NTL][4];
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        gw[nt][q] = *reinterpret_cast<const floatx4 *>(epi.gate + n0 + wave * WN + nt * 32 + 8 * q +
+                                                                        4 * g);
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt) {
+                    const int m = m0 + mt * 32 + li;
+                    const float *const rrow = epi.res + (size_t)m * epi.ldr + n0 + wave * WN + 4 * g;
+                    float *const orow = out + (size_t)m * ldo + n0 + wave * WN + 4 * g;
+                    floatx4 rv[C::NTL][4];
+#pragma unroll
+                    for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            rv[nt][q] = *reinterpret_cast<const floatx4 *>(rrow + nt * 32 + 8 * q);
+#pragma unroll
+                    for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            floatx4 o;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float yv = acc[mt][nt][4 * q + r];
+                                bad += cnt && !__builtin_isfinite(yv);
+                                o[r] = gate_residual(rv[nt][q][r], gw[nt][q][r], yv);
+                            }
+                            *reinterpret_cast<floatx4 *>(orow + nt * 32 + 8 * q) = o;
+                        }
+                }
+                count_nonfinite(nonfinite, bad);
+                return 1; // a store count the tile-start waits do not model
+            }
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt) {
                 const int m = m0 + mt * 32 + li;
@@ -973,18 +1015,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int n = n0 + wave * WN + nt * 32 + 8 * q + 4 * g;
-                        if (fullr) {
-                            const floatx4 rv = *reinterpret_cast<const floatx4 *>(epi.res + (size_t)m * epi.ldr + n);
-                            const floatx4 gw = *reinterpret_cast<const floatx4 *>(epi.gate + n);
-                            floatx4 o;
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const float yv = acc[mt][nt][4 * q + r];
-                                bad += cnt && !__builtin_isfinite(yv);
-                                o[r] = gate_residual(rv[r], gw[r], yv);
-                            }
-                            *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + n) = o;
-                        } else if (m < M) {
+                        if (m < M) {
 #pragma unroll
                             for (int r = 0; r < 4; ++r) {
                                 if (n + r < N) {
