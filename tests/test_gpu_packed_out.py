@@ -121,3 +121,30 @@ def test_packed_output_repeats_bit_identically(torch, b1):
     torch.cuda.synchronize()
     assert torch.equal(o1[:260], o2)
     assert torch.equal(q1[:q2.numel()], q2)
+
+
+def test_packed_output_in_captured_graph(torch, b1):
+    """The entry allocates nothing, so it can be captured: three replays,
+    each after eager work on the same buffers, equal the eager result."""
+    from bonsai_b1 import synth
+    m, k, n, split = 384, 768, 2048, 512
+    say("packed-output graph capture")
+    a = synth.device_activations(m, k, 87)
+    w = synth.device_packed_weights(n, k, 88)
+    p = b1.pack_act_f16(a)
+    out = torch.empty((m, split), device="cuda")
+    pk = torch.empty(m * (n - split) * 2, dtype=torch.uint8, device="cuda")
+    b1.linear_packed_f16_to_packed(p, w, k, n, m, split, "gelu_tanh", out=out, packed_out=pk)
+    torch.cuda.synchronize()
+    want_o, want_p = out.clone(), pk.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        b1.linear_packed_f16_to_packed(p, w, k, n, m, split, "gelu_tanh", out=out, packed_out=pk)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        pk.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want_o), f"replay {rep}"
+        assert torch.equal(pk, want_p), f"replay {rep}"
