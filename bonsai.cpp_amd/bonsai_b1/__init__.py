@@ -20,6 +20,7 @@ from .capi import (  # noqa: F401
     norm_mod,
     linear_packed_f16_epi,
     linear_packed_f16_to_packed,
+    packed_epilogue,
     ACTS,
     EPILOGUES,
     gelu_tanh,

@@ -36,13 +36,14 @@ class B1WeightsC(ctypes.Structure):
                 ("nbytes", ctypes.c_size_t), ("device", ctypes.c_int)]
 
 
-EPILOGUES = {"none": 0, "gate_residual": 1, "swiglu": 2}
+EPILOGUES = {"none": 0, "gate_residual": 1, "swiglu": 2, "packed": 3}
 ACTS = {"none": 0, "gelu_tanh": 1, "swiglu": 2}
 
 
 class Epilogue(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_int), ("gate", ctypes.c_void_p), ("residual", ctypes.c_void_p),
-                ("ldr", ctypes.c_int64)]
+                ("ldr", ctypes.c_int64), ("split", ctypes.c_int), ("act", ctypes.c_int),
+                ("packed", ctypes.c_void_p), ("ldp", ctypes.c_int64)]
 
 
 class LinearOp(ctypes.Structure):
@@ -297,11 +298,13 @@ def _batch_ops(ops):
         o = arr[i].op if with_epi else arr[i]
         o.act, o.lda = act.data_ptr(), act.stride(0)
         o.w = ctypes.pointer(w)
-        o.out, o.ldo = out.data_ptr(), out.stride(0)
+        o.out, o.ldo = (out.data_ptr(), out.stride(0)) if out is not None else (None, 0)
         o.batch = act.shape[0]
         if with_epi:
             spec = op[3] if len(op) > 3 else "none"
-            if isinstance(spec, str):
+            if isinstance(spec, Epilogue):
+                arr[i].epi = spec
+            elif isinstance(spec, str):
                 arr[i].epi = _epilogue(spec, None, None, w.out_dim, act.shape[0])
             else:
                 arr[i].epi = _epilogue(spec[0], spec[1], spec[2], w.out_dim, act.shape[0])
@@ -320,8 +323,10 @@ def linear_batch_workspace_bytes(ops, mode: str = "auto") -> int:
 def linear_batch(ops, mode: str = "auto", nonfinite=None, workspace=None, stream=None):
     """bonsai_b1_linear_batch over [(act, B1WeightsC, out), ...] (cuda
     tensors, act/out 2-D fp32 with unit column stride).  An op may carry a
-    fourth item, its epilogue: "swiglu", or ("gate_residual", gate,
-    residual); then bonsai_b1_linear_batch_epi runs the list."""
+    fourth item, its epilogue: "swiglu", ("gate_residual", gate,
+    residual) or a packed_epilogue() (then out holds the split fp32
+    columns, or is None when split == 0); then bonsai_b1_linear_batch_epi
+    runs the list."""
     arr, with_epi, keep = _batch_ops(ops)
     bad = ctypes.c_int(-1)
     nf = nonfinite.data_ptr() if nonfinite is not None else None
@@ -405,6 +410,15 @@ def _epilogue(kind: str, gate, residual, n_out: int, m: int):
     return e
 
 
+def packed_epilogue(split: int, act: str, packed, ldp: int):
+    """The BONSAI_B1_EPI_PACKED epilogue: y columns [0, split) stay fp32 in
+    the op's out, columns [split, N) go through `act` ("none", "gelu_tanh",
+    "swiglu") into the packed fp16 activations `packed` (a uint8 cuda view
+    starting at the target column, rows of ldp fp16 elements)."""
+    return Epilogue(EPILOGUES["packed"], None, None, 0, split, ACTS[act],
+                    packed.data_ptr() if packed is not None else None, ldp)
+
+
 def linear_epi_workspace_bytes(batch: int, in_dim: int, out_dim: int, epilogue: str, mode: str = "auto") -> int:
     return int(load().bonsai_b1_linear_epi_workspace_bytes(batch, in_dim, out_dim, EPILOGUES[epilogue],
                                                             MODES[mode]))
@@ -414,21 +428,27 @@ def linear_epi(act, w_packed, out_dim: int, epilogue: str, gate=None, residual=N
                mode: str = "auto", nonfinite=None, workspace=None, stream=None):
     """The linear with a fused epilogue (bonsai_b1_linear_epi_f32):
     "gate_residual" -> out = residual + gate * y (residual may be out);
-    "swiglu" -> out[:, j] = silu(y[:, j]) * y[:, H + j], H = out_dim / 2."""
+    "swiglu" -> out[:, j] = silu(y[:, j]) * y[:, H + j], H = out_dim / 2;
+    or a packed_epilogue(): out [M, >=split] (None when split == 0) and the
+    epilogue's packed fp16 output.  Returns out."""
     import torch
     m, k = act.shape
-    cols = out_dim // 2 if epilogue == "swiglu" else out_dim
-    if out is None:
+    if isinstance(epilogue, Epilogue):     # packed_epilogue(): out holds the split fp32 columns
+        e, cols = epilogue, epilogue.split
+    else:
+        e, cols = _epilogue(epilogue, gate, residual, out_dim, m), (out_dim // 2 if epilogue == "swiglu"
+                                                                   else out_dim)
+    if out is None and cols > 0:
         out = torch.empty((m, cols), dtype=torch.float32, device=act.device)
-    if out.dim() != 2 or out.shape[0] != m or out.shape[1] < cols or out.stride(1) != 1:
+    if out is not None and (out.dim() != 2 or out.shape[0] != m or out.shape[1] < cols or out.stride(1) != 1):
         raise ValueError("out must be [M, >=cols] fp32 with unit column stride")
-    e = _epilogue(epilogue, gate, residual, out_dim, m)
     nf = nonfinite.data_ptr() if nonfinite is not None else None
     ws, wsb = (workspace.data_ptr(), workspace.numel() * workspace.element_size()) if workspace is not None \
         else (None, 0)
     st = load().bonsai_b1_linear_epi_f32(act.data_ptr(), act.stride(0), w_packed.data_ptr(), k, out_dim, m,
-                                         out.data_ptr(), out.stride(0), ctypes.byref(e), MODES[mode], nf, ws, wsb,
-                                         _stream_handle(stream))
+                                         out.data_ptr() if out is not None else None,
+                                         out.stride(0) if out is not None else 0, ctypes.byref(e), MODES[mode],
+                                         nf, ws, wsb, _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_linear_epi_f32")
     return out

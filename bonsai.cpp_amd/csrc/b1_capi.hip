@@ -394,6 +394,35 @@ static int epi_args(const bonsai_b1_epilogue *epi, int out_dim, int batch, const
         if (out_dim % 64 != 0 || ldo < out_dim / 2) return BONSAI_B1_ERR_ARG;
         g->glu_h = out_dim / 2;
         return BONSAI_B1_OK;
+    case BONSAI_B1_EPI_PACKED: {
+        const int split = epi->split, act = epi->act;
+        if (split < 0 || split > out_dim || split % BONSAI_B1_BLOCK_SIZE || out_dim % BONSAI_B1_BLOCK_SIZE)
+            return BONSAI_B1_ERR_ARG;
+        if (act != BONSAI_B1_ACT_NONE && act != BONSAI_B1_ACT_GELU_TANH && act != BONSAI_B1_ACT_SWIGLU)
+            return BONSAI_B1_ERR_ARG;
+        const bool glu = act == BONSAI_B1_ACT_SWIGLU;
+        if (glu && (split % 64 || (out_dim - split) % 64)) return BONSAI_B1_ERR_ARG;
+        // packed columns written: SwiGLU halves its [gate | value] columns
+        const int pcols = glu ? (out_dim - split) / 2 : out_dim - split;
+        auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+        if (split > 0 && (!al16(out) || ldo < split || ldo % 4)) return BONSAI_B1_ERR_ARG;
+        if (pcols > 0 && (!al16(epi->packed) || epi->ldp < pcols || epi->ldp % 8)) return BONSAI_B1_ERR_ARG;
+        if (batch > 0) {
+            if ((split > 0 && !out) || (pcols > 0 && !epi->packed)) return BONSAI_B1_ERR_ARG;
+            if (split > 0 && pcols > 0) {
+                const uintptr_t p0 = reinterpret_cast<uintptr_t>(epi->packed);
+                const auto po = std::pair<uintptr_t, uintptr_t>(
+                    p0, p0 + ((size_t)(batch - 1) * (size_t)epi->ldp + (size_t)pcols) * 2);
+                if (overlap(po, span(out, batch, ldo, split))) return BONSAI_B1_ERR_ARG;
+            }
+        }
+        g->pk = static_cast<uint32_t *>(epi->packed);
+        g->ldpw = epi->ldp / 2;
+        g->split = split;
+        g->act = act;
+        g->glu_h = glu ? pcols : 0;
+        return BONSAI_B1_OK;
+    }
     default:
         return BONSAI_B1_ERR_ARG;
     }
@@ -425,49 +454,38 @@ int bonsai_b1_linear_packed_f16_to_packed(const void *packed_act, const void *w,
                                           float *out, int64_t ldo, int split, int act, void *packed_out,
                                           int64_t ldp, int32_t *nonfinite, hipStream_t stream) {
     if (in_dim <= 0 || out_dim <= 0 || batch < 0) return BONSAI_B1_ERR_ARG;
-    if (split < 0 || split > out_dim || split % BONSAI_B1_BLOCK_SIZE || out_dim % BONSAI_B1_BLOCK_SIZE)
+    bonsai_b1_epilogue e = {};
+    e.kind = BONSAI_B1_EPI_PACKED;
+    e.split = split;
+    e.act = act;
+    e.packed = packed_out;
+    e.ldp = ldp;
+    int kind;
+    b1::GemmEpi g;
+    const int st = epi_args(&e, out_dim, batch, out, ldo, &kind, &g);
+    if (st != BONSAI_B1_OK) return st;
+    if ((reinterpret_cast<uintptr_t>(packed_act) & 15u) || (reinterpret_cast<uintptr_t>(w) & 3u))
         return BONSAI_B1_ERR_ARG;
-    if (act != BONSAI_B1_ACT_NONE && act != BONSAI_B1_ACT_GELU_TANH && act != BONSAI_B1_ACT_SWIGLU)
-        return BONSAI_B1_ERR_ARG;
-    const bool glu = act == BONSAI_B1_ACT_SWIGLU;
-    if (glu && (split % 64 || (out_dim - split) % 64)) return BONSAI_B1_ERR_ARG;
-    // packed columns written: SwiGLU halves its [gate | value] columns
-    const int pcols = glu ? (out_dim - split) / 2 : out_dim - split;
-    auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (!al16(packed_act) || (reinterpret_cast<uintptr_t>(w) & 3u)) return BONSAI_B1_ERR_ARG;
-    if (split > 0 && (!al16(out) || ldo < split || ldo % 4)) return BONSAI_B1_ERR_ARG;
-    if (pcols > 0 && (!al16(packed_out) || ldp < pcols || ldp % 8)) return BONSAI_B1_ERR_ARG;
     if (!b1::gemm_packed_ok(batch > 0 ? batch : 1, in_dim, out_dim)) return BONSAI_B1_ERR_ARG;
     if (batch > 0) {
-        if (!packed_act || !w || (split > 0 && !out) || (pcols > 0 && !packed_out)) return BONSAI_B1_ERR_ARG;
+        if (!packed_act || !w) return BONSAI_B1_ERR_ARG;
         // the outputs lie apart from the activations the GEMM still reads
-        // and from each other
-        auto span = [](const void *p, int rows, int64_t ld_bytes, int64_t row_bytes) {
-            const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-            return std::pair<uintptr_t, uintptr_t>(a, a + (size_t)(rows - 1) * (size_t)ld_bytes + (size_t)row_bytes);
+        const uintptr_t a0 = reinterpret_cast<uintptr_t>(packed_act);
+        const uintptr_t a1 = a0 + (size_t)batch * (size_t)in_dim * 2;
+        auto apart = [&](const void *p, int64_t ld_bytes, int64_t row_bytes) {
+            const uintptr_t p0 = reinterpret_cast<uintptr_t>(p);
+            const uintptr_t p1 = p0 + (size_t)(batch - 1) * (size_t)ld_bytes + (size_t)row_bytes;
+            return !(p0 < a1 && a0 < p1);
         };
-        auto overlap = [](std::pair<uintptr_t, uintptr_t> x, std::pair<uintptr_t, uintptr_t> y) {
-            return x.first < y.second && y.first < x.second;
-        };
-        const auto in = span(packed_act, batch, (int64_t)in_dim * 2, (int64_t)in_dim * 2);
-        if (split > 0 && overlap(in, span(out, batch, ldo * 4, (int64_t)split * 4))) return BONSAI_B1_ERR_ARG;
-        if (pcols > 0) {
-            const auto po = span(packed_out, batch, ldp * 2, (int64_t)pcols * 2);
-            if (overlap(in, po)) return BONSAI_B1_ERR_ARG;
-            if (split > 0 && overlap(po, span(out, batch, ldo * 4, (int64_t)split * 4))) return BONSAI_B1_ERR_ARG;
-        }
+        const int pcols = g.glu_h ? g.glu_h : out_dim - split;
+        if (split > 0 && !apart(out, ldo * 4, (int64_t)split * 4)) return BONSAI_B1_ERR_ARG;
+        if (pcols > 0 && !apart(packed_out, ldp * 2, (int64_t)pcols * 2)) return BONSAI_B1_ERR_ARG;
     }
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     if (batch == 0) return BONSAI_B1_OK;
-    b1::GemmEpi g;
-    g.pk = static_cast<uint32_t *>(packed_out);
-    g.ldpw = ldp / 2;
-    g.split = split;
-    g.act = act;
-    g.glu_h = glu ? pcols : 0;
     return b1::launch_gemm_packed_epi(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
-                                      nonfinite, dev->num_cus, 3, g, stream) == hipSuccess
+                                      nonfinite, dev->num_cus, kind, g, stream) == hipSuccess
                ? BONSAI_B1_OK
                : BONSAI_B1_ERR_HIP;
 }
@@ -498,7 +516,9 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
     if (kind == BONSAI_B1_EPI_NONE)
         return linear_impl(act, lda, w, in_dim, out_dim, batch, out, ldo, mode, nonfinite, workspace ? 1 : 0,
                            workspace, workspace_bytes, stream);
-    st = check_args(act, lda, w, in_dim, out_dim, batch, out, out_dim);
+    // (the packed-output epilogue's out may be NULL: its checks are done)
+    const bool packed_out = kind == BONSAI_B1_EPI_PACKED;
+    st = check_args(act, lda, w, in_dim, out_dim, batch, packed_out ? act : out, out_dim);
     if (st != BONSAI_B1_OK) return st;
     if (mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_GEMV) return BONSAI_B1_ERR_ARG;
     DeviceInfo *dev = current_device(nullptr);
@@ -522,6 +542,19 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
     }
     if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
         return BONSAI_B1_ERR_ARG;
+    if (packed_out) {
+        // the outputs lie apart from the workspace the GEMM or the
+        // separate passes read
+        const uintptr_t w0 = reinterpret_cast<uintptr_t>(workspace), w1 = w0 + need;
+        auto apart = [&](const void *p, size_t bytes) {
+            const uintptr_t p0 = reinterpret_cast<uintptr_t>(p);
+            return bytes == 0 || !(p0 < w1 && w0 < p0 + bytes);
+        };
+        const int pcols = g.glu_h ? g.glu_h : out_dim - g.split;
+        if (!apart(out, g.split ? ((size_t)(batch - 1) * ldo + g.split) * 4 : 0) ||
+            !apart(epi->packed, pcols ? ((size_t)(batch - 1) * epi->ldp + pcols) * 2 : 0))
+            return BONSAI_B1_ERR_ARG;
+    }
     hipError_t e;
     if (fused) {
         e = b1::launch_pack(act, lda, batch, in_dim, workspace, in_dim, stream);
@@ -533,7 +566,8 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
         float *y = static_cast<float *>(workspace);
         st = linear_impl(act, lda, w, in_dim, out_dim, batch, y, out_dim, mode, nonfinite, 1, nullptr, 0, stream);
         if (st != BONSAI_B1_OK) return st;
-        e = b1::launch_epi(y, out_dim, batch, out_dim, kind, g, out, ldo, stream);
+        e = packed_out ? b1::launch_epi_packed(y, out_dim, batch, out_dim, g, out, ldo, stream)
+                       : b1::launch_epi(y, out_dim, batch, out_dim, kind, g, out, ldo, stream);
     }
     return e == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
 }
@@ -577,9 +611,12 @@ static b1::LinearArgs batch_args(const bonsai_b1_linear_op &op) {
 // columns, or out_dim / 2 after SwiGLU (epi_args checks that case).
 static bool batch_op_ok(const bonsai_b1_linear_op &op, const bonsai_b1_epilogue *epi = nullptr) {
     if (!op.w || !op.w->data) return false;
-    const int64_t ldo = (epi && epi->kind == BONSAI_B1_EPI_SWIGLU) ? op.w->out_dim : op.ldo;
-    return check_args(op.act, op.lda, op.w->data, op.w->in_dim, op.w->out_dim, op.batch, op.out, ldo) ==
-           BONSAI_B1_OK;
+    // the SwiGLU and packed-output epilogues check their outputs themselves
+    // (epi_args): out may be narrower, or NULL for a wholly packed output
+    const bool own = epi && (epi->kind == BONSAI_B1_EPI_SWIGLU || epi->kind == BONSAI_B1_EPI_PACKED);
+    const float *out = epi && epi->kind == BONSAI_B1_EPI_PACKED ? op.act : op.out;
+    return check_args(op.act, op.lda, op.w->data, op.w->in_dim, op.w->out_dim, op.batch, out,
+                      own ? op.w->out_dim : op.ldo) == BONSAI_B1_OK;
 }
 
 extern "C++" {
@@ -735,7 +772,9 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
             case BatchPath::Gemv: e = b1::launch_gemv(la, dev->num_cus, stream); break;
             default: e = b1::launch_gemm(la, dev->num_cus, nullptr, 0, stream); break;
             }
-            if (e == hipSuccess && kind != BONSAI_B1_EPI_NONE)
+            if (e == hipSuccess && kind == BONSAI_B1_EPI_PACKED)
+                e = b1::launch_epi_packed(ybuf, a.N, a.M, a.N, g, a.out, a.ldo, stream);
+            else if (e == hipSuccess && kind != BONSAI_B1_EPI_NONE)
                 e = b1::launch_epi(ybuf, a.N, a.M, a.N, kind, g, a.out, a.ldo, stream);
         } else {
             int n_sum;
@@ -766,11 +805,22 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
         // An output written over the packed activations' source invalidates
         // the packing.
         if (packed_act) {
-            const uintptr_t o0 = reinterpret_cast<uintptr_t>(a.out);
-            const uintptr_t o1 = o0 + ((size_t)(a.M - 1) * (size_t)a.ldo + (size_t)out_cols) * sizeof(float);
             const uintptr_t p0 = reinterpret_cast<uintptr_t>(packed_act);
             const uintptr_t p1 = p0 + ((size_t)(packed_m - 1) * (size_t)packed_lda + (size_t)packed_k) * sizeof(float);
-            if (o0 < p1 && p0 < o1) packed_act = nullptr;
+            auto hits = [&](const void *o, int64_t ld_bytes, int64_t row_bytes) {
+                const uintptr_t o0 = reinterpret_cast<uintptr_t>(o);
+                const uintptr_t o1 = o0 + (size_t)(a.M - 1) * (size_t)ld_bytes + (size_t)row_bytes;
+                return o0 < p1 && p0 < o1;
+            };
+            if (kind == BONSAI_B1_EPI_PACKED) {
+                // the fp32 columns and the packed fp16 columns
+                const int pcols = g.glu_h ? g.glu_h : a.N - g.split;
+                if ((g.split > 0 && hits(a.out, a.ldo * 4, (int64_t)g.split * 4)) ||
+                    (pcols > 0 && hits(bo.epi->packed, bo.epi->ldp * 2, (int64_t)pcols * 2)))
+                    packed_act = nullptr;
+            } else if (hits(a.out, a.ldo * 4, (int64_t)out_cols * 4)) {
+                packed_act = nullptr;
+            }
         }
     }
     return BONSAI_B1_OK;

@@ -86,6 +86,11 @@ hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, i
 // of y; kind 2 writes glu_h of them).
 hipError_t launch_epi(const float *y, int64_t ldy, int M, int N, int kind, const GemmEpi &epi, float *out,
                       int64_t ldo, hipStream_t s);
+// Kind 3 as separate passes over y [M][ldy] (16-byte aligned, ldy % 4 ==
+// 0): columns [0, split) copied to out, the rest through the producer of
+// epi.act into epi.pk -- the values the fused epilogue writes.
+hipError_t launch_epi_packed(const float *y, int64_t ldy, int M, int N, const GemmEpi &epi, float *out,
+                             int64_t ldo, hipStream_t s);
 
 // LayerNorm (no affine, eps inside the square root) + modulation
 // x_n * (scale + 1) + shift over rows of H (H % 32 == 0, 16-byte aligned

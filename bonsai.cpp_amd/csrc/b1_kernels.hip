@@ -1882,6 +1882,25 @@ hipError_t launch_epi(const float *y, int64_t ldy, int M, int N, int kind, const
     return hipGetLastError();
 }
 
+hipError_t launch_epi_packed(const float *y, int64_t ldy, int M, int N, const GemmEpi &epi, float *out,
+                             int64_t ldo, hipStream_t s) {
+    if (epi.split > 0) {
+        const hipError_t e = hipMemcpy2DAsync(out, (size_t)ldo * sizeof(float), y, (size_t)ldy * sizeof(float),
+                                              (size_t)epi.split * sizeof(float), (size_t)M,
+                                              hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) return e;
+    }
+    if (epi.split >= N) return hipSuccess;
+    const float *src = y + epi.split;
+    const int64_t ldp = epi.ldpw * 2;
+    switch (epi.act) {
+    case 0: return launch_pack(src, ldy, M, N - epi.split, epi.pk, ldp, s);
+    case 1: return launch_gelu_pack(src, ldy, M, N - epi.split, epi.pk, ldp, s);
+    case 2: return launch_swiglu_pack(src, ldy, M, epi.glu_h, epi.pk, ldp, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gelu(const float *x, int64_t ldx, float *y, int64_t ldy, int cols, int rows, hipStream_t s) {
     const int64_t units = (int64_t)rows * (cols / 4);
     const int64_t want = (units + 255) / 256;

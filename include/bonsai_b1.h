@@ -282,6 +282,11 @@ int bonsai_b1_weights_concat(const B1Weights *parts, int n_parts,
  *    value] (weights rows [0, H) then [H, 2H)); out[m][j] = silu(y[m][j]) *
  *    y[m][H + j], H columns (ggml_swiglu on FF-in, :453-456, 228).
  *    H % 32 == 0; silu(x) = x / (1 + exp(-x)) in fp32.
+ *  - BONSAI_B1_EPI_PACKED: the output of bonsai_b1_linear_packed_f16_to_packed
+ *    (declared below): columns [0, split) of y as fp32 in out (ldo >= split;
+ *    out may be NULL when split == 0), columns [split, out_dim) through
+ *    `act` into the packed fp16 activations `packed` (row stride ldp), with
+ *    that entry's requirements.
  * The non-finite counter counts the linear's own outputs y, as the
  * reference's abort checks them (src/b1_0_kernel.h:194-198).
  * No reference counterpart: the reference runs these as separate ggml ops.
@@ -289,13 +294,18 @@ int bonsai_b1_weights_concat(const B1Weights *parts, int n_parts,
 enum {
     BONSAI_B1_EPI_NONE = 0,
     BONSAI_B1_EPI_GATE_RESIDUAL = 1,
-    BONSAI_B1_EPI_SWIGLU = 2
+    BONSAI_B1_EPI_SWIGLU = 2,
+    BONSAI_B1_EPI_PACKED = 3
 };
 typedef struct bonsai_b1_epilogue {
     int kind;
     const float *gate;     /* GATE_RESIDUAL: [out_dim], device */
     const float *residual; /* GATE_RESIDUAL: [batch][ldr], device */
     int64_t ldr;
+    int split;             /* PACKED: fp32 columns, a multiple of 32 */
+    int act;               /* PACKED: BONSAI_B1_ACT_* */
+    void *packed;          /* PACKED: packed fp16 output, device */
+    int64_t ldp;           /* PACKED: its row stride in fp16 elements */
 } bonsai_b1_epilogue;
 
 /* An op of bonsai_b1_linear_batch_epi: the linear and its epilogue. */

@@ -241,3 +241,37 @@ def test_packed_output_linear_rejects_before_device():
     assert call(pk=a + 64) == capi.ERR_ARG               # packed_out overlaps the input
     assert call(out=p) == capi.ERR_ARG                   # the outputs overlap
     assert call(k=3000) == capi.ERR_ARG                  # in_dim % 384
+
+
+def test_epilogue_struct_layout():
+    """bonsai_b1_epilogue: the packed-output fields follow the original four,
+    whose offsets are unchanged (int kind; gate; residual; int64 ldr; int
+    split; int act; packed; int64 ldp)."""
+    E = capi.Epilogue
+    assert (E.kind.offset, E.gate.offset, E.residual.offset, E.ldr.offset) == (0, 8, 16, 24)
+    assert (E.split.offset, E.act.offset, E.packed.offset, E.ldp.offset) == (32, 36, 40, 48)
+    assert ctypes.sizeof(E) == 56
+    assert ctypes.sizeof(capi.LinearOpEpi) == ctypes.sizeof(capi.LinearOp) + 56
+
+
+def test_packed_epilogue_rejected_before_device():
+    """The packed-output epilogue of bonsai_b1_linear_epi_f32 and of a batch
+    op is checked like bonsai_b1_linear_packed_f16_to_packed."""
+    lib = bonsai_b1.load()
+    act, w, out, pk = 0x1000000, 0x2000000, 0x40000000, 0x80000000
+    m, k, n = 64, 3072, 2048
+
+    def call(split=512, a=1, packed=pk, ldp=1536, o=out, ldo=512):
+        e = capi.Epilogue(3, None, None, 0, split, a, packed, ldp)
+        return lib.bonsai_b1_linear_epi_f32(act, k, w, k, n, m, o, ldo, ctypes.byref(e), 0, None, None, 0, None)
+
+    assert call() == capi.ERR_DEVICE
+    assert call(split=0, o=None, ldo=0, ldp=2048) == capi.ERR_DEVICE     # no fp32 columns: out may be NULL
+    assert call(split=100) == capi.ERR_ARG
+    assert call(a=5) == capi.ERR_ARG
+    assert call(a=2, split=544) == capi.ERR_ARG                          # SwiGLU split % 64
+    assert call(ldp=1500) == capi.ERR_ARG
+    assert call(ldo=500) == capi.ERR_ARG
+    assert call(packed=pk + 4) == capi.ERR_ARG
+    assert call(packed=out + 64) == capi.ERR_ARG                         # outputs overlap
+    assert call(o=None) == capi.ERR_ARG

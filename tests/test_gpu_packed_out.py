@@ -148,3 +148,70 @@ def test_packed_output_in_captured_graph(torch, b1):
         torch.cuda.synchronize()
         assert torch.equal(out, want_o), f"replay {rep}"
         assert torch.equal(pk, want_p), f"replay {rep}"
+
+
+@pytest.mark.parametrize("m,mode,act", [(300, "auto", "gelu_tanh"), (300, "auto", "swiglu"),
+                                        (300, "exact", "gelu_tanh"), (96, "exact", "swiglu"),
+                                        (5, "auto", "swiglu"), (5, "auto", "none")])
+def test_packed_epilogue_of_fp32_entry(torch, b1, m, mode, act):
+    """bonsai_b1_linear_epi_f32 with the packed-output epilogue: the fused
+    FAST path equals pack + bonsai_b1_linear_packed_f16_to_packed; EXACT
+    mode and the small-batch kernel (separate passes over the linear's
+    output) equal that mode's own linear followed by the producers."""
+    from bonsai_b1 import synth
+    k, n, split, col0, ldp = 768, 2048, 512, 64, 1600
+    say(f"packed epilogue, fp32 entry m={m} mode={mode} act={act}")
+    a = synth.device_activations(m, k, 91)
+    w = synth.device_packed_weights(n, k, 92)
+    cols = (n - split) // 2 if act == "swiglu" else n - split
+    nbytes = ((m - 1) * ldp + col0 + cols) * 2
+    got = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device="cuda")
+    want = got.clone()
+    out = torch.full((m, split), float("nan"), device="cuda")
+    e = b1.packed_epilogue(split, act, got[col0 * 2:], ldp)
+    b1.linear_epi(a, w, n, e, out=out, mode=mode)
+    if mode == "auto" and m > 16:
+        o2, _ = b1.linear_packed_f16_to_packed(b1.pack_act_f16(a), w, k, n, m, split, act,
+                                               packed_out=want[col0 * 2:], ldp=ldp)
+        y_head = o2
+    else:
+        y = b1.linear(a, w, n, mode=mode)
+        y_head = y[:, :split]
+        produce(b1, y[:, split:], act, want[col0 * 2:], ldp)
+    torch.cuda.synchronize()
+    assert torch.equal(out, y_head)
+    assert torch.equal(got, want)
+
+
+def test_packed_epilogue_in_batch(torch, b1):
+    """A batch with packed-output ops (q/k/v + SwiGLU MLP of a single block,
+    a double block's FF-in) beside plain ops equals the ops one by one."""
+    from bonsai_b1 import synth
+    m, k = 320, 768
+    say("packed epilogue in a batch")
+    a = synth.device_activations(m, k, 93)
+    a2 = synth.device_activations(m, k, 94)
+    w1 = synth.device_packed_weights(2560, k, 95)     # [qkv 1024 | gate 768 | value 768]
+    w2 = synth.device_packed_weights(1536, k, 96)     # FF-in: [gate 768 | value 768]
+    w3 = synth.device_packed_weights(384, k, 97)      # plain
+    W1, W2, W3 = (b1.device_weights(w1, k, 2560), b1.device_weights(w2, k, 1536),
+                  b1.device_weights(w3, k, 384))
+    p_out1 = torch.zeros(m * 1024 * 2, dtype=torch.uint8, device="cuda")    # [attn 256 | mlp 768]
+    p_out2 = torch.zeros(m * 768 * 2, dtype=torch.uint8, device="cuda")
+    qkv = torch.empty((m, 1024), device="cuda")
+    y3 = torch.empty((m, 384), device="cuda")
+    ops = [(a, W1, qkv, b1.packed_epilogue(1024, "swiglu", p_out1[256 * 2:], 1024)),
+           (a, W3, y3),
+           (a2, W2, None, b1.packed_epilogue(0, "swiglu", p_out2, 768))]
+    b1.linear_batch(ops)
+    torch.cuda.synchronize()
+    p1_full = torch.zeros_like(p_out1)
+    q_want, _ = b1.linear_packed_f16_to_packed(b1.pack_act_f16(a), w1, k, 2560, m, 1024, "swiglu",
+                                               packed_out=p1_full[256 * 2:], ldp=1024)
+    _, p2_want = b1.linear_packed_f16_to_packed(b1.pack_act_f16(a2), w2, k, 1536, m, 0, "swiglu")
+    y3_want = b1.linear(a, w3, 384)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv, q_want)
+    assert torch.equal(p_out1, p1_full)
+    assert torch.equal(p_out2, p2_want)
+    assert torch.equal(y3, y3_want)
