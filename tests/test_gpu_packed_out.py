@@ -62,7 +62,30 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("m,k,n,split,act,col0,ldp", CASES)
+def _sweep(count=10, seed=2024):
+    """Seeded extra cases: row counts around tile edges, widths and split
+    points on 32- (64- for SwiGLU) column boundaries, column offsets and
+    padded row strides."""
+    import random
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        act = rng.choice(["none", "gelu_tanh", "swiglu"])
+        q = 64 if act == "swiglu" else 32
+        m = rng.choice([1, 17, 127, 128, 129, 255, 383, 640])
+        k = rng.choice([384, 768, 1152])
+        n = q * rng.randint(2, 48)
+        split = q * rng.randint(0, n // q)
+        cols = (n - split) // 2 if act == "swiglu" else n - split
+        col0 = 32 * rng.randint(0, 3)
+        ldp = None if col0 == 0 and rng.random() < 0.5 else col0 + cols + 8 * rng.randint(0, 8)
+        if ldp is None:
+            col0 = 0
+        cases.append((m, k, n, split, act, col0, ldp))
+    return cases
+
+
+@pytest.mark.parametrize("m,k,n,split,act,col0,ldp", CASES + _sweep())
 def test_packed_output_equals_linear_then_producer(torch, b1, m, k, n, split, act, col0, ldp):
     from bonsai_b1 import synth
     say(f"packed-output linear m={m} k={k} n={n} split={split} act={act} col0={col0} ldp={ldp}")
