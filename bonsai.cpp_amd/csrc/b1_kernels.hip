@@ -674,6 +674,11 @@ __global__ __launch_bounds__(256) void b1_quantize_kernel(const float *__restric
 // word (row, 16 blk + d) holds (a[row][32 blk + d], a[row][32 blk + d + 16]).
 // The GEMM then streams this straight into LDS with no per-tile conversion.
 
+// NT: the fp32 input is read with non-temporal loads, for inputs larger
+// than the Infinity Cache that are read exactly once (4608 x 15360: 65.6 vs
+// 72.9 us); a cache-resident input is faster with the default policy
+// (4096 x 3072: 11.5 vs 13.4 us).
+template <bool NT>
 __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restrict__ act, int64_t lda,
                                                           uint32_t *__restrict__ ah, int64_t ldw, int M, int K) {
     const int nb = K / 32;
@@ -682,8 +687,14 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
         const int c = u & 3, rb = u >> 2;
         const int row = rb / nb, blk = rb - row * nb;
         const float *src = act + (size_t)row * lda + blk * 32 + c * 4;
-        const floatx4 lo = *reinterpret_cast<const floatx4 *>(src);
-        const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + 16);
+        floatx4 lo, hi;
+        if constexpr (NT) {
+            lo = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(src));
+            hi = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(src + 16));
+        } else {
+            lo = *reinterpret_cast<const floatx4 *>(src);
+            hi = *reinterpret_cast<const floatx4 *>(src + 16);
+        }
         u32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = pack_f16(lo[j], hi[j]);
@@ -1717,8 +1728,9 @@ bool pack_supported(const float *act, int64_t lda, int M, int K) {
 hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed, int64_t ldp, hipStream_t s) {
     const int units = M * (K / 32) * 4;
     const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
-    hipLaunchKernelGGL(b1_pack_act_kernel, dim3(pgrid), dim3(256), 0, s, act, lda, static_cast<uint32_t *>(packed),
-                       ldp / 2, M, K);
+    const bool nt = (uint64_t)M * (uint64_t)K * 4 > (128ull << 20);
+    hipLaunchKernelGGL(nt ? b1_pack_act_kernel<true> : b1_pack_act_kernel<false>, dim3(pgrid), dim3(256), 0, s, act,
+                       lda, static_cast<uint32_t *>(packed), ldp / 2, M, K);
     return hipGetLastError();
 }
 
