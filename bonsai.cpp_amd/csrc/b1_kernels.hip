@@ -363,6 +363,19 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void b1_gemm_fused_kern
     count_nonfinite(p.nonfinite, bad);
 }
 
+// A 16-byte fp32 load; NT: non-temporal, for producer inputs larger than
+// the Infinity Cache that are read exactly once (see b1_pack_act_kernel).
+template <bool NT>
+__device__ __forceinline__ floatx4 load_f4(const float *p) {
+    if constexpr (NT)
+        return __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(p));
+    else
+        return *reinterpret_cast<const floatx4 *>(p);
+}
+
+// Producer inputs from this size on are streamed with non-temporal loads.
+constexpr uint64_t kNtInputBytes = 128ull << 20;
+
 // ------------------------------------------------------------- GELU-tanh --
 //
 // 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), elementwise in
@@ -400,6 +413,7 @@ __global__ __launch_bounds__(256) void b1_gelu_kernel(const float *__restrict__ 
     }
 }
 
+template <bool NT>
 __global__ __launch_bounds__(256) void b1_gelu_pack_kernel(const float *__restrict__ act, int64_t lda,
                                                            uint32_t *__restrict__ ah, int64_t ldw, int M, int K) {
     const int nb = K / 32;
@@ -408,8 +422,8 @@ __global__ __launch_bounds__(256) void b1_gelu_pack_kernel(const float *__restri
         const int c = u & 3, rb = u >> 2;
         const int row = rb / nb, blk = rb - row * nb;
         const float *src = act + (size_t)row * lda + blk * 32 + c * 4;
-        const floatx4 lo = *reinterpret_cast<const floatx4 *>(src);
-        const floatx4 hi = *reinterpret_cast<const floatx4 *>(src + 16);
+        const floatx4 lo = load_f4<NT>(src);
+        const floatx4 hi = load_f4<NT>(src + 16);
         u32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = pack_f16(gelu_tanh(lo[j]), gelu_tanh(hi[j]));
@@ -439,6 +453,7 @@ __device__ __forceinline__ float mul_f32(float a, float b) {
 // SwiGLU (ggml_swiglu: silu of the first half of a row times its second
 // half) fused with the fp16 packing, written at a packed row stride of ldw
 // words: act [M][lda] holds 2H columns, the packed output H.
+template <bool NT>
 __global__ __launch_bounds__(256) void b1_swiglu_pack_kernel(const float *__restrict__ act, int64_t lda,
                                                              uint32_t *__restrict__ ah, int64_t ldw, int M, int H) {
     const int nb = H / 32;
@@ -448,10 +463,10 @@ __global__ __launch_bounds__(256) void b1_swiglu_pack_kernel(const float *__rest
         const int row = rb / nb, blk = rb - row * nb;
         const float *g = act + (size_t)row * lda + blk * 32 + c * 4;
         const float *v = g + H;
-        const floatx4 glo = *reinterpret_cast<const floatx4 *>(g);
-        const floatx4 ghi = *reinterpret_cast<const floatx4 *>(g + 16);
-        const floatx4 vlo = *reinterpret_cast<const floatx4 *>(v);
-        const floatx4 vhi = *reinterpret_cast<const floatx4 *>(v + 16);
+        const floatx4 glo = load_f4<NT>(g);
+        const floatx4 ghi = load_f4<NT>(g + 16);
+        const floatx4 vlo = load_f4<NT>(v);
+        const floatx4 vhi = load_f4<NT>(v + 16);
         u32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -687,14 +702,8 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
         const int c = u & 3, rb = u >> 2;
         const int row = rb / nb, blk = rb - row * nb;
         const float *src = act + (size_t)row * lda + blk * 32 + c * 4;
-        floatx4 lo, hi;
-        if constexpr (NT) {
-            lo = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(src));
-            hi = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(src + 16));
-        } else {
-            lo = *reinterpret_cast<const floatx4 *>(src);
-            hi = *reinterpret_cast<const floatx4 *>(src + 16);
-        }
+        const floatx4 lo = load_f4<NT>(src);
+        const floatx4 hi = load_f4<NT>(src + 16);
         u32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = pack_f16(lo[j], hi[j]);
@@ -1728,7 +1737,7 @@ bool pack_supported(const float *act, int64_t lda, int M, int K) {
 hipError_t launch_pack(const float *act, int64_t lda, int M, int K, void *packed, int64_t ldp, hipStream_t s) {
     const int units = M * (K / 32) * 4;
     const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
-    const bool nt = (uint64_t)M * (uint64_t)K * 4 > (128ull << 20);
+    const bool nt = (uint64_t)M * (uint64_t)K * 4 > kNtInputBytes;
     hipLaunchKernelGGL(nt ? b1_pack_act_kernel<true> : b1_pack_act_kernel<false>, dim3(pgrid), dim3(256), 0, s, act,
                        lda, static_cast<uint32_t *>(packed), ldp / 2, M, K);
     return hipGetLastError();
@@ -1925,8 +1934,9 @@ hipError_t launch_gelu_pack(const float *act, int64_t lda, int M, int K, void *p
                             hipStream_t s) {
     const int units = M * (K / 32) * 4;
     const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
-    hipLaunchKernelGGL(b1_gelu_pack_kernel, dim3(pgrid), dim3(256), 0, s, act, lda,
-                       static_cast<uint32_t *>(packed), ldp / 2, M, K);
+    const bool nt = (uint64_t)M * (uint64_t)K * 4 > kNtInputBytes;
+    hipLaunchKernelGGL(nt ? b1_gelu_pack_kernel<true> : b1_gelu_pack_kernel<false>, dim3(pgrid), dim3(256), 0, s,
+                       act, lda, static_cast<uint32_t *>(packed), ldp / 2, M, K);
     return hipGetLastError();
 }
 
@@ -1934,8 +1944,9 @@ hipError_t launch_swiglu_pack(const float *act, int64_t lda, int M, int H, void 
                               hipStream_t s) {
     const int units = M * (H / 32) * 4;
     const int pgrid = (units + 255) / 256 < 65535 ? (units + 255) / 256 : 65535;
-    hipLaunchKernelGGL(b1_swiglu_pack_kernel, dim3(pgrid), dim3(256), 0, s, act, lda,
-                       static_cast<uint32_t *>(packed), ldp / 2, M, H);
+    const bool nt = (uint64_t)M * (uint64_t)H * 8 > kNtInputBytes;
+    hipLaunchKernelGGL(nt ? b1_swiglu_pack_kernel<true> : b1_swiglu_pack_kernel<false>, dim3(pgrid), dim3(256), 0,
+                       s, act, lda, static_cast<uint32_t *>(packed), ldp / 2, M, H);
     return hipGetLastError();
 }
 
