@@ -15,6 +15,9 @@ BLOCK_BYTES = 6
 MAGIC = 0x31423142
 
 OK, ERR_ARG, ERR_HIP, ERR_NONFINITE, ERR_DEVICE = 0, 1, 2, 3, 4
+ERR_SCRATCH = 8
+# bytes of the static device workspace of bonsai_b1_linear_f32_noalloc
+NOALLOC_SCRATCH_BYTES = 32 << 20
 MODES = {"auto": 0, "fast": 1, "exact": 2, "gemm": 3, "gemv": 4}
 
 _lib = None
@@ -79,6 +82,8 @@ def load():
     L.bonsai_b1_linear_f32.restype = i
     L.bonsai_b1_linear_f32_ws.argtypes = [vp, i64, vp, i, i, i, vp, i64, i, vp, vp, ctypes.c_size_t, vp]
     L.bonsai_b1_linear_f32_ws.restype = i
+    L.bonsai_b1_linear_f32_noalloc.argtypes = [vp, i64, vp, i, i, i, vp, i64, i, vp, vp]
+    L.bonsai_b1_linear_f32_noalloc.restype = i
     L.bonsai_b1_workspace_bytes.argtypes = [i, i, i, i]
     L.bonsai_b1_workspace_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_linear.argtypes = [vp, ctypes.POINTER(B1WeightsC), i, vp,

@@ -13,6 +13,13 @@
 #include "bonsai_b1.h"
 #include "b1_internal.h"
 
+// The workspace of bonsai_b1_linear_f32_noalloc: one copy per device, held
+// by the loaded code object until the process ends.  Host code never uses
+// this name as an address (on the host it is only a handle for the runtime's
+// symbol lookup); it uses the device address hipGetSymbolAddress returns for
+// the current device, kept in DeviceInfo::scratch.
+static __device__ __align__(256) uint8_t scratch[BONSAI_B1_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 constexpr int kMaxDevices = 64;
@@ -33,12 +40,27 @@ struct DeviceInfo {
     int32_t *cb_counter = nullptr; // non-finite counter for the callback
     Workspace ws[kWsSlots];
     uint64_t tick = 0;
+    // this device's address of `scratch` (0: not looked up, 1: found, -1:
+    // the lookup failed)
+    int scratch_state = 0;
+    void *scratch = nullptr;
 };
 
 std::mutex g_mu;
 DeviceInfo g_dev[kMaxDevices];
 
-// Returns the current device's info, probing it once.
+// Looks up the current device's address of `scratch` (with that device
+// current, under g_mu); nullptr when the lookup fails.
+void lookup_scratch(DeviceInfo *d) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    d->scratch = e == hipSuccess ? p : nullptr;
+    d->scratch_state = d->scratch ? 1 : -1;
+}
+
+// Returns the current device's info, probing it once.  The probe, which the
+// first call of any entry point on a device makes, also looks up that
+// device's copy of `scratch`.
 DeviceInfo *current_device(int *dev_out) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
@@ -52,9 +74,16 @@ DeviceInfo *current_device(int *dev_out) {
         } else {
             d.state = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
             d.num_cus = prop.multiProcessorCount;
+            if (d.state == 1) lookup_scratch(&d);
         }
     }
     return d.state == 1 ? &d : nullptr;
+}
+
+// This device's address of `scratch` (nullptr if its lookup failed).
+void *device_scratch(DeviceInfo *d) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return d->scratch_state == 1 ? d->scratch : nullptr;
 }
 
 // Library-owned workspace for `stream` on the current device, grown to at
@@ -126,6 +155,7 @@ const char *bonsai_b1_status_string(int status) {
     case BONSAI_B1_ERR_NOT_FOUND: return "tensor not found";
     case BONSAI_B1_ERR_FORMAT: return "malformed file or not a B1_0 tensor";
     case BONSAI_B1_ERR_IO: return "file could not be opened";
+    case BONSAI_B1_ERR_SCRATCH: return "call needs more workspace than the no-alloc scratch holds";
     default: return "unknown status";
     }
 }
@@ -214,6 +244,24 @@ int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
                             hipStream_t stream) {
     return linear_impl(act, lda, w, in_dim, out_dim, batch, out, ldo, mode, nonfinite, 1, workspace,
                        workspace_bytes, stream);
+}
+
+int bonsai_b1_linear_f32_noalloc(const float *act, int64_t lda, const void *w, int in_dim, int out_dim, int batch,
+                                 float *out, int64_t ldo, int mode, int32_t *nonfinite, hipStream_t stream) {
+    // the argument checks of the shared body come first, so a bad call is
+    // ERR_ARG whatever its size
+    int st = check_args(act, lda, w, in_dim, out_dim, batch, out, ldo);
+    if (st != BONSAI_B1_OK) return st;
+    if (mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_GEMV) return BONSAI_B1_ERR_ARG;
+    DeviceInfo *dev = current_device(nullptr);
+    if (!dev) return BONSAI_B1_ERR_DEVICE;
+    if (batch == 0) return BONSAI_B1_OK;
+    if (bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) > BONSAI_B1_NOALLOC_SCRATCH_BYTES)
+        return BONSAI_B1_ERR_SCRATCH;
+    void *ws = device_scratch(dev);
+    if (!ws) return BONSAI_B1_ERR_HIP;
+    return linear_impl(act, lda, w, in_dim, out_dim, batch, out, ldo, mode, nonfinite, 1, ws,
+                       BONSAI_B1_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int bonsai_b1_gelu_tanh_f32(const float *x, int64_t ldx, float *y, int64_t ldy, int cols, int rows,

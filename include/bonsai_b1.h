@@ -62,7 +62,8 @@ enum {
     BONSAI_B1_ERR_DEVICE = 4,    /* no usable gfx950 device */
     BONSAI_B1_ERR_NOT_FOUND = 5, /* no tensor of that name in the file */
     BONSAI_B1_ERR_FORMAT = 6,    /* malformed file or not a B1_0 tensor */
-    BONSAI_B1_ERR_IO = 7         /* file could not be opened or mapped */
+    BONSAI_B1_ERR_IO = 7,        /* file could not be opened or mapped */
+    BONSAI_B1_ERR_SCRATCH = 8    /* call needs more than the static scratch */
 };
 
 /* Arithmetic modes.
@@ -124,6 +125,28 @@ int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
 
 /* Frees every library-owned workspace (all devices); waits for the device. */
 void bonsai_b1_release_workspaces(void);
+
+/*
+ * bonsai_b1_linear_f32 for callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  No counterpart in the reference (its CPU op needs no
+ * workspace).  Same arguments, kernels and results, bit for bit, as
+ * bonsai_b1_linear_f32; the workspace those kernels use (the fp16 packing
+ * of the activations and the split-K partials) is a static device array of
+ * BONSAI_B1_NOALLOC_SCRATCH_BYTES that the library holds on each device it
+ * runs on until the process ends.  Never calls hipMalloc or hipFree.
+ * Returns BONSAI_B1_ERR_SCRATCH, launching nothing, when the call needs
+ * more than that (bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) >
+ * BONSAI_B1_NOALLOC_SCRATCH_BYTES).  Every call on a device shares that
+ * device's array and leaves its contents behind: calls that overlap in time
+ * on one device (other streams, other threads) race and must be serialised
+ * by the caller; calls on one stream are ordered.
+ */
+#define BONSAI_B1_NOALLOC_SCRATCH_BYTES (32u << 20)
+int bonsai_b1_linear_f32_noalloc(const float *act, int64_t lda, const void *w,
+                                 int in_dim, int out_dim, int batch,
+                                 float *out, int64_t ldo, int mode,
+                                 int32_t *nonfinite, hipStream_t stream);
 
 /*
  * The FAST GEMM in two halves, for a producer of activations that can emit
