@@ -28,6 +28,7 @@ from .capi import (  # noqa: F401
     library_path,
     linear,
     linear_packed_f16,
+    linear_packed_workspace_bytes,
     linear_raw,
     load,
     pack_act_f16,

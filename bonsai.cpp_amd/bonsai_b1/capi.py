@@ -123,6 +123,10 @@ def load():
     L.bonsai_b1_pack_act_f16_ld.restype = i
     L.bonsai_b1_linear_packed_f16.argtypes = [vp, vp, i, i, i, vp, i64, vp, vp]
     L.bonsai_b1_linear_packed_f16.restype = i
+    L.bonsai_b1_linear_packed_f16_ws.argtypes = [vp, vp, i, i, i, vp, i64, vp, vp, ctypes.c_size_t, vp]
+    L.bonsai_b1_linear_packed_f16_ws.restype = i
+    L.bonsai_b1_linear_packed_workspace_bytes.argtypes = [i, i, i]
+    L.bonsai_b1_linear_packed_workspace_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_linear_packed_f16_epi.argtypes = [vp, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), vp, vp]
     L.bonsai_b1_linear_packed_f16_epi.restype = i
     L.bonsai_b1_linear_packed_f16_to_packed.argtypes = [vp, vp, i, i, i, vp, i64, i, i, vp, i64, vp, vp]
@@ -383,17 +387,28 @@ def pack_act_f16(act, packed=None, stream=None, ldp=None):
     return packed
 
 
+def linear_packed_workspace_bytes(batch: int, in_dim: int, out_dim: int) -> int:
+    return int(load().bonsai_b1_linear_packed_workspace_bytes(batch, in_dim, out_dim))
+
+
 def linear_packed_f16(packed, w_packed, in_dim: int, out_dim: int, batch: int, out=None, nonfinite=None,
-                      stream=None):
-    """out[batch, out_dim] from packed fp16 activations (bonsai_b1_linear_packed_f16)."""
+                      stream=None, workspace=None):
+    """out[batch, out_dim] from packed fp16 activations (bonsai_b1_linear_packed_f16;
+    with `workspace`, a cuda tensor, bonsai_b1_linear_packed_f16_ws)."""
     import torch
     if out is None:
         out = torch.empty((batch, out_dim), dtype=torch.float32, device=packed.device)
     if out.dim() != 2 or out.shape[0] != batch or out.shape[1] < out_dim or out.stride(1) != 1:
         raise ValueError("out must be [batch, >=out_dim] fp32 with unit column stride")
     nf = nonfinite.data_ptr() if nonfinite is not None else None
-    st = load().bonsai_b1_linear_packed_f16(packed.data_ptr(), w_packed.data_ptr(), in_dim, out_dim, batch,
-                                            out.data_ptr(), out.stride(0), nf, _stream_handle(stream))
+    if workspace is not None:
+        st = load().bonsai_b1_linear_packed_f16_ws(packed.data_ptr(), w_packed.data_ptr(), in_dim, out_dim, batch,
+                                                   out.data_ptr(), out.stride(0), nf, workspace.data_ptr(),
+                                                   workspace.numel() * workspace.element_size(),
+                                                   _stream_handle(stream))
+    else:
+        st = load().bonsai_b1_linear_packed_f16(packed.data_ptr(), w_packed.data_ptr(), in_dim, out_dim, batch,
+                                                out.data_ptr(), out.stride(0), nf, _stream_handle(stream))
     if st != OK:
         raise B1Error(st, "bonsai_b1_linear_packed_f16")
     return out

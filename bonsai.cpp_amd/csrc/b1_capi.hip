@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <list>
 #include <mutex>
 #include <utility>
 #include <stdio.h>
@@ -24,21 +25,28 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 
-constexpr int kWsSlots = 8; // cached workspaces per device (one per stream)
+constexpr int kWsFree = 8; // unpinned workspaces kept per device (about one per stream)
 
+// A library-owned workspace of one stream.  `pins`: handed out while the
+// stream was being captured, so a graph may hold its address; a pinned
+// buffer is never freed or evicted (growing allocates a new one), only
+// bonsai_b1_release_workspaces frees it.  `users`: entry-point calls that
+// hold it between the hand-out and their last launch; never evicted then
+// (another thread may not free it under a call that has not launched yet).
 struct Workspace {
     hipStream_t stream = nullptr;
     void *ptr = nullptr;
     size_t bytes = 0;
     uint64_t last_use = 0;
-    bool used = false;
+    int pins = 0;
+    int users = 0;
 };
 
 struct DeviceInfo {
     int state = 0; // 0 unknown, 1 usable gfx950, -1 unusable
     int num_cus = 0;
     int32_t *cb_counter = nullptr; // non-finite counter for the callback
-    Workspace ws[kWsSlots];
+    std::list<Workspace> ws;       // stable element addresses
     uint64_t tick = 0;
     // this device's address of `scratch` (0: not looked up, 1: found, -1:
     // the lookup failed)
@@ -86,45 +94,85 @@ void *device_scratch(DeviceInfo *d) {
     return d->scratch_state == 1 ? d->scratch : nullptr;
 }
 
-// Library-owned workspace for `stream` on the current device, grown to at
-// least `need` bytes.  Returns nullptr (the caller then uses a kernel that
-// needs none) when the stream is being captured and no large enough buffer
-// exists yet, or when allocation fails.  Growing frees the old buffer
-// (hipFree waits for work that may still use it).
-void *stream_workspace(DeviceInfo *d, hipStream_t stream, size_t need) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    Workspace *hit = nullptr, *victim = &d->ws[0];
-    for (Workspace &w : d->ws) {
-        if (w.used && w.stream == stream) hit = &w;
-        if (!w.used) {
-            if (victim->used) victim = &w;
-        } else if (victim->used && w.last_use < victim->last_use) {
-            victim = &w;
+// A library-owned workspace handed to one entry-point call, released (the
+// user count dropped) when the call has launched its kernels.  ptr is
+// nullptr when none could be had: the stream is being captured and owns no
+// large enough buffer (a capture never allocates), or allocation failed, or
+// every buffer is pinned or in use by another call.
+class WsLease {
+  public:
+    WsLease() = default;
+    WsLease(const WsLease &) = delete;
+    WsLease &operator=(const WsLease &) = delete;
+    ~WsLease() { drop(); }
+    void *ptr() const { return w_ ? w_->ptr : nullptr; }
+    void acquire(DeviceInfo *d, hipStream_t stream, size_t need);
+
+  private:
+    void drop() {
+        if (w_) {
+            std::lock_guard<std::mutex> lk(g_mu);
+            --w_->users;
+            w_ = nullptr;
         }
     }
-    if (hit && hit->bytes >= need) {
-        hit->last_use = ++d->tick;
-        return hit->ptr;
-    }
+    Workspace *w_ = nullptr;
+};
+
+// Hands out this stream's most recently used buffer of at least `need`
+// bytes (pinning it when the stream is being captured), or, outside a
+// capture, a new one.  A new buffer takes the place of an unpinned buffer
+// no call holds: this stream's own smaller one, or the least recently used
+// one once kWsFree unpinned buffers exist; freeing waits for the device
+// (hipFree), so work already launched on the old buffer completes first.
+void WsLease::acquire(DeviceInfo *d, hipStream_t stream, size_t need) {
+    drop();
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    Workspace *w = hit ? hit : victim;
-    if (w->ptr) {
-        (void)hipFree(w->ptr);
-        w->ptr = nullptr;
-        w->bytes = 0;
-        w->used = false;
+    const bool capturing = hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Workspace *hit = nullptr;
+    for (Workspace &w : d->ws)
+        if (w.stream == stream && w.bytes >= need && (!hit || w.last_use > hit->last_use)) hit = &w;
+    if (hit) {
+        hit->last_use = ++d->tick;
+        ++hit->users;
+        if (capturing) ++hit->pins;
+        w_ = hit;
+        return;
+    }
+    if (capturing) return;
+    Workspace *own = nullptr, *lru = nullptr;
+    int unpinned = 0;
+    for (Workspace &w : d->ws) {
+        if (w.pins) continue;
+        ++unpinned;
+        if (w.users) continue;
+        if (w.stream == stream) own = &w;
+        if (!lru || w.last_use < lru->last_use) lru = &w;
+    }
+    Workspace *slot = own ? own : unpinned >= kWsFree ? lru : nullptr;
+    if (slot) {
+        (void)hipFree(slot->ptr);
+        slot->ptr = nullptr;
+        slot->bytes = 0;
     }
     const size_t bytes = (need + (2u << 20) - 1) & ~((size_t)(2u << 20) - 1);
-    if (hipMalloc(&w->ptr, bytes) != hipSuccess) {
-        w->ptr = nullptr;
-        return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        if (slot) d->ws.remove_if([slot](const Workspace &w) { return &w == slot; });
+        return;
     }
-    w->stream = stream;
-    w->bytes = bytes;
-    w->used = true;
-    w->last_use = ++d->tick;
-    return w->ptr;
+    if (!slot) {
+        d->ws.emplace_back();
+        slot = &d->ws.back();
+    }
+    slot->stream = stream;
+    slot->ptr = p;
+    slot->bytes = bytes;
+    slot->last_use = ++d->tick;
+    slot->pins = 0;
+    slot->users = 1;
+    w_ = slot;
 }
 
 int check_args(const float *act, int64_t lda, const void *w, int in_dim,
@@ -183,13 +231,22 @@ static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim,
     a.ldo = ldo;
     a.nonfinite = nonfinite;
 
-    auto gemm = [&]() {
-        const size_t need = b1::gemm_workspace_bytes_total(a, dev->num_cus);
+    // the library's workspace for this stream (ws_mode 0), or the caller's
+    WsLease lease;
+    auto workspace = [&](size_t need) {
         if (need > 0 && ws_mode == 0) {
-            ws = stream_workspace(dev, stream, need);
+            lease.acquire(dev, stream, need);
+            ws = lease.ptr();
             ws_bytes = ws ? need : 0;
         }
+    };
+    auto gemm = [&]() {
+        workspace(b1::gemm_workspace_bytes_total(a, dev->num_cus));
         return b1::launch_gemm(a, dev->num_cus, ws, ws_bytes, stream);
+    };
+    auto gemv = [&]() {
+        workspace(b1::gemv_workspace_bytes(a));
+        return b1::launch_gemv_ws(a, dev->num_cus, ws, ws_bytes, stream);
     };
 
     hipError_t e;
@@ -203,11 +260,11 @@ static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim,
         break;
     case BONSAI_B1_MODE_GEMV:
         if (!b1::gemv_supported(a)) return BONSAI_B1_ERR_ARG;
-        e = b1::launch_gemv(a, dev->num_cus, stream);
+        e = gemv();
         break;
     default: // AUTO, FAST
         if (b1::gemv_supported(a))
-            e = b1::launch_gemv(a, dev->num_cus, stream);
+            e = gemv();
         else if (b1::gemm_supported(a))
             e = gemm();
         else
@@ -226,15 +283,21 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
 
 size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode) {
     if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
-    if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return 0;
-    if ((mode == BONSAI_B1_MODE_AUTO || mode == BONSAI_B1_MODE_FAST) && batch <= b1::kGemvMaxM) return 0;
-    if (!b1::gemm_packed_ok(batch, in_dim, out_dim)) return 0;
-    // the packing, then (on a device where the shape splits along K) the
-    // split-K partials
-    const size_t pack = (size_t)batch * (size_t)in_dim * 2;
+    if (mode < BONSAI_B1_MODE_AUTO || mode > BONSAI_B1_MODE_GEMV || mode == BONSAI_B1_MODE_EXACT) return 0;
+    // the calls' own choice of kernel, on aligned activations
+    b1::LinearArgs a{};
+    a.K = in_dim;
+    a.N = out_dim;
+    a.M = batch;
+    a.lda = in_dim;
+    a.act = reinterpret_cast<const float *>(uintptr_t(256));
+    a.w = reinterpret_cast<const uint8_t *>(uintptr_t(256));
+    if (mode == BONSAI_B1_MODE_GEMV || (mode != BONSAI_B1_MODE_GEMM && batch <= b1::kGemvMaxM))
+        return b1::gemv_workspace_bytes(a);
+    // the range-safe packing, then (on a device where the shape splits
+    // along K) the split-K partials
     const DeviceInfo *dev = current_device(nullptr);
-    const int splits = dev ? b1::gemm_splits(batch, in_dim, out_dim, dev->num_cus) : 1;
-    return splits > 1 ? ((pack + 255) & ~(size_t)255) + b1::gemm_split_bytes(batch, out_dim, splits) : pack;
+    return b1::gemm_workspace_bytes_total(a, dev ? dev->num_cus : 0);
 }
 
 int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
@@ -379,25 +442,65 @@ int bonsai_b1_pack_act_f16(const float *act, int64_t lda, int in_dim, int batch,
     return bonsai_b1_pack_act_f16_ld(act, lda, in_dim, batch, packed, in_dim, stream);
 }
 
-int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
-                                float *out, int64_t ldo, int32_t *nonfinite, hipStream_t stream) {
+size_t bonsai_b1_linear_packed_workspace_bytes(int batch, int in_dim, int out_dim) {
+    if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || !b1::gemm_packed_ok(batch, in_dim, out_dim)) return 0;
+    if (b1::gemv_packed_ok(batch, in_dim, out_dim)) return 0;
+    const DeviceInfo *dev = current_device(nullptr);
+    const int splits = dev ? b1::gemm_splits(batch, in_dim, out_dim, dev->num_cus) : 1;
+    return b1::gemm_split_bytes(batch, out_dim, splits);
+}
+
+// Shared body of the packed entry points.  ws_mode: 0 = library-owned
+// workspace for the split-K partials, 1 = caller's (may be NULL / small:
+// then unsplit).
+static int linear_packed_impl(const void *packed_act, const void *w, int in_dim, int out_dim, int batch, float *out,
+                              int64_t ldo, int32_t *nonfinite, int ws_mode, void *ws, size_t ws_bytes,
+                              hipStream_t stream) {
     if (in_dim <= 0 || out_dim <= 0 || batch < 0 || ldo < out_dim) return BONSAI_B1_ERR_ARG;
     if (batch > 0 && (!packed_act || !w || !out)) return BONSAI_B1_ERR_ARG;
     if ((reinterpret_cast<uintptr_t>(packed_act) & 15u) || (reinterpret_cast<uintptr_t>(w) & 3u) ||
-        (reinterpret_cast<uintptr_t>(out) & 3u))
+        (reinterpret_cast<uintptr_t>(out) & 3u) || (reinterpret_cast<uintptr_t>(ws) & 15u))
         return BONSAI_B1_ERR_ARG;
     if (!b1::gemm_packed_ok(batch > 0 ? batch : 1, in_dim, out_dim)) return BONSAI_B1_ERR_ARG;
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     if (batch == 0) return BONSAI_B1_OK;
-    // a few tokens: the bandwidth-bound small-M kernel, not a 128-row tile
-    const hipError_t e =
-        b1::gemv_packed_ok(batch, in_dim, out_dim)
-            ? b1::launch_gemv_packed(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
-                                     nonfinite, dev->num_cus, stream)
-            : b1::launch_gemm_packed(packed_act, static_cast<const uint8_t *>(w), in_dim, out_dim, batch, out, ldo,
-                                     nonfinite, dev->num_cus, stream);
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+    hipError_t e;
+    if (b1::gemv_packed_ok(batch, in_dim, out_dim)) {
+        // a few tokens: the bandwidth-bound small-M kernel, not a 128-row tile
+        e = b1::launch_gemv_packed(packed_act, wb, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus, stream);
+    } else {
+        // split along K as bonsai_b1_linear_f32 splits the same shape, when
+        // the partials have room: the two entries then agree bit for bit
+        const int splits = b1::gemm_splits(batch, in_dim, out_dim, dev->num_cus);
+        const size_t need = b1::gemm_split_bytes(batch, out_dim, splits);
+        WsLease lease;
+        if (need > 0 && ws_mode == 0) {
+            lease.acquire(dev, stream, need);
+            ws = lease.ptr();
+            ws_bytes = ws ? need : 0;
+        }
+        if (need > 0 && ws && ws_bytes >= need)
+            e = b1::launch_gemm_packed_split(packed_act, wb, in_dim, out_dim, batch, out, ldo, nonfinite,
+                                             dev->num_cus, splits, ws, stream);
+        else
+            e = b1::launch_gemm_packed(packed_act, wb, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus,
+                                       stream);
+    }
     return e == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
+}
+
+int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
+                                float *out, int64_t ldo, int32_t *nonfinite, hipStream_t stream) {
+    return linear_packed_impl(packed_act, w, in_dim, out_dim, batch, out, ldo, nonfinite, 0, nullptr, 0, stream);
+}
+
+int bonsai_b1_linear_packed_f16_ws(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
+                                   float *out, int64_t ldo, int32_t *nonfinite, void *workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+    return linear_packed_impl(packed_act, w, in_dim, out_dim, batch, out, ldo, nonfinite, 1, workspace,
+                              workspace_bytes, stream);
 }
 
 // Checks an epilogue against a linear of out_dim outputs (weight rows) and
@@ -538,6 +641,10 @@ int bonsai_b1_linear_packed_f16_to_packed(const void *packed_act, const void *w,
                : BONSAI_B1_ERR_HIP;
 }
 
+// The fp32 output of a linear whose epilogue runs as a separate pass, in a
+// workspace (256-byte multiple, so what follows stays aligned).
+static size_t epi_y_bytes(int batch, int out_dim) { return ((size_t)batch * out_dim * 4 + 255) & ~(size_t)255; }
+
 // Whether a linear runs the packed FAST GEMM (as linear_impl decides).
 static bool packed_path(const b1::LinearArgs &a, int mode) {
     if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return false;
@@ -548,9 +655,13 @@ static bool packed_path(const b1::LinearArgs &a, int mode) {
 size_t bonsai_b1_linear_epi_workspace_bytes(int batch, int in_dim, int out_dim, int kind, int mode) {
     if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
     if (kind == BONSAI_B1_EPI_NONE) return bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode);
-    // either the fp16 packing (fused path) or the linear's output (separate pass)
-    const size_t pack = b1::gemm_packed_ok(batch, in_dim, out_dim) ? (size_t)batch * in_dim * 2 : 0;
-    const size_t y = (size_t)batch * out_dim * 4;
+    // either the range-safe packing (fused path) or the linear's output
+    // (separate pass) followed by the small-M kernel's packing
+    const size_t pack = b1::gemm_packed_ok(batch, in_dim, out_dim) ? b1::pack_area_bytes(batch, in_dim) : 0;
+    const size_t y = epi_y_bytes(batch, out_dim) + bonsai_b1_workspace_bytes(batch, in_dim, out_dim,
+                                                                             mode == BONSAI_B1_MODE_EXACT
+                                                                                 ? mode
+                                                                                 : BONSAI_B1_MODE_GEMV);
     return pack > y ? pack : y;
 }
 
@@ -583,9 +694,17 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
     a.ldo = ldo;
     a.nonfinite = nonfinite;
     const bool fused = packed_path(a, mode);
-    const size_t need = fused ? (size_t)batch * in_dim * 2 : (size_t)batch * out_dim * 4;
+    // separate pass: y, then what the linear's own kernel can use
+    const size_t y_bytes = epi_y_bytes(batch, out_dim);
+    const size_t lin_ws = fused || !b1::gemv_supported(a) || mode == BONSAI_B1_MODE_EXACT ||
+                                  mode == BONSAI_B1_MODE_GEMM
+                              ? 0
+                              : b1::gemv_workspace_bytes(a);
+    const size_t need = fused ? b1::pack_area_bytes(batch, in_dim) : y_bytes + lin_ws;
+    WsLease lease;
     if (!workspace) {
-        workspace = stream_workspace(dev, stream, need);
+        lease.acquire(dev, stream, need);
+        workspace = lease.ptr();
         workspace_bytes = workspace ? need : 0;
     }
     if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
@@ -605,14 +724,16 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
     }
     hipError_t e;
     if (fused) {
-        e = b1::launch_pack(act, lda, batch, in_dim, workspace, in_dim, stream);
+        e = b1::launch_pack_rows(act, lda, batch, in_dim, workspace, stream);
+        g.rsc = b1::pack_area_rsc(workspace, batch, in_dim);
         if (e == hipSuccess)
             e = b1::launch_gemm_packed_epi(workspace, a.w, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus,
                                            kind, g, stream);
     } else {
         // the linear into the workspace, then the epilogue pass
         float *y = static_cast<float *>(workspace);
-        st = linear_impl(act, lda, w, in_dim, out_dim, batch, y, out_dim, mode, nonfinite, 1, nullptr, 0, stream);
+        void *rest = lin_ws ? static_cast<uint8_t *>(workspace) + y_bytes : nullptr;
+        st = linear_impl(act, lda, w, in_dim, out_dim, batch, y, out_dim, mode, nonfinite, 1, rest, lin_ws, stream);
         if (st != BONSAI_B1_OK) return st;
         e = packed_out ? b1::launch_epi_packed(y, out_dim, batch, out_dim, g, out, ldo, stream)
                        : b1::launch_epi(y, out_dim, batch, out_dim, kind, g, out, ldo, stream);
@@ -623,23 +744,31 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
 void bonsai_b1_release_workspaces(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     for (DeviceInfo &d : g_dev) {
-        for (Workspace &w : d.ws) {
-            if (w.ptr) (void)hipFree(w.ptr);
-            w = Workspace();
-        }
+        // buffers an unfinished call still holds stay (it frees nothing it
+        // has not launched on yet); pinned ones go, as documented
+        d.ws.remove_if([](Workspace &w) {
+            if (w.users) return false;
+            (void)hipFree(w.ptr);
+            return true;
+        });
     }
 }
 
 // How one op of a batch runs (the same choice linear_impl makes).
-enum class BatchPath { Exact, Gemv, Packed, Fused };
+// Gemv: the small-M kernel converting fp32 itself; GemvPacked: the small-M
+// kernel over the (shared) range-safe packing; Packed: the packed GEMM;
+// Fused: the fused-conversion GEMM.
+enum class BatchPath { Exact, Gemv, GemvPacked, Packed, Fused };
 
 static BatchPath batch_path(const b1::LinearArgs &a, int mode) {
     if (mode == BONSAI_B1_MODE_EXACT) return BatchPath::Exact;
-    if (b1::gemv_supported(a)) return BatchPath::Gemv;
+    if (b1::gemv_supported(a)) return b1::gemv_workspace_bytes(a) > 0 ? BatchPath::GemvPacked : BatchPath::Gemv;
     if (b1::gemm_supported(a))
         return b1::gemm_workspace_bytes(a) > 0 ? BatchPath::Packed : BatchPath::Fused;
     return BatchPath::Exact;
 }
+
+static bool uses_packing(BatchPath p) { return p == BatchPath::Packed || p == BatchPath::GemvPacked; }
 
 static b1::LinearArgs batch_args(const bonsai_b1_linear_op &op) {
     b1::LinearArgs a;
@@ -700,7 +829,8 @@ static int fuse_span(int n_ops, int mode, int num_cus, OpAt at, int i, int *n_su
             (size_t)p.w->out_dim * (size_t)(p.w->in_dim / BONSAI_B1_BLOCK_SIZE) * BONSAI_B1_BLOCK_BYTES;
         if (epi_kind(qb.epi) != BONSAI_B1_EPI_NONE || q.batch != a.M || q.act != a.act || q.lda != a.lda ||
             q.w->in_dim != a.K || q.ldo != a.ldo || q.w->data != static_cast<const uint8_t *>(p.w->data) + p_bytes ||
-            q.out != p.out + p.w->out_dim || *n_sum + (int64_t)q.w->out_dim > INT32_MAX)
+            q.out != p.out + p.w->out_dim || *n_sum + (int64_t)q.w->out_dim > INT32_MAX ||
+            !b1::gemm_packed_ok(a.M, a.K, *n_sum + q.w->out_dim))
             break;
         const b1::LinearArgs qa = batch_args(q);
         if (batch_path(qa, mode) != BatchPath::Packed || b1::gemm_splits(qa.M, qa.K, qa.N, num_cus) != splits) break;
@@ -721,10 +851,10 @@ static int fuse_span(int n_ops, int mode, int num_cus, OpAt at, int i, int *n_su
 }
 
 // Workspace areas of a batch, laid out [pack][split][y], each 256-byte
-// aligned: the largest fp16 packing among its packed-GEMM ops, the largest
-// split-K partial area among its plain packed GEMMs (fused runs included),
-// and the largest fp32 linear output among its ops whose epilogue runs as a
-// separate pass (the other paths).
+// aligned: the largest range-safe packing among its packed-GEMM and packed
+// small-M ops, the largest split-K partial area among its plain packed GEMMs
+// (fused runs included), and the largest fp32 linear output among its ops
+// whose epilogue runs as a separate pass (the other paths).
 struct BatchAreas {
     size_t pack = 0, split = 0, y = 0;
     size_t split_off() const { return round256(pack); }
@@ -739,8 +869,9 @@ static BatchAreas batch_areas(int n_ops, int mode, int num_cus, OpAt at) {
         const BatchOp b = at(i);
         if (!batch_op_ok(*b.op, b.epi) || b.op->batch == 0) continue;
         const b1::LinearArgs a = batch_args(*b.op);
-        if (batch_path(a, mode) == BatchPath::Packed) {
-            r.pack = std::max(r.pack, b1::gemm_workspace_bytes(a));
+        const BatchPath path = batch_path(a, mode);
+        if (uses_packing(path)) r.pack = std::max(r.pack, b1::pack_area_bytes(a.M, a.K));
+        if (path == BatchPath::Packed) {
             if (epi_kind(b.epi) == BONSAI_B1_EPI_NONE) {
                 int n_sum;
                 const int last = fuse_span(n_ops, mode, num_cus, at, i, &n_sum);
@@ -780,9 +911,11 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     BatchAreas areas = batch_areas(n_ops, mode, dev->num_cus, at);
+    WsLease lease;
     if (areas.need() > 0) {
         if (!workspace) {
-            workspace = stream_workspace(dev, stream, areas.need());
+            lease.acquire(dev, stream, areas.need());
+            workspace = lease.ptr();
             workspace_bytes = workspace ? areas.need() : 0;
         }
         // a workspace without room for the split-K partials runs every GEMM
@@ -790,6 +923,40 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
         if (workspace && workspace_bytes < areas.need()) areas.split = 0;
         if (!workspace || workspace_bytes < areas.need() || (reinterpret_cast<uintptr_t>(workspace) & 15u))
             return BONSAI_B1_ERR_ARG;
+        if (!lease.ptr()) {
+            // the caller's workspace lies apart from every op's input and
+            // outputs (the library's own cannot overlap them)
+            const uintptr_t w0 = reinterpret_cast<uintptr_t>(workspace), w1 = w0 + areas.need();
+            auto apart = [&](const void *p, int rows, int64_t ld_bytes, int64_t row_bytes) {
+                if (!p || rows <= 0 || row_bytes <= 0) return true;
+                const uintptr_t p0 = reinterpret_cast<uintptr_t>(p);
+                const uintptr_t p1 = p0 + (size_t)(rows - 1) * (size_t)ld_bytes + (size_t)row_bytes;
+                return !(p0 < w1 && w0 < p1);
+            };
+            for (int i = 0; i < n_ops; ++i) {
+                const BatchOp b = at(i);
+                const bonsai_b1_linear_op &op = *b.op;
+                const int kind = epi_kind(b.epi);
+                const int n = op.w->out_dim;
+                bool ok = apart(op.act, op.batch, op.lda * 4, (int64_t)op.w->in_dim * 4);
+                if (kind == BONSAI_B1_EPI_PACKED) {
+                    const int split = b.epi->split;
+                    const int pcols = b.epi->act == BONSAI_B1_ACT_SWIGLU ? (n - split) / 2 : n - split;
+                    ok = ok && apart(op.out, op.batch, op.ldo * 4, (int64_t)split * 4) &&
+                         apart(b.epi->packed, op.batch, b.epi->ldp * 2, (int64_t)pcols * 2);
+                } else {
+                    ok = ok && apart(op.out, op.batch, op.ldo * 4,
+                                     (int64_t)(kind == BONSAI_B1_EPI_SWIGLU ? n / 2 : n) * 4);
+                }
+                if (kind == BONSAI_B1_EPI_GATE_RESIDUAL && b.epi->residual != op.out)
+                    ok = ok && apart(b.epi->residual, op.batch, b.epi->ldr * 4, (int64_t)n * 4) &&
+                         apart(b.epi->gate, 1, (int64_t)n * 4, (int64_t)n * 4);
+                if (!ok) {
+                    if (bad_op) *bad_op = i;
+                    return BONSAI_B1_ERR_ARG;
+                }
+            }
+        }
     }
     float *ybuf = areas.y ? reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + areas.y_off()) : nullptr;
     void *split_area = areas.split ? static_cast<uint8_t *>(workspace) + areas.split_off() : nullptr;
@@ -808,6 +975,19 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
         int out_cols = kind == BONSAI_B1_EPI_SWIGLU ? a.N / 2 : a.N;
         const BatchPath path = batch_path(a, mode);
         hipError_t e = hipSuccess;
+        // the range-safe packing of this op's input, unless the workspace
+        // holds it already
+        const float *rsc = nullptr;
+        if (uses_packing(path)) {
+            if (!(packed_act == a.act && packed_lda == a.lda && packed_m == a.M && packed_k == a.K)) {
+                e = b1::launch_pack_rows(a.act, a.lda, a.M, a.K, workspace, stream);
+                packed_act = a.act;
+                packed_lda = a.lda;
+                packed_m = a.M;
+                packed_k = a.K;
+            }
+            rsc = b1::pack_area_rsc(workspace, a.M, a.K);
+        }
         if (path != BatchPath::Packed) {
             // the linear, into the workspace first when an epilogue follows
             b1::LinearArgs la = a;
@@ -815,10 +995,16 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
                 la.out = ybuf;
                 la.ldo = a.N;
             }
-            switch (path) {
-            case BatchPath::Exact: e = b1::launch_exact(la, stream); break;
-            case BatchPath::Gemv: e = b1::launch_gemv(la, dev->num_cus, stream); break;
-            default: e = b1::launch_gemm(la, dev->num_cus, nullptr, 0, stream); break;
+            if (e == hipSuccess) {
+                switch (path) {
+                case BatchPath::Exact: e = b1::launch_exact(la, stream); break;
+                case BatchPath::Gemv: e = b1::launch_gemv_ws(la, dev->num_cus, nullptr, 0, stream); break;
+                case BatchPath::GemvPacked:
+                    e = b1::launch_gemv_packed(workspace, la.w, la.K, la.N, la.M, la.out, la.ldo, nonfinite,
+                                               dev->num_cus, stream, rsc);
+                    break;
+                default: e = b1::launch_gemm(la, dev->num_cus, nullptr, 0, stream); break;
+                }
             }
             if (e == hipSuccess && kind == BONSAI_B1_EPI_PACKED)
                 e = b1::launch_epi_packed(ybuf, a.N, a.M, a.N, g, a.out, a.ldo, stream);
@@ -827,18 +1013,12 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
         } else {
             int n_sum;
             const int last = fuse_span(n_ops, mode, dev->num_cus, at, i, &n_sum);
-            if (!(packed_act == a.act && packed_lda == a.lda && packed_m == a.M && packed_k == a.K)) {
-                e = b1::launch_pack(a.act, a.lda, a.M, a.K, workspace, a.K, stream);
-                packed_act = a.act;
-                packed_lda = a.lda;
-                packed_m = a.M;
-                packed_k = a.K;
-            }
             const int splits = kind == BONSAI_B1_EPI_NONE ? b1::gemm_splits(a.M, a.K, a.N, dev->num_cus) : 1;
+            g.rsc = rsc;
             if (e == hipSuccess) {
                 if (splits > 1 && split_area && areas.split >= b1::gemm_split_bytes(a.M, n_sum, splits))
                     e = b1::launch_gemm_packed_split(workspace, a.w, a.K, n_sum, a.M, a.out, a.ldo, nonfinite,
-                                                     dev->num_cus, splits, split_area, stream);
+                                                     dev->num_cus, splits, split_area, stream, rsc);
                 else
                     e = b1::launch_gemm_packed_epi(workspace, a.w, a.K, n_sum, a.M, a.out, a.ldo, nonfinite,
                                                    dev->num_cus, kind, g, stream);
@@ -943,15 +1123,24 @@ void bonsai_b1_linear_f32_f32(bonsai_b1_tensor *dst, int ith, int nth,
     }
     hipStream_t s = hipStreamPerThread;
     int32_t bad = 0;
-    int st = hipMemsetAsync(di->cb_counter, 0, sizeof(int32_t), s) == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
-    if (st == BONSAI_B1_OK)
-        st = bonsai_b1_linear_f32(static_cast<const float *>(act->data), lda, wt->data, in_dim, out_dim,
-                                  batch, static_cast<float *>(dst->data), ldo, BONSAI_B1_MODE_AUTO,
-                                  di->cb_counter, s);
-    if (st == BONSAI_B1_OK &&
-        (hipMemcpyAsync(&bad, di->cb_counter, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
-         hipStreamSynchronize(s) != hipSuccess))
-        st = BONSAI_B1_ERR_HIP;
+    // The op in AUTO mode, then, if that made non-finite outputs, again in
+    // EXACT mode (the reference's scalar arithmetic): the reference aborts
+    // only when its own fp32 sums are non-finite, so a value FAST mode alone
+    // cannot represent must not abort here.
+    auto run = [&](int mode) {
+        int st = hipMemsetAsync(di->cb_counter, 0, sizeof(int32_t), s) == hipSuccess ? BONSAI_B1_OK
+                                                                                      : BONSAI_B1_ERR_HIP;
+        if (st == BONSAI_B1_OK)
+            st = bonsai_b1_linear_f32(static_cast<const float *>(act->data), lda, wt->data, in_dim, out_dim, batch,
+                                      static_cast<float *>(dst->data), ldo, mode, di->cb_counter, s);
+        if (st == BONSAI_B1_OK &&
+            (hipMemcpyAsync(&bad, di->cb_counter, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+             hipStreamSynchronize(s) != hipSuccess))
+            st = BONSAI_B1_ERR_HIP;
+        return st;
+    };
+    int st = run(BONSAI_B1_MODE_AUTO);
+    if (st == BONSAI_B1_OK && bad) st = run(BONSAI_B1_MODE_EXACT);
     if (st != BONSAI_B1_OK) {
         fprintf(stderr, "B1_FATAL: b1_linear failed: %s (in_dim=%d out_dim=%d)\n",
                 bonsai_b1_status_string(st), in_dim, out_dim);

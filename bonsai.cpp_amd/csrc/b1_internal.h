@@ -23,6 +23,10 @@ struct GemmEpi {
     int64_t ldpw = 0;       // its row stride in dwords (a multiple of 4)
     int split = 0;          // a multiple of 32
     int act = 0;            // 0 none, 1 GELU-tanh
+    // per-row output scales of range-safe packing ([M], powers of two; 1
+    // for rows packed unscaled), or nullptr: y[m][n] *= rsc[m] before the
+    // epilogue
+    const float *rsc = nullptr;
 };
 
 struct LinearArgs {
@@ -33,6 +37,7 @@ struct LinearArgs {
     float *out;         // [M][ldo] fp32
     int64_t ldo;        // elements
     int32_t *nonfinite; // optional device counter
+    const float *rsc = nullptr; // packed inputs only: row scales (see GemmEpi)
 };
 
 // fp32 VALU kernel in the reference scalar order; any K % 32 == 0.
@@ -40,9 +45,9 @@ hipError_t launch_exact(const LinearArgs &a, hipStream_t s);
 
 // fp16 MFMA GEMM; requires K % 64 == 0, lda % 4 == 0, act 16-byte aligned.
 // With a workspace of gemm_workspace_bytes(a) bytes (> 0 when K % 384 == 0)
-// the activations are packed to fp16
-// once and streamed into LDS directly; otherwise the kernel converts them
-// while staging each tile.
+// the activations are packed to fp16 once (range-safe, launch_pack_rows)
+// and streamed into LDS directly; otherwise the kernel converts them while
+// staging each tile, and launch_fixup_rows follows.
 bool gemm_supported(const LinearArgs &a);
 size_t gemm_workspace_bytes(const LinearArgs &a);
 // With room for the split-K partials after the packing (256-byte aligned),
@@ -73,7 +78,23 @@ hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N
 // order by a second kernel.
 hipError_t launch_gemm_packed_split(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
                                     int64_t ldo, int32_t *nonfinite, int num_cus, int splits, void *partials,
-                                    hipStream_t s);
+                                    hipStream_t s, const float *rsc = nullptr);
+
+// Range-safe packing of the fp32 entry points' activations into a packing
+// area of pack_area_bytes(M, K) bytes (16-byte aligned): the packed fp16
+// rows (row stride K) and, 256-byte aligned after them, M row scales
+// (pack_area_rsc): a row whose largest |a| would overflow fp16 is packed
+// times 2^-e and gets scale 2^e (every other row 1 and the plain packing's
+// bits), for the GEMM's epilogue to undo.
+size_t pack_area_bytes(int M, int K);
+float *pack_area_rsc(void *area, int M, int K);
+hipError_t launch_pack_rows(const float *act, int64_t lda, int M, int K, void *area, hipStream_t s);
+
+// Rows of a linear holding activations beyond the fp16 range (|a| >=
+// 65520), recomputed exactly (EXACT mode's bits) over what a kernel that
+// converts fp32 activations itself wrote; other rows are only read.  Needs
+// 16-byte aligned activation rows.
+hipError_t launch_fixup_rows(const LinearArgs &a, hipStream_t s);
 // The same GEMM with a fused epilogue (kind 0 plain, 1 gate-residual,
 // 2 SwiGLU with N = 2 glu_h, glu_h % 32 == 0, out [M][ldo >= glu_h],
 // 3 fp32 / packed fp16 columns with N % 32 == 0; with split > 0, out 16-byte
@@ -106,11 +127,20 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s);
 
 constexpr int kGemvMaxM = 16;
 
+// The small-M kernel from fp32 activations, range-safe: with a workspace of
+// gemv_workspace_bytes(a) bytes (> 0 when K % 256 == 0) they are packed
+// once (launch_pack_rows) and the kernel reads the packing; otherwise it
+// converts them itself and launch_fixup_rows follows.
+size_t gemv_workspace_bytes(const LinearArgs &a);
+hipError_t launch_gemv_ws(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s);
+
 // The small-M kernel over packed fp16 activations (the layout launch_pack
-// writes, row stride K): M <= 16, gemm_packed_ok(M, K, N), K % 256 == 0.
+// writes, row stride K): M <= 16, K % 256 == 0, weights and packing under
+// 2^31 bytes (gemv_packed_ok adds the packed entry's gemm_packed_ok); rsc:
+// row scales of launch_pack_rows, or nullptr.
 bool gemv_packed_ok(int M, int K, int N);
 hipError_t launch_gemv_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
-                              int32_t *nonfinite, int num_cus, hipStream_t s);
+                              int32_t *nonfinite, int num_cus, hipStream_t s, const float *rsc = nullptr);
 
 // GELU-tanh over [rows][cols] fp32 (cols % 4 == 0, rows 16-byte aligned via
 // ld % 4 == 0); the fused form writes packed fp16 activations (pack rules).

@@ -96,6 +96,10 @@ __device__ __forceinline__ void dma_lds16(const void *src, void *lds) {
 __device__ __forceinline__ void dma_lds12(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 12, 0, 0);
 }
+// global_load_lds_dword: lane i's 4 bytes land at lds + 4 i.
+__device__ __forceinline__ void dma_lds4(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 4, 0, 0);
+}
 
 // Raw buffer loads with range checking (offsets at or past num_records read
 // zeros); word 3 of the resource for gfx9-family raw buffers.
@@ -711,6 +715,153 @@ __global__ __launch_bounds__(256) void b1_pack_act_kernel(const float *__restric
     }
 }
 
+// The same packing for the fp32 entry points, range-safe: a row whose
+// largest |a| would overflow fp16 (>= 65520, the RNE rounding threshold of
+// 65504) is first multiplied by 2^-e, e >= 1 chosen so that its largest
+// magnitude lands in [2^14, 2^15), and rsc[row] = 2^e tells the GEMM to
+// multiply that row's outputs back.  Scaling by a power of two is exact in
+// fp32 and in the fp16 rounding (short of the fp16 subnormal range, where
+// values are below 2^-24 of the row's largest), so the row keeps fp16
+// relative precision instead of turning into +-inf; every other row has e =
+// 0, rsc = 1, and exactly the bits of b1_pack_act_kernel.  NaN inputs stay
+// NaN; an inf keeps e = 0 (the reference's fp32 sums are non-finite there
+// too).  One row is handled by 1, 2 or 4 waves (wpr = 1 << wpr_log2) of a
+// 4-wave work-group, each lane holding up to U (block, quad) units of 8
+// elements in registers, so the row is read once; U == 0: any length, read
+// twice.
+template <int U, bool NT>
+__global__ __launch_bounds__(256) void b1_pack_rows_kernel(const float *__restrict__ act, int64_t lda,
+                                                           uint32_t *__restrict__ ah, int64_t ldw,
+                                                           float *__restrict__ rsc, int M, int K, int wpr_log2) {
+    __shared__ float wmax[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wpr = 1 << wpr_log2;
+    const int row = blockIdx.x * (4 >> wpr_log2) + (wave >> wpr_log2);
+    const int sub = wave & (wpr - 1);
+    const bool valid = row < M;
+    const int units = K / 8; // (block, quad): elements 32 blk + 4 c .. +3 and 16 later
+    const float *xr = act + (size_t)(valid ? row : 0) * lda;
+    uint32_t *pr = ah + (size_t)(valid ? row : 0) * ldw;
+    auto col = [](int u) { return (u >> 2) * 32 + (u & 3) * 4; };
+    auto amax4 = [](float m, const floatx4 &v) {
+        return __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fmaxf(__builtin_fabsf(v[0]), __builtin_fabsf(v[1]))),
+                               __builtin_fmaxf(__builtin_fabsf(v[2]), __builtin_fabsf(v[3])));
+    };
+    const int stride = 64 * wpr; // units between a lane's consecutive units
+    const int u0 = sub * 64 + lane;
+
+    floatx4 lo[U > 0 ? U : 1], hi[U > 0 ? U : 1];
+    float m = 0.0f;
+    if constexpr (U > 0) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int u = u0 + i * stride;
+            if (valid && u < units) {
+                lo[i] = load_f4<NT>(xr + col(u));
+                hi[i] = load_f4<NT>(xr + col(u) + 16);
+            } else {
+                lo[i] = hi[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < U; ++i) m = amax4(amax4(m, lo[i]), hi[i]);
+    } else {
+        for (int u = u0; valid && u < units; u += stride)
+            m = amax4(amax4(m, load_f4<NT>(xr + col(u))), load_f4<NT>(xr + col(u) + 16));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
+    if (wpr > 1) {
+        if (lane == 0) wmax[wave] = m;
+        __syncthreads();
+        const int w0 = wave & ~(wpr - 1);
+        for (int j = 0; j < wpr; ++j) m = __builtin_fmaxf(m, wmax[w0 + j]);
+    }
+    // e = 0 unless the row overflows fp16; then m = 2^E (1.f), E >= 15 and
+    // e = E - 14 (at most 113, so 2^-e and 2^e are normal floats)
+    int e = 0;
+    if (m >= 65520.0f && m <= 3.40282347e38f) e = (int)((__builtin_bit_cast(uint32_t, m) >> 23) & 0xff) - 127 - 14;
+    const float down = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
+    if (valid && sub == 0 && lane == 0) rsc[row] = __builtin_bit_cast(float, (uint32_t)(127 + e) << 23);
+    auto store = [&](int u, floatx4 l, floatx4 h) {
+        if (e) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                l[j] *= down;
+                h[j] *= down;
+            }
+        }
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = pack_f16(l[j], h[j]);
+        *reinterpret_cast<u32x4 *>(pr + (u >> 2) * 16 + (u & 3) * 4) = v;
+    };
+    if constexpr (U > 0) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int u = u0 + i * stride;
+            if (valid && u < units) store(u, lo[i], hi[i]);
+        }
+    } else {
+        for (int u = u0; valid && u < units; u += stride)
+            store(u, load_f4<NT>(xr + col(u)), load_f4<NT>(xr + col(u) + 16));
+    }
+}
+
+// Exact recomputation of the rows that the paths converting fp32
+// activations inside their own kernel (the fused-conversion GEMM and the
+// small-M kernels, used without a workspace) cannot take in fp16: a row
+// holding an |a| >= 65520 (or an inf) is computed again in the reference's
+// scalar order, the arithmetic of b1_exact_kernel, so its outputs are
+// EXACT mode's bit for bit.  One work-group per row; other rows only cost a
+// read (16-byte aligned rows: the callers' fp32 kernels require them).  The
+// non-finite counter is corrected by the change in the count of non-finite
+// values the row's outputs make.
+constexpr int kFixKC = 2048; // activations staged in LDS per pass
+__global__ __launch_bounds__(256) void b1_fixup_rows_kernel(LinearArgs p) {
+#pragma clang fp contract(off)
+    __shared__ float as[kFixKC];
+    const int row = blockIdx.x;
+    const float *xr = p.act + (size_t)row * p.lda;
+    int over = 0;
+    for (int k = threadIdx.x * 4; k < p.K; k += 1024) {
+        const floatx4 v = *reinterpret_cast<const floatx4 *>(xr + k);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) over |= __builtin_fabsf(v[j]) >= 65520.0f;
+    }
+    if (!__syncthreads_or(over)) return;
+    const int nb = p.K / 32;
+    int delta = 0;
+    for (int n0 = 0; n0 < p.N; n0 += 256) {
+        const int n = n0 + threadIdx.x;
+        const uint16_t *wr = reinterpret_cast<const uint16_t *>(p.w + (size_t)(n < p.N ? n : 0) * nb * 6);
+        float sum = 0.0f;
+        for (int kc = 0; kc < p.K; kc += kFixKC) {
+            const int klen = min(kFixKC, p.K - kc);
+            __syncthreads();
+            for (int i = threadIdx.x; i < klen; i += 256) as[i] = xr[kc + i];
+            __syncthreads();
+            for (int b = 0; b < klen / 32; ++b) {
+                const uint16_t *blk = wr + (size_t)(kc / 32 + b) * 3;
+                const float scale = (float)__builtin_bit_cast(_Float16, blk[0]);
+                const uint32_t bits = (uint32_t)blk[1] | ((uint32_t)blk[2] << 16);
+                float bs = 0.0f;
+                for (int i = 0; i < 32; ++i) {
+                    const float a = as[b * 32 + i];
+                    bs = ((bits >> i) & 1u) ? bs + a : bs - a;
+                }
+                sum = sum + scale * bs;
+            }
+        }
+        if (n < p.N) {
+            float *o = p.out + (size_t)row * p.ldo + n;
+            delta += !__builtin_isfinite(sum) - !__builtin_isfinite(*o);
+            *o = sum;
+        }
+    }
+    if (p.nonfinite && delta) atomicAdd(p.nonfinite, delta);
+}
+
 // ------------------------------------------------------------- gemm (lds) --
 //
 // Wide-tile GEMM over pre-packed fp16 activations.  Work-group tile BM x BN,
@@ -746,9 +897,12 @@ struct GemmLdsCfg {
     static constexpr int CG = WN / 64;                // 64-column weight load groups per wave
     static constexpr int BWAVE = CG * 2 * 1024;       // weight bytes per wave per slot
     static constexpr int BSTAGE = NW * BWAVE;         // weight bytes per slot
-    // Weight slots take the bottom of LDS and activation slots follow.
+    // Weight slots take the bottom of LDS and activation slots follow; then
+    // two tile-parity buffers of the BM rows' output scales (row scales of
+    // range-safe packing, when the launch has them).
     static constexpr int ABASE = STAGES * BSTAGE;
-    static constexpr int LDS = STAGES * (ASTAGE + BSTAGE);
+    static constexpr int RSC = STAGES * (ASTAGE + BSTAGE);
+    static constexpr int LDS = RSC + 2 * BM * 4;
     static constexpr int GROUP_M = 4;                 // tile grouping along M
     static constexpr int EPI_STORES = MT * NTL * 4;   // 16-byte stores per lane, full tile
     static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
@@ -1204,8 +1358,19 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
         kst0 = split * nstage;
         uout = out + (size_t)split * (size_t)pstride;
     };
+    // Row scales of the tile (epi.rsc, range-safe packing): waves 0 and 1
+    // copy the BM values into the tile's parity buffer, ahead of its first
+    // stage, so they count as part of that stage in the vmcnt waits.
+    const bool rows_scaled = epi.rsc != nullptr && ksplit == 1;
+    int parity = 0;
+    auto issue_rsc = [&](int par) {
+        static_assert(BM == 128, "two waves copy the row scales");
+        if (rows_scaled && wave < 2)
+            dma_lds4(epi.rsc + min(m0 + 64 * wave + lane, M - 1), smem + C::RSC + par * BM * 4 + wave * 256);
+    };
     unit_origin(unit);
     setup(m0, n0);
+    issue_rsc(parity);
 #pragma unroll
     for (int t = 0; t < STAGES - 1; ++t) issue(kst0 + t, t);
     int prev_stores = 0; // stores the previous epilogue left: 0 none, 1 scalar, 2 vector
@@ -1254,15 +1419,38 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 
         // Slots 0..STAGES-2 were last read before the final barrier: fetch
         // the next tile's first STAGES-1 stages now, then store this tile.
-        const int cm0 = m0, cn0 = n0;
+        const int cm0 = m0, cn0 = n0, cpar = parity;
         float *const cout = uout;
         unit += gridDim.x;
         const bool more = unit < nunits;
         if (more) {
             unit_origin(unit);
             setup(m0, n0);
+            parity ^= 1;
+            issue_rsc(parity);
 #pragma unroll
             for (int t = 0; t < STAGES - 1; ++t) issue(kst0 + t, t);
+        }
+        if (rows_scaled) {
+            // this tile's rows: token m0 + 32 mt + li in every accumulator
+            // element of lane (li, g), sub-tile mt; the scales landed before
+            // the tile's last barrier (its last stage waits for everything)
+            const float *rs = reinterpret_cast<const float *>(smem + C::RSC + cpar * BM * 4);
+            float sc[C::MT];
+            int any = 0;
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt) {
+                sc[mt] = rs[32 * mt + li];
+                any |= sc[mt] != 1.0f;
+            }
+            if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) acc[mt][nt][v] *= sc[mt];
+            }
         }
         prev_stores = epilogue(cm0, cn0, cout);
         if (!more) break;
@@ -1272,10 +1460,12 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 // Split-K reduction: out[m][n] = sum over s = 0..S-1, in that order, of
 // part[s][m][n] (slices pstride apart, rows ldp apart, ldp % 4 == 0), with
 // the non-finite count of the sums.
+// rsc: row scales of range-safe packing (or nullptr), applied to the sum.
 __global__ __launch_bounds__(256) void b1_splitk_reduce_kernel(const float *__restrict__ part, int64_t ldp,
                                                                int64_t pstride, int S, int M, int N,
                                                                float *__restrict__ out, int64_t ldo,
-                                                               int32_t *nonfinite, int vec) {
+                                                               int32_t *nonfinite, int vec,
+                                                               const float *__restrict__ rsc) {
     const int q = (N + 3) / 4; // 4-column units per row
     const int64_t units = (int64_t)M * q;
     int bad = 0;
@@ -1287,6 +1477,11 @@ __global__ __launch_bounds__(256) void b1_splitk_reduce_kernel(const float *__re
             const floatx4 v = *reinterpret_cast<const floatx4 *>(src + (size_t)sp * pstride);
 #pragma unroll
             for (int r = 0; r < 4; ++r) sum[r] += v[r];
+        }
+        if (rsc) {
+            const float sc = rsc[m];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sum[r] *= sc;
         }
         float *dst = out + (size_t)m * ldo + c;
         if (vec && c + 4 <= N) {
@@ -1683,6 +1878,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv2_kernel(LinearArgs p, i
         for (int w = 0; w < kGvWaves; ++w) sum += red[(w * kGvMaxRG + r) * 64 + ln][v];
         const int n = (rg0 + r) * 16 + c;
         if (tok < p.M && n < p.N) {
+            if (PACKED && p.rsc) sum *= p.rsc[tok];
             bad += !__builtin_isfinite(sum);
             p.out[(size_t)tok * p.ldo + n] = sum;
         }
@@ -1725,8 +1921,52 @@ bool gemm_packed_ok(int M, int K, int N) {
            w_bytes < (1ull << 32);
 }
 
+static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t pack_area_bytes(int M, int K) { return round256((size_t)M * K * 2) + round256((size_t)M * 4); }
+
 size_t gemm_workspace_bytes(const LinearArgs &a) {
-    return gemm_packed_ok(a.M, a.K, a.N) && fast_layout_ok(a) ? (size_t)a.M * a.K * 2 : 0;
+    return gemm_packed_ok(a.M, a.K, a.N) && fast_layout_ok(a) ? pack_area_bytes(a.M, a.K) : 0;
+}
+
+float *pack_area_rsc(void *area, int M, int K) {
+    return reinterpret_cast<float *>(static_cast<uint8_t *>(area) + round256((size_t)M * K * 2));
+}
+
+hipError_t launch_pack_rows(const float *act, int64_t lda, int M, int K, void *area, hipStream_t s) {
+    const int units = K / 8;
+    int wl = 0, per = 0;
+    for (wl = 0; wl <= 2; ++wl) {
+        per = (units + (64 << wl) - 1) / (64 << wl);
+        if (per <= 8) break;
+    }
+    if (wl > 2) {
+        wl = 2;
+        per = 0; // read twice
+    }
+    const int rows_per_wg = 4 >> wl;
+    const dim3 grid((M + rows_per_wg - 1) / rows_per_wg);
+    const bool nt = (uint64_t)M * (uint64_t)K * 4 > kNtInputBytes;
+    uint32_t *pk = static_cast<uint32_t *>(area);
+    float *rsc = pack_area_rsc(area, M, K);
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, act, lda, pk, (int64_t)K / 2, rsc, M, K, wl);
+    };
+#define B1_PACK_ROWS(U)                                                                                         \
+    (nt ? go(b1_pack_rows_kernel<U, true>) : go(b1_pack_rows_kernel<U, false>))
+    if (per == 0) B1_PACK_ROWS(0);
+    else if (per <= 1) B1_PACK_ROWS(1);
+    else if (per <= 2) B1_PACK_ROWS(2);
+    else if (per <= 4) B1_PACK_ROWS(4);
+    else if (per <= 6) B1_PACK_ROWS(6);
+    else B1_PACK_ROWS(8);
+#undef B1_PACK_ROWS
+    return hipGetLastError();
+}
+
+hipError_t launch_fixup_rows(const LinearArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(b1_fixup_rows_kernel, dim3(a.M), dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 bool pack_supported(const float *act, int64_t lda, int M, int K) {
@@ -1778,6 +2018,8 @@ template <int EPI>
 static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
                                        int64_t ldo, int32_t *nonfinite, int num_cus, const GemmEpi &epi,
                                        hipStream_t s, int ksplit = 1, float *partials = nullptr) {
+    // (with ksplit > 1 the row scales epi.rsc go to the reduction, not the
+    // GEMM, which writes plain partial products)
     auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages, EPI>;
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
@@ -1805,7 +2047,7 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
         const int64_t want = (q + 255) / 256, cap = (int64_t)(num_cus > 0 ? num_cus : 256) * 8;
         const int rgrid = (int)(want < cap ? want : cap);
         hipLaunchKernelGGL(b1_splitk_reduce_kernel, dim3(rgrid), dim3(256), 0, s, partials, ldp, pstride, ksplit, M,
-                           N, out, ldo, nonfinite, (int)(al16(out) && ldo % 4 == 0));
+                           N, out, ldo, nonfinite, (int)(al16(out) && ldo % 4 == 0), epi.rsc);
         return hipGetLastError();
     }
     int vec_store = al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 22);
@@ -1823,8 +2065,10 @@ hipError_t launch_gemm_packed(const void *packed, const uint8_t *w, int K, int N
 
 hipError_t launch_gemm_packed_split(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
                                     int64_t ldo, int32_t *nonfinite, int num_cus, int splits, void *partials,
-                                    hipStream_t s) {
-    return launch_gemm_packed_t<0>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, GemmEpi{}, s, splits,
+                                    hipStream_t s, const float *rsc) {
+    GemmEpi epi;
+    epi.rsc = rsc;
+    return launch_gemm_packed_t<0>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s, splits,
                                    static_cast<float *>(partials));
 }
 
@@ -1843,30 +2087,34 @@ hipError_t launch_gemm_packed_epi(const void *packed, const uint8_t *w, int K, i
 hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s) {
     const size_t need = gemm_workspace_bytes(a);
     if (need == 0 || workspace == nullptr || ws_bytes < need) {
-        // Fused-conversion kernel: no workspace needed.
+        // Fused-conversion kernel: no workspace needed; rows its fp16
+        // conversion overflows are then computed exactly.
         constexpr int BM = 128, BN = 512, WM = 128, WN = 64;
         using C = GemmCfg<BM, BN, WM, WN>;
         const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
         hipLaunchKernelGGL((b1_gemm_fused_kernel<BM, BN, WM, WN>), dim3(tiles_m * tiles_n), dim3(C::NT), 0, s, a,
                            tiles_n);
-        return hipGetLastError();
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? launch_fixup_rows(a, s) : e;
     }
-    hipError_t e = launch_pack(a.act, a.lda, a.M, a.K, workspace, a.K, s);
+    hipError_t e = launch_pack_rows(a.act, a.lda, a.M, a.K, workspace, s);
     if (e != hipSuccess) return e;
+    const float *rsc = pack_area_rsc(workspace, a.M, a.K);
     // the split-K partials after the packing, when the workspace holds them
     const int splits = gemm_splits(a.M, a.K, a.N, num_cus);
-    const size_t pack_area = (need + 255) & ~(size_t)255;
-    if (splits > 1 && ws_bytes >= pack_area + gemm_split_bytes(a.M, a.N, splits))
+    if (splits > 1 && ws_bytes >= need + gemm_split_bytes(a.M, a.N, splits))
         return launch_gemm_packed_split(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, splits,
-                                        static_cast<uint8_t *>(workspace) + pack_area, s);
-    return launch_gemm_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, s);
+                                        static_cast<uint8_t *>(workspace) + need, s, rsc);
+    GemmEpi epi;
+    epi.rsc = rsc;
+    return launch_gemm_packed_epi(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, 0, epi, s);
 }
 
 size_t gemm_workspace_bytes_total(const LinearArgs &a, int num_cus) {
     const size_t pack = gemm_workspace_bytes(a);
     if (pack == 0) return 0;
     const int splits = gemm_splits(a.M, a.K, a.N, num_cus);
-    return splits > 1 ? ((pack + 255) & ~(size_t)255) + gemm_split_bytes(a.M, a.N, splits) : pack;
+    return splits > 1 ? pack + gemm_split_bytes(a.M, a.N, splits) : pack;
 }
 
 hipError_t launch_quantize(const float *w, int64_t ldw, int K, int N, void *packed, int order, hipStream_t s) {
@@ -1999,16 +2247,36 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
     return hipGetLastError();
 }
 
+size_t gemv_workspace_bytes(const LinearArgs &a) {
+    return gemv_supported(a) && gemv_staged(a.K, a.N) && (uint64_t)a.M * (uint64_t)a.K * 2 < (1ull << 31)
+               ? pack_area_bytes(a.M, a.K)
+               : 0;
+}
+
+hipError_t launch_gemv_ws(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s) {
+    const size_t need = gemv_workspace_bytes(a);
+    hipError_t e;
+    if (need == 0 || workspace == nullptr || ws_bytes < need) {
+        // conversion inside the small-M kernel, then the exact rows
+        e = launch_gemv(a, num_cus, s);
+        return e == hipSuccess ? launch_fixup_rows(a, s) : e;
+    }
+    e = launch_pack_rows(a.act, a.lda, a.M, a.K, workspace, s);
+    if (e != hipSuccess) return e;
+    return launch_gemv_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, s,
+                              pack_area_rsc(workspace, a.M, a.K));
+}
+
 bool gemv_packed_ok(int M, int K, int N) {
     return M >= 1 && M <= kGemvMaxM && gemm_packed_ok(M, K, N) && gemv_staged(K, N) &&
            (uint64_t)M * (uint64_t)K * 2 < (1ull << 31);
 }
 
 hipError_t launch_gemv_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
-                              int32_t *nonfinite, int num_cus, hipStream_t s) {
+                              int32_t *nonfinite, int num_cus, hipStream_t s, const float *rsc) {
     const hipError_t attr_err = gemv_attrs();
     if (attr_err != hipSuccess) return attr_err;
-    const LinearArgs a{static_cast<const float *>(packed), K, w, K, N, M, out, ldo, nonfinite};
+    const LinearArgs a{static_cast<const float *>(packed), K, w, K, N, M, out, ldo, nonfinite, rsc};
     int nwg, groups, mp_log2;
     gemv_grid(a, num_cus, &nwg, &groups, &mp_log2);
     hipLaunchKernelGGL(b1_gemv2_kernel<true>, dim3(nwg), dim3(kGvWaves * 64), kGv2Lds, s, a, groups, mp_log2);

@@ -70,8 +70,16 @@ enum {
  *  AUTO  : FAST numerics; small batches (M <= 16) take the bandwidth-bound
  *          kernel, larger ones the MFMA GEMM.
  *  FAST  : activations rounded to fp16 (RNE), weights expanded to exactly
- *          +-scale in fp16, fp32 MFMA accumulation.  Requires |act| < 65504.
- *          Per-element error vs the reference <= 1e-2 of max(|y|, rms(y)).
+ *          +-scale in fp16, fp32 MFMA accumulation.  Per-element error vs
+ *          the reference <= 1e-2 of max(|y|, rms(y)).  Any finite fp32
+ *          activation is accepted by the fp32 entry points: a row whose
+ *          largest |act| would overflow fp16 (>= 65520) is packed times a
+ *          power of two 2^-e, and its outputs are multiplied by 2^e, which
+ *          keeps fp16 relative precision; where the kernel converts
+ *          activations itself (no workspace, see below) such a row is
+ *          computed again in EXACT arithmetic instead.  Entry points that
+ *          take packed fp16 activations get whatever their producer wrote
+ *          (its inputs beyond 65504 are +-inf there).
  *  EXACT : fp32 VALU in the reference's scalar summation order
  *          (src/b1_0_kernel.h:253-277); bit-identical to that path.
  *  GEMM / GEMV : FAST numerics with the kernel forced (for benchmarks). */
@@ -104,16 +112,25 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
                          hipStream_t stream);
 
 /*
- * The FAST GEMM packs the activations to fp16 once into a device workspace
- * of bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) bytes (0 when
- * the call needs none).  bonsai_b1_linear_f32 keeps one library-owned
- * workspace per (device, stream), grown on demand with hipMalloc; while a
- * stream is being captured it never allocates and, lacking a large enough
- * buffer, runs the GEMM variant that converts activations tile by tile.
- * bonsai_b1_linear_f32_ws takes the caller's workspace instead (NULL or too
- * small selects that same variant) and never allocates.  Results do not
- * depend on the variant.  Concurrent calls on one stream are ordered; calls
- * on different streams use different workspaces.
+ * The FAST kernels pack the activations to fp16 once (with the row scales
+ * of the range-safe packing, and, for shapes that split along K, the split
+ * partials after them) into a device workspace of
+ * bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) bytes (0 when the
+ * call needs none).  bonsai_b1_linear_f32 keeps library-owned workspaces
+ * per (device, stream), grown on demand with hipMalloc; while a stream is
+ * being captured it never allocates and, lacking a large enough buffer,
+ * runs the kernel variant that converts activations tile by tile.  A buffer
+ * handed out during a capture is pinned, since the graph holds its address:
+ * the library never frees or replaces it (growth allocates another one) and
+ * later calls on the capture stream may share it, so replay such a graph on
+ * that stream (or ordered with it).  bonsai_b1_linear_f32_ws takes the
+ * caller's workspace instead (NULL or too small selects that same variant)
+ * and never allocates.  The variants agree bit for bit, except (a) for a
+ * shape split along K, which the variant without room for the partials sums
+ * unsplit (the same values up to the order of the K summation), and (b) for
+ * rows beyond the fp16 range, which the converting variant computes in
+ * EXACT arithmetic.  Concurrent calls on one stream are ordered; calls on
+ * different streams use different workspaces.
  */
 size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode);
 
@@ -123,7 +140,9 @@ int bonsai_b1_linear_f32_ws(const float *act, int64_t lda, const void *w,
                             void *workspace, size_t workspace_bytes,
                             hipStream_t stream);
 
-/* Frees every library-owned workspace (all devices); waits for the device. */
+/* Frees every library-owned workspace (all devices), pinned ones included:
+ * destroy graphs captured with the library's workspace first.  Waits for
+ * the device. */
 void bonsai_b1_release_workspaces(void);
 
 /*
@@ -185,11 +204,24 @@ int bonsai_b1_pack_act_f16_ld(const float *act, int64_t lda, int in_dim,
 /* out[m][n] for packed activations (in_dim % 384 == 0, packed 16-byte
  * aligned, w 4-byte aligned); same outputs as bonsai_b1_linear_f32 in
  * FAST/GEMM mode on the activations that were packed, or, for batch <= 16
- * with in_dim % 256 == 0, as its small-M (GEMV) mode.  Never allocates. */
+ * with in_dim % 256 == 0, as its small-M (GEMV) mode, bit for bit (for
+ * activations within the fp16 range).  A shape that bonsai_b1_linear_f32
+ * splits along K is split the same way, with the partials in the library's
+ * per-stream workspace (allocated on demand like bonsai_b1_linear_f32's;
+ * under capture without one it runs unsplit).  The _ws form takes the
+ * caller's workspace of bonsai_b1_linear_packed_workspace_bytes bytes
+ * (0: none needed; NULL or smaller: unsplit) and never allocates. */
 int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w,
                                 int in_dim, int out_dim, int batch,
                                 float *out, int64_t ldo, int32_t *nonfinite,
                                 hipStream_t stream);
+size_t bonsai_b1_linear_packed_workspace_bytes(int batch, int in_dim,
+                                               int out_dim);
+int bonsai_b1_linear_packed_f16_ws(const void *packed_act, const void *w,
+                                   int in_dim, int out_dim, int batch,
+                                   float *out, int64_t ldo,
+                                   int32_t *nonfinite, void *workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
 
 /*
  * A sequence of B1_0 linears on one stream: the linear dispatch of a
@@ -255,8 +287,10 @@ int bonsai_b1_linear(const float *act, const B1Weights *w, int batch,
  * dst->src[0] = act, dst->src[1] = packed weights, the userdata holds
  * {magic, in_dim, out_dim}.  Task ith == 0 runs the whole op on the calling
  * thread's current stream (hipStreamPerThread) and synchronises it; other
- * tasks return at once.  Like the reference, a non-finite output prints
- * "B1_FATAL_OUT" to stderr and abort()s.  Returns nothing.
+ * tasks return at once.  When AUTO mode's outputs hold a non-finite value
+ * the op runs again in EXACT mode (the reference's scalar arithmetic); like
+ * the reference, a non-finite output of that prints "B1_FATAL_OUT" to
+ * stderr and abort()s.  Returns nothing.
  */
 typedef struct bonsai_b1_tensor {
     int64_t ne[4];                    /* ne[0] = in_dim/out_dim, ne[1] = rows */

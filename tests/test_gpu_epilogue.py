@@ -49,9 +49,12 @@ def b1(torch):
 
 def plain_linear(torch, b1, a, w, n, mode):
     """The linear without an epilogue, as the fused-epilogue GEMM computes
-    it: a workspace that holds the packing only keeps the GEMM unsplit along
+    it: a workspace that holds the packing only (m*k fp16 values and m row
+    scales, each area rounded up to 256 bytes) keeps the GEMM unsplit along
     K (a split sums the K ranges in another order)."""
-    ws = torch.empty(a.shape[0] * a.shape[1] * 2 + 16, dtype=torch.uint8, device="cuda")
+    m, k = a.shape
+    ws = torch.empty((m * k * 2 + 255) // 256 * 256 + (m * 4 + 255) // 256 * 256, dtype=torch.uint8,
+                     device="cuda")
     return b1.linear(a, w, n, mode=mode, workspace=ws)
 
 
@@ -189,7 +192,7 @@ def test_norm_mod_matches_oracle(torch, b1, oracle, rows, h):
         from bonsai_b1 import synth
         n = 512
         w = synth.device_packed_weights(n, h, 82)
-        a = plain_linear(torch, b1, y, w, n, "gemm")
+        a = b1.linear(y, w, n, mode="gemm")     # split along K as the packed entry splits
         c = b1.linear_packed_f16(packed, w, h, n, rows)
         torch.cuda.synchronize()
         assert torch.equal(a, c)

@@ -374,23 +374,28 @@ def test_pack_act_layout_bit_exact(torch, b1, oracle):
     assert np.array_equal(got, want)
 
 
+def pack_area_bytes(m, k):
+    """The range-safe packing of an fp32 call: m*k fp16 values, then m row
+    scales, each area rounded up to 256 bytes."""
+    return (m * k * 2 + 255) // 256 * 256 + (m * 4 + 255) // 256 * 256
+
+
 def unsplit_linear(torch, b1, a, w, n, mode):
     """The fp32 entry with a workspace that holds the packing only, so the
-    GEMM runs unsplit along K (the packed entry, which takes no workspace,
-    never splits)."""
-    ws = torch.empty(a.shape[0] * a.shape[1] * 2 + 16, dtype=torch.uint8, device="cuda")
+    GEMM runs unsplit along K."""
+    ws = torch.empty(pack_area_bytes(*a.shape), dtype=torch.uint8, device="cuda")
     return b1.linear(a, w, n, mode=mode, workspace=ws)
 
 
 @pytest.mark.parametrize("m,k,n", [(200, 768, 600), (128, 384, 512), (1, 384, 40)])
 def test_linear_packed_matches_fused_entry(torch, b1, m, k, n):
     """pack + linear_packed gives bit-for-bit what bonsai_b1_linear_f32 gives
-    in GEMM mode unsplit along K (same kernels), including a padded output
-    stride."""
+    in GEMM mode (same kernels, split along K the same way), including a
+    padded output stride."""
     from bonsai_b1 import synth
     a = synth.device_activations(m, k, 41)
     w = synth.device_packed_weights(n, k, 42)
-    ref = unsplit_linear(torch, b1, a, w, n, "gemm")
+    ref = b1.linear(a, w, n, mode="gemm")
     out = torch.full((m, n + 12), 7.0, device="cuda")
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     packed = b1.pack_act_f16(a)
@@ -413,7 +418,7 @@ def test_linear_packed_small_m(torch, b1, m, k, n, mode):
     say(f"packed small-M ({m},{k},{n}) vs {mode}")
     a = synth.device_activations(m, k, 43)
     w = synth.device_packed_weights(n, k, 44)
-    ref = unsplit_linear(torch, b1, a, w, n, mode)
+    ref = b1.linear(a, w, n, mode=mode)
     out = torch.full((m, n + 12), 7.0, device="cuda")
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     packed = b1.pack_act_f16(a)
@@ -685,7 +690,7 @@ def test_split_k_counts_nonfinite(torch, b1):
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     y = b1.linear(a, w, n, mode="gemm", nonfinite=nf)
     nfu = torch.zeros(1, dtype=torch.int32, device="cuda")
-    ws = torch.empty(m * k * 2 + 16, dtype=torch.uint8, device="cuda")
+    ws = torch.empty(pack_area_bytes(m, k), dtype=torch.uint8, device="cuda")
     yu = b1.linear(a, w, n, mode="gemm", nonfinite=nfu, workspace=ws)
     torch.cuda.synchronize()
     bad = int((~torch.isfinite(y)).sum())

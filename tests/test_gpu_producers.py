@@ -57,9 +57,8 @@ def test_strided_producers_build_concatenated_input(torch, b1, m, k1, k2):
         w = synth.device_packed_weights(384, k, 73)
         y = b1.linear_packed_f16(buf, w, k, 384, m)
         cat = torch.cat([a1, b1.gelu_tanh(a2.contiguous())], 1)
-        # the fp32 entry unsplit along K, as the packed entry (no workspace) runs
-        ws = torch.empty(m * k * 2 + 16, dtype=torch.uint8, device="cuda")
-        yr = b1.linear(cat, w, 384, workspace=ws)
+        # the fp32 entry, split along K as the packed entry splits
+        yr = b1.linear(cat, w, 384)
         torch.cuda.synchronize()
         assert torch.equal(y, yr)
 
@@ -71,7 +70,9 @@ def test_swiglu_pack_matches_fused_epilogue(torch, b1, oracle, m, k, h):
     a = synth.device_activations(m, k, 74)
     w = synth.device_packed_weights(2 * h, k, 75)
     pa = b1.pack_act_f16(a)
-    y = b1.linear_packed_f16(pa, w, k, 2 * h, m)                 # [gates | values]
+    # [gates | values], unsplit along K as the fused epilogue runs (a
+    # workspace too small for split-K partials)
+    y = b1.linear_packed_f16(pa, w, k, 2 * h, m, workspace=torch.empty(16, dtype=torch.uint8, device="cuda"))
     p1 = b1.swiglu_pack_f16(y)
     out = b1.linear_packed_f16_epi(pa, w, k, 2 * h, m, "swiglu")  # fp32 [m, h]
     p2 = b1.pack_act_f16(out)
