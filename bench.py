@@ -4,13 +4,17 @@
 Default workload: the B1_0 GEMM at M=4096 (tokens), K=3072, N=12288 on
 synthetic data (activations N(0,1) fp32, random sign words, fp16 scales
 U[0.005, 0.05]), inputs resident in HBM before timing.  One step = one
-B1_0 linear over that batch.  Prints ONE JSON line (rank 0) with the metric,
-the MFMA roofline of the GEMM kernel, the small-M GEMV bandwidth (M=8,
-K=3072, N=18432, weight copies rotated past the 256 MB Infinity Cache) and
-the CPU baseline (the oracle's restatement of the reference AVX2 path) timed
-on this host on a bounded sample.
+B1_0 linear over that batch (the range-safe fp16 pack pass + the MFMA GEMM).
+Before any timing the shader clock is settled by running the step for a
+fixed wall time (--settle-s), and read while the GPU is still busy.  Prints
+ONE JSON line with the metric, the MFMA roofline of the GEMM kernel (and
+the pack pass timed alone), the small-M GEMV bandwidth (M=8, K=3072,
+N=18432, weight copies rotated past the 256 MB Infinity Cache), the other
+config shapes (C1, C3, C4, the C5 38-block step) and the CPU baseline (the
+oracle's restatement of the reference AVX2 path on this host, at the host's
+thread share and at the reference's default of 4 threads).
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--all] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--settle-s S] [--gpus 1] [--all] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -54,31 +58,34 @@ def time_launches(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall
 
 
-def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto", sample_clock=False):
-    a = synth.device_activations(m, k, 1)
-    w = synth.device_packed_weights(n, k, 2)
+def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto", inputs=None):
+    """The whole op from fp32 activations, bonsai_b1_linear_f32 with the
+    library's workspace: the range-safe pack pass, then the GEMM (split
+    along K where the shape asks for it)."""
+    if inputs is None:
+        inputs = (synth.device_activations(m, k, 1), synth.device_packed_weights(n, k, 2))
+    a, w = inputs
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    sclk = []
-    if sample_clock:   # read the shader clock ~1 s into the warm-up, while the GPU is busy
-        import threading
-        th = threading.Thread(target=lambda: (time.sleep(1.0), sclk.append(observed_sclk_mhz())), daemon=True)
-        th.start()
     ms, wall = time_launches(torch, lambda i: b1.linear(a, w, n, out=y, mode=mode), steps, warmup)
     flop = 2.0 * m * n * k
     return {"shape": [m, k, n], "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12,
-            "frac": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "wall_s": wall,
-            "sclk": sclk[0] if sclk else None, "inputs": (a, w)}
+            "frac": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "wall_s": wall, "inputs": (a, w)}
 
 
-def bench_gemm_kernel(torch, b1, a, w, n, steps, warmup):
-    """The GEMM kernel alone, launched through bonsai_b1_linear_packed_f16 on
-    activations packed once, timed with HIP events on its launch stream."""
+def bench_step_kernels(torch, b1, a, w, n, steps, warmup):
+    """The two kernels of the step, each timed alone with HIP events on its
+    launch stream: the GEMM kernel over packed activations
+    (bonsai_b1_linear_packed_f16_scaled: b1_gemm_kernel alone at an unsplit
+    shape) and the range-safe pack pass (bonsai_b1_pack_act_f16_scaled:
+    b1_pack_rows_kernel alone).  Returns (gemm ms, pack ms)."""
     m, k = a.shape
-    packed = b1.pack_act_f16(a)
+    packed, rs = b1.pack_act_f16_scaled(a)
     y = torch.empty((m, n), dtype=torch.float32, device="cuda")
-    ms, _ = time_launches(torch, lambda i: b1.linear_packed_f16(packed, w, k, n, m, out=y), steps, warmup)
-    return ms
+    kern_ms, _ = time_launches(torch, lambda i: b1.linear_packed_f16_scaled(packed, rs, w, k, n, m, out=y), steps,
+                               warmup)
+    pack_ms, _ = time_launches(torch, lambda i: b1.pack_act_f16_scaled(a, packed=packed, row_scale=rs), steps,
+                               warmup)
+    return kern_ms, pack_ms
 
 
 def committed_traffic(name):
@@ -275,16 +282,19 @@ def bench_single_stream_step(torch, b1, synth, blocks=38):
     return r
 
 
-def bench_c5_block_chain(torch, b1, synth, blocks=38):
-    """The C5 single-stream blocks as a chain of this library's kernels,
-    attention aside (src/diffuser_graph.cpp:477-538 in shape): per block,
-    LayerNorm + modulation written as packed fp16, linear1 3072 -> 21504,
-    the packed linear2 input built in place by two producers (the q columns
-    standing in for the attention output, columns 0-3071; GELU-tanh of the
-    MLP part, columns 3072-15359), and linear2 15360 -> 3072 with the
-    gate-residual epilogue updating the residual stream in place.  Block
-    i + 1 reads what block i wrote.  Timed again with GELU(MLP) written by
-    linear1's epilogue into linear2's packed input (4 kernels per block)."""
+def bench_c5_block_chain(torch, b1, synth, blocks=38, producer_form=False):
+    """The C5 step: 38 single-stream blocks as a chain of this library's
+    kernels, attention aside (src/diffuser_graph.cpp:477-538 in shape),
+    each block with its own resident weights (807 MB packed).  Per block:
+    LayerNorm + modulation written as packed fp16, linear1 3072 -> 21504
+    with its epilogue writing q/k/v as fp32 and GELU-tanh(MLP) straight into
+    columns 3072-15359 of linear2's packed input, the q columns (standing in
+    for the attention output) packed into columns 0-3071, and linear2 15360
+    -> 3072 with the gate-residual epilogue updating the residual stream in
+    place; block i + 1 reads what block i wrote.  Timed as a HIP graph
+    replay.  Also timed: the 76 GEMMs alone over inputs already packed (the
+    step's GEMM work), and, with producer_form, the chain with GELU(MLP) made
+    by a separate producer pass over linear1's fp32 output."""
     m, h, n1, k2 = 4608, 3072, 21504, 15360
     w1 = [synth.device_packed_weights(n1, h, 500 + i) for i in range(blocks)]
     w2 = [synth.device_packed_weights(h, k2, 600 + i) for i in range(blocks)]
@@ -297,7 +307,7 @@ def bench_c5_block_chain(torch, b1, synth, blocks=38):
     y1 = torch.empty((m, n1), device="cuda")
     p2 = torch.empty(m * k2 * 2, dtype=torch.uint8, device="cuda")
 
-    def step():
+    def step_producers():
         for i in range(blocks):
             b1.norm_mod(x, scale[i], shift[i], packed=p1)
             b1.linear_packed_f16(p1, w1[i], h, n1, m, out=y1)
@@ -305,9 +315,7 @@ def bench_c5_block_chain(torch, b1, synth, blocks=38):
             b1.gelu_tanh_pack_f16(y1[:, 3 * h:], packed=p2[h * 2:], ldp=k2)
             b1.linear_packed_f16_epi(p2, w2[i], k2, h, m, "gate_residual", gate=gate[i], residual=x, out=x)
 
-    def step_epilogue():
-        # linear1's epilogue: q/k/v as fp32, GELU(MLP) straight into
-        # columns 3072-15359 of linear2's packed input
+    def step():
         for i in range(blocks):
             b1.norm_mod(x, scale[i], shift[i], packed=p1)
             b1.linear_packed_f16_to_packed(p1, w1[i], h, n1, m, 3 * h, "gelu_tanh", out=y1[:, :3 * h],
@@ -315,15 +323,82 @@ def bench_c5_block_chain(torch, b1, synth, blocks=38):
             b1.pack_act_f16(y1[:, :h], packed=p2, ldp=k2)
             b1.linear_packed_f16_epi(p2, w2[i], k2, h, m, "gate_residual", gate=gate[i], residual=x, out=x)
 
+    o2 = torch.empty((m, h), device="cuda")
+
+    def step_gemms():
+        for i in range(blocks):
+            b1.linear_packed_f16(p1, w1[i], h, n1, m, out=y1)
+            b1.linear_packed_f16(p2, w2[i], k2, h, m, out=o2)
+
+    flop = 2.0 * m * (h * n1 + k2 * h) * blocks
     ms = graph_ms(torch, step, reps=2)
     finite = bool(torch.isfinite(x).all())
-    ms_epi = graph_ms(torch, step_epilogue, reps=2)
-    finite = finite and bool(torch.isfinite(x).all())
-    flop = 2.0 * m * (h * n1 + k2 * h) * blocks
+    ms_gemms = graph_ms(torch, step_gemms, reps=2)
+    r = {"blocks": blocks, "ms_per_step": ms, "gemm_tflops": flop / (ms * 1e-3) / 1e12,
+         "frac": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "kernels_per_block": 4,
+         "ms_per_step_gemms_only": ms_gemms, "gemms_only_tflops": flop / (ms_gemms * 1e-3) / 1e12,
+         "gemms_only_frac": flop / (ms_gemms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
+         "packed_weight_bytes": sum(t.numel() for t in w1 + w2)}
+    if producer_form:
+        r["ms_per_step_producer_form"] = graph_ms(torch, step_producers, reps=2)
+        finite = finite and bool(torch.isfinite(x).all())
+    r["residual_finite"] = finite
     del w1, w2
-    return {"blocks": blocks, "ms_per_step": ms, "gemm_tflops": flop / (ms * 1e-3) / 1e12,
-            "kernels_per_block": 5, "ms_per_step_epilogue": ms_epi,
-            "gemm_tflops_epilogue": flop / (ms_epi * 1e-3) / 1e12, "residual_finite": finite}
+    return r
+
+
+def bench_configs(torch, b1, synth, steps, warmup):
+    """The other config shapes, each from fp32 activations through
+    bonsai_b1_linear_f32 (pack pass + GEMM; split along K where the shape
+    asks for it): C1 (256 x 3072 -> 3072), C3 q/k/v and out-projection,
+    C4 up- and down-projection, GELU-tanh between them, and the C4 chain in
+    its fused form (GELU in the up-projection's epilogue, written as the
+    down-projection's packed input); then the C5 38-block step."""
+    out = {}
+    for name, shp in [("c1_parity", (256, 3072, 3072)), ("c3_qkv", (4608, 3072, 9216)),
+                      ("c3_out", (4608, 3072, 3072)), ("c4_up", (4608, 3072, 12288)),
+                      ("c4_down", (4608, 12288, 3072))]:
+        r = bench_gemm(torch, b1, synth, *shp, steps, warmup)
+        out[name] = {"shape": list(shp), "us": round(r["ms"] * 1e3, 2), "tflops": round(r["tflops"], 1),
+                     "frac": round(r["frac"], 4)}
+        log(f"[bench] {name} {shp}: {r['ms']*1e3:.1f} us {r['tflops']:.1f} TFLOP/s ({100*r['frac']:.1f}% of peak)")
+        del r
+    m, k, hid = 4608, 3072, 12288
+    a = synth.device_activations(m, k, 11)
+    wu = synth.device_packed_weights(hid, k, 12)
+    wd = synth.device_packed_weights(k, hid, 13)
+    y1 = torch.empty((m, hid), device="cuda")
+    g = torch.empty((m, hid), device="cuda")
+    pa = torch.empty(m * k * 2, dtype=torch.uint8, device="cuda")
+    rs = torch.empty(m, dtype=torch.float32, device="cuda")
+    ph = torch.empty(m * hid * 2, dtype=torch.uint8, device="cuda")
+    y2 = torch.empty((m, k), device="cuda")
+    b1.linear(a, wu, hid, out=y1)
+    gelu_ms = graph_ms(torch, lambda: [b1.gelu_tanh(y1, out=g) for _ in range(4)]) / 4
+
+    def chain():
+        b1.pack_act_f16_scaled(a, packed=pa, row_scale=rs)
+        b1.linear_packed_f16_to_packed(pa, wu, k, hid, m, 0, "gelu_tanh", packed_out=ph)
+        b1.linear_packed_f16(ph, wd, hid, k, m, out=y2)
+    chain_ms = graph_ms(torch, chain)
+    flop = 2.0 * m * k * hid * 2
+    out["c4_gelu"] = {"shape": [m, hid], "us": round(gelu_ms * 1e3, 2),
+                      "GBps": round(m * hid * 8 / (gelu_ms * 1e-3) / 1e9, 1),
+                      "frac_hbm": round(m * hid * 8 / (gelu_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    out["c4_chain"] = {"shape": [m, k, hid], "us": round(chain_ms * 1e3, 2),
+                       "tflops": round(flop / (chain_ms * 1e-3) / 1e12, 1),
+                       "frac": round(flop / (chain_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                       "form": "pack, up-projection with GELU-tanh in its epilogue written packed, down-projection"}
+    log(f"[bench] c4 GELU {gelu_ms*1e3:.1f} us; c4 chain {chain_ms*1e3:.1f} us "
+        f"({out['c4_chain']['tflops']:.0f} TFLOP/s)")
+    del a, wu, wd, y1, g, pa, ph, y2
+    torch.cuda.empty_cache()
+    c5 = bench_c5_block_chain(torch, b1, synth)
+    out["c5_step"] = {x: (round(v, 4) if isinstance(v, float) else v) for x, v in c5.items()}
+    log(f"[bench] c5 step (38 blocks): {c5['ms_per_step']:.2f} ms ({c5['gemm_tflops']:.0f} TFLOP/s of GEMM work, "
+        f"{100*c5['frac']:.1f}% of peak); the 76 GEMMs alone {c5['ms_per_step_gemms_only']:.2f} ms")
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_klein_step(torch, b1, synth):
@@ -560,9 +635,31 @@ def bench_copy(torch, nbytes, steps, warmup):
 
 
 def observed_sclk_mhz():
-    """Current shader clock from rocm-smi (best effort; None if unavailable)."""
+    """The shader clock now, in MHz: the current level of the amdgpu sysfs
+    DPM table (the line marked '*'), else the mean of amd-smi's per-XCD
+    current clocks, else rocm-smi's; None if none answers."""
+    import glob
     import re
     import subprocess
+    for f in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
+        try:
+            for line in open(f):
+                if line.rstrip().endswith("*"):
+                    m = re.search(r"(\d+)\s*mhz", line, re.I)
+                    if m:
+                        return int(m.group(1))
+        except OSError:
+            pass
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-c", "-g", "0", "--json"], capture_output=True, text=True,
+                             timeout=20).stdout
+        data = json.loads(out)
+        gpu = data["gpu_data"][0] if isinstance(data, dict) else data[0]
+        clks = [v["clk"]["value"] for k, v in gpu["clock"].items() if k.startswith("gfx")]
+        if clks:
+            return int(round(sum(clks) / len(clks)))
+    except Exception:
+        pass
     try:
         out = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True, timeout=20).stdout
         m = re.search(r"sclk clock level:.*?\((\d+)Mhz\)", out)
@@ -571,34 +668,87 @@ def observed_sclk_mhz():
         return None
 
 
-def cpu_baseline(a_dev, w_dev, n, rows, threads, reps=3):
-    """The oracle's AVX2 restatement of src/b1_0_kernel.h:79-239 (ggml row
-    split, nth = threads) on the first `rows` rows of the same device inputs
-    the GPU leg timed (copied to host)."""
+def settle_clock(torch, fn, seconds):
+    """Runs fn back to back for `seconds` of wall time, so that the shader
+    clock has ramped and settled under sustained MFMA load before anything
+    is timed, and reads the clock once while the GPU is still busy (the
+    reading runs in a thread; the launches go on until it has returned).
+    Returns (seconds spent, clock in MHz or None)."""
+    import threading
+    sclk = []
+    th = threading.Thread(target=lambda: sclk.append(observed_sclk_mhz()), daemon=True)
+    t0 = time.perf_counter()
+    started = False
+    i = 0
+    while True:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        if not started and el >= 0.5 * seconds:
+            th.start()
+            started = True
+        if el >= seconds and started and not th.is_alive():
+            break
+    th.join()
+    return time.perf_counter() - t0, (sclk[0] if sclk else None)
+
+
+def cpu_time(fn, reps):
+    """Median wall time of fn over reps runs, after one warm-up run."""
     import numpy as np
-    from oracle import b1_oracle as o
-    k = a_dev.shape[1]
-    act = a_dev[:rows].cpu().numpy()
-    raw = w_dev.cpu().numpy().reshape(n, -1)
-    o.linear(act[:4], raw, n, variant="avx2", nth=threads, nthreads=threads)   # warm-up
+    fn()
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        o.linear(act, raw, n, variant="avx2", nth=threads, nthreads=threads)
+        fn()
         ts.append(time.perf_counter() - t0)
-    dt = float(np.median(ts))
-    return 2.0 * rows * n * k / dt / 1e12, dt
+    return float(np.median(ts))
+
+
+def cpu_baselines(a_dev, w_dev, n, threads_share):
+    """The oracle's AVX2 restatement of src/b1_0_kernel.h:79-239 (ggml row
+    split over nth threads, :75-77) on this host, on the same device inputs
+    the GPU legs timed (copied to host): the headline GEMM on all 4096 rows
+    at the host's thread share, on its first 1024 rows at nth = 4 (the
+    reference's --threads default, src/diffuser.cpp:63), and the M=8
+    small-M shape (K=3072, N=18432) at both thread counts, median of 3."""
+    import numpy as np
+    from bonsai_b1 import synth
+    from oracle import b1_oracle as o
+    k = a_dev.shape[1]
+    act = a_dev.cpu().numpy()
+    raw = w_dev.cpu().numpy().reshape(n, -1)
+
+    def run(a, r, nn, th):
+        return lambda: o.linear(a, r, nn, variant="avx2", nth=th, nthreads=th)
+    res = {}
+    for th, rows in ((threads_share, act.shape[0]), (4, 1024)):
+        dt = cpu_time(run(act[:rows], raw, n, th), 3)
+        res[th] = {"tflops": 2.0 * rows * n * k / dt / 1e12, "s": dt, "rows": rows}
+    gm, gk, gn = GEMV
+    ga = synth.activations(gm, gk, 3)
+    graw = synth.packed_weights(gn, gk, 4)
+    nbytes = gn * (gk // 32) * 6
+    gemv = {}
+    for th in (threads_share, 4):
+        dt = cpu_time(run(ga, graw, gn, th), 3)
+        gemv[th] = {"us": dt * 1e6, "GBps_packed": nbytes / dt / 1e9}
+    return res, gemv
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    # ~1.5 s of GEMM before timing: the shader clock ramps for about a
-    # second under sustained MFMA load before it settles
-    ap.add_argument("--warmup", type=int, default=5000)
-    ap.add_argument("--all", action="store_true", help="also time the other config shapes (stderr)")
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    # the shader clock ramps for about a second under sustained MFMA load
+    # before it settles; nothing is timed before this much wall time of it
+    ap.add_argument("--settle-s", type=float, default=2.0)
+    ap.add_argument("--all", action="store_true", help="also time the secondary legs (stderr and JSON)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1/C3/C4/C5 config legs")
     ap.add_argument("--only", choices=["gemm", "gemv", "copy", "c5chain"], default=None,
                     help="run one leg only (profiler runs); prints that leg's numbers")
     args = ap.parse_args()
@@ -619,7 +769,7 @@ def main():
         print(json.dumps({"copy": c}), flush=True)
         return
     if args.only == "c5chain":
-        ch = bench_c5_block_chain(torch, b1, synth)
+        ch = bench_c5_block_chain(torch, b1, synth, producer_form=True)
         print(json.dumps({"c5_block_chain": ch}), flush=True)
         return
     if args.only == "gemv":
@@ -627,21 +777,26 @@ def main():
         v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400))
         print(json.dumps({"gemv": {x: v[x] for x in v}}), flush=True)
         return
+    a = synth.device_activations(m, k, 1)
+    w = synth.device_packed_weights(n, k, 2)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    settle_s, sclk = settle_clock(torch, lambda i: b1.linear(a, w, n, out=y), args.settle_s)
+    log(f"[bench] clock settled over {settle_s:.2f} s of the step (sclk under load: {sclk} MHz)")
     log(f"[bench] GEMM M={m} K={k} N={n} steps={args.steps} warmup={args.warmup}")
-    g = bench_gemm(torch, b1, synth, m, k, n, args.steps, args.warmup, sample_clock=True)
-    sclk = g["sclk"]
-    log(f"[bench] GEMM {g['ms']*1e3:.1f} us  {g['tflops']:.1f} TFLOP/s  {100*g['frac']:.1f}% of fp16 MFMA peak"
-        f" (sclk during warm-up: {sclk} MHz)")
-    kern_ms = bench_gemm_kernel(torch, b1, *g["inputs"], n, args.steps, min(args.warmup, 1000))
-    pack_ms = g["ms"] - kern_ms   # the fp16 pack pass, the other kernel of the step
+    g = bench_gemm(torch, b1, synth, m, k, n, args.steps, args.warmup, inputs=(a, w))
+    log(f"[bench] GEMM {g['ms']*1e3:.1f} us  {g['tflops']:.1f} TFLOP/s  {100*g['frac']:.1f}% of fp16 MFMA peak")
+    # the kernels alone: at least 100 launches each for a stable event average
+    kern_ms, pack_ms = bench_step_kernels(torch, b1, a, w, n, max(args.steps, 100), max(args.warmup, 10))
     kern_tflops = 2.0 * m * n * k / (kern_ms * 1e-3) / 1e12
+    pack_gbs = m * k * 6 / (pack_ms * 1e-3) / 1e9
     log(f"[bench] GEMM kernel alone {kern_ms*1e3:.1f} us  {kern_tflops:.1f} TFLOP/s  "
-        f"{100*kern_tflops/PEAK_FP16_TFLOPS:.1f}% of peak; step - kernel (pack pass) {pack_ms*1e3:.1f} us")
+        f"{100*kern_tflops/PEAK_FP16_TFLOPS:.1f}% of peak; pack pass alone {pack_ms*1e3:.1f} us "
+        f"({pack_gbs:.0f} GB/s)")
     if args.only == "gemm":
         print(json.dumps({"gemm": {x: g[x] for x in g if x != "inputs"}, "kernel_ms": kern_ms,
-                          "pack_ms": pack_ms}), flush=True)
+                          "pack_ms": pack_ms, "sclk_mhz": sclk}), flush=True)
         return
-    dense = bench_dense_reference(torch, m, k, n)
+    dense = bench_dense_reference(torch, m, k, n, steps=max(args.steps, 100), warmup=max(args.warmup, 50))
     log(f"[bench] dense fp16 GEMM, same shape ({dense['library']}, {dense['out']} out): {dense['us']:.1f} us "
         f"{dense['tflops']:.1f} TFLOP/s; B1_0 kernel / dense = {kern_ms * 1e3 / dense['us']:.3f}")
 
@@ -656,73 +811,62 @@ def main():
     log(f"[bench] GEMV M={gm} over packed fp16 activations {vp['us']:.2f} us/launch  {vp['gbs']:.0f} GB/s "
         f"({100 * vp['frac']:.1f}% of HBM peak)")
 
-    extra = {}
+    configs = {}
+    if not args.no_configs:
+        configs = bench_configs(torch, b1, synth, max(args.steps // 4, 20), max(args.warmup, 10))
     if args.all:
-        for name, shp in [("c1_parity", (256, 3072, 3072)),
-                          ("c3_qkv", (4608, 3072, 9216)), ("c3_out", (4608, 3072, 3072)),
-                          ("c4_up", (4608, 3072, 12288)), ("c4_down", (4608, 12288, 3072)),
-                          ("c5_linear1", (4608, 3072, 21504)), ("c5_linear2", (4608, 15360, 3072))]:
-            r = bench_gemm(torch, b1, synth, *shp, max(10, args.steps // 4), 200)
-            extra[name] = {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 1),
-                           "frac": round(r["frac"], 4)}
-            log(f"[bench] {name} {shp}: {r['ms']*1e3:.1f} us {r['tflops']:.1f} TFLOP/s")
         mlp = bench_mlp(torch, b1, synth)
-        extra["c4_mlp"] = {x: round(v, 4) for x, v in mlp.items()}
-        log(f"[bench] c4 MLP: up {mlp['up']*1e3:.1f} us, GELU {mlp['gelu']*1e3:.1f} us "
-            f"({mlp['gelu_GBps']:.0f} GB/s), down {mlp['down']*1e3:.1f} us; chain {mlp['chain']*1e3:.1f} us "
-            f"({mlp['chain_tflops']:.0f} TFLOP/s), GELU fused into the pack {mlp['chain_fused_gelu']*1e3:.1f} us, "
-            f"GELU in the up-projection's epilogue {mlp['chain_epilogue_gelu']*1e3:.1f} us "
-            f"({mlp['chain_epilogue_tflops']:.0f} TFLOP/s)")
+        configs["c4_mlp_forms"] = {x: round(v_, 4) for x, v_ in mlp.items()}
+        log(f"[bench] c4 MLP forms: chain {mlp['chain']*1e3:.1f} us, GELU fused into the pack "
+            f"{mlp['chain_fused_gelu']*1e3:.1f} us, GELU in the up-projection's epilogue "
+            f"{mlp['chain_epilogue_gelu']*1e3:.1f} us")
         ff = bench_ff_epilogues(torch, b1, synth)
-        extra["ff_epilogues"] = {x: round(v, 4) for x, v in ff.items()}
+        configs["ff_epilogues"] = {x: round(v_, 4) for x, v_ in ff.items()}
         log(f"[bench] double-block FF (4096 x 3072 -> 2x9216, SwiGLU, -> 3072, gate-residual): separate "
             f"passes {ff['separate']*1e3:.1f} us, fused epilogues {ff['fused']*1e3:.1f} us "
             f"({ff['fused_tflops']:.0f} TFLOP/s); SwiGLU epilogue writing FF-out's packed input "
             f"{ff['fused_packed_out']*1e3:.1f} us ({ff['fused_packed_out_tflops']:.0f} TFLOP/s)")
         nm = bench_norm_mod(torch, b1, synth)
-        extra["norm_mod"] = {x: round(v, 4) for x, v in nm.items()}
+        configs["norm_mod"] = {x: round(v_, 4) for x, v_ in nm.items()}
         log(f"[bench] LayerNorm+modulation 4096x3072 -> packed fp16: {nm['fused_pack']*1e3:.1f} us "
             f"({nm['fused_GBps']:.0f} GB/s); fp32 then pack {nm['fp32_then_pack']*1e3:.1f} us")
         torch.cuda.empty_cache()
         c5 = bench_single_stream_step(torch, b1, synth)
-        extra["c5_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in c5.items()}
-        log(f"[bench] c5 single-stream step (38 blocks): {c5['ms_per_step']:.2f} ms ({c5['tflops']:.0f} TFLOP/s) "
-            f"from fp32 activations; {c5['ms_per_step_packed_inputs']:.2f} ms "
-            f"({c5['tflops_packed_inputs']:.0f} TFLOP/s) over producer-packed fp16 inputs")
-        torch.cuda.empty_cache()
-        ch = bench_c5_block_chain(torch, b1, synth)
-        extra["c5_block_chain"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in ch.items()}
-        log(f"[bench] c5 block chain (38 single-stream blocks, attention aside: norm+mod -> packed, linear1, "
-            f"packed [q | GELU(MLP)], linear2 + gate-residual): {ch['ms_per_step']:.2f} ms "
-            f"({ch['gemm_tflops']:.0f} TFLOP/s of GEMM work); GELU(MLP) from linear1's epilogue "
-            f"{ch['ms_per_step_epilogue']:.2f} ms ({ch['gemm_tflops_epilogue']:.0f} TFLOP/s)")
+        configs["c5_step_fp32_inputs"] = {x: round(v_, 4) if isinstance(v_, float) else v_ for x, v_ in c5.items()}
+        log(f"[bench] c5 38 blocks of (linear1, linear2) from fp32 activations: {c5['ms_per_step']:.2f} ms "
+            f"({c5['tflops']:.0f} TFLOP/s)")
         torch.cuda.empty_cache()
         wl = bench_weights_load(torch, b1)
-        extra["weights_load"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in wl.items()}
+        configs["weights_load"] = {x: round(v_, 4) if isinstance(v_, float) else v_ for x, v_ in wl.items()}
         log(f"[bench] weight residency, C5 model ({wl['tensors']} tensors, {wl['bytes'] / 1e6:.0f} MB) from "
             f".safetensors: pinned pipeline {wl['pinned_s'] * 1e3:.0f} ms ({wl['pinned_GBps']:.1f} GB/s), "
             f"per-tensor upload from the mapping {wl['pageable_s'] * 1e3:.0f} ms ({wl['pageable_GBps']:.1f} GB/s)")
         torch.cuda.empty_cache()
         kl = bench_klein_step(torch, b1, synth)
-        extra["klein_step"] = {x: round(v, 4) if isinstance(v, float) else v for x, v in kl.items()}
+        configs["klein_step"] = {x: round(v_, 4) if isinstance(v_, float) else v_ for x, v_ in kl.items()}
         log(f"[bench] Klein step (100 linears): {kl['ms_per_step']:.2f} ms ({kl['tflops']:.0f} TFLOP/s); "
-            f"q/k/v as three GEMMs {kl['ms_per_step_separate_qkv']:.2f} ms; over producer-packed fp16 inputs "
-            f"{kl['ms_per_step_packed_inputs']:.2f} ms ({kl['tflops_packed_inputs']:.0f} TFLOP/s); with FF-in and "
-            f"linear1 writing SwiGLU as the next packed input {kl['ms_per_step_swiglu_epilogues']:.2f} ms "
-            f"({kl['tflops_swiglu_epilogues']:.0f} TFLOP/s)")
+            f"over producer-packed fp16 inputs {kl['ms_per_step_packed_inputs']:.2f} ms; with FF-in and "
+            f"linear1 writing SwiGLU as the next packed input {kl['ms_per_step_swiglu_epilogues']:.2f} ms")
         torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        rows = m
-        log(f"[bench] CPU baseline: oracle AVX2, {threads} threads, {rows} of {m} rows")
-        tf, dt = cpu_baseline(*g["inputs"], n, rows, threads)
-        cpu = {"value": round(tf, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-               "sample": f"M={rows} of {m} rows, K={k}, N={n}; AVX2 restatement of "
+        share = min(16, len(os.sched_getaffinity(0)))
+        log(f"[bench] CPU baseline: oracle AVX2, {share} and 4 threads")
+        res, gemv_cpu = cpu_baselines(a, w, n, share)
+        top = res[share]
+        cpu = {"value": round(top["tflops"], 5), "unit": "TFLOP/s", "cores": share, "kind": "port",
+               "host_cpus": os.cpu_count(),
+               "sample": f"M={top['rows']} of {m} rows, K={k}, N={n}; AVX2 restatement of "
                          f"src/b1_0_kernel.h:79-239, gcc -O3 -mavx2 -mfma -mf16c -ffp-contract=off, "
-                         f"ggml row split nth={threads}; median of 3 ({dt:.2f} s)"}
-        log(f"[bench] CPU {tf*1e3:.1f} GFLOP/s")
+                         f"ggml row split nth={share}; median of 3 ({top['s']:.2f} s)",
+               "nth4": {"value": round(res[4]["tflops"], 5), "unit": "TFLOP/s",
+                        "sample": f"M={res[4]['rows']} rows, nth=4 (src/diffuser.cpp:63 default); "
+                                  f"median of 3 ({res[4]['s']:.2f} s)"},
+               "gemv_m8": {f"nth{th}": {"us": round(r_["us"], 1), "GBps_packed": round(r_["GBps_packed"], 2)}
+                           for th, r_ in gemv_cpu.items()}}
+        log(f"[bench] CPU {top['tflops']*1e3:.1f} GFLOP/s at {share} threads, {res[4]['tflops']*1e3:.1f} at 4; "
+            f"GEMV M=8 {gemv_cpu[share]['us']:.0f} us at {share} threads")
 
     flop = 2.0 * m * n * k
     line = {
@@ -740,16 +884,19 @@ def main():
         "data": "synthetic (N(0,1) fp32 activations, random B1_0 packed weights)",
         "config": {"workload": "b1_0_gemm", "M": m, "K": k, "N": n, "mode": "fast",
                    "parallelism": "single-gpu"},
+        "settle_s": round(settle_s, 3),
+        "sclk_mhz_under_load": sclk,
         "roofline": {"bound": "mfma", "achieved": round(kern_tflops, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(kern_tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": committed_traffic(TRAFFIC_PROFILE),
                      "kernel": "b1_gemm_kernel<128,512,64,3,0>", "kernel_us": round(kern_ms * 1e3, 2),
-                     "algorithmic_flop": flop, "sclk_mhz_observed": sclk,
-                     "step_minus_kernel_us": round(pack_ms * 1e3, 2),
-                     "traffic_source": f"profiles/{TRAFFIC_PROFILE}.md",
+                     "algorithmic_flop": flop, "traffic_source": f"profiles/{TRAFFIC_PROFILE}.md",
+                     "pack_pass": {"kernel": "b1_pack_rows_kernel", "us": round(pack_ms * 1e3, 2),
+                                   "GBps": round(pack_gbs, 1), "frac_hbm": round(pack_gbs / PEAK_HBM_GBS, 4),
+                                   "algorithmic_bytes": m * k * 6},
                      "note": "value/ms_per_step: whole op from fp32 activations (pack pass + GEMM); "
-                             "achieved: GEMM kernel alone"},
-        "dense_reference": {x: (round(y, 2) if isinstance(y, float) else y) for x, y in dense.items()},
+                             "achieved: GEMM kernel alone; pack_pass: the other kernel of the step, alone"},
+        "dense_reference": {x: (round(y_, 2) if isinstance(y_, float) else y_) for x, y_ in dense.items()},
         "gemv": {"M": gm, "K": gk, "N": gn, "us_per_call": round(v["us"], 3),
                  "GBps_packed": round(v["gbs"], 1), "frac_hbm": round(v["frac"], 4),
                  "packed_bytes": v["packed_bytes"], "weight_copies": v["weight_copies"],
@@ -760,8 +907,8 @@ def main():
                  "packed_input_frac_hbm": round(vp["frac"], 4)},
         "cpu_baseline": cpu,
     }
-    if extra:
-        line["configs"] = extra
+    if configs:
+        line["configs"] = configs
     print(json.dumps(line), flush=True)
 
 

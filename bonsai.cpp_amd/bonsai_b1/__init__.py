@@ -28,6 +28,8 @@ from .capi import (  # noqa: F401
     library_path,
     linear,
     linear_packed_f16,
+    linear_packed_f16_scaled,
+    pack_act_f16_scaled,
     linear_packed_workspace_bytes,
     linear_raw,
     load,

@@ -125,6 +125,10 @@ def load():
     L.bonsai_b1_linear_packed_f16.restype = i
     L.bonsai_b1_linear_packed_f16_ws.argtypes = [vp, vp, i, i, i, vp, i64, vp, vp, ctypes.c_size_t, vp]
     L.bonsai_b1_linear_packed_f16_ws.restype = i
+    L.bonsai_b1_pack_act_f16_scaled.argtypes = [vp, i64, i, i, vp, vp, vp]
+    L.bonsai_b1_pack_act_f16_scaled.restype = i
+    L.bonsai_b1_linear_packed_f16_scaled.argtypes = [vp, vp, vp, i, i, i, vp, i64, vp, vp]
+    L.bonsai_b1_linear_packed_f16_scaled.restype = i
     L.bonsai_b1_linear_packed_workspace_bytes.argtypes = [i, i, i]
     L.bonsai_b1_linear_packed_workspace_bytes.restype = ctypes.c_size_t
     L.bonsai_b1_linear_packed_f16_epi.argtypes = [vp, vp, i, i, i, vp, i64, ctypes.POINTER(Epilogue), vp, vp]
@@ -385,6 +389,41 @@ def pack_act_f16(act, packed=None, stream=None, ldp=None):
     if st != OK:
         raise B1Error(st, "bonsai_b1_pack_act_f16")
     return packed
+
+
+def pack_act_f16_scaled(act, packed=None, row_scale=None, stream=None):
+    """Range-safe packing (bonsai_b1_pack_act_f16_scaled): returns (packed
+    uint8 [M*K*2], row_scale fp32 [M])."""
+    import torch
+    if act.dim() != 2 or act.dtype != torch.float32 or not act.is_cuda or act.stride(1) != 1:
+        raise ValueError("act must be a 2-D fp32 cuda tensor with unit column stride")
+    m, k = act.shape
+    packed = _packed_target(act, packed, None)
+    if row_scale is None:
+        row_scale = torch.empty(m, dtype=torch.float32, device=act.device)
+    st = load().bonsai_b1_pack_act_f16_scaled(act.data_ptr(), act.stride(0), k, m, packed.data_ptr(),
+                                              row_scale.data_ptr(), _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_pack_act_f16_scaled")
+    return packed, row_scale
+
+
+def linear_packed_f16_scaled(packed, row_scale, w_packed, in_dim: int, out_dim: int, batch: int, out=None,
+                             nonfinite=None, stream=None):
+    """bonsai_b1_linear_packed_f16_scaled: the packed linear with row m's
+    outputs multiplied by row_scale[m]."""
+    import torch
+    if out is None:
+        out = torch.empty((batch, out_dim), dtype=torch.float32, device=packed.device)
+    if out.dim() != 2 or out.shape[0] != batch or out.shape[1] < out_dim or out.stride(1) != 1:
+        raise ValueError("out must be [batch, >=out_dim] fp32 with unit column stride")
+    nf = nonfinite.data_ptr() if nonfinite is not None else None
+    st = load().bonsai_b1_linear_packed_f16_scaled(packed.data_ptr(), row_scale.data_ptr(), w_packed.data_ptr(),
+                                                   in_dim, out_dim, batch, out.data_ptr(), out.stride(0), nf,
+                                                   _stream_handle(stream))
+    if st != OK:
+        raise B1Error(st, "bonsai_b1_linear_packed_f16_scaled")
+    return out
 
 
 def linear_packed_workspace_bytes(batch: int, in_dim: int, out_dim: int) -> int:

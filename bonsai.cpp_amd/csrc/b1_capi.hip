@@ -442,6 +442,16 @@ int bonsai_b1_pack_act_f16(const float *act, int64_t lda, int in_dim, int batch,
     return bonsai_b1_pack_act_f16_ld(act, lda, in_dim, batch, packed, in_dim, stream);
 }
 
+int bonsai_b1_pack_act_f16_scaled(const float *act, int64_t lda, int in_dim, int batch, void *packed,
+                                  float *row_scale, hipStream_t stream) {
+    if (batch > 0 && (!row_scale || (reinterpret_cast<uintptr_t>(row_scale) & 3u))) return BONSAI_B1_ERR_ARG;
+    const int st = pack_args(act, lda, in_dim, batch, packed, in_dim);
+    if (st != BONSAI_B1_OK || batch == 0) return st;
+    return b1::launch_pack_rows_to(act, lda, batch, in_dim, packed, row_scale, stream) == hipSuccess
+               ? BONSAI_B1_OK
+               : BONSAI_B1_ERR_HIP;
+}
+
 size_t bonsai_b1_linear_packed_workspace_bytes(int batch, int in_dim, int out_dim) {
     if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || !b1::gemm_packed_ok(batch, in_dim, out_dim)) return 0;
     if (b1::gemv_packed_ok(batch, in_dim, out_dim)) return 0;
@@ -453,13 +463,14 @@ size_t bonsai_b1_linear_packed_workspace_bytes(int batch, int in_dim, int out_di
 // Shared body of the packed entry points.  ws_mode: 0 = library-owned
 // workspace for the split-K partials, 1 = caller's (may be NULL / small:
 // then unsplit).
-static int linear_packed_impl(const void *packed_act, const void *w, int in_dim, int out_dim, int batch, float *out,
-                              int64_t ldo, int32_t *nonfinite, int ws_mode, void *ws, size_t ws_bytes,
-                              hipStream_t stream) {
+static int linear_packed_impl(const void *packed_act, const float *rsc, const void *w, int in_dim, int out_dim,
+                              int batch, float *out, int64_t ldo, int32_t *nonfinite, int ws_mode, void *ws,
+                              size_t ws_bytes, hipStream_t stream) {
     if (in_dim <= 0 || out_dim <= 0 || batch < 0 || ldo < out_dim) return BONSAI_B1_ERR_ARG;
     if (batch > 0 && (!packed_act || !w || !out)) return BONSAI_B1_ERR_ARG;
     if ((reinterpret_cast<uintptr_t>(packed_act) & 15u) || (reinterpret_cast<uintptr_t>(w) & 3u) ||
-        (reinterpret_cast<uintptr_t>(out) & 3u) || (reinterpret_cast<uintptr_t>(ws) & 15u))
+        (reinterpret_cast<uintptr_t>(out) & 3u) || (reinterpret_cast<uintptr_t>(ws) & 15u) ||
+        (reinterpret_cast<uintptr_t>(rsc) & 3u))
         return BONSAI_B1_ERR_ARG;
     if (!b1::gemm_packed_ok(batch > 0 ? batch : 1, in_dim, out_dim)) return BONSAI_B1_ERR_ARG;
     DeviceInfo *dev = current_device(nullptr);
@@ -469,7 +480,8 @@ static int linear_packed_impl(const void *packed_act, const void *w, int in_dim,
     hipError_t e;
     if (b1::gemv_packed_ok(batch, in_dim, out_dim)) {
         // a few tokens: the bandwidth-bound small-M kernel, not a 128-row tile
-        e = b1::launch_gemv_packed(packed_act, wb, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus, stream);
+        e = b1::launch_gemv_packed(packed_act, wb, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus, stream,
+                                   rsc);
     } else {
         // split along K as bonsai_b1_linear_f32 splits the same shape, when
         // the partials have room: the two entries then agree bit for bit
@@ -481,25 +493,36 @@ static int linear_packed_impl(const void *packed_act, const void *w, int in_dim,
             ws = lease.ptr();
             ws_bytes = ws ? need : 0;
         }
+        b1::GemmEpi epi;
+        epi.rsc = rsc;
         if (need > 0 && ws && ws_bytes >= need)
             e = b1::launch_gemm_packed_split(packed_act, wb, in_dim, out_dim, batch, out, ldo, nonfinite,
-                                             dev->num_cus, splits, ws, stream);
+                                             dev->num_cus, splits, ws, stream, rsc);
         else
-            e = b1::launch_gemm_packed(packed_act, wb, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus,
-                                       stream);
+            e = b1::launch_gemm_packed_epi(packed_act, wb, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus,
+                                           0, epi, stream);
     }
     return e == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
 }
 
+int bonsai_b1_linear_packed_f16_scaled(const void *packed_act, const float *row_scale, const void *w, int in_dim,
+                                       int out_dim, int batch, float *out, int64_t ldo, int32_t *nonfinite,
+                                       hipStream_t stream) {
+    if (batch > 0 && !row_scale) return BONSAI_B1_ERR_ARG;
+    return linear_packed_impl(packed_act, row_scale, w, in_dim, out_dim, batch, out, ldo, nonfinite, 0, nullptr, 0,
+                              stream);
+}
+
 int bonsai_b1_linear_packed_f16(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
                                 float *out, int64_t ldo, int32_t *nonfinite, hipStream_t stream) {
-    return linear_packed_impl(packed_act, w, in_dim, out_dim, batch, out, ldo, nonfinite, 0, nullptr, 0, stream);
+    return linear_packed_impl(packed_act, nullptr, w, in_dim, out_dim, batch, out, ldo, nonfinite, 0, nullptr, 0,
+                              stream);
 }
 
 int bonsai_b1_linear_packed_f16_ws(const void *packed_act, const void *w, int in_dim, int out_dim, int batch,
                                    float *out, int64_t ldo, int32_t *nonfinite, void *workspace,
                                    size_t workspace_bytes, hipStream_t stream) {
-    return linear_packed_impl(packed_act, w, in_dim, out_dim, batch, out, ldo, nonfinite, 1, workspace,
+    return linear_packed_impl(packed_act, nullptr, w, in_dim, out_dim, batch, out, ldo, nonfinite, 1, workspace,
                               workspace_bytes, stream);
 }
 

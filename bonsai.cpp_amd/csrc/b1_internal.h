@@ -89,6 +89,10 @@ hipError_t launch_gemm_packed_split(const void *packed, const uint8_t *w, int K,
 size_t pack_area_bytes(int M, int K);
 float *pack_area_rsc(void *area, int M, int K);
 hipError_t launch_pack_rows(const float *act, int64_t lda, int M, int K, void *area, hipStream_t s);
+// The same into a packing (row stride K, 16-byte aligned) and M row scales
+// at places of the caller's choosing.
+hipError_t launch_pack_rows_to(const float *act, int64_t lda, int M, int K, void *packed, float *rsc,
+                               hipStream_t s);
 
 // Rows of a linear holding activations beyond the fp16 range (|a| >=
 // 65520), recomputed exactly (EXACT mode's bits) over what a kernel that

@@ -1934,6 +1934,11 @@ float *pack_area_rsc(void *area, int M, int K) {
 }
 
 hipError_t launch_pack_rows(const float *act, int64_t lda, int M, int K, void *area, hipStream_t s) {
+    return launch_pack_rows_to(act, lda, M, K, area, pack_area_rsc(area, M, K), s);
+}
+
+hipError_t launch_pack_rows_to(const float *act, int64_t lda, int M, int K, void *packed, float *rsc,
+                               hipStream_t s) {
     const int units = K / 8;
     int wl = 0, per = 0;
     for (wl = 0; wl <= 2; ++wl) {
@@ -1947,8 +1952,7 @@ hipError_t launch_pack_rows(const float *act, int64_t lda, int M, int K, void *a
     const int rows_per_wg = 4 >> wl;
     const dim3 grid((M + rows_per_wg - 1) / rows_per_wg);
     const bool nt = (uint64_t)M * (uint64_t)K * 4 > kNtInputBytes;
-    uint32_t *pk = static_cast<uint32_t *>(area);
-    float *rsc = pack_area_rsc(area, M, K);
+    uint32_t *pk = static_cast<uint32_t *>(packed);
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, act, lda, pk, (int64_t)K / 2, rsc, M, K, wl);
     };

@@ -224,6 +224,29 @@ int bonsai_b1_linear_packed_f16_ws(const void *packed_act, const void *w,
                                    size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * The two halves of bonsai_b1_linear_f32's range-safe FAST path, for callers
+ * that pack an input once for several linears (q/k/v of a block,
+ * src/diffuser_graph.cpp:354-361) and still take any finite activation.
+ * _pack_act_f16_scaled writes the packing of bonsai_b1_pack_act_f16
+ * (row stride in_dim, same requirements) of act[m][:] * 2^-e[m] and
+ * row_scale[m] = 2^e[m] (batch floats, 4-byte aligned): e[m] = 0 for a row
+ * within the fp16 range (the same bits as bonsai_b1_pack_act_f16), else the
+ * smallest shift that brings its largest |act| below 2^15.
+ * _linear_packed_f16_scaled is bonsai_b1_linear_packed_f16 with row m's
+ * outputs multiplied by row_scale[m] (exact: powers of two); together they
+ * give bonsai_b1_linear_f32's FAST results bit for bit.  No reference
+ * counterpart (the reference's single op has no such split).
+ */
+int bonsai_b1_pack_act_f16_scaled(const float *act, int64_t lda, int in_dim,
+                                  int batch, void *packed, float *row_scale,
+                                  hipStream_t stream);
+int bonsai_b1_linear_packed_f16_scaled(const void *packed_act,
+                                       const float *row_scale, const void *w,
+                                       int in_dim, int out_dim, int batch,
+                                       float *out, int64_t ldo,
+                                       int32_t *nonfinite, hipStream_t stream);
+
+/*
  * A sequence of B1_0 linears on one stream: the linear dispatch of a
  * diffusion step (the b1 lambda at src/diffuser_graph.cpp:277-281 and its
  * call sites, :354-361,434-457,482,536), run in the order given.  Each op is

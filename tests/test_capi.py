@@ -33,6 +33,24 @@ def test_version_and_status_strings():
     assert lib.bonsai_b1_status_string(0) == b"ok"
     assert lib.bonsai_b1_status_string(3) == b"non-finite output"
     assert lib.bonsai_b1_status_string(99) == b"unknown status"
+    assert b"scratch" in lib.bonsai_b1_status_string(8)
+
+
+def test_new_entries_reject_before_device():
+    """The no-alloc, scaled and packed-with-workspace entries check their
+    arguments before touching a device."""
+    lib = bonsai_b1.load()
+    fake = 0x10000
+    assert lib.bonsai_b1_linear_f32_noalloc(fake, 64, fake, 63, 32, 1, fake, 32, 0, None, None) == capi.ERR_ARG
+    assert lib.bonsai_b1_linear_f32_noalloc(fake, 64, fake, 64, 32, 1, fake, 32, 7, None, None) == capi.ERR_ARG
+    # no row scales for a non-empty batch
+    assert lib.bonsai_b1_pack_act_f16_scaled(fake, 384, 384, 4, fake, None, None) == capi.ERR_ARG
+    assert lib.bonsai_b1_pack_act_f16_scaled(fake, 384, 384, 4, fake, fake + 2, None) == capi.ERR_ARG
+    assert lib.bonsai_b1_linear_packed_f16_scaled(fake, None, fake, 384, 64, 4, fake, 64, None,
+                                                  None) == capi.ERR_ARG
+    # a misaligned caller workspace
+    assert lib.bonsai_b1_linear_packed_f16_ws(fake, fake, 384, 64, 4, fake, 64, None, fake + 8, 1 << 20,
+                                              None) == capi.ERR_ARG
 
 
 @pytest.mark.parametrize("args", [

@@ -135,9 +135,12 @@ def test_small_m_config(torch, b1, oracle, m):
 
 @pytest.mark.parametrize("shape", [
     (4096, 3072, 12288),   # headline GEMM
-    (4608, 3072, 9216),    # fused QKV projection
-    (4608, 12288, 3072),   # MLP down projection
-    (4608, 15360, 3072),   # single-stream linear2
+    (4608, 3072, 9216),    # C3 fused QKV projection
+    (4608, 3072, 3072),    # C3 out-projection
+    (4608, 3072, 12288),   # C4 MLP up-projection
+    (4608, 12288, 3072),   # C4 MLP down-projection
+    (4608, 3072, 21504),   # C5 single-stream linear1
+    (4608, 15360, 3072),   # C5 single-stream linear2
 ])
 def test_full_size_properties(torch, b1, shape):
     from bonsai_b1 import synth

@@ -259,3 +259,28 @@ def test_packed_entry_splits_like_fp32_entry(torch, b1, m, k, n):
     torch.cuda.synchronize()
     assert torch.equal(y, ref)
     assert torch.equal(y2, ref)
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 3072, 3072), (2048, 768, 4608), (8, 3072, 4096)])
+def test_scaled_halves_equal_fp32_entry(torch, b1, m, k, n):
+    """bonsai_b1_pack_act_f16_scaled + bonsai_b1_linear_packed_f16_scaled
+    give bonsai_b1_linear_f32's FAST results bit for bit (split-K, unsplit
+    and small-M shapes), on activations beyond the fp16 range too; on rows
+    within range the scaled packing is bonsai_b1_pack_act_f16's, with
+    scale 1."""
+    from bonsai_b1 import synth
+    act = big_activations(m, k, 13)
+    a = torch.from_numpy(act).cuda()
+    w = torch.from_numpy(synth.packed_weights(n, k, 14).ravel()).cuda()
+    ref = b1.linear(a, w, n)
+    packed, rs = b1.pack_act_f16_scaled(a)
+    y = b1.linear_packed_f16_scaled(packed, rs, w, k, n, m)
+    plain = b1.pack_act_f16(a)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    scales = rs.cpu().numpy()
+    keep = [i for i in range(m) if i not in BIG_ROWS]
+    assert bool((scales[keep] == 1.0).all())
+    assert bool((scales[list(BIG_ROWS)] > 1.0).all())
+    pk = packed.view(m, k * 2).cpu().numpy()
+    assert np.array_equal(pk[keep], plain.view(m, k * 2).cpu().numpy()[keep])
