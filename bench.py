@@ -606,6 +606,51 @@ def bench_gemv(torch, b1, synth, m, k, n, steps, warmup, packed_input=False):
             "eager_us": eager_ms * 1e3, "wall_s": wall}
 
 
+MOD_GROUP = (1, 3072, [18432, 18432, 9216, 6144])   # a step's modulation projections over vec_silu
+
+
+def bench_gemv_group(torch, b1, synth, m, k, ns, steps, warmup):
+    """Consecutive small-M linears on one input (a diffusion step's
+    modulation projections): one bonsai_b1_linear_batch call, which packs the
+    input once and runs them as one launch, against the same linears as
+    separate calls.  Weight sets rotated past the MALL, launches captured in
+    a HIP graph as in bench_gemv."""
+    nbytes = sum(n * (k // 32) * 6 for n in ns)
+    copies = max(2, (2 * MALL_BYTES) // nbytes + 1)
+    wsets = [[synth.device_packed_weights(n, k, 500 + 10 * c + i) for i, n in enumerate(ns)] for c in range(copies)]
+    a = synth.device_activations(m, k, 5)
+    outs = [torch.empty((m, n), dtype=torch.float32, device="cuda") for n in ns]
+    views = [[b1.device_weights(w, k, n) for w, n in zip(ws, ns)] for ws in wsets]
+    ops = [[(a, v, o) for v, o in zip(vs, outs)] for vs in views]
+    wsp = torch.empty(max(16, b1.linear_batch_workspace_bytes(ops[0])), dtype=torch.uint8, device="cuda")
+
+    def grouped(c):
+        b1.linear_batch(ops[c], workspace=wsp)
+
+    def separate(c):
+        for w, n, o in zip(wsets[c], ns, outs):
+            b1.linear(a, w, n, out=o)
+    res = {}
+    for name, fn in (("grouped", grouped), ("separate", separate)):
+        fn(0)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for c in range(copies):
+                fn(c)
+        reps = max(1, steps // copies)
+        ms, _ = time_launches(torch, lambda i: graph.replay(), reps, max(1, warmup // copies))
+        res[name] = ms / copies
+    ref = [o.clone() for o in outs]
+    grouped(copies - 1)
+    torch.cuda.synchronize()
+    same = all(torch.equal(o, r) for o, r in zip(outs, ref))
+    return {"shape": [m, k, ns], "grouped_us": res["grouped"] * 1e3, "separate_us": res["separate"] * 1e3,
+            "grouped_GBps": nbytes / (res["grouped"] * 1e-3) / 1e9,
+            "separate_GBps": nbytes / (res["separate"] * 1e-3) / 1e9, "packed_bytes": nbytes,
+            "weight_sets": copies, "grouped_equals_separate": same}
+
+
 def bench_dense_reference(torch, m, k, n, steps=1000, warmup=3000):
     """The vendor library's dense GEMM at the headline shape on the same
     GPU, for context: torch.mm over fp16 operands (hipBLASLt), fp32 output
@@ -775,7 +820,12 @@ def main():
     if args.only == "gemv":
         gm, gk, gn = GEMV
         v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400))
-        print(json.dumps({"gemv": {x: v[x] for x in v}}), flush=True)
+        vp = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400),
+                        packed_input=True)
+        v1 = bench_gemv(torch, b1, synth, 1, gk, gn, max(args.steps, 200), min(args.warmup, 400))
+        vg = bench_gemv_group(torch, b1, synth, *MOD_GROUP, max(args.steps, 200), min(args.warmup, 400))
+        print(json.dumps({"gemv": {x: v[x] for x in v}, "gemv_packed": {x: vp[x] for x in vp},
+                          "gemv_m1": {x: v1[x] for x in v1}, "modulation_group": vg}), flush=True)
         return
     a = synth.device_activations(m, k, 1)
     w = synth.device_packed_weights(n, k, 2)
@@ -810,6 +860,10 @@ def main():
     vp = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400), packed_input=True)
     log(f"[bench] GEMV M={gm} over packed fp16 activations {vp['us']:.2f} us/launch  {vp['gbs']:.0f} GB/s "
         f"({100 * vp['frac']:.1f}% of HBM peak)")
+    vg = bench_gemv_group(torch, b1, synth, *MOD_GROUP, max(args.steps, 200), min(args.warmup, 400))
+    log(f"[bench] modulation projections M={MOD_GROUP[0]} K={MOD_GROUP[1]} N={MOD_GROUP[2]}: one batch call "
+        f"{vg['grouped_us']:.2f} us ({vg['grouped_GBps']:.0f} GB/s), separate calls {vg['separate_us']:.2f} us "
+        f"({vg['separate_GBps']:.0f} GB/s); equal {vg['grouped_equals_separate']}")
 
     configs = {}
     if not args.no_configs:
@@ -904,7 +958,13 @@ def main():
                  "eager_us_per_call": round(v["eager_us"], 3),
                  "M1_us_per_call": round(v1["us"], 3), "M1_GBps_packed": round(v1["gbs"], 1),
                  "packed_input_us_per_call": round(vp["us"], 3), "packed_input_GBps": round(vp["gbs"], 1),
-                 "packed_input_frac_hbm": round(vp["frac"], 4)},
+                 "packed_input_frac_hbm": round(vp["frac"], 4),
+                 "modulation_group": {"M": MOD_GROUP[0], "K": MOD_GROUP[1], "N": MOD_GROUP[2],
+                                      "batch_call_us": round(vg["grouped_us"], 3),
+                                      "batch_call_GBps": round(vg["grouped_GBps"], 1),
+                                      "separate_calls_us": round(vg["separate_us"], 3),
+                                      "separate_calls_GBps": round(vg["separate_GBps"], 1),
+                                      "equal": vg["grouped_equals_separate"]}},
         "cpu_baseline": cpu,
     }
     if configs:

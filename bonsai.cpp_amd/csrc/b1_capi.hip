@@ -244,10 +244,7 @@ static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim,
         workspace(b1::gemm_workspace_bytes_total(a, dev->num_cus));
         return b1::launch_gemm(a, dev->num_cus, ws, ws_bytes, stream);
     };
-    auto gemv = [&]() {
-        workspace(b1::gemv_workspace_bytes(a));
-        return b1::launch_gemv_ws(a, dev->num_cus, ws, ws_bytes, stream);
-    };
+    auto gemv = [&]() { return b1::launch_gemv(a, dev->num_cus, stream); };
 
     hipError_t e;
     switch (mode) {
@@ -292,8 +289,8 @@ size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode) {
     a.lda = in_dim;
     a.act = reinterpret_cast<const float *>(uintptr_t(256));
     a.w = reinterpret_cast<const uint8_t *>(uintptr_t(256));
-    if (mode == BONSAI_B1_MODE_GEMV || (mode != BONSAI_B1_MODE_GEMM && batch <= b1::kGemvMaxM))
-        return b1::gemv_workspace_bytes(a);
+    // the small-M kernel converts the activations itself
+    if (mode == BONSAI_B1_MODE_GEMV || (mode != BONSAI_B1_MODE_GEMM && batch <= b1::kGemvMaxM)) return 0;
     // the range-safe packing, then (on a device where the shape splits
     // along K) the split-K partials
     const DeviceInfo *dev = current_device(nullptr);
@@ -719,11 +716,7 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
     const bool fused = packed_path(a, mode);
     // separate pass: y, then what the linear's own kernel can use
     const size_t y_bytes = epi_y_bytes(batch, out_dim);
-    const size_t lin_ws = fused || !b1::gemv_supported(a) || mode == BONSAI_B1_MODE_EXACT ||
-                                  mode == BONSAI_B1_MODE_GEMM
-                              ? 0
-                              : b1::gemv_workspace_bytes(a);
-    const size_t need = fused ? b1::pack_area_bytes(batch, in_dim) : y_bytes + lin_ws;
+    const size_t need = fused ? b1::pack_area_bytes(batch, in_dim) : y_bytes;
     WsLease lease;
     if (!workspace) {
         lease.acquire(dev, stream, need);
@@ -753,10 +746,10 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
             e = b1::launch_gemm_packed_epi(workspace, a.w, in_dim, out_dim, batch, out, ldo, nonfinite, dev->num_cus,
                                            kind, g, stream);
     } else {
-        // the linear into the workspace, then the epilogue pass
+        // the linear into the workspace (a kernel that needs no workspace of
+        // its own), then the epilogue pass
         float *y = static_cast<float *>(workspace);
-        void *rest = lin_ws ? static_cast<uint8_t *>(workspace) + y_bytes : nullptr;
-        st = linear_impl(act, lda, w, in_dim, out_dim, batch, y, out_dim, mode, nonfinite, 1, rest, lin_ws, stream);
+        st = linear_impl(act, lda, w, in_dim, out_dim, batch, y, out_dim, mode, nonfinite, 1, nullptr, 0, stream);
         if (st != BONSAI_B1_OK) return st;
         e = packed_out ? b1::launch_epi_packed(y, out_dim, batch, out_dim, g, out, ldo, stream)
                        : b1::launch_epi(y, out_dim, batch, out_dim, kind, g, out, ldo, stream);
@@ -778,20 +771,18 @@ void bonsai_b1_release_workspaces(void) {
 }
 
 // How one op of a batch runs (the same choice linear_impl makes).
-// Gemv: the small-M kernel converting fp32 itself; GemvPacked: the small-M
-// kernel over the (shared) range-safe packing; Packed: the packed GEMM;
-// Fused: the fused-conversion GEMM.
-enum class BatchPath { Exact, Gemv, GemvPacked, Packed, Fused };
+// Gemv: the small-M kernel (converting fp32 itself, or over the batch's
+// range-safe packing when it runs in a group, gemv_span); Packed: the packed
+// GEMM; Fused: the fused-conversion GEMM.
+enum class BatchPath { Exact, Gemv, Packed, Fused };
 
 static BatchPath batch_path(const b1::LinearArgs &a, int mode) {
     if (mode == BONSAI_B1_MODE_EXACT) return BatchPath::Exact;
-    if (b1::gemv_supported(a)) return b1::gemv_workspace_bytes(a) > 0 ? BatchPath::GemvPacked : BatchPath::Gemv;
+    if (b1::gemv_supported(a)) return BatchPath::Gemv;
     if (b1::gemm_supported(a))
         return b1::gemm_workspace_bytes(a) > 0 ? BatchPath::Packed : BatchPath::Fused;
     return BatchPath::Exact;
 }
-
-static bool uses_packing(BatchPath p) { return p == BatchPath::Packed || p == BatchPath::GemvPacked; }
 
 static b1::LinearArgs batch_args(const bonsai_b1_linear_op &op) {
     b1::LinearArgs a;
@@ -847,6 +838,7 @@ static int fuse_span(int n_ops, int mode, int num_cus, OpAt at, int i, int *n_su
     while (epi_kind(bi.epi) == BONSAI_B1_EPI_NONE && last + 1 < n_ops) {
         const BatchOp pb = at(last), qb = at(last + 1);
         const bonsai_b1_linear_op &p = *pb.op, &q = *qb.op;
+        if (!batch_op_ok(q, qb.epi)) break;
         // the packed size from the dimensions (nbytes is not trusted)
         const size_t p_bytes =
             (size_t)p.w->out_dim * (size_t)(p.w->in_dim / BONSAI_B1_BLOCK_SIZE) * BONSAI_B1_BLOCK_BYTES;
@@ -873,9 +865,51 @@ static int fuse_span(int n_ops, int mode, int num_cus, OpAt at, int i, int *n_su
     return last;
 }
 
+// The ops from i on that run as one grouped small-M launch with op i over
+// one range-safe packing of their input: consecutive plain small-M ops on
+// the same input (the modulation projections of src/diffuser_graph.cpp:308-311,
+// 470-471 and 548 all read vec_silu at one token), at most kGemvGroupMax,
+// whose outputs lie apart from that input and from one another (the group
+// writes them in no particular order).  Returns the last op of the run, i
+// when op i runs alone; fills ops[0 .. last - i].
+template <class OpAt>
+static int gemv_span(int n_ops, int mode, OpAt at, int i, b1::GemvGroupOp *ops) {
+    const BatchOp bi = at(i);
+    const b1::LinearArgs a = batch_args(*bi.op);
+    if (epi_kind(bi.epi) != BONSAI_B1_EPI_NONE || batch_path(a, mode) != BatchPath::Gemv ||
+        !b1::pack_supported(a.act, a.lda, a.M, a.K))
+        return i;
+    auto range = [](const void *p, int rows, int64_t ld, int cols, size_t elt, uintptr_t *r0, uintptr_t *r1) {
+        *r0 = reinterpret_cast<uintptr_t>(p);
+        *r1 = *r0 + ((size_t)(rows - 1) * (size_t)ld + (size_t)cols) * elt;
+    };
+    uintptr_t in0, in1;
+    range(a.act, a.M, a.lda, a.K, sizeof(float), &in0, &in1);
+    uintptr_t o0[b1::kGemvGroupMax], o1[b1::kGemvGroupMax];
+    int n = 0;
+    for (int j = i; j < n_ops && n < b1::kGemvGroupMax; ++j) {
+        const BatchOp bj = at(j);
+        const bonsai_b1_linear_op &q = *bj.op;
+        if (!batch_op_ok(q, bj.epi) || epi_kind(bj.epi) != BONSAI_B1_EPI_NONE || q.batch != a.M ||
+            q.act != a.act || q.lda != a.lda || q.w->in_dim != a.K || batch_path(batch_args(q), mode) != BatchPath::Gemv)
+            break;
+        uintptr_t q0, q1;
+        range(q.out, q.batch, q.ldo, q.w->out_dim, sizeof(float), &q0, &q1);
+        bool apart = !(q0 < in1 && in0 < q1);
+        for (int k = 0; k < n && apart; ++k) apart = !(q0 < o1[k] && o0[k] < q1);
+        if (!apart) break;
+        ops[n] = b1::GemvGroupOp{static_cast<const uint8_t *>(q.w->data), q.w->out_dim, q.out, q.ldo};
+        o0[n] = q0;
+        o1[n] = q1;
+        ++n;
+    }
+    if (n < 2 || !b1::gemv_group_ok(a.M, a.K, ops, n)) return i;
+    return i + n - 1;
+}
+
 // Workspace areas of a batch, laid out [pack][split][y], each 256-byte
-// aligned: the largest range-safe packing among its packed-GEMM and packed
-// small-M ops, the largest split-K partial area among its plain packed GEMMs
+// aligned: the largest range-safe packing among its packed GEMMs and
+// grouped small-M runs, the largest split-K partial area among its plain packed GEMMs
 // (fused runs included), and the largest fp32 linear output among its ops
 // whose epilogue runs as a separate pass (the other paths).
 struct BatchAreas {
@@ -893,7 +927,16 @@ static BatchAreas batch_areas(int n_ops, int mode, int num_cus, OpAt at) {
         if (!batch_op_ok(*b.op, b.epi) || b.op->batch == 0) continue;
         const b1::LinearArgs a = batch_args(*b.op);
         const BatchPath path = batch_path(a, mode);
-        if (uses_packing(path)) r.pack = std::max(r.pack, b1::pack_area_bytes(a.M, a.K));
+        if (path == BatchPath::Gemv) {
+            b1::GemvGroupOp ops[b1::kGemvGroupMax];
+            const int last = gemv_span(n_ops, mode, at, i, ops);
+            if (last > i) {
+                r.pack = std::max(r.pack, b1::pack_area_bytes(a.M, a.K));
+                i = last;
+                continue;
+            }
+        }
+        if (path == BatchPath::Packed) r.pack = std::max(r.pack, b1::pack_area_bytes(a.M, a.K));
         if (path == BatchPath::Packed) {
             if (epi_kind(b.epi) == BONSAI_B1_EPI_NONE) {
                 int n_sum;
@@ -997,11 +1040,13 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
         (void)epi_args(bo.epi, a.N, a.M, a.out, a.ldo, &kind, &g);
         int out_cols = kind == BONSAI_B1_EPI_SWIGLU ? a.N / 2 : a.N;
         const BatchPath path = batch_path(a, mode);
+        b1::GemvGroupOp gops[b1::kGemvGroupMax];
+        const int glast = path == BatchPath::Gemv ? gemv_span(n_ops, mode, at, i, gops) : i;
         hipError_t e = hipSuccess;
         // the range-safe packing of this op's input, unless the workspace
         // holds it already
         const float *rsc = nullptr;
-        if (uses_packing(path)) {
+        if (path == BatchPath::Packed || glast > i) {
             if (!(packed_act == a.act && packed_lda == a.lda && packed_m == a.M && packed_k == a.K)) {
                 e = b1::launch_pack_rows(a.act, a.lda, a.M, a.K, workspace, stream);
                 packed_act = a.act;
@@ -1011,7 +1056,13 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
             }
             rsc = b1::pack_area_rsc(workspace, a.M, a.K);
         }
-        if (path != BatchPath::Packed) {
+        if (glast > i) {
+            // the run's outputs lie apart from the packed input (gemv_span)
+            if (e == hipSuccess)
+                e = b1::launch_gemv_group(workspace, rsc, a.K, a.M, gops, glast - i + 1, nonfinite, dev->num_cus,
+                                          stream);
+            i = glast;
+        } else if (path != BatchPath::Packed) {
             // the linear, into the workspace first when an epilogue follows
             b1::LinearArgs la = a;
             if (kind != BONSAI_B1_EPI_NONE) {
@@ -1021,11 +1072,7 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
             if (e == hipSuccess) {
                 switch (path) {
                 case BatchPath::Exact: e = b1::launch_exact(la, stream); break;
-                case BatchPath::Gemv: e = b1::launch_gemv_ws(la, dev->num_cus, nullptr, 0, stream); break;
-                case BatchPath::GemvPacked:
-                    e = b1::launch_gemv_packed(workspace, la.w, la.K, la.N, la.M, la.out, la.ldo, nonfinite,
-                                               dev->num_cus, stream, rsc);
-                    break;
+                case BatchPath::Gemv: e = b1::launch_gemv(la, dev->num_cus, stream); break;
                 default: e = b1::launch_gemm(la, dev->num_cus, nullptr, 0, stream); break;
                 }
             }

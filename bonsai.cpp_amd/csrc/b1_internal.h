@@ -125,18 +125,13 @@ hipError_t launch_norm_mod(const float *x, int64_t ldx, int H, int rows, const f
                            float eps, float *y, int64_t ldy, void *packed, hipStream_t s);
 
 // Small-M (M <= 16) bandwidth-bound kernel; requires K % 64 == 0,
-// lda % 4 == 0, act 16-byte aligned.
+// lda % 4 == 0, act 16-byte aligned.  Range-safe: rows of tokens with an
+// activation beyond the fp16 range come out in EXACT mode's arithmetic
+// (inside the kernel when K % 256 == 0, else by launch_fixup_rows after it).
 bool gemv_supported(const LinearArgs &a);
 hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s);
 
 constexpr int kGemvMaxM = 16;
-
-// The small-M kernel from fp32 activations, range-safe: with a workspace of
-// gemv_workspace_bytes(a) bytes (> 0 when K % 256 == 0) they are packed
-// once (launch_pack_rows) and the kernel reads the packing; otherwise it
-// converts them itself and launch_fixup_rows follows.
-size_t gemv_workspace_bytes(const LinearArgs &a);
-hipError_t launch_gemv_ws(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s);
 
 // The small-M kernel over packed fp16 activations (the layout launch_pack
 // writes, row stride K): M <= 16, K % 256 == 0, weights and packing under
@@ -145,6 +140,20 @@ hipError_t launch_gemv_ws(const LinearArgs &a, int num_cus, void *workspace, siz
 bool gemv_packed_ok(int M, int K, int N);
 hipError_t launch_gemv_packed(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
                               int32_t *nonfinite, int num_cus, hipStream_t s, const float *rsc = nullptr);
+
+// Up to kGemvGroupMax small-M linears over one packed activation matrix in
+// one launch (M <= 16, K % 256 == 0, K <= 3072, each op's weights under
+// 2^31 bytes); the outputs must not overlap one another.
+constexpr int kGemvGroupMax = 8;
+struct GemvGroupOp {
+    const uint8_t *w;
+    int N;
+    float *out;
+    int64_t ldo;
+};
+bool gemv_group_ok(int M, int K, const GemvGroupOp *ops, int nops);
+hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M, const GemvGroupOp *ops, int nops,
+                             int32_t *nonfinite, int num_cus, hipStream_t s);
 
 // GELU-tanh over [rows][cols] fp32 (cols % 4 == 0, rows 16-byte aligned via
 // ld % 4 == 0); the fused form writes packed fp16 activations (pack rules).

@@ -1667,42 +1667,164 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
 }
 
 
-// The same kernel with the weights staged through LDS (K % 256 == 0, so rows
-// are 16-byte multiples): coalesced 1 KB buffer loads instead of per-lane
-// 8-byte gathers, which cost one L2 request per row touched.
-constexpr int kGv2RowChunks = kGvChunk * 6 / 16 + 1;          // 37: 36 data + 1 pad
-constexpr int kGv2RowBytes = kGv2RowChunks * 16;              // 592: conflict-free row stride
-constexpr int kGv2RgSlots = 16 * kGv2RowChunks;                                  // 592 per row group
-constexpr int kGv2Insts = (kGvMaxRG * kGv2RgSlots + 64 * kGvWaves - 1) / (64 * kGvWaves); // 7 per wave
-// The weight area holds every slot the kGv2Insts x kGvWaves loads write
-// (1 KB each), not only the kGvMaxRG * 16 rows in use.
-constexpr int kGv2Lds = kGvLds + kGv2Insts * kGvWaves * 1024; // 98304 + 57344
-static_assert(kGv2Insts * kGvWaves * 1024 >= kGvMaxRG * 16 * kGv2RowBytes, "weight rows fit");
-static_assert(kGv2Lds <= 160 * 1024, "gfx950 LDS");
+// The small-M kernel for K % 256 == 0 (rows are then 16-byte multiples):
+// the same per-wave K slices and cross-wave reduction as b1_gemv_kernel, with
+// every load a whole-instruction DMA and no work-group barrier before the
+// reduction.
+//  * Weights: each wave stages, for every row of its work-group's row
+//    groups, exactly its own K slice (72 bytes: 12 blocks, fetched as the 5
+//    aligned 16-byte chunks that cover it) into its own LDS area, rows 80
+//    bytes apart.  A wave therefore waits only for its own DMAs (vmcnt),
+//    row group by row group, and never for the other waves.
+//  * Activations, packed fp16 (PACKED): fragment (q, t) of the MFMA A
+//    operand is 16 token slots x 32 K; with S <= 16 slots in use (the power
+//    of two >= M) one 1 KB DMA carries 16 / S fragments, slot (g, tok) of
+//    fragment f at f % F * 64 S + (g S + tok) * 16, tokens past M and slots
+//    past S zero.  fp32 (!PACKED): lane (g, tok) loads the 8 elements of
+//    its fragment slot from the fp32 rows and converts them to fp16 pairs
+//    (round to nearest even) in registers; a lane that met an |a| >= 65520
+//    (beyond the fp16 range) flags its token, and after the reduction the
+//    work-group computes its rows of flagged tokens again in the reference's
+//    scalar arithmetic (EXACT mode's bits), correcting the non-finite count.
+//  * Order of the loads: activations first, then the weight row groups, so
+//    that vmcnt (which retires in issue order) tells when each has landed.
+// One pass covers 96 blocks (K 3072, 12 per wave); longer K runs more
+// passes over the same LDS areas.
+constexpr int kG3Chunk = kGvWaves * kGvBPW;                    // 96 blocks per pass
+constexpr int kG3RowCh = 5;                                    // 16-byte chunks per row per wave
+constexpr int kG3RowB = kG3RowCh * 16;                         // 80: wave-private row stride
+constexpr int kG3WInst = (kGvMaxRG * 16 * kG3RowCh + 63) / 64; // 8 weight DMAs per wave
+constexpr int kG3WLds = kG3WInst * 1024;                       // 8 KB of weights per wave
+constexpr int kG3ALds = kGvBPW * 1024;                         // 12 KB of fragments per wave
+constexpr int kG3WaveLds = kG3WLds + kG3ALds;
+constexpr int kG3Lds = kGvWaves * kG3WaveLds;                  // 160 KB
+static_assert(kG3Lds <= 160 * 1024, "gfx950 LDS");
+static_assert(kGvWaves * kGvMaxRG * 64 * 16 <= kG3Lds, "the reduction fits");
+static_assert(kG3RowB >= 72 + 8, "a slice plus its alignment slack");
 
-// Weight loads of one wave per pass: slot sl = 64 j + lane of instruction j
-// (j = wave, wave + 8, ...) covers LDS row sl / 37, chunk sl % 37; a fixed
-// count so that vmcnt waits are immediates (unused slots read zeros).
-// Instructions of one wave that cover row groups 0..r (an upper bound over
-// the 8 waves): all of them must have landed before row group r is used.
-__device__ constexpr int gv2_done_before(int r) {
-    const int j_end = ((r + 1) * kGv2RgSlots + 63) / 64; // instructions needed
-    return (j_end + kGvWaves - 1) / kGvWaves;
+// Row group R of the chunk being decoded has landed: all DMAs covering its
+// rows are done.  AHEAD more DMAs (the next chunk's, in the grouped kernel)
+// were issued after them; DMAs retire in issue order.
+template <int R, int AHEAD>
+__device__ __forceinline__ void g3_wait_rg() {
+    constexpr int j = ((R + 1) * 16 * kG3RowCh + 63) / 64;
+    wait_vmcnt<kG3WInst - j + AHEAD>();
+}
+template <int AHEAD>
+__device__ __forceinline__ void g3_wait(int r) {
+    switch (r) {
+    case 0: g3_wait_rg<0, AHEAD>(); break;
+    case 1: g3_wait_rg<1, AHEAD>(); break;
+    case 2: g3_wait_rg<2, AHEAD>(); break;
+    case 3: g3_wait_rg<3, AHEAD>(); break;
+    case 4: g3_wait_rg<4, AHEAD>(); break;
+    default: g3_wait_rg<5, AHEAD>(); break;
+    }
 }
 
-constexpr int kGvRgPerSync = 2; // row groups made visible per barrier
-
-template <int R>
-__device__ __forceinline__ void gv2_wait_rg() {
-    wait_vmcnt<kGv2Insts - gv2_done_before(R)>();
+// Decode and MFMA of row groups [0, nrg) of a pass, from a wave's staged
+// rows (wbuf, 80 bytes apart) and its activation fragments af.  The slice
+// of wave w starts 8 (w odd) bytes into its first chunk; block 4q + g sits
+// at 6 (4q + g) bytes into the slice, read as the aligned 8-byte window
+// that holds it (2 bytes earlier for odd g).  Each row group is decoded as
+// soon as its own DMAs have landed (AHEAD: DMAs issued after this chunk's).
+template <int AHEAD>
+__device__ __forceinline__ void g3_decode(const uint8_t *wbuf, int nrg, int wave, int lane, const u32x4 (&af)[kGvQuads][4],
+                                          floatx4 (&acc)[kGvMaxRG]) {
+    const int col = lane & 15, g = lane >> 4, odd = g & 1;
+    const uint32_t sel_word = odd ? 0x07060504u : 0x05040302u;
+    const uint32_t sel_scale = odd ? 0x03020302u : 0x01000100u;
+    const int wshift = 8 * (wave & 1);
+#pragma unroll
+    for (int r = 0; r < kGvMaxRG; ++r) {
+        if (r < nrg) {
+            g3_wait<AHEAD>(r);
+            uint32_t wd[kGvQuads][2];
+#pragma unroll
+            for (int q = 0; q < kGvQuads; ++q) {
+                const __attribute__((address_space(3))) uint32_t *src =
+                    reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
+                        (__attribute__((address_space(3))) uint8_t *)wbuf + (r * 16 + col) * kG3RowB +
+                        (4 * q + g) * 6 + wshift - 2 * odd);
+                wd[q][0] = src[0];
+                wd[q][1] = src[1];
+            }
+#pragma unroll
+            for (int q = 0; q < kGvQuads; ++q) {
+                const uint32_t s2 = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_scale);
+                const uint32_t w = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_word);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    u32x4 bd;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) bd[jj] = wpair(w, 15 - 4 * t - jj, s2);
+                    acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, af[q][t]),
+                                                                    __builtin_bit_cast(half8, bd), acc[r], 0, 0, 0);
+                }
+            }
+        }
+    }
 }
 
-// PACKED: p.act points at packed fp16 activations ([M][K] in the K-slot
-// pairing, row stride K), which go global -> LDS straight into the fragment
-// layout (no conversion); token slots past M read row M - 1 and are zeroed
-// at the fragment read like the fp32 path's.
-template <bool PACKED>
-__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv2_kernel(LinearArgs p, int groups, int mp_log2) {
+// The activation DMAs of a wave's pass (packed fp16, S slots): F = 16 / S
+// fragments per 1 KB DMA, kGvBPW fragments.
+template <int S>
+__device__ __forceinline__ void g3_issue_act(__amdgpu_buffer_rsrc_t ars, uint8_t *abuf, int lane, int wb0, int nb, int M,
+                                             int K) {
+    constexpr int F = (16 / S) < kGvBPW ? 16 / S : kGvBPW;
+    constexpr int NA = (kGvBPW + F - 1) / F;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int sub = lane / (4 * S), within = lane % (4 * S);
+        const int ag = within / S, tok = within % S;
+        const int f = i * F + sub;
+        const int blk = wb0 + 4 * (f >> 2) + ag;
+        const bool ok = f < kGvBPW && tok < M && blk < nb;
+        dma_buf_lds16(ars, abuf + i * 1024,
+                      ok ? (uint32_t)tok * (uint32_t)K * 2u + (uint32_t)blk * 64u + (uint32_t)(f & 3) * 16u
+                         : 0xFFFFFFF0u);
+    }
+}
+
+template <int S>
+__device__ __forceinline__ void g3_read_act(const uint8_t *abuf, int lane, u32x4 (&af)[kGvQuads][4]) {
+    constexpr int F = (16 / S) < kGvBPW ? 16 / S : kGvBPW;
+    const int col = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int q = 0; q < kGvQuads; ++q)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int f = 4 * q + t;
+            af[q][t] = col < S ? *reinterpret_cast<const u32x4 *>(abuf + f / F * 1024 + (f % F * 4 * S + g * S + col) * 16)
+                               : u32x4{0u, 0u, 0u, 0u};
+        }
+}
+
+// Cross-wave reduction of a chunk's partial tiles (waves' partials at
+// `red` + wave * wstride, [rg][lane] floatx4) in wave order, then the
+// outputs of row groups [0, nrg) starting at row n0 of out, times the row
+// scales rsc when given.  Returns the non-finite count.
+__device__ __forceinline__ int g3_reduce_store(const uint8_t *red, int wstride, int nrg, int tid, int M, int N, int n0,
+                                               float *out, int64_t ldo, const float *rsc) {
+    int bad = 0;
+    for (int e = tid; e < nrg * 256; e += kGvWaves * 64) {
+        const int c = e & 15, tok = (e >> 4) & 15, r = e >> 8;
+        const int ln = 16 * (tok >> 2) + c, v = tok & 3;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kGvWaves; ++w) sum += reinterpret_cast<const floatx4 *>(red + w * wstride)[r * 64 + ln][v];
+        const int n = n0 + r * 16 + c;
+        if (tok < M && n < N) {
+            if (rsc) sum *= rsc[tok];
+            bad += !__builtin_isfinite(sum);
+            out[(size_t)tok * ldo + n] = sum;
+        }
+    }
+    return bad;
+}
+
+template <int S, bool PACKED>
+__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, int groups) {
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
@@ -1712,176 +1834,215 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv2_kernel(LinearArgs p, i
     const int nrg = rg1 - rg0;
     const int nb = p.K / 32;
     const uint32_t rs = (uint32_t)nb * 6;
-    const int mp = 1 << mp_log2; // token slots, power of two >= M
-    uint8_t *abuf = gsm + wave * kGvWaveLds;
-    uint8_t *wbuf = gsm + kGvLds;
+    uint8_t *wbuf = gsm + wave * kG3WaveLds;
+    uint8_t *abuf = wbuf + kG3WLds;
     const __amdgpu_buffer_rsrc_t wrs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p.w), (short)0, (int)(p.N * rs), kBufferFlags);
-    const int odd = g & 1;
-    const uint32_t sel_word = odd ? 0x07060504u : 0x05040302u;
-    const uint32_t sel_scale = odd ? 0x03020302u : 0x01000100u;
+    // this wave's slice: bytes [72 w, 72 w + 72) of a pass's row part,
+    // fetched from the aligned 72 w - 8 (w odd) as kG3RowCh chunks
+    const uint32_t slice0 = (uint32_t)(72 * wave) & ~15u;
 
     floatx4 acc[kGvMaxRG];
 #pragma unroll
     for (int r = 0; r < kGvMaxRG; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+    int ovf = 0; // fp32: this lane converted an activation beyond the fp16 range
 
-    for (int kb0 = 0; kb0 < nb; kb0 += kGvChunk) {
+    for (int kb0 = 0; kb0 < nb; kb0 += kG3Chunk) {
         const int wb0 = kb0 + wave * kGvBPW;
-        const int pass_blocks = min(kGvChunk, nb - kb0);
-        const int row_chunks = pass_blocks * 6 / 16;
-
-        // 1. This wave's activation loads, unit u = (bl*4 + t)*mp + tok
-        //    covering a[tok][32 (wb0+bl) + 4t .. +3] and the 4 elements 16
-        //    later; 64 * kGvAUnits units per batch (one batch for M <= 8).
-        //    Packed: fragment (q, t) is one 1 KB load, lane (g, tok) reading
-        //    the 16 bytes of dwords 4t..4t+3 of block 4q + g of row tok.
-        const int units = PACKED ? 0 : 48 << mp_log2;
-        floatx4 lo[kGvAUnits], hi[kGvAUnits];
-        auto load_units = [&](int base) {
-#pragma unroll
-            for (int i = 0; i < kGvAUnits; ++i) {
-                const int u = min(base + i * 64 + lane, units - 1);
-                const int tok = min(u & (mp - 1), p.M - 1);
-                const int bt = u >> mp_log2;
-                const int blk = min(wb0 + (bt >> 2), nb - 1);
-                const float *src = p.act + (size_t)tok * p.lda + (size_t)blk * 32 + 4 * (bt & 3);
-                lo[i] = *reinterpret_cast<const floatx4 *>(src);
-                hi[i] = *reinterpret_cast<const floatx4 *>(src + 16);
-            }
-        };
-        auto store_units = [&](int base) {
-#pragma unroll
-            for (int i = 0; i < kGvAUnits; ++i) {
-                const int u = base + i * 64 + lane;
-                const int tok = u & (mp - 1), bt = u >> mp_log2;
-                const int bl = bt >> 2, t = bt & 3;
-                if (u < units) {
-                    const bool ok = wb0 + bl < nb;
-                    u32x4 v;
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) v[jj] = ok ? pack_f16(lo[i][jj], hi[i][jj]) : 0u;
-                    *reinterpret_cast<u32x4 *>(abuf + ((((bl >> 2) * 4 + t) * 64) + (bl & 3) * 16 + tok) * 16) = v;
-                }
-            }
-        };
+        // 1. activations
+        floatx4 xa[PACKED ? 1 : kGvBPW][2];
         if constexpr (PACKED) {
             const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float *>(p.act), (short)0, (int)((uint32_t)p.M * (uint32_t)p.K * 2u), kBufferFlags);
-            const uint32_t trow = (uint32_t)min(lane & 15, p.M - 1) * (uint32_t)p.K * 2u;
-#pragma unroll
-            for (int q = 0; q < kGvQuads; ++q) {
-                const int blk = wb0 + 4 * q + (lane >> 4);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint32_t voff = blk < nb ? trow + (uint32_t)blk * 64u + (uint32_t)t * 16u : 0xFFFFFFF0u;
-                    dma_buf_lds16(ars, abuf + (q * 4 + t) * 1024, voff);
-                }
-            }
+            g3_issue_act<S>(ars, abuf, lane, wb0, nb, p.M, p.K);
         } else {
-            load_units(0);
-        }
-
-        // 2. The work-group's weight rows of this pass, row group by row
-        //    group, as whole 1 KB runs straight into LDS.
+            // lane (g, col): elements 32 blk + 4 t .. +3 and 16 later of token
+            // col, blk = wb0 + 4 q + g, for fragment (q, t)
 #pragma unroll
-        for (int i = 0; i < kGv2Insts; ++i) {
-            const int j = wave + kGvWaves * i;
-            const int sl = j * 64 + lane;
-            const int row = sl / kGv2RowChunks, ch = sl - row * kGv2RowChunks;
-            const uint32_t voff = (row < nrg * 16 && ch < row_chunks)
-                                      ? (uint32_t)(rg0 * 16 + row) * rs + (uint32_t)kb0 * 6 + (uint32_t)ch * 16
-                                      : 0xFFFFFFF0u;
-            dma_buf_lds16(wrs, wbuf + j * 1024, voff);
-        }
-
-        // 3. Activations -> fp16 fragments in this wave's LDS area; the
-        //    weight loads, issued after the first batch, stay in flight.
-        wait_vmcnt<kGv2Insts>();
-        if constexpr (!PACKED) {
-            store_units(0);
-            for (int base = 64 * kGvAUnits; base < units; base += 64 * kGvAUnits) { // M > 8
-                load_units(base);
-                wait_vmcnt<0>();
-                store_units(base);
+            for (int f = 0; f < kGvBPW; ++f) {
+                const int blk = wb0 + 4 * (f >> 2) + g;
+                if (col < p.M && blk < nb) {
+                    const float *src = p.act + (size_t)col * p.lda + (size_t)blk * 32 + 4 * (f & 3);
+                    xa[f][0] = *reinterpret_cast<const floatx4 *>(src);
+                    xa[f][1] = *reinterpret_cast<const floatx4 *>(src + 16);
+                } else {
+                    xa[f][0] = xa[f][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+                }
             }
         }
+        // 2. this wave's slice of every row of the work-group's row groups
+#pragma unroll
+        for (int i = 0; i < kG3WInst; ++i) {
+            const int sl = i * 64 + lane;
+            const int row = sl / kG3RowCh, ch = sl - row * kG3RowCh;
+            const uint32_t inrow = (uint32_t)kb0 * 6u + slice0 + (uint32_t)ch * 16u;
+            dma_buf_lds16(wrs, wbuf + i * 1024,
+                          (row < nrg * 16 && inrow < rs) ? (uint32_t)(rg0 * 16 + row) * rs + inrow : 0xFFFFFFF0u);
+        }
+        // 3. the activations (issued first) have landed when at most the
+        //    weight DMAs are outstanding
+        wait_vmcnt<kG3WInst>();
         u32x4 af[kGvQuads][4];
+        if constexpr (PACKED) {
+            g3_read_act<S>(abuf, lane, af);
+        } else {
 #pragma unroll
-        for (int q = 0; q < kGvQuads; ++q)
+            for (int f = 0; f < kGvBPW; ++f)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const u32x4 v = *reinterpret_cast<const u32x4 *>(abuf + ((q * 4 + t) * 64 + lane) * 16);
-                af[q][t] = col < p.M ? v : u32x4{0u, 0u, 0u, 0u};
-            }
-
-        // 4. Row group by row group: once its rows have landed for every
-        //    wave, decode and multiply while later groups still stream.
-#pragma unroll
-        for (int r = 0; r < kGvMaxRG; ++r) {
-            if (r < nrg) {
-                if (r % kGvRgPerSync == 0) {
-                    // row groups r .. r + kGvRgPerSync - 1 have landed
-                    switch (min(r + kGvRgPerSync - 1, kGvMaxRG - 1)) {
-                    case 0: gv2_wait_rg<0>(); break;
-                    case 1: gv2_wait_rg<1>(); break;
-                    case 2: gv2_wait_rg<2>(); break;
-                    case 3: gv2_wait_rg<3>(); break;
-                    case 4: gv2_wait_rg<4>(); break;
-                    default: gv2_wait_rg<5>(); break;
-                    }
-                    lds_barrier();
+                for (int j = 0; j < 4; ++j) {
+                    ovf |= (__builtin_fabsf(xa[f][0][j]) >= 65520.0f) | (__builtin_fabsf(xa[f][1][j]) >= 65520.0f);
+                    af[f >> 2][f & 3][j] = pack_f16(xa[f][0][j], xa[f][1][j]);
                 }
-                uint32_t wd[kGvQuads][2];
-#pragma unroll
-                for (int q = 0; q < kGvQuads; ++q) {
-                    const int bl = wave * kGvBPW + 4 * q + g; // block within the pass
-                    const __attribute__((address_space(3))) uint32_t *src =
-                        reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
-                            (__attribute__((address_space(3))) uint8_t *)wbuf + (r * 16 + col) * kGv2RowBytes +
-                            bl * 6 - 2 * odd);
-                    wd[q][0] = src[0];
-                    wd[q][1] = src[1];
-                }
-#pragma unroll
-                for (int q = 0; q < kGvQuads; ++q) {
-                    const uint32_t s2 = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_scale);
-                    const uint32_t w = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_word);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        u32x4 bd;
-#pragma unroll
-                        for (int jj = 0; jj < 4; ++jj) bd[jj] = wpair(w, 15 - 4 * t - jj, s2);
-                        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(half8, af[q][t]), __builtin_bit_cast(half8, bd), acc[r], 0, 0, 0);
-                    }
-                }
-            }
         }
+        // 4. row group by row group, as this wave's own DMAs land
+        g3_decode<0>(wbuf, nrg, wave, lane, af, acc);
         wait_vmcnt<0>();
-        __syncthreads(); // all reads of wbuf and abuf done before they are reused
+        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): LDS reads done before the next pass's DMAs
     }
 
-    // Cross-wave (split-K) reduction in a fixed order, in LDS reused from the
-    // activation fragments, then store.  16x16 accumulator layout: lane
-    // column = lane & 15 (weight row), rows 4*(lane >> 4) + v (tokens).
+    // cross-wave reduction in a fixed order
+    __syncthreads();
     floatx4 *red = reinterpret_cast<floatx4 *>(gsm); // [wave][rg][lane]
 #pragma unroll
     for (int r = 0; r < kGvMaxRG; ++r)
         if (r < nrg) red[(wave * kGvMaxRG + r) * 64 + lane] = acc[r];
     __syncthreads();
-    int bad = 0;
-    for (int e = tid; e < nrg * 256; e += kGvWaves * 64) {
-        const int c = e & 15, tok = (e >> 4) & 15, r = e >> 8;
-        const int ln = 16 * (tok >> 2) + c, v = tok & 3;
-        float sum = 0.0f;
+    int bad = g3_reduce_store(gsm, kGvMaxRG * 64 * 16, nrg, tid, p.M, p.N, rg0 * 16, p.out, p.ldo,
+                              PACKED ? p.rsc : nullptr);
+    if constexpr (!PACKED) {
+        // tokens with an activation beyond the fp16 range: a flag word per
+        // wave, their OR, then this work-group's rows of those tokens again
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(ovf != 0);
+        const uint32_t toks = (uint32_t)((bal | (bal >> 16) | (bal >> 32) | (bal >> 48)) & 0xFFFFu);
+        __syncthreads();
+        uint32_t *flags = reinterpret_cast<uint32_t *>(gsm);
+        if (lane == 0) flags[wave] = toks;
+        __syncthreads();
+        uint32_t all = 0;
 #pragma unroll
-        for (int w = 0; w < kGvWaves; ++w) sum += red[(w * kGvMaxRG + r) * 64 + ln][v];
-        const int n = (rg0 + r) * 16 + c;
-        if (tok < p.M && n < p.N) {
-            if (PACKED && p.rsc) sum *= p.rsc[tok];
-            bad += !__builtin_isfinite(sum);
-            p.out[(size_t)tok * p.ldo + n] = sum;
+        for (int w = 0; w < kGvWaves; ++w) all |= flags[w];
+        if (all) {
+#pragma clang fp contract(off)
+            for (int e = tid; e < 16 * nrg * 16; e += kGvWaves * 64) {
+                const int tok = e / (nrg * 16), rr = e - tok * (nrg * 16);
+                const int n = rg0 * 16 + rr;
+                if (tok >= p.M || n >= p.N || !((all >> tok) & 1u)) continue;
+                const float *xr = p.act + (size_t)tok * p.lda;
+                const uint16_t *wr = reinterpret_cast<const uint16_t *>(p.w + (size_t)n * rs);
+                float sum = 0.0f;
+                for (int b = 0; b < nb; ++b) {
+                    const float scale = (float)__builtin_bit_cast(_Float16, wr[3 * b]);
+                    const uint32_t bits = (uint32_t)wr[3 * b + 1] | ((uint32_t)wr[3 * b + 2] << 16);
+                    float bs = 0.0f;
+                    for (int i = 0; i < 32; ++i) {
+                        const float a = xr[32 * b + i];
+                        bs = ((bits >> i) & 1u) ? bs + a : bs - a;
+                    }
+                    sum = sum + scale * bs;
+                }
+                float *o = p.out + (size_t)tok * p.ldo + n;
+                bad += !__builtin_isfinite(sum) - !__builtin_isfinite(*o);
+                *o = sum;
+            }
         }
+    }
+    count_nonfinite(p.nonfinite, bad);
+}
+
+// Several small-M linears over one packed activation matrix in one launch
+// (the modulation projections of a step, q/k/v of the text stream at a few
+// tokens): persistent work-groups over the row groups of all the ops,
+// in chunks of at most kGvMaxRG row groups of one op; the activation
+// fragments (K <= 3072: one pass) are loaded once per work-group and held in
+// registers, and the weight DMAs of the next chunk are issued before the
+// current one is decoded, into the wave's other LDS buffer.  Each chunk is
+// reduced across the waves through the buffer it was decoded from.
+struct GemvGroup {
+    const uint8_t *w[kGemvGroupMax];
+    float *out[kGemvGroupMax];
+    int64_t ldo[kGemvGroupMax];
+    int N[kGemvGroupMax];
+    int gstart[kGemvGroupMax + 1]; // first global row group of each op; gstart[nops..] = total
+    int nops, groups, K, M;
+    const void *act;             // packed fp16 [M][K]
+    const float *rsc;            // row scales of the packing, or nullptr
+    int32_t *nonfinite;
+};
+
+template <int S>
+__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_group_kernel(GemvGroup p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nb = p.K / 32;
+    const uint32_t rs = (uint32_t)nb * 6;
+    uint8_t *bufA = gsm + wave * kG3WaveLds; // 8 KB
+    uint8_t *bufB = bufA + kG3WLds;          // 12 KB: the activations, then weights
+    const uint32_t slice0 = (uint32_t)(72 * wave) & ~15u;
+    const int nwg = gridDim.x, bid = blockIdx.x;
+    const int G0 = (int)(((int64_t)p.groups * bid) / nwg);
+    const int G1 = (int)(((int64_t)p.groups * (bid + 1)) / nwg);
+    auto op_of = [&](int gg) {
+        int op = 0;
+#pragma unroll
+        for (int o = 1; o < kGemvGroupMax; ++o) op += gg >= p.gstart[o] ? 1 : 0;
+        return op;
+    };
+    auto chunk_len = [&](int cg0, int op) { return min(min(kGvMaxRG, G1 - cg0), p.gstart[op + 1] - cg0); };
+    auto issue_w = [&](int cg0, int cng, int op, uint8_t *buf) {
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(p.w[op]), (short)0, (int)((uint32_t)p.N[op] * rs), kBufferFlags);
+        const int n0 = (cg0 - p.gstart[op]) * 16;
+#pragma unroll
+        for (int i = 0; i < kG3WInst; ++i) {
+            const int sl = i * 64 + lane;
+            const int row = sl / kG3RowCh, ch = sl - row * kG3RowCh;
+            const uint32_t inrow = slice0 + (uint32_t)ch * 16u;
+            dma_buf_lds16(wrs, buf + i * 1024,
+                          (row < cng * 16 && inrow < rs) ? (uint32_t)(n0 + row) * rs + inrow : 0xFFFFFFF0u);
+        }
+    };
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(p.act), (short)0, (int)((uint32_t)p.M * (uint32_t)p.K * 2u), kBufferFlags);
+    g3_issue_act<S>(ars, bufB, lane, wave * kGvBPW, nb, p.M, p.K);
+    int cg0 = G0;
+    int op = G0 < G1 ? op_of(G0) : 0;
+    int cng = G0 < G1 ? chunk_len(G0, op) : 0;
+    if (cng > 0) issue_w(cg0, cng, op, bufA);
+    wait_vmcnt<kG3WInst>();
+    u32x4 af[kGvQuads][4];
+    g3_read_act<S>(bufB, lane, af);
+    __builtin_amdgcn_s_waitcnt(0xc07f); // the fragments are in registers before bufB takes weights
+
+    int bad = 0;
+    for (int c = 0; cg0 < G1; ++c) {
+        uint8_t *cur = (c & 1) ? bufB : bufA;
+        uint8_t *nxt = (c & 1) ? bufA : bufB;
+        const int ng0 = cg0 + cng;
+        const bool more = ng0 < G1;
+        const int nop = more ? op_of(ng0) : 0;
+        const int nng = more ? chunk_len(ng0, nop) : 0;
+        if (more) issue_w(ng0, nng, nop, nxt);
+        floatx4 acc[kGvMaxRG];
+#pragma unroll
+        for (int r = 0; r < kGvMaxRG; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // the next chunk's DMAs (and earlier chunks' output stores, which
+        // only make the wait stricter) were issued after the current chunk's
+        if (more)
+            g3_decode<kG3WInst>(cur, cng, wave, lane, af, acc);
+        else
+            g3_decode<0>(cur, cng, wave, lane, af, acc);
+        __builtin_amdgcn_s_waitcnt(0xc07f); // this wave's reads of `cur` are done
+        floatx4 *mine = reinterpret_cast<floatx4 *>(cur);
+#pragma unroll
+        for (int r = 0; r < kGvMaxRG; ++r)
+            if (r < cng) mine[r * 64 + lane] = acc[r];
+        __syncthreads();
+        bad += g3_reduce_store(gsm + ((c & 1) ? kG3WLds : 0), kG3WaveLds, cng, tid, p.M, p.N[op],
+                               (cg0 - p.gstart[op]) * 16, p.out[op], p.ldo[op], p.rsc);
+        __syncthreads(); // every wave's partials read before `cur` takes a later chunk
+        cg0 = ng0;
+        op = nop;
+        cng = nng;
     }
     count_nonfinite(p.nonfinite, bad);
 }
@@ -2208,14 +2369,24 @@ static hipError_t gemv_attrs() {
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(attr_once, [] {
+        const void *g3[] = {
+            reinterpret_cast<const void *>(&b1_gemv3_kernel<16, false>),
+            reinterpret_cast<const void *>(&b1_gemv3_kernel<1, true>),
+            reinterpret_cast<const void *>(&b1_gemv3_kernel<2, true>),
+            reinterpret_cast<const void *>(&b1_gemv3_kernel<4, true>),
+            reinterpret_cast<const void *>(&b1_gemv3_kernel<8, true>),
+            reinterpret_cast<const void *>(&b1_gemv3_kernel<16, true>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<1>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<2>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<4>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<8>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<16>),
+        };
         attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kGvLds);
-        if (attr_err == hipSuccess)
-            attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv2_kernel<false>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGv2Lds);
-        if (attr_err == hipSuccess)
-            attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv2_kernel<true>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGv2Lds);
+        for (const void *f : g3)
+            if (attr_err == hipSuccess)
+                attr_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kG3Lds);
     });
     return attr_err;
 }
@@ -2226,49 +2397,34 @@ static bool gemv_staged(int K, int N) {
     return K % 256 == 0 && (uint64_t)N * (uint64_t)(K / 32) * 6 < (1ull << 31);
 }
 
-static void gemv_grid(const LinearArgs &a, int num_cus, int *nwg_out, int *groups_out, int *mp_log2_out) {
-    const int groups = (a.N + 15) / 16;
+// One work-group per CU, at most kGvMaxRG row groups each, at least one.
+static void gemv_grid(int N, int num_cus, int *nwg_out, int *groups_out) {
+    const int groups = (N + 15) / 16;
     int nwg = num_cus > 0 ? num_cus : 256;
     const int need = (groups + kGvMaxRG - 1) / kGvMaxRG;
     if (nwg < need) nwg = need;
     if (nwg > groups) nwg = groups;
-    int mp_log2 = 0;
-    while ((1 << mp_log2) < a.M) ++mp_log2;
     *nwg_out = nwg;
     *groups_out = groups;
-    *mp_log2_out = mp_log2;
 }
 
 hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
     const hipError_t attr_err = gemv_attrs();
     if (attr_err != hipSuccess) return attr_err;
-    int nwg, groups, mp_log2;
-    gemv_grid(a, num_cus, &nwg, &groups, &mp_log2);
-    if (gemv_staged(a.K, a.N))
-        hipLaunchKernelGGL(b1_gemv2_kernel<false>, dim3(nwg), dim3(kGvWaves * 64), kGv2Lds, s, a, groups, mp_log2);
-    else
-        hipLaunchKernelGGL(b1_gemv_kernel, dim3(nwg), dim3(kGvWaves * 64), kGvLds, s, a, groups, mp_log2);
-    return hipGetLastError();
-}
-
-size_t gemv_workspace_bytes(const LinearArgs &a) {
-    return gemv_supported(a) && gemv_staged(a.K, a.N) && (uint64_t)a.M * (uint64_t)a.K * 2 < (1ull << 31)
-               ? pack_area_bytes(a.M, a.K)
-               : 0;
-}
-
-hipError_t launch_gemv_ws(const LinearArgs &a, int num_cus, void *workspace, size_t ws_bytes, hipStream_t s) {
-    const size_t need = gemv_workspace_bytes(a);
-    hipError_t e;
-    if (need == 0 || workspace == nullptr || ws_bytes < need) {
-        // conversion inside the small-M kernel, then the exact rows
-        e = launch_gemv(a, num_cus, s);
-        return e == hipSuccess ? launch_fixup_rows(a, s) : e;
+    int nwg, groups;
+    gemv_grid(a.N, num_cus, &nwg, &groups);
+    if (gemv_staged(a.K, a.N)) {
+        // converts and repairs out-of-range tokens itself
+        LinearArgs b = a;
+        b.rsc = nullptr;
+        hipLaunchKernelGGL((b1_gemv3_kernel<16, false>), dim3(nwg), dim3(kGvWaves * 64), kG3Lds, s, b, groups);
+        return hipGetLastError();
     }
-    e = launch_pack_rows(a.act, a.lda, a.M, a.K, workspace, s);
-    if (e != hipSuccess) return e;
-    return launch_gemv_packed(workspace, a.w, a.K, a.N, a.M, a.out, a.ldo, a.nonfinite, num_cus, s,
-                              pack_area_rsc(workspace, a.M, a.K));
+    int mp_log2 = 0;
+    while ((1 << mp_log2) < a.M) ++mp_log2;
+    hipLaunchKernelGGL(b1_gemv_kernel, dim3(nwg), dim3(kGvWaves * 64), kGvLds, s, a, groups, mp_log2);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? launch_fixup_rows(a, s) : e;
 }
 
 bool gemv_packed_ok(int M, int K, int N) {
@@ -2281,9 +2437,69 @@ hipError_t launch_gemv_packed(const void *packed, const uint8_t *w, int K, int N
     const hipError_t attr_err = gemv_attrs();
     if (attr_err != hipSuccess) return attr_err;
     const LinearArgs a{static_cast<const float *>(packed), K, w, K, N, M, out, ldo, nonfinite, rsc};
-    int nwg, groups, mp_log2;
-    gemv_grid(a, num_cus, &nwg, &groups, &mp_log2);
-    hipLaunchKernelGGL(b1_gemv2_kernel<true>, dim3(nwg), dim3(kGvWaves * 64), kGv2Lds, s, a, groups, mp_log2);
+    int nwg, groups;
+    gemv_grid(N, num_cus, &nwg, &groups);
+    const dim3 grid(nwg), block(kGvWaves * 64);
+    if (M <= 1)
+        hipLaunchKernelGGL((b1_gemv3_kernel<1, true>), grid, block, kG3Lds, s, a, groups);
+    else if (M <= 2)
+        hipLaunchKernelGGL((b1_gemv3_kernel<2, true>), grid, block, kG3Lds, s, a, groups);
+    else if (M <= 4)
+        hipLaunchKernelGGL((b1_gemv3_kernel<4, true>), grid, block, kG3Lds, s, a, groups);
+    else if (M <= 8)
+        hipLaunchKernelGGL((b1_gemv3_kernel<8, true>), grid, block, kG3Lds, s, a, groups);
+    else
+        hipLaunchKernelGGL((b1_gemv3_kernel<16, true>), grid, block, kG3Lds, s, a, groups);
+    return hipGetLastError();
+}
+
+bool gemv_group_ok(int M, int K, const GemvGroupOp *ops, int nops) {
+    if (nops < 1 || nops > kGemvGroupMax || M < 1 || M > kGemvMaxM || K < 1 || K > kG3Chunk * 32) return false;
+    int64_t groups = 0;
+    for (int i = 0; i < nops; ++i) {
+        if (ops[i].N < 1 || !gemv_staged(K, ops[i].N)) return false;
+        groups += (ops[i].N + 15) / 16;
+    }
+    return groups <= INT32_MAX;
+}
+
+hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M, const GemvGroupOp *ops, int nops,
+                             int32_t *nonfinite, int num_cus, hipStream_t s) {
+    const hipError_t attr_err = gemv_attrs();
+    if (attr_err != hipSuccess) return attr_err;
+    GemvGroup p{};
+    int gs = 0;
+    for (int o = 0; o < kGemvGroupMax; ++o) {
+        p.gstart[o] = gs;
+        const GemvGroupOp &op = ops[o < nops ? o : 0];
+        p.w[o] = op.w;
+        p.out[o] = op.out;
+        p.ldo[o] = o < nops ? op.ldo : 0;
+        p.N[o] = o < nops ? op.N : 0;
+        if (o < nops) gs += (op.N + 15) / 16;
+    }
+    // ops past nops start at the end: no row group maps to them
+    for (int o = nops; o <= kGemvGroupMax; ++o) p.gstart[o] = gs;
+    p.nops = nops;
+    p.groups = gs;
+    p.K = K;
+    p.M = M;
+    p.act = packed;
+    p.rsc = rsc;
+    p.nonfinite = nonfinite;
+    int nwg = num_cus > 0 ? num_cus : 256;
+    if (nwg > gs) nwg = gs;
+    const dim3 grid(nwg), block(kGvWaves * 64);
+    if (M <= 1)
+        hipLaunchKernelGGL((b1_gemv_group_kernel<1>), grid, block, kG3Lds, s, p);
+    else if (M <= 2)
+        hipLaunchKernelGGL((b1_gemv_group_kernel<2>), grid, block, kG3Lds, s, p);
+    else if (M <= 4)
+        hipLaunchKernelGGL((b1_gemv_group_kernel<4>), grid, block, kG3Lds, s, p);
+    else if (M <= 8)
+        hipLaunchKernelGGL((b1_gemv_group_kernel<8>), grid, block, kG3Lds, s, p);
+    else
+        hipLaunchKernelGGL((b1_gemv_group_kernel<16>), grid, block, kG3Lds, s, p);
     return hipGetLastError();
 }
 

@@ -112,11 +112,12 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
                          hipStream_t stream);
 
 /*
- * The FAST kernels pack the activations to fp16 once (with the row scales
+ * The GEMM kernels pack the activations to fp16 once (with the row scales
  * of the range-safe packing, and, for shapes that split along K, the split
  * partials after them) into a device workspace of
  * bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) bytes (0 when the
- * call needs none).  bonsai_b1_linear_f32 keeps library-owned workspaces
+ * call needs none: EXACT, and small batches, whose kernel converts the
+ * activations itself).  bonsai_b1_linear_f32 keeps library-owned workspaces
  * per (device, stream), grown on demand with hipMalloc; while a stream is
  * being captured it never allocates and, lacking a large enough buffer,
  * runs the kernel variant that converts activations tile by tile.  A buffer
@@ -234,7 +235,9 @@ int bonsai_b1_linear_packed_f16_ws(const void *packed_act, const void *w,
  * smallest shift that brings its largest |act| below 2^15.
  * _linear_packed_f16_scaled is bonsai_b1_linear_packed_f16 with row m's
  * outputs multiplied by row_scale[m] (exact: powers of two); together they
- * give bonsai_b1_linear_f32's FAST results bit for bit.  No reference
+ * give bonsai_b1_linear_f32's FAST results bit for bit (for batch <= 16 on
+ * rows within the fp16 range: bonsai_b1_linear_f32 computes the others in
+ * EXACT arithmetic there).  No reference
  * counterpart (the reference's single op has no such split).
  */
 int bonsai_b1_pack_act_f16_scaled(const float *act, int64_t lda, int in_dim,
@@ -255,8 +258,16 @@ int bonsai_b1_linear_packed_f16_scaled(const void *packed_act,
  * :354-361) share one fp16 packing of them, so only the first pays the pack
  * pass; when their weights are also adjacent row ranges of one buffer
  * (bonsai_b1_weights_concat) and their outputs adjacent column ranges with
- * one row stride, they run as a single GEMM over the concatenated rows.  workspace: device buffer of bonsai_b1_linear_batch_workspace_bytes
- * bytes, or NULL for the library's per-stream workspace.  On an invalid op
+ * one row stride, they run as a single GEMM over the concatenated rows.
+ * Up to 8 consecutive small-batch ops (batch <= 16, in_dim % 256 == 0,
+ * in_dim <= 3072, no epilogue) on the same activations -- the modulation
+ * projections of a step, all over vec_silu at one token (:308-311,
+ * 470-471,548) -- run as one launch over one packing when their outputs lie
+ * apart from those activations and from one another; each op's outputs are
+ * those of its own small-batch call, bit for bit, for activations within
+ * the fp16 range.  workspace: device buffer of
+ * bonsai_b1_linear_batch_workspace_bytes bytes, or NULL for the library's
+ * per-stream workspace.  On an invalid op
  * nothing is launched and *bad_op (if given) receives its index.
  * No reference counterpart: the reference builds one ggml node per linear.
  */

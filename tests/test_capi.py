@@ -176,28 +176,28 @@ def pack_area(m, k):
 def test_epilogue_workspace_bytes():
     """The larger of the range-safe packing (fused path) and the linear's
     fp32 output (separate epilogue pass); a plain small-batch linear needs
-    the small-M kernel's packing."""
+    nothing (the small-M kernel converts the activations itself)."""
     lib = bonsai_b1.load()
     assert lib.bonsai_b1_linear_epi_workspace_bytes(256, 3072, 6144, 2, 0) == max(pack_area(256, 3072),
                                                                                   256 * 6144 * 4)
     assert lib.bonsai_b1_linear_epi_workspace_bytes(256, 3072, 1024, 1, 0) == max(pack_area(256, 3072),
                                                                                   256 * 1024 * 4)
-    assert lib.bonsai_b1_linear_epi_workspace_bytes(8, 3072, 1024, 0, 0) == pack_area(8, 3072)
+    assert lib.bonsai_b1_linear_epi_workspace_bytes(8, 3072, 1024, 0, 0) == 0
     assert lib.bonsai_b1_linear_epi_workspace_bytes(8, 3000, 1024, 1, 0) == 0   # in_dim % 32
 
 
 def test_workspace_bytes_by_kernel():
     """What each kernel choice needs (no device here, so no split-K): the
-    packed GEMM and the small-M kernel the range-safe packing, EXACT and
-    the fused-conversion GEMM (K % 384 != 0) nothing; small-M with K % 256
-    != 0 converts in the kernel (nothing)."""
+    packed GEMM the range-safe packing; EXACT, the fused-conversion GEMM
+    (K % 384 != 0) and the small-M kernel (which converts the activations
+    itself) nothing."""
     lib = bonsai_b1.load()
     auto, exact, gemm, gemv = 0, 2, 3, 4
     assert lib.bonsai_b1_workspace_bytes(4096, 3072, 12288, auto) == pack_area(4096, 3072)
     assert lib.bonsai_b1_workspace_bytes(4096, 3072, 12288, exact) == 0
     assert lib.bonsai_b1_workspace_bytes(4096, 448, 128, gemm) == 0
-    assert lib.bonsai_b1_workspace_bytes(8, 3072, 18432, auto) == pack_area(8, 3072)
-    assert lib.bonsai_b1_workspace_bytes(8, 3072, 18432, gemv) == pack_area(8, 3072)
+    assert lib.bonsai_b1_workspace_bytes(8, 3072, 18432, auto) == 0
+    assert lib.bonsai_b1_workspace_bytes(8, 3072, 18432, gemv) == 0
     assert lib.bonsai_b1_workspace_bytes(8, 3072, 18432, gemm) == pack_area(8, 3072)
     assert lib.bonsai_b1_workspace_bytes(8, 448, 64, auto) == 0
     assert lib.bonsai_b1_workspace_bytes(17, 3072, 64, gemv) == 0   # not a small-M batch

@@ -640,6 +640,88 @@ def test_linear_batch_fuses_concatenated_qkv(torch, b1):
     assert lib.bonsai_b1_weights_free(ctypes.byref(cat)) == capi.OK
 
 
+GROUP_CASES = [  # (m, k, output widths): consecutive small-M ops on one input
+    (1, 3072, [18432, 18432, 9216, 6144]),            # a step's modulation projections
+    (5, 1536, [1000, 48, 4096, 16, 777, 1024, 3000, 2048, 500]),  # 8 grouped + 1 alone
+    (16, 256, [64, 96]),
+]
+
+
+@pytest.mark.parametrize("m,k,ns", GROUP_CASES)
+def test_linear_batch_groups_small_m_ops(torch, b1, oracle, m, k, ns):
+    """Consecutive small-M ops on the same input run as one launch over one
+    range-safe packing (up to 8): each output bit for bit the op's own
+    small-M call, the counter of non-finite outputs unchanged, the workspace
+    the packing; within the FAST bar of the float64 oracle."""
+    from bonsai_b1 import capi, synth
+    say(f"group m={m} k={k} ns={ns}")
+    x = synth.device_activations(m, k, 300 + m)
+    ws = [synth.device_packed_weights(n, k, 310 + i) for i, n in enumerate(ns)]
+    outs = [torch.full((m, n + 8), 7.0, device="cuda")[:, :n] for n in ns]
+    ops = [(x, b1.device_weights(w, k, n), o) for w, n, o in zip(ws, ns, outs)]
+    pack = (m * k * 2 + 255) // 256 * 256 + (m * 4 + 255) // 256 * 256
+    assert capi.linear_batch_workspace_bytes(ops) == pack
+    assert capi.linear_batch_workspace_bytes(ops[:1]) == 0       # alone: converts itself
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    b1.linear_batch(ops, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    for i, (w, n, o) in enumerate(zip(ws, ns, outs)):
+        ref = b1.linear(x, w, n)
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref), f"op {i}"
+        assert bool((o.as_strided((m, 8), (o.stride(0), 1), o.storage_offset() + n) == 7.0).all()), f"op {i} pad"
+    xh = x.cpu().numpy()
+    for i in (0, len(ns) - 1):
+        raw = ws[i].cpu().numpy()
+        assert_fast_close(outs[i].cpu().numpy(), oracle.linear_f64(xh, raw, ns[i]), f"group op {i} vs fp64")
+
+
+def test_linear_batch_group_order_and_range(torch, b1):
+    """Small-M ops whose outputs overlap one another or the shared input are
+    not grouped (the batch keeps their order); a row beyond the fp16 range
+    in a group gives the scaled packing's results (the fp32 entry computes
+    it in EXACT arithmetic instead), and a non-finite output is counted."""
+    from bonsai_b1 import synth
+    m, k, n = 4, 3072, 1024
+    x = synth.device_activations(m, k, 401)
+    wa, wb, wc = (synth.device_packed_weights(n, k, 402 + i) for i in range(3))
+    # two ops into one output: the second wins
+    o = torch.empty((m, n), device="cuda")
+    o2 = torch.empty((m, n), device="cuda")
+    b1.linear_batch([(x, b1.device_weights(wa, k, n), o), (x, b1.device_weights(wb, k, n), o),
+                     (x, b1.device_weights(wc, k, n), o2)])
+    ref_b, ref_c = b1.linear(x, wb, n), b1.linear(x, wc, n)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref_b) and torch.equal(o2, ref_c)
+    # the first output overwrites the input the second reads
+    buf = torch.zeros((m, k), device="cuda")
+    buf.copy_(x)
+    b1.linear_batch([(buf, b1.device_weights(wa, k, n), buf[:, :n]),
+                     (buf, b1.device_weights(wb, k, n), o)])
+    x1 = x.clone()
+    x1[:, :n] = b1.linear(x, wa, n)
+    ref = b1.linear(x1, wb, n)
+    torch.cuda.synchronize()
+    assert torch.equal(buf[:, :n], x1[:, :n]) and torch.equal(o, ref)
+    # beyond the fp16 range: row 1 x 1e5, row 2 all 3e38 (outputs overflow fp32)
+    xb = x.clone()
+    xb[1] *= 1e5
+    xb[2] = 3.0e38
+    ga, gb = torch.empty((m, n), device="cuda"), torch.empty((m, n), device="cuda")
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    b1.linear_batch([(xb, b1.device_weights(wa, k, n), ga), (xb, b1.device_weights(wb, k, n), gb)], nonfinite=nf)
+    packed, rs = b1.pack_act_f16_scaled(xb)
+    ya = b1.linear_packed_f16_scaled(packed, rs, wa, k, n, m)
+    yb = b1.linear_packed_f16_scaled(packed, rs, wb, k, n, m)
+    torch.cuda.synchronize()
+    assert torch.equal(ga, ya) and torch.equal(gb, yb)
+    bad = int((~torch.isfinite(ga)).sum() + (~torch.isfinite(gb)).sum())
+    say(f"  non-finite outputs {bad}, counted {int(nf.item())}")
+    assert bad > 0 and int(nf.item()) == bad
+    assert bool(torch.isfinite(ga[[0, 1, 3]]).all())
+
+
 # ---------------------------------------------------------------- split-K --
 
 SPLIT_CASES = [  # (m, k, n): shapes whose 128 x 512 tiles leave most CUs idle
