@@ -1040,10 +1040,14 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 
     floatx16 acc[C::MT][C::NTL];
 
-    // One stage = 8 steps (block b = step/2, half h = step%2).  The fragment
-    // reads of step+1 are issued before the MFMAs of step, into a second
-    // buffer; a scheduling fence per step keeps the compiler from hoisting
-    // every read of the stage.
+    // One stage = 8 steps (block b = step/2, half h = step%2).  Software
+    // pipelined: the wave's own weight dwords of the whole stage are read at
+    // its top, activation fragments two steps ahead (three buffers), and the
+    // weights of step+1 are expanded while the MFMAs of step run.  A
+    // scheduling fence per step keeps the compiler from hoisting every read
+    // of the stage.  (With the fragments read one step ahead, the compiler
+    // issued them just before the step's last MFMA and the next step waited
+    // for them: 1-1.5 % slower at the headline shape.)
     auto compute = [&](int slot, auto &&after_first_reads) {
         lds_u8 *sq = qa + slot * C::BSTAGE;
         auto read_frags = [&](int step, half8 (&af)[C::MT]) {
@@ -1053,43 +1057,59 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
             for (int mt = 0; mt < C::MT; ++mt)
                 af[mt] = *reinterpret_cast<const __attribute__((address_space(3))) half8 *>(fb + mt * 32 * C::ROWB);
         };
-        half8 afa[C::MT], afb[C::MT];
-        uint32_t d[C::NTL][3], s2[C::NTL], wg[C::NTL];
-        read_frags(0, afa);
-        after_first_reads();
+        // weight column nt*32 + li: blocks 0-1 in the first 1 KB half of its
+        // load group, blocks 2-3 in the second, 12 bytes each
+        uint32_t d[C::NTL][2][3];
 #pragma unroll
-        for (int step = 0; step < 8; ++step) {
-            const int b = step >> 1, h = step & 1;
-            half8 (&cur)[C::MT] = (step & 1) ? afb : afa;
-            half8 (&nxt)[C::MT] = (step & 1) ? afa : afb;
-            if (step + 1 < 8) read_frags(step + 1, nxt);
-            if (h == 0) {
+        for (int nt = 0; nt < C::NTL; ++nt)
 #pragma unroll
-                for (int nt = 0; nt < C::NTL; ++nt) {
-                    if ((b & 1) == 0) {
-                        const __attribute__((address_space(3))) uint32_t *q =
-                            reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
-                                sq + (nt >> 1) * 2048 + (b >> 1) * 1024 + (nt & 1) * 512);
-                        d[nt][0] = q[0];
-                        d[nt][1] = q[1];
-                        d[nt][2] = q[2];
-                        s2[nt] = dup_lo16(d[nt][0]);
-                        wg[nt] = __builtin_amdgcn_alignbit(d[nt][1], d[nt][0], 16) >> (4 * g);
-                    } else {
-                        s2[nt] = dup_hi16(d[nt][1]);
-                        wg[nt] = d[nt][2] >> (4 * g);
-                    }
-                }
+            for (int bp = 0; bp < 2; ++bp) {
+                const __attribute__((address_space(3))) uint32_t *q =
+                    reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
+                        sq + (nt >> 1) * 2048 + bp * 1024 + (nt & 1) * 512);
+                d[nt][bp][0] = q[0];
+                d[nt][bp][1] = q[1];
+                d[nt][bp][2] = q[2];
             }
+        half8 af[3][C::MT];
+        read_frags(0, af[0]);
+        read_frags(1, af[1]);
+        after_first_reads();
+        // the expanded weights of a step: block b = step / 2 has its scale
+        // and sign word at 6 (b % 2) bytes into its 12-byte pair; lane group
+        // g takes dwords 8h + 4g .. +3 of the block (elements d, d + 16)
+        uint32_t s2[C::NTL], wg[C::NTL];
+        u32x4 bw[2][C::NTL];
+        auto expand = [&](int step, u32x4 (&bo)[C::NTL]) {
+            const int b = step >> 1, h = step & 1;
 #pragma unroll
             for (int nt = 0; nt < C::NTL; ++nt) {
-                u32x4 bd;
+                if (h == 0) {
+                    const uint32_t *dd = d[nt][b >> 1];
+                    if ((b & 1) == 0) {
+                        s2[nt] = dup_lo16(dd[0]);
+                        wg[nt] = __builtin_amdgcn_alignbit(dd[1], dd[0], 16) >> (4 * g);
+                    } else {
+                        s2[nt] = dup_hi16(dd[1]);
+                        wg[nt] = dd[2] >> (4 * g);
+                    }
+                }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) bd[j] = wpair(wg[nt], 15 - 8 * h - j, s2[nt]);
-                const half8 bf = __builtin_bit_cast(half8, bd);
+                for (int j = 0; j < 4; ++j) bo[nt][j] = wpair(wg[nt], 15 - 8 * h - j, s2[nt]);
+            }
+        };
+        expand(0, bw[0]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int step = 0; step < 8; ++step) {
+            if (step + 2 < 8) read_frags(step + 2, af[(step + 2) % 3]);
+            if (step + 1 < 8) expand(step + 1, bw[(step + 1) & 1]);
+#pragma unroll
+            for (int nt = 0; nt < C::NTL; ++nt) {
+                const half8 bf = __builtin_bit_cast(half8, bw[step & 1][nt]);
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf, cur[mt], acc[mt][nt], 0, 0, 0);
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf, af[step % 3][mt], acc[mt][nt], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
