@@ -85,17 +85,11 @@ __device__ __forceinline__ void lds_barrier() {
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Global -> LDS copies without VGPR staging.  `lds` must be wave-uniform
-// (it goes through M0).  global_load_lds_dwordx4: lane i's 16 bytes land at
-// lds + 16 i.  global_load_lds_dwordx3: lane i's 12 bytes also land at
-// lds + 16 i (a 16-byte lane stride, measured on gfx950), leaving 4 bytes
-// untouched per lane.  Kept as plain device functions so that kernel
-// templates using them still instantiate on the host pass.
-__device__ __forceinline__ void dma_lds16(const void *src, void *lds) {
-    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 16, 0, 0);
-}
-__device__ __forceinline__ void dma_lds12(const void *src, void *lds) {
-    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 12, 0, 0);
-}
+// (it goes through M0).  Lane i's 16 bytes land at lds + 16 i; 12-byte
+// loads also land at lds + 16 i (a 16-byte lane stride, measured on gfx950
+// for the global and the buffer forms), leaving 4 bytes untouched per lane.
+// Kept as plain device functions: a kernel template that calls these
+// builtins directly loses its host-side launch stub.
 // global_load_lds_dword: lane i's 4 bytes land at lds + 4 i.
 __device__ __forceinline__ void dma_lds4(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 4, 0, 0);
@@ -114,6 +108,16 @@ constexpr int kStoreNT = 0;
 // lds + 16 * lane (wave-uniform lds, through M0).
 __device__ __forceinline__ void dma_buf_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds, 16, voff, 0, 0, 0);
+}
+// The same, 16 or 12 bytes per lane (12-byte lanes also land 16 bytes
+// apart), with a wave-uniform byte offset soff (an SGPR) added to voff.  A
+// constant offset goes into soff, not the instruction's offset field: for
+// these loads the instruction offset moves the LDS destination as well.
+__device__ __forceinline__ void dma_buf_lds16s(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma_buf_lds12s(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds, 12, voff, soff, 0, 0);
 }
 
 __device__ __forceinline__ uint32_t dup_lo16(uint32_t d) {
@@ -1001,19 +1005,24 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
             boff[cg] = (uint32_t)row * rs;
         }
     };
-    // The stage offset goes into the wave-uniform base, so each load is a
-    // scalar base plus the lane's 32-bit offset (no per-lane 64-bit adds).
+    // Buffer loads: the operand in the resource, the lane's 32-bit offset in
+    // a VGPR and the stage offset in an SGPR, so no load needs address
+    // arithmetic (with 64-bit global addresses, one v_lshl_add_u64 each).
+    // The host keeps both operands under 2^32 bytes (gemm_packed_ok).
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(abase), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(w), (short)0, (int)((uint32_t)N * rs), kBufferFlags);
     auto issue = [&](int ks, int slot) {
         uint8_t *sa = smem + C::ABASE + slot * C::ASTAGE + wave * C::LPW * 1024;
         uint8_t *sw = smem + slot * C::BSTAGE + wave * C::BWAVE;
-        const uint8_t *ab = abase + (uint32_t)ks * C::ROWB;
-        const uint8_t *wb = w + (uint32_t)ks * 24;
+        const uint32_t aso = (uint32_t)ks * C::ROWB, wso = (uint32_t)ks * 24;
 #pragma unroll
-        for (int i = 0; i < C::LPW; ++i) dma_lds16(ab + aoff[i], sa + i * 1024);
+        for (int i = 0; i < C::LPW; ++i) dma_buf_lds16s(ars, sa + i * 1024, aoff[i], aso);
 #pragma unroll
         for (int cg = 0; cg < C::CG; ++cg) {
-            dma_lds12(wb + boff[cg], sw + cg * 2048);
-            dma_lds12(wb + 12 + boff[cg], sw + cg * 2048 + 1024);
+            dma_buf_lds12s(wrs, sw + cg * 2048, boff[cg], wso);
+            dma_buf_lds12s(wrs, sw + cg * 2048 + 1024, boff[cg], wso + 12);
         }
     };
 
@@ -1088,7 +1097,11 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                     const uint32_t *dd = d[nt][b >> 1];
                     if ((b & 1) == 0) {
                         s2[nt] = dup_lo16(dd[0]);
-                        wg[nt] = __builtin_amdgcn_alignbit(dd[1], dd[0], 16) >> (4 * g);
+                        // the sign word shifted right by 4g in one funnel
+                        // shift; its bits above 27 are not those of the
+                        // plain shift, but only bits 8h + j and 16 + 8h + j
+                        // (<= 27) reach the mask
+                        wg[nt] = __builtin_amdgcn_alignbit(dd[1], dd[0], 16 + 4 * g);
                     } else {
                         s2[nt] = dup_hi16(dd[1]);
                         wg[nt] = dd[2] >> (4 * g);
