@@ -1130,10 +1130,103 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 
     // Epilogue.  Accumulator (n, m) layout of the 32x32 MFMA with weights as
     // A: lane column li = token m0 + 32 mt + li, rows 8*(v/4) + 4*g + v%4 =
-    // output columns; v = 4q..4q+3 are 4 consecutive columns, stored as one
-    // 16-byte vector (one store instruction covers 32 output rows x 32
-    // bytes).  Non-finite outputs are counted only when the caller passed a
-    // counter.
+    // output columns; v = 4q..4q+3 are 4 consecutive columns.  Stored as one
+    // 16-byte vector each, one store instruction would cover a quarter of 32
+    // lines (32 rows x 32 bytes).  Full tiles instead go through LDS and are
+    // stored as whole 128-byte lines (below).  Non-finite outputs are
+    // counted only when the caller passed a counter.
+    //
+    // The transpose area is the wave's own 2 KB weight area of the last
+    // stage's slot (slot 2: the stage count is a multiple of 3), free from
+    // the wave's last read of it until the wave itself refills it during the
+    // next tile's first stage.  It holds 16 rows of 128 bytes, 16-byte chunk
+    // c of row r at position c ^ ((r >> 1) & 7), which spreads both the
+    // writes (a lane's row, chunks 2j + g) and the reads (8 lanes per row)
+    // over all 16 bank groups.  Then 8 lanes store one row's 128 bytes, a
+    // whole line (261.3 -> 252.2 us at M=4096 K=3072 N=12288 for the plain
+    // fp32 output).
+    typedef __attribute__((address_space(3))) uint8_t lds_u8w;
+    typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+    lds_u8w *const tb = (lds_u8w *)smem + 2 * C::BSTAGE + wave * C::BWAVE;
+    static_assert(C::STAGES == 3 && 16 * 128 <= C::BWAVE, "the transpose area");
+    const int rr0 = lane >> 3, cc = lane & 7;
+    // Rows 16 half .. 16 half + 15 of a 32-row piece, 128 bytes each: the
+    // lanes holding them (li >> 4 == half) write their four chunks v[j] at
+    // chunk 2j + g of row li & 15; then every lane reads chunk cc of rows
+    // rr0 and rr0 + 8 into vr.
+    auto transpose = [&](const u32x4(&v)[4], int half, u32x4(&vr)[2]) {
+        if ((li >> 4) == half) {
+            const int r = li & 15;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *(lds_u32x4 *)(tb + r * 128 + ((2 * j + g) ^ ((r >> 1) & 7)) * 16) = v[j];
+        }
+        // Every lane reads below.  Without this fence the compiler moved the
+        // reads into the branch above, where only the writing half of the
+        // wave runs them.
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int rr = rr0 + 8 * k;
+            vr[k] = *(const lds_u32x4 *)(tb + rr * 128 + (cc ^ ((rr >> 1) & 7)) * 16);
+        }
+    };
+    // accumulator tile (mt, nt) of lane (li, g) as raw words, chunk q =
+    // columns 8q + 4g .. +3 (element values are copied out first: a bit cast
+    // of a vector element reads element 0 in this clang)
+    auto acc_chunks = [&](int mt, int nt, u32x4(&v)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x = acc[mt][nt][4 * q + e];
+                v[q][e] = __builtin_bit_cast(uint32_t, x);
+            }
+    };
+    // A row stride in bytes, opaque to the compiler: the store offsets
+    // derived from it are then computed in each epilogue rather than hoisted
+    // out of the tile loop into scalar registers the main loop would carry.
+    auto stride_bytes = [](int64_t ld) {
+        int b = (int)ld * 4;
+        asm volatile("" : "+s"(b));
+        return b;
+    };
+    auto count_tile = [&](int &bad) {
+        if (nonfinite != nullptr) {
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) bad += !__builtin_isfinite(acc[mt][nt][v]);
+        }
+    };
+    // The fp32 tile through the transpose, whole-line buffer stores into the
+    // wave's columns of `out` (row stride ldo, ldb = 4 ldo bytes; 128 rows
+    // span < 2^31 bytes).  32 stores per lane.
+    auto store_f32_lines = [&](int m0, int n0, float *__restrict__ out, int ldb) {
+        const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+            out + (size_t)m0 * ldo + n0 + wave * WN, (short)0, (int)(BM * ldo * 4), kBufferFlags);
+        const int lvoff = rr0 * ldb + 16 * cc;
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    u32x4 v[4], vr[2];
+                    acc_chunks(mt, nt, v);
+                    transpose(v, half, vr);
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const int ro = (mt * 32 + 16 * half + 8 * k) * ldb + nt * 128;
+                        __builtin_amdgcn_raw_buffer_store_b128(vr[k], ors, lvoff, ro, kStoreNT);
+                    }
+                }
+    };
+
+    // Returns what the tile-start vmcnt waits may assume about the stores
+    // left in flight: 0 none, 1 unknown (wait for all), 2 EPI_STORES vector
+    // stores per lane, 3 EPI_STORES / 2.
     auto epilogue = [&](int m0, int n0, float *__restrict__ out) -> int {
         int bad = 0;
         const bool cnt = nonfinite != nullptr;
@@ -1166,53 +1259,64 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                 }
             }
             count_nonfinite(nonfinite, bad);
-            return 1; // a store count the tile-start waits do not model
+            return 1;
         }
         if constexpr (EPI == 1) {
-            // residual and gate read at the accumulator's own positions:
-            // lane (li, g) holds 4 consecutive columns of token 32 mt + li
             const bool fullr = vec_store && m0 + BM <= M && n0 + BN <= N;
             if (fullr) {
-                // The residual may be `out` itself, so the compiler keeps
-                // every load behind the stores before it in program order.
-                // The gate is loaded once and each 32-row group's residual
-                // before any of its stores: 5 memory round trips a tile
-                // instead of 32 (each element is still read before it is
-                // written, which the in-place form needs).
-                floatx4 gw[C::NTL][4];
+                // y through the transpose; the residual read as whole lines
+                // at the same positions, P of the 16 (mt, nt, half) pieces
+                // ahead; out = residual + gate * y stored as whole lines.
+                // The residual may be `out` itself: each element is read by
+                // the lane that later writes it, and every piece's loads are
+                // issued before any store of a later piece.
+                count_tile(bad);
+                const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+                    out + (size_t)m0 * ldo + n0 + wave * WN, (short)0, (int)(BM * ldo * 4), kBufferFlags);
+                const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<float *>(epi.res) + (size_t)m0 * epi.ldr + n0 + wave * WN, (short)0,
+                    (int)(BM * epi.ldr * 4), kBufferFlags);
+                const int ldb = stride_bytes(ldo), lrb = stride_bytes(epi.ldr);
+                const int lvoff = rr0 * ldb + 16 * cc, lroff = rr0 * lrb + 16 * cc;
+                floatx4 gq[C::NTL];
 #pragma unroll
                 for (int nt = 0; nt < C::NTL; ++nt)
+                    gq[nt] = *reinterpret_cast<const floatx4 *>(epi.gate + n0 + wave * WN + nt * 32 + 4 * cc);
+                constexpr int NP = C::MT * C::NTL * 2, P = 4;
+                u32x4 rv[NP][2];
+                auto load_res = [&](int j) {
+                    const int mt = j / (2 * C::NTL), nt = (j >> 1) % C::NTL, half = j & 1;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        gw[nt][q] = *reinterpret_cast<const floatx4 *>(epi.gate + n0 + wave * WN + nt * 32 + 8 * q +
-                                                                        4 * g);
+                    for (int k = 0; k < 2; ++k)
+                        rv[j][k] = __builtin_amdgcn_raw_buffer_load_b128(
+                            rrs, lroff, (mt * 32 + 16 * half + 8 * k) * lrb + nt * 128, 0);
+                };
 #pragma unroll
-                for (int mt = 0; mt < C::MT; ++mt) {
-                    const int m = m0 + mt * 32 + li;
-                    const float *const rrow = epi.res + (size_t)m * epi.ldr + n0 + wave * WN + 4 * g;
-                    float *const orow = out + (size_t)m * ldo + n0 + wave * WN + 4 * g;
-                    floatx4 rv[C::NTL][4];
+                for (int j = 0; j < P; ++j) load_res(j);
 #pragma unroll
-                    for (int nt = 0; nt < C::NTL; ++nt)
+                for (int j = 0; j < NP; ++j) {
+                    if (j + P < NP) load_res(j + P);
+                    const int mt = j / (2 * C::NTL), nt = (j >> 1) % C::NTL, half = j & 1;
+                    u32x4 v[4], vr[2];
+                    acc_chunks(mt, nt, v);
+                    transpose(v, half, vr);
 #pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            rv[nt][q] = *reinterpret_cast<const floatx4 *>(rrow + nt * 32 + 8 * q);
+                    for (int k = 0; k < 2; ++k) {
+                        u32x4 o;
 #pragma unroll
-                    for (int nt = 0; nt < C::NTL; ++nt)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            floatx4 o;
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const float yv = acc[mt][nt][4 * q + r];
-                                bad += cnt && !__builtin_isfinite(yv);
-                                o[r] = gate_residual(rv[nt][q][r], gw[nt][q][r], yv);
-                            }
-                            *reinterpret_cast<floatx4 *>(orow + nt * 32 + 8 * q) = o;
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t yu = vr[k][e], ru = rv[j][k][e];
+                            const float gv = gq[nt][e];
+                            const float ov =
+                                gate_residual(__builtin_bit_cast(float, ru), gv, __builtin_bit_cast(float, yu));
+                            o[e] = __builtin_bit_cast(uint32_t, ov);
                         }
+                        const int ro = (mt * 32 + 16 * half + 8 * k) * ldb + nt * 128;
+                        __builtin_amdgcn_raw_buffer_store_b128(o, ors, lvoff, ro, kStoreNT);
+                    }
                 }
                 count_nonfinite(nonfinite, bad);
-                return 1; // a store count the tile-start waits do not model
+                return 2;
             }
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt) {
@@ -1237,20 +1341,66 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                 }
             }
             count_nonfinite(nonfinite, bad);
-            return 1; // a store count the tile-start waits do not model
+            return 1;
         }
         if constexpr (EPI == 3) {
-            // Columns below split: 16-byte fp32 stores.  From split on, the
-            // packed fp16 activations of the next linear: a packed block's
-            // dword d holds columns (d, d + 16) of its 32, and lane (li, g)
-            // holds columns 8q + 4g + r of each 32-column tile, so
-            // registers 4q + r and 4q + 8 + r (q < 2) form dword 8q + 4g +
-            // r and 4 consecutive dwords are one 16-byte store.  split and
-            // N are multiples of 32 (64 for SwiGLU), so a tile (a wave's 64
-            // columns for SwiGLU) is wholly one kind.
+            // Columns below split: fp32.  From split on, the packed fp16
+            // activations of the next linear: a packed block's dword d holds
+            // columns (d, d + 16) of its 32, and lane (li, g) holds columns
+            // 8q + 4g + r of each 32-column tile, so registers 4q + r and
+            // 4q + 8 + r (q < 2) form dword 8q + 4g + r and 4 consecutive
+            // dwords are one 16-byte chunk.  split and N are multiples of 32
+            // (64 for SwiGLU), so a tile (a wave's 64 columns for SwiGLU) is
+            // wholly one kind.
             static_assert(C::NTL == 2, "SwiGLU pairs one gate and one value tile per wave");
             const int wb = n0 + wave * WN; // wave-uniform
-            if (epi.act == 2 && wb >= epi.split) {
+            const bool pcols = wb >= epi.split;
+            if (vec_store && m0 + BM <= M && n0 + BN <= N && !(epi.act == 2 && pcols) &&
+                (pcols || wb + WN <= epi.split)) {
+                // A full tile whose wave columns are all of one kind: whole
+                // lines through the transpose.
+                count_tile(bad);
+                if (!pcols) {
+                    store_f32_lines(m0, n0, out, stride_bytes(ldo));
+                    count_nonfinite(nonfinite, bad);
+                    return 2;
+                }
+                // The wave's two blocks are 128 consecutive bytes of a packed
+                // row: block nt's dwords 8q + 4g .. +3 are its chunk
+                // 2 (2 nt + q) + g.  The values are made by every lane before
+                // the transpose, which writes half the lanes at a time.
+                const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+                    epi.pk + (size_t)m0 * epi.ldpw + ((wb - epi.split) >> 5) * 16, (short)0,
+                    (int)(BM * epi.ldpw * 4), kBufferFlags);
+                const int lpb = stride_bytes(epi.ldpw);
+                const int lpoff = rr0 * lpb + 16 * cc;
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt) {
+                    u32x4 v[4];
+#pragma unroll
+                    for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                        for (int q = 0; q < 2; ++q)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float y0 = acc[mt][nt][4 * q + r], y1 = acc[mt][nt][4 * q + 8 + r];
+                                v[2 * nt + q][r] = epi.act ? pack_f16(gelu_tanh(y0), gelu_tanh(y1)) : pack_f16(y0, y1);
+                            }
+#pragma unroll
+                    for (int half = 0; half < 2; ++half) {
+                        u32x4 vr[2];
+                        transpose(v, half, vr);
+#pragma unroll
+                        for (int k = 0; k < 2; ++k) {
+                            const int ro = (mt * 32 + 16 * half + 8 * k) * lpb;
+                            __builtin_amdgcn_raw_buffer_store_b128(vr[k], prs, lpoff, ro, 0);
+                        }
+                    }
+                }
+                count_nonfinite(nonfinite, bad);
+                return 3;
+            }
+            if (epi.act == 2 && pcols) {
                 // tile 0 holds the gates, tile 1 their values, of the 32
                 // outputs of packed block (wb - split) / 64
                 if (wb < N) {
@@ -1318,83 +1468,12 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                 }
             }
             count_nonfinite(nonfinite, bad);
-            return 1; // a store count the tile-start waits do not model
+            return 1;
         }
         const bool full = vec_store && m0 + BM <= M && n0 + BN <= N;
         if (full) {
-            // the count, outside the store path
-            if (cnt) {
-#pragma unroll
-                for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-                    for (int nt = 0; nt < C::NTL; ++nt)
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) bad += !__builtin_isfinite(acc[mt][nt][v]);
-            }
-            // Buffer stores of the accumulator layout: the wave's tile origin
-            // in the resource, the lane part in one VGPR and the (mt, nt, q)
-            // offset in an SGPR, so the 32 stores need no per-store address
-            // arithmetic.  Each covers 32 rows x 32 bytes.  The host enables
-            // vector stores only when 128 rows span < 2^31 bytes.
-            const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
-                out + (size_t)m0 * ldo + n0 + wave * WN, (short)0, (int)(BM * ldo * 4), kBufferFlags);
-            // Whole-line stores: each 32x32 accumulator tile goes through
-            // the wave's own 2 KB weight area of the last stage's slot (slot
-            // 2: the stage count is a multiple of 3), free from the wave's
-            // last read of it until the wave itself refills it during the
-            // next tile's first stage.  Two halves of 16 rows, 128 bytes a
-            // row, 16-byte chunk c of row r at position c ^ ((r >> 1) & 7),
-            // which spreads both the writes (lane row li, chunk 2q + g) and
-            // the reads (8 lanes per row) over all 16 bank groups.  Then 8
-            // lanes store one row's 128 bytes, a whole line, where the
-            // accumulator layout alone gives each store instruction a
-            // quarter of 32 lines (261.3 -> 252.2 us at M=4096 K=3072
-            // N=12288).  Same store count per lane, so the tile-start vmcnt
-            // waits are unchanged.
-            typedef __attribute__((address_space(3))) uint8_t lds_u8w;
-            typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-            lds_u8w *const tb = (lds_u8w *)smem + 2 * C::BSTAGE + wave * C::BWAVE;
-            static_assert(C::STAGES == 3 && 16 * 128 <= C::BWAVE, "the transpose area");
-            const int rr0 = lane >> 3, cc = lane & 7;
-            const int lvoff = 4 * (rr0 * (int)ldo + 4 * cc);
-#pragma unroll
-            for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < C::NTL; ++nt)
-#pragma unroll
-                    for (int half = 0; half < 2; ++half) {
-                        if ((li >> 4) == half) {
-                            const int r = li & 15;
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                // element values are copied out first: a bit
-                                // cast of a vector element reads element 0 in
-                                // this clang
-                                u32x4 v;
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) {
-                                    const float x = acc[mt][nt][4 * q + e];
-                                    v[e] = __builtin_bit_cast(uint32_t, x);
-                                }
-                                *(lds_u32x4 *)(tb + r * 128 + ((2 * q + g) ^ ((r >> 1) & 7)) * 16) = v;
-                            }
-                        }
-                        // Every lane reads below.  Without this fence the
-                        // compiler moved the reads into the branch above,
-                        // where only the writing half of the wave runs them.
-                        asm volatile("" ::: "memory");
-                        u32x4 vr[2];
-#pragma unroll
-                        for (int k = 0; k < 2; ++k) {
-                            const int rr = rr0 + 8 * k;
-                            vr[k] = *(const lds_u32x4 *)(tb + rr * 128 + (cc ^ ((rr >> 1) & 7)) * 16);
-                        }
-#pragma unroll
-                        for (int k = 0; k < 2; ++k) {
-                            const int ro = 4 * ((mt * 32 + 16 * half + 8 * k) * (int)ldo + nt * 32);
-                            __builtin_amdgcn_raw_buffer_store_b128(vr[k], ors, lvoff, ro, kStoreNT);
-                        }
-                    }
+            count_tile(bad);
+            store_f32_lines(m0, n0, out, 4 * (int)ldo);
         } else {
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt) {
@@ -1445,7 +1524,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
     issue_rsc(parity);
 #pragma unroll
     for (int t = 0; t < STAGES - 1; ++t) issue(kst0 + t, t);
-    int prev_stores = 0; // stores the previous epilogue left: 0 none, 1 scalar, 2 vector
+    int prev_stores = 0; // what the previous epilogue left in flight (its return value)
     for (;;) {
 #pragma unroll
         for (int i = 0; i < C::MT; ++i)
@@ -1462,10 +1541,12 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
         // stores share vmcnt, so "stage s has landed" is "at most the
         // operations issued after it are outstanding": stage s+1's LPW + 2
         // loads, plus, in the first two stages of a tile, the previous
-        // tile's 32 vector stores per lane (issued after stages 0 and 1 of
-        // this tile).  Those stores thus drain under two stages of MFMA
-        // work instead of stalling the tile change.  A ragged previous tile
-        // stored a variable count with scalar stores: wait for everything.
+        // tile's 32 (or 16) vector stores per lane, issued after stages 0
+        // and 1 of this tile (a gate-residual epilogue also issued loads
+        // there, which only adds to the operations after those stages).
+        // Those stores thus drain under two stages of MFMA work instead of
+        // stalling the tile change.  A ragged previous tile stored a
+        // variable count with scalar stores: wait for everything.
         // Unrolled by three so that slots are compile-time; the stage count
         // is a multiple of three, so the loop has no exit mid-body.
         for (int s = 0; s < nstage; s += STAGES) {
@@ -1475,6 +1556,8 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                     wait_vmcnt<0>();
                 else if (C::COUNT_STORES && s == 0 && u < STAGES - 1 && prev_stores == 2)
                     wait_vmcnt<(C::COUNT_STORES ? C::EPI_STORES + C::AHEAD : 0)>();
+                else if (C::COUNT_STORES && s == 0 && u < STAGES - 1 && prev_stores == 3)
+                    wait_vmcnt<(C::COUNT_STORES ? C::EPI_STORES / 2 + C::AHEAD : 0)>();
                 else if (s == 0 && u == 0 && prev_stores != 0)
                     wait_vmcnt<0>();
                 else
@@ -2290,6 +2373,11 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
     int vec_store = al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 22);
     if (EPI == 1)
         vec_store = vec_store && al16(epi.res) && al16(epi.gate) && epi.ldr % 4 == 0 && epi.ldr < (int64_t(1) << 22);
+    if (EPI == 3)
+        // each part the epilogue writes: 16-byte aligned rows (the caller
+        // checks these) and 128 rows under 2^31 bytes for the buffer stores
+        vec_store = (epi.split == 0 || (al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 22))) &&
+                    (epi.split >= N || (al16(epi.pk) && epi.ldpw % 4 == 0 && epi.ldpw < (int64_t(1) << 22)));
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
                        K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store, epi, 1, (int64_t)0);
     return hipGetLastError();
