@@ -1680,6 +1680,16 @@ constexpr int kGvAUnits = 6;                   // activation units per lane per 
 constexpr int kGvWaveLds = kGvBPW * 4 * 16 * 16; // fp16 fragments of one wave (12 KB)
 constexpr int kGvLds = kGvWaves * kGvWaveLds;  // 96 KB; the reduction reuses it
 
+// Row groups [rg0, rg1) of work-group bid when `groups` are split over nwg
+// work-groups as evenly as possible (the first groups % nwg get one more).
+// 32-bit: a 64-bit division costs each work-group some 130 scalar
+// instructions before its first load.
+__device__ __forceinline__ void wg_row_groups(int groups, int nwg, int bid, int &rg0, int &rg1) {
+    const int q = groups / nwg, r = groups - q * nwg;
+    rg0 = bid * q + min(bid, r);
+    rg1 = rg0 + q + (bid < r ? 1 : 0);
+}
+
 // The activation slice of a wave (Mp token slots x 12 blocks) is read with
 // coalesced float4 loads in units (block, t, token) -- token fastest, so
 // each unit pair covers 64 contiguous bytes of one token row -- converted to
@@ -1691,8 +1701,8 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, g = lane >> 4;
     const int nwg = gridDim.x, bid = blockIdx.x;
-    const int rg0 = (int)(((int64_t)groups * bid) / nwg);
-    const int rg1 = (int)(((int64_t)groups * (bid + 1)) / nwg);
+    int rg0, rg1;
+    wg_row_groups(groups, nwg, bid, rg0, rg1);
     const int nrg = rg1 - rg0;
     const int nb = p.K / 32;
     const size_t rs = (size_t)nb * 6;
@@ -1832,15 +1842,20 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_kernel(LinearArgs p, in
 //    bytes apart.  A wave therefore waits only for its own DMAs (vmcnt),
 //    row group by row group, and never for the other waves.
 //  * Activations, packed fp16 (PACKED): fragment (q, t) of the MFMA A
-//    operand is 16 token slots x 32 K; with S <= 16 slots in use (the power
-//    of two >= M) one 1 KB DMA carries 16 / S fragments, slot (g, tok) of
-//    fragment f at f % F * 64 S + (g S + tok) * 16, tokens past M and slots
-//    past S zero.  fp32 (!PACKED): lane (g, tok) loads the 8 elements of
-//    its fragment slot from the fp32 rows and converts them to fp16 pairs
-//    (round to nearest even) in registers; a lane that met an |a| >= 65520
-//    (beyond the fp16 range) flags its token, and after the reduction the
-//    work-group computes its rows of flagged tokens again in the reference's
-//    scalar arithmetic (EXACT mode's bits), correcting the non-finite count.
+//    operand is 16 token slots x 32 K, S <= 16 slots in use (the power of
+//    two >= M).  S <= 8: one 1 KB DMA per slot, the token's 12 blocks as
+//    they lie in its row; S = 16: each 1 KB DMA carries one fragment in
+//    fragment order (g3_issue_act).  Tokens past M and slots past S zero.
+//  * Activations, fp32 (!PACKED): lane (g, tok) takes the 8 elements of its
+//    fragment slot (S = 8: from the slot slices DMAs staged in LDS,
+//    g3_issue_act_f32; S = 16: straight from the fp32 rows) and converts
+//    them to fp16 pairs (round to nearest even) in registers; a lane that
+//    met an |a| >= 65520 (beyond the fp16 range) flags its token, and after
+//    the reduction the work-group computes its rows of flagged tokens again
+//    in the reference's scalar arithmetic (EXACT mode's bits), correcting
+//    the non-finite count.  (Loading the fragment slots straight from the
+//    rows touches a separate 64-byte line per lane; staging the slices
+//    takes 11.1 -> 10.1 us at M=8 K=3072 N=18432.)
 //  * Order of the loads: activations first, then the weight row groups, so
 //    that vmcnt (which retires in issue order) tells when each has landed.
 // One pass covers 96 blocks (K 3072, 12 per wave); longer K runs more
@@ -1921,37 +1936,60 @@ __device__ __forceinline__ void g3_decode(const uint8_t *wbuf, int nrg, int wave
     }
 }
 
-// The activation DMAs of a wave's pass (packed fp16, S slots): F = 16 / S
-// fragments per 1 KB DMA, kGvBPW fragments.
+// The activation DMAs of a wave's pass (packed fp16, S slots).  S <= 8: one
+// 1 KB DMA per token slot, contiguous in the token's row from the wave's
+// first block (its 12 blocks are the first 768 bytes), landing at abuf +
+// 1040 t; the row stride of 65 16-byte chunks puts the 8 slots' chunks of a
+// fragment read in distinct bank groups.  Lanes past K and slots past M read
+// zeros.  (Fragment-ordered DMAs touch a separate 64-byte line per lane, and
+// the whole-row form makes the weight DMAs, issued after them, start
+// earlier: 8.28 -> 7.97 us per launch at M=8 K=3072 N=18432.)  S = 16: F =
+// 16 / S fragments per 1 KB DMA in fragment order, kGvBPW fragments.
+constexpr int kG3ARow = 1040;
+static_assert(8 * kG3ARow <= kG3ALds, "eight contiguous token rows");
 template <int S>
 __device__ __forceinline__ void g3_issue_act(__amdgpu_buffer_rsrc_t ars, uint8_t *abuf, int lane, int wb0, int nb, int M,
                                              int K) {
-    constexpr int F = (16 / S) < kGvBPW ? 16 / S : kGvBPW;
-    constexpr int NA = (kGvBPW + F - 1) / F;
+    if constexpr (S <= 8) {
+        const uint32_t inrow = (uint32_t)wb0 * 64u + (uint32_t)lane * 16u;
+        const bool kin = inrow < (uint32_t)nb * 64u;
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
-        const int sub = lane / (4 * S), within = lane % (4 * S);
-        const int ag = within / S, tok = within % S;
-        const int f = i * F + sub;
-        const int blk = wb0 + 4 * (f >> 2) + ag;
-        const bool ok = f < kGvBPW && tok < M && blk < nb;
-        dma_buf_lds16(ars, abuf + i * 1024,
-                      ok ? (uint32_t)tok * (uint32_t)K * 2u + (uint32_t)blk * 64u + (uint32_t)(f & 3) * 16u
-                         : 0xFFFFFFF0u);
+        for (int t = 0; t < S; ++t)
+            dma_buf_lds16(ars, abuf + t * kG3ARow,
+                          (kin && t < M) ? (uint32_t)t * (uint32_t)K * 2u + inrow : 0xFFFFFFF0u);
+    } else {
+        constexpr int F = (16 / S) < kGvBPW ? 16 / S : kGvBPW;
+        constexpr int NA = (kGvBPW + F - 1) / F;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int sub = lane / (4 * S), within = lane % (4 * S);
+            const int ag = within / S, tok = within % S;
+            const int f = i * F + sub;
+            const int blk = wb0 + 4 * (f >> 2) + ag;
+            const bool ok = f < kGvBPW && tok < M && blk < nb;
+            dma_buf_lds16(ars, abuf + i * 1024,
+                          ok ? (uint32_t)tok * (uint32_t)K * 2u + (uint32_t)blk * 64u + (uint32_t)(f & 3) * 16u
+                             : 0xFFFFFFF0u);
+        }
     }
 }
 
 template <int S>
 __device__ __forceinline__ void g3_read_act(const uint8_t *abuf, int lane, u32x4 (&af)[kGvQuads][4]) {
-    constexpr int F = (16 / S) < kGvBPW ? 16 / S : kGvBPW;
     const int col = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int q = 0; q < kGvQuads; ++q)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const int f = 4 * q + t;
-            af[q][t] = col < S ? *reinterpret_cast<const u32x4 *>(abuf + f / F * 1024 + (f % F * 4 * S + g * S + col) * 16)
-                               : u32x4{0u, 0u, 0u, 0u};
+            if constexpr (S <= 8) {
+                af[q][t] = col < S ? *reinterpret_cast<const u32x4 *>(abuf + col * kG3ARow + (4 * q + g) * 64 + t * 16)
+                                   : u32x4{0u, 0u, 0u, 0u};
+            } else {
+                constexpr int F = (16 / S) < kGvBPW ? 16 / S : kGvBPW;
+                const int f = 4 * q + t;
+                af[q][t] = col < S ? *reinterpret_cast<const u32x4 *>(abuf + f / F * 1024 + (f % F * 4 * S + g * S + col) * 16)
+                                   : u32x4{0u, 0u, 0u, 0u};
+            }
         }
 }
 
@@ -1978,14 +2016,43 @@ __device__ __forceinline__ int g3_reduce_store(const uint8_t *red, int wstride, 
     return bad;
 }
 
+// fp32 activations, at most 8 token slots, through LDS: slot t's 12 blocks
+// (1536 bytes of its row from the wave's first block) land as chunk c (16
+// bytes) of its first 1024 bytes at abuf + 1024 t + 16 (c ^ t), and chunk c
+// of its last 512 bytes at abuf + 8192 + 1024 (t / 2) + 512 (t % 2) +
+// 16 (c ^ t): two slots' tails share one DMA.  The XOR puts the 8 slots'
+// copies of one chunk in distinct bank groups.  Chunks past K and slots past
+// M read zeros.  frs: the rows, (M - 1) lda + K floats.
+__device__ __forceinline__ void g3_issue_act_f32(__amdgpu_buffer_rsrc_t frs, uint8_t *abuf, int lane, int wb0, int nb,
+                                                 int M, int64_t lda) {
+    const uint32_t base = (uint32_t)wb0 * 128u, limit = (uint32_t)nb * 128u;
+    const uint32_t rowb = (uint32_t)lda * 4u;
+    for (int t = 0; t < M; ++t) {
+        const uint32_t inrow = base + (uint32_t)(lane ^ t) * 16u;
+        dma_buf_lds16(frs, abuf + 1024 * t, inrow < limit ? (uint32_t)t * rowb + inrow : 0xFFFFFFF0u);
+    }
+    for (int pr = 0; 2 * pr < M; ++pr) {
+        const int t = 2 * pr + (lane >> 5);
+        const uint32_t inrow = base + (64u + (uint32_t)((lane & 31) ^ t)) * 16u;
+        dma_buf_lds16(frs, abuf + 8192 + 1024 * pr, (t < M && inrow < limit) ? (uint32_t)t * rowb + inrow : 0xFFFFFFF0u);
+    }
+}
+static_assert(8 * 1024 + 4 * 1024 <= kG3ALds, "eight fp32 slot slices");
+
+// Chunk c (of 96) of slot t's slice, as g3_issue_act_f32 placed it.
+__device__ __forceinline__ floatx4 g3_act_f32(const uint8_t *abuf, int t, int c) {
+    const int off = c < 64 ? 1024 * t + 16 * (c ^ t) : 8192 + 1024 * (t >> 1) + 512 * (t & 1) + 16 * ((c - 64) ^ t);
+    return *reinterpret_cast<const floatx4 *>(abuf + off);
+}
+
 template <int S, bool PACKED>
 __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, int groups) {
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
     const int nwg = gridDim.x, bid = blockIdx.x;
-    const int rg0 = (int)(((int64_t)groups * bid) / nwg);
-    const int rg1 = (int)(((int64_t)groups * (bid + 1)) / nwg);
+    int rg0, rg1;
+    wg_row_groups(groups, nwg, bid, rg0, rg1);
     const int nrg = rg1 - rg0;
     const int nb = p.K / 32;
     const uint32_t rs = (uint32_t)nb * 6;
@@ -2005,11 +2072,17 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
     for (int kb0 = 0; kb0 < nb; kb0 += kG3Chunk) {
         const int wb0 = kb0 + wave * kGvBPW;
         // 1. activations
-        floatx4 xa[PACKED ? 1 : kGvBPW][2];
+        constexpr bool F32LDS = !PACKED && S <= 8;
+        floatx4 xa[PACKED || F32LDS ? 1 : kGvBPW][2];
         if constexpr (PACKED) {
             const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float *>(p.act), (short)0, (int)((uint32_t)p.M * (uint32_t)p.K * 2u), kBufferFlags);
             g3_issue_act<S>(ars, abuf, lane, wb0, nb, p.M, p.K);
+        } else if constexpr (F32LDS) {
+            const __amdgpu_buffer_rsrc_t frs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(p.act), (short)0,
+                (int)(((uint32_t)(p.M - 1) * (uint32_t)p.lda + (uint32_t)p.K) * 4u), kBufferFlags);
+            g3_issue_act_f32(frs, abuf, lane, wb0, nb, p.M, p.lda);
         } else {
             // lane (g, col): elements 32 blk + 4 t .. +3 and 16 later of token
             // col, blk = wb0 + 4 q + g, for fragment (q, t)
@@ -2040,6 +2113,24 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
         u32x4 af[kGvQuads][4];
         if constexpr (PACKED) {
             g3_read_act<S>(abuf, lane, af);
+        } else if constexpr (F32LDS) {
+            // lane (g, col), fragment (q, t): chunks 8 blk + t and + 4 of its
+            // slot's slice, blk = 4 q + g (elements 32 blk + 4 t .. +3 and 16
+            // later)
+#pragma unroll
+            for (int f = 0; f < kGvBPW; ++f) {
+                const int bl = 4 * (f >> 2) + g, c = 8 * bl + (f & 3);
+                floatx4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = x0;
+                if (col < p.M && wb0 + bl < nb) {
+                    x0 = g3_act_f32(abuf, col, c);
+                    x1 = g3_act_f32(abuf, col, c + 4);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    ovf |= (__builtin_fabsf(x0[j]) >= 65520.0f) | (__builtin_fabsf(x1[j]) >= 65520.0f);
+                    af[f >> 2][f & 3][j] = pack_f16(x0[j], x1[j]);
+                }
+            }
         } else {
 #pragma unroll
             for (int f = 0; f < kGvBPW; ++f)
@@ -2134,8 +2225,8 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_group_kernel(GemvGroup 
     uint8_t *bufB = bufA + kG3WLds;          // 12 KB: the activations, then weights
     const uint32_t slice0 = (uint32_t)(72 * wave) & ~15u;
     const int nwg = gridDim.x, bid = blockIdx.x;
-    const int G0 = (int)(((int64_t)p.groups * bid) / nwg);
-    const int G1 = (int)(((int64_t)p.groups * (bid + 1)) / nwg);
+    int G0, G1;
+    wg_row_groups(p.groups, nwg, bid, G0, G1);
     auto op_of = [&](int gg) {
         int op = 0;
 #pragma unroll
@@ -2530,6 +2621,7 @@ static hipError_t gemv_attrs() {
     static hipError_t attr_err = hipSuccess;
     std::call_once(attr_once, [] {
         const void *g3[] = {
+            reinterpret_cast<const void *>(&b1_gemv3_kernel<8, false>),
             reinterpret_cast<const void *>(&b1_gemv3_kernel<16, false>),
             reinterpret_cast<const void *>(&b1_gemv3_kernel<1, true>),
             reinterpret_cast<const void *>(&b1_gemv3_kernel<2, true>),
@@ -2577,7 +2669,11 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
         // converts and repairs out-of-range tokens itself
         LinearArgs b = a;
         b.rsc = nullptr;
-        hipLaunchKernelGGL((b1_gemv3_kernel<16, false>), dim3(nwg), dim3(kGvWaves * 64), kG3Lds, s, b, groups);
+        // up to 8 tokens whose rows lie in a buffer resource: through LDS
+        if (a.M <= 8 && ((uint64_t)(a.M - 1) * (uint64_t)a.lda + (uint64_t)a.K) * 4u < (1ull << 31))
+            hipLaunchKernelGGL((b1_gemv3_kernel<8, false>), dim3(nwg), dim3(kGvWaves * 64), kG3Lds, s, b, groups);
+        else
+            hipLaunchKernelGGL((b1_gemv3_kernel<16, false>), dim3(nwg), dim3(kGvWaves * 64), kG3Lds, s, b, groups);
         return hipGetLastError();
     }
     int mp_log2 = 0;

@@ -88,6 +88,7 @@ PATHS = [
     (16, 768, 640, "gemm", "lib"),        # GEMM tile for a few rows
     (300, 768, 600, "gemm", None),        # fused-conversion GEMM + exact rows
     (16, 6144, 1000, "gemv", None),       # small-M, two K passes, ragged N
+    (8, 3328, 1000, "gemv", None),        # small-M over fp32 rows staged in LDS, ragged second K pass
     (12, 448, 96, "auto", "lib"),         # K % 256 != 0: small-M + fix-up kernel
     (200, 448, 320, "auto", "lib"),       # K % 384 != 0: fused-conversion GEMM + exact rows
 ]
