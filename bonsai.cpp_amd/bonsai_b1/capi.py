@@ -98,6 +98,10 @@ def load():
     L.bonsai_b1_version.restype = i
     L.bonsai_b1_linear_f32_f32.argtypes = [vp, i, i, vp]
     L.bonsai_b1_linear_f32_f32.restype = None
+    L.bonsai_b1_callback_defer.argtypes = [i]
+    L.bonsai_b1_callback_defer.restype = i
+    L.bonsai_b1_callback_finish.argtypes = [ctypes.POINTER(ctypes.c_int32)]
+    L.bonsai_b1_callback_finish.restype = i
     L.bonsai_b1_linear_batch.argtypes = [ctypes.POINTER(LinearOp), i, i, vp, vp, ctypes.c_size_t,
                                          ctypes.POINTER(i), vp]
     L.bonsai_b1_linear_batch.restype = i

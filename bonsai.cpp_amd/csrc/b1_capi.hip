@@ -45,7 +45,6 @@ struct Workspace {
 struct DeviceInfo {
     int state = 0; // 0 unknown, 1 usable gfx950, -1 unusable
     int num_cus = 0;
-    int32_t *cb_counter = nullptr; // non-finite counter for the callback
     std::list<Workspace> ws;       // stable element addresses
     uint64_t tick = 0;
     // this device's address of `scratch` (0: not looked up, 1: found, -1:
@@ -1163,6 +1162,36 @@ int bonsai_b1_linear(const float *act, const B1Weights *w, int batch,
                                 batch, out, w->out_dim, mode, nonfinite, stream);
 }
 
+namespace {
+// The callback's non-finite counters, per thread (its ops run on the
+// thread's hipStreamPerThread) and device: [0] for per-op checking, [1] the
+// deferred count.  Allocated by the thread's first op on a device; they live
+// until the process ends.
+thread_local bool t_cb_defer = false;
+thread_local int32_t *t_cb_count[kMaxDevices][2] = {};
+} // namespace
+
+int bonsai_b1_callback_defer(int on) {
+    t_cb_defer = on != 0;
+    return BONSAI_B1_OK;
+}
+
+int bonsai_b1_callback_finish(int32_t *count) {
+    int dev = 0;
+    if (!current_device(&dev)) return BONSAI_B1_ERR_DEVICE;
+    hipStream_t s = hipStreamPerThread;
+    int32_t bad = 0;
+    int32_t *cnt = t_cb_count[dev][1];
+    if (cnt) {
+        if (hipMemcpyAsync(&bad, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipMemsetAsync(cnt, 0, sizeof(int32_t), s) != hipSuccess)
+            return BONSAI_B1_ERR_HIP;
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) return BONSAI_B1_ERR_HIP;
+    if (count) *count = bad;
+    return bad ? BONSAI_B1_ERR_NONFINITE : BONSAI_B1_OK;
+}
+
 void bonsai_b1_linear_f32_f32(bonsai_b1_tensor *dst, int ith, int nth,
                               void *userdata) {
     (void)nth;
@@ -1184,27 +1213,38 @@ void bonsai_b1_linear_f32_f32(bonsai_b1_tensor *dst, int ith, int nth,
         fprintf(stderr, "B1_FATAL: no usable gfx950 device\n");
         abort();
     }
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        if (!di->cb_counter && hipMalloc(reinterpret_cast<void **>(&di->cb_counter), sizeof(int32_t)) != hipSuccess) {
-            fprintf(stderr, "B1_FATAL: hipMalloc of the status counter failed\n");
-            abort();
-        }
+    // this thread's counter on this device for the mode in use (threads run
+    // their ops on their own streams, so each counts into its own)
+    int32_t *&cnt = t_cb_count[dev][t_cb_defer ? 1 : 0];
+    if (!cnt && (hipMalloc(reinterpret_cast<void **>(&cnt), sizeof(int32_t)) != hipSuccess ||
+                 hipMemset(cnt, 0, sizeof(int32_t)) != hipSuccess)) {
+        fprintf(stderr, "B1_FATAL: allocation of the status counter failed\n");
+        abort();
     }
     hipStream_t s = hipStreamPerThread;
+    if (t_cb_defer) {
+        // enqueue only; the non-finite outputs add to the counter
+        const int st = bonsai_b1_linear_f32(static_cast<const float *>(act->data), lda, wt->data, in_dim, out_dim,
+                                            batch, static_cast<float *>(dst->data), ldo, BONSAI_B1_MODE_AUTO, cnt, s);
+        if (st != BONSAI_B1_OK) {
+            fprintf(stderr, "B1_FATAL: b1_linear failed: %s (in_dim=%d out_dim=%d)\n",
+                    bonsai_b1_status_string(st), in_dim, out_dim);
+            abort();
+        }
+        return;
+    }
     int32_t bad = 0;
     // The op in AUTO mode, then, if that made non-finite outputs, again in
     // EXACT mode (the reference's scalar arithmetic): the reference aborts
     // only when its own fp32 sums are non-finite, so a value FAST mode alone
     // cannot represent must not abort here.
     auto run = [&](int mode) {
-        int st = hipMemsetAsync(di->cb_counter, 0, sizeof(int32_t), s) == hipSuccess ? BONSAI_B1_OK
-                                                                                      : BONSAI_B1_ERR_HIP;
+        int st = hipMemsetAsync(cnt, 0, sizeof(int32_t), s) == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
         if (st == BONSAI_B1_OK)
             st = bonsai_b1_linear_f32(static_cast<const float *>(act->data), lda, wt->data, in_dim, out_dim, batch,
-                                      static_cast<float *>(dst->data), ldo, mode, di->cb_counter, s);
+                                      static_cast<float *>(dst->data), ldo, mode, cnt, s);
         if (st == BONSAI_B1_OK &&
-            (hipMemcpyAsync(&bad, di->cb_counter, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+            (hipMemcpyAsync(&bad, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
              hipStreamSynchronize(s) != hipSuccess))
             st = BONSAI_B1_ERR_HIP;
         return st;

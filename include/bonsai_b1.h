@@ -337,6 +337,27 @@ void bonsai_b1_linear_f32_f32(bonsai_b1_tensor *dst, int ith, int nth,
                               void *userdata);
 
 /*
+ * Deferred checking for bonsai_b1_linear_f32_f32 on the calling thread (no
+ * counterpart in the reference, whose CPU op finishes before the callback
+ * returns; for graph runners that do not want a host synchronisation per
+ * op).  After bonsai_b1_callback_defer(1) the callback runs each op in AUTO
+ * mode on hipStreamPerThread and returns without synchronising: no EXACT
+ * rerun, no abort; the op's non-finite outputs are added to a counter of
+ * this thread and device (the first deferred op on a device allocates it,
+ * so run one before capturing a graph).  bonsai_b1_callback_finish
+ * synchronises the thread's stream once, stores that count in *count
+ * (count may be NULL), resets it, and returns BONSAI_B1_ERR_NONFINITE when
+ * it was non-zero -- the caller then aborts as the reference would have
+ * after the op -- else BONSAI_B1_OK.  bonsai_b1_callback_defer(0) restores
+ * the per-op behaviour.  AUTO mode is range-safe: a finite activation never
+ * makes an output non-finite that the reference's fp32 sums keep finite,
+ * short of sums near FLT_MAX, so skipping the EXACT rerun changes no
+ * finite result.
+ */
+int bonsai_b1_callback_defer(int on);
+int bonsai_b1_callback_finish(int32_t *count);
+
+/*
  * Weight residency; replaces load_b1 (src/diffuser.cpp:39-50, memcpy of the
  * safetensors U8 [out_dim, in_dim/32*6] tensor into a ggml I8 tensor) and the
  * deferred upload of the WebGPU driver (src/diffuser_webgpu.cpp:49-64,

@@ -326,6 +326,74 @@ def test_residency_builder_and_callback(torch, b1, oracle):
     W.free()
 
 
+def test_callback_deferred_checking(torch, b1):
+    """bonsai_b1_callback_defer(1): the callback enqueues each op without a
+    host synchronisation; bonsai_b1_callback_finish synchronises once,
+    reports the non-finite outputs of every op since the last finish and
+    resets.  Outputs equal the library's AUTO linear."""
+    import ctypes
+    from bonsai_b1 import capi, synth
+    m, k, n = 6, 512, 96
+    act = synth.activations(m, k, 19)
+    raw = synth.packed_weights(n, k, 20)
+    W = b1.Weights(raw, k, n)
+    a = torch.from_numpy(act).cuda()
+    bad = act.copy()
+    bad[2, 5] = np.inf                       # every output of token 2 is infinite
+    abad = torch.from_numpy(bad).cuda()
+    ref = W.linear(a).cpu().numpy()
+    ref_bad = W.linear(abad).cpu().numpy()
+
+    class T(ctypes.Structure):
+        pass
+    T._fields_ = [("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_size_t * 4),
+                  ("src", ctypes.POINTER(T) * 2), ("data", ctypes.c_void_p)]
+    keep = []
+
+    def node(x, o):
+        ta, tw, td = T(), T(), T()
+        ta.ne[:] = [k, m, 1, 1]
+        ta.nb[:] = [4, 4 * k, 4 * k * m, 4 * k * m]
+        ta.data = x.data_ptr()
+        tw.ne[:] = [W.c.nbytes, 1, 1, 1]
+        tw.data = W.c.data
+        td.ne[:] = [n, m, 1, 1]
+        td.nb[:] = [4, 4 * n, 4 * n * m, 4 * n * m]
+        td.src[0] = ctypes.pointer(ta)
+        td.src[1] = ctypes.pointer(tw)
+        td.data = o.data_ptr()
+        keep.extend([ta, tw, td])
+        return td
+
+    ud = capi.B1LinearUserData(0x31423142, k, n)
+    lib = b1.load()
+    torch.cuda.synchronize()
+    cnt = ctypes.c_int32(-1)
+    say("deferred callback: nothing pending")
+    assert lib.bonsai_b1_callback_finish(ctypes.byref(cnt)) == capi.OK and cnt.value == 0
+    assert lib.bonsai_b1_callback_defer(1) == capi.OK
+    try:
+        outs = [torch.full((m, n), 7.0, device="cuda") for _ in range(3)]
+        say("deferred callback: three ops, the second with an infinite activation")
+        for x, o in zip((a, abad, a), outs):
+            lib.bonsai_b1_linear_f32_f32(ctypes.byref(node(x, o)), 0, 1, ctypes.byref(ud))
+        assert lib.bonsai_b1_callback_finish(ctypes.byref(cnt)) == capi.ERR_NONFINITE
+        assert cnt.value == n
+        assert lib.bonsai_b1_callback_finish(ctypes.byref(cnt)) == capi.OK and cnt.value == 0
+    finally:
+        lib.bonsai_b1_callback_defer(0)
+    y = [o.cpu().numpy() for o in outs]
+    assert np.array_equal(y[0], ref) and np.array_equal(y[2], ref)
+    assert np.array_equal(y[1].view(np.uint32), ref_bad.view(np.uint32))
+    assert not np.isfinite(y[1][2]).any() and np.isfinite(np.delete(y[1], 2, axis=0)).all()
+    say("per-op callback again")
+    o = torch.empty((m, n), device="cuda")
+    lib.bonsai_b1_linear_f32_f32(ctypes.byref(node(a, o)), 0, 1, ctypes.byref(ud))
+    torch.cuda.synchronize()
+    assert np.array_equal(o.cpu().numpy(), ref)
+    W.free()
+
+
 @pytest.mark.parametrize("mode,m", [("gemv", 8), ("gemm", 256), ("gemm", 4608)])
 def test_graph_replay_matches_eager(torch, b1, mode, m):
     """Launches captured into a HIP graph (as the benchmark does) with the
