@@ -1512,14 +1512,14 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
         kst0 = split * nstage;
         uout = out + (size_t)split * (size_t)pstride;
     };
-    // Row scales of the tile (epi.rsc, range-safe packing): waves 0 and 1
-    // copy the BM values into the tile's parity buffer, ahead of its first
+    // Row scales of the tile (epi.rsc, range-safe packing): waves 0 .. BM/64
+    // - 1 copy the BM values into the tile's parity buffer, ahead of its first
     // stage, so they count as part of that stage in the vmcnt waits.
     const bool rows_scaled = epi.rsc != nullptr && ksplit == 1;
     int parity = 0;
     auto issue_rsc = [&](int par) {
-        static_assert(BM == 128, "two waves copy the row scales");
-        if (rows_scaled && wave < 2)
+        static_assert(BM % 64 == 0 && BM / 64 <= C::NW, "one wave copies 64 row scales");
+        if (rows_scaled && wave < BM / 64)
             dma_lds4(epi.rsc + min(m0 + 64 * wave + lane, M - 1), smem + C::RSC + par * BM * 4 + wave * 256);
     };
     unit_origin(unit);
@@ -2319,6 +2319,9 @@ namespace {
 // one work-group per CU.
 constexpr int kBM = 128, kBN = 512, kWN = 64, kStages = 3, kWgPerCu = 1;
 using KCfg = GemmLdsCfg<kBM, kBN, kWN, kStages>;
+// Half-height tiles for the last, partial round of some shapes.
+constexpr int kBMH = 64;
+using KCfgH = GemmLdsCfg<kBMH, kBN, kWN, kStages>;
 } // namespace
 
 // GEMM over pre-packed activations: the stage count K/128 is a multiple of
@@ -2472,6 +2475,39 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
         // checks these) and 128 rows under 2^31 bytes for the buffer stores
         vec_store = (epi.split == 0 || (al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 22))) &&
                     (epi.split >= N || (al16(epi.pk) && epi.ldpw % 4 == 0 && epi.ldpw < (int64_t(1) << 22)));
+    // The persistent grid runs ceil(tiles / slots) rounds.  When the tiles
+    // of the full rounds are whole tile rows and the last, partial round
+    // has at most half the slots' tiles, its rows run as 64-row tiles in a
+    // second launch: twice the tiles, each ~0.6 of a 128-row tile's time
+    // (at M=4608 K=3072 N=12288: 768 tiles in 3 rounds, then 192 half tiles
+    // instead of 96).  Every output is the same sum in the same order.
+    const int tiles = tiles_m * tiles_n;
+    const int full = num_cus > 0 ? tiles / slots * slots : 0;
+    if (full > 0 && full < tiles && full % tiles_n == 0 && 2 * (tiles - full) <= slots) {
+        auto tail = &b1_gemm_kernel<kBMH, kBN, kWN, kStages, EPI>;
+        static std::once_flag tail_once;
+        static hipError_t tail_err = hipSuccess;
+        std::call_once(tail_once, [tail] {
+            tail_err = hipFuncSetAttribute(reinterpret_cast<const void *>(tail),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, KCfgH::LDS);
+        });
+        if (tail_err != hipSuccess) return tail_err;
+        const int ms = full / tiles_n * kBM; // rows of the full rounds
+        hipLaunchKernelGGL(kernel, dim3(slots), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
+                           K, N, ms, out, ldo, nonfinite, full / tiles_n, tiles_n, vec_store, epi, 1, (int64_t)0);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        GemmEpi et = epi;
+        if (et.res) et.res += (size_t)ms * (size_t)et.ldr;
+        if (et.pk) et.pk += (size_t)ms * (size_t)et.ldpw;
+        if (et.rsc) et.rsc += ms;
+        const int mt = M - ms, tm = (mt + kBMH - 1) / kBMH;
+        hipLaunchKernelGGL(tail, dim3(tm * tiles_n), dim3(KCfgH::NT), KCfgH::LDS, s,
+                           static_cast<const uint16_t *>(packed) + (size_t)ms * (size_t)K, w, K, N, mt,
+                           out ? out + (size_t)ms * (size_t)ldo : out, ldo, nonfinite, tm, tiles_n, vec_store, et, 1,
+                           (int64_t)0);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
                        K, N, M, out, ldo, nonfinite, tiles_m, tiles_n, vec_store, epi, 1, (int64_t)0);
     return hipGetLastError();

@@ -394,6 +394,61 @@ def test_callback_deferred_checking(torch, b1):
     W.free()
 
 
+@pytest.mark.parametrize("kind", ["plain", "scaled", "gate_residual", "swiglu", "gelu_packed"])
+def test_tail_rows_as_half_height_tiles(torch, b1, kind):
+    """M=4608 K=3072 N=12288 on 256 CUs runs its 768 full-round tiles of 128
+    rows, then rows 4096..4607 as 64-row tiles in a second launch.  Every
+    output is the same sum in the same order as in two separate calls over
+    rows [0, 4096) and [4096, 4608), which take no such split: bit for bit,
+    for each epilogue kind.  (The plain reference goes through the
+    epilogue entry with no epilogue: the plain entry would split the
+    512-row call along K.)  With range-safe row scales, the scaled rows
+    equal the unscaled ones times their scales."""
+    from bonsai_b1 import synth
+    m, k, n, ms = 4608, 3072, 12288, 4096
+    say(f"tail rows as half-height tiles: {kind} ({torch.cuda.get_device_properties(0).multi_processor_count} CUs)")
+    a = synth.device_activations(m, k, 61)
+    w = synth.device_packed_weights(n, k, 62)
+    if kind == "scaled":
+        a[10] *= 3.0e5
+        a[4200] *= 2.0e6
+        pa, rsc = b1.pack_act_f16_scaled(a)
+    else:
+        pa = b1.pack_act_f16(a)
+    rb = k * 2                                   # packed bytes per row
+
+    def run(rows, r0, whole=False):
+        p = pa[r0 * rb:(r0 + rows) * rb]
+        if kind == "plain":
+            if whole:
+                return b1.linear_packed_f16(p, w, k, n, rows)
+            return b1.linear_packed_f16_epi(p, w, k, n, rows, "none")
+        if kind == "gate_residual":
+            return b1.linear_packed_f16_epi(p, w, k, n, rows, "gate_residual", gate=gate, residual=res[r0:r0 + rows])
+        if kind == "swiglu":
+            return b1.linear_packed_f16_epi(p, w, k, n, rows, "swiglu")
+        _, po = b1.linear_packed_f16_to_packed(p, w, k, n, rows, 0, "gelu_tanh")
+        return po
+
+    g = torch.Generator(device="cuda").manual_seed(63)
+    gate = 0.1 * torch.randn(n, device="cuda", generator=g)
+    res = torch.randn((m, n), device="cuda", generator=g)
+    if kind == "scaled":
+        # the scaled entry splits a 512-row call along K too; its rows are the
+        # unscaled products times their scales, one fp32 multiply each
+        full = b1.linear_packed_f16_scaled(pa, rsc, w, k, n, m)
+        ref = b1.linear_packed_f16_epi(pa, w, k, n, m, "none") * rsc[:, None]
+        torch.cuda.synchronize()
+        assert bool((rsc[ms:] != 1.0).any()), "a tail row needs a row scale"
+        assert torch.equal(full.view(torch.uint8), ref.view(torch.uint8)), kind
+        return
+    full = run(m, 0, whole=True)
+    head, tail = run(ms, 0), run(m - ms, ms)
+    torch.cuda.synchronize()
+    joined = torch.cat([head.reshape(-1), tail.reshape(-1)])
+    assert torch.equal(full.reshape(-1).view(torch.uint8), joined.view(torch.uint8)), kind
+
+
 @pytest.mark.parametrize("mode,m", [("gemv", 8), ("gemm", 256), ("gemm", 4608)])
 def test_graph_replay_matches_eager(torch, b1, mode, m):
     """Launches captured into a HIP graph (as the benchmark does) with the
