@@ -2475,15 +2475,20 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
         // checks these) and 128 rows under 2^31 bytes for the buffer stores
         vec_store = (epi.split == 0 || (al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 22))) &&
                     (epi.split >= N || (al16(epi.pk) && epi.ldpw % 4 == 0 && epi.ldpw < (int64_t(1) << 22)));
-    // The persistent grid runs ceil(tiles / slots) rounds.  When the tiles
-    // of the full rounds are whole tile rows and the last, partial round
-    // has at most half the slots' tiles, its rows run as 64-row tiles in a
-    // second launch: twice the tiles, each ~0.6 of a 128-row tile's time
-    // (at M=4608 K=3072 N=12288: 768 tiles in 3 rounds, then 192 half tiles
-    // instead of 96).  Every output is the same sum in the same order.
+    // The persistent grid runs ceil(tiles / slots) rounds.  When the whole
+    // tile rows that fit in the full rounds leave at most one round of
+    // 64-row tiles, those rows run with 128-row tiles (still the same
+    // number of rounds) and the rest as 64-row tiles in a second launch:
+    // twice the tiles, each ~0.6 of a 128-row tile's time (at M=4608 K=3072
+    // N=12288: 768 tiles in 3 rounds, then 192 half tiles instead of 96;
+    // at M=4096 N=9216: 504 tiles in 2 rounds, then 144 half tiles instead
+    // of a third round of 72).  Every output is the same sum in the same
+    // order.
     const int tiles = tiles_m * tiles_n;
     const int full = num_cus > 0 ? tiles / slots * slots : 0;
-    if (full > 0 && full < tiles && full % tiles_n == 0 && 2 * (tiles - full) <= slots) {
+    const int head_rows = full / tiles_n;                        // whole tile rows in the full rounds
+    const int tail_tiles = ((M - head_rows * kBM + kBMH - 1) / kBMH) * tiles_n;
+    if (full > 0 && full < tiles && tiles_n < slots && head_rows > 0 && tail_tiles <= slots) {
         auto tail = &b1_gemm_kernel<kBMH, kBN, kWN, kStages, EPI>;
         static std::once_flag tail_once;
         static hipError_t tail_err = hipSuccess;
@@ -2492,9 +2497,11 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
                                            hipFuncAttributeMaxDynamicSharedMemorySize, KCfgH::LDS);
         });
         if (tail_err != hipSuccess) return tail_err;
-        const int ms = full / tiles_n * kBM; // rows of the full rounds
-        hipLaunchKernelGGL(kernel, dim3(slots), dim3(KCfg::NT), KCfg::LDS, s, static_cast<const uint16_t *>(packed), w,
-                           K, N, ms, out, ldo, nonfinite, full / tiles_n, tiles_n, vec_store, epi, 1, (int64_t)0);
+        const int ms = head_rows * kBM;
+        const int hunits = head_rows * tiles_n;
+        hipLaunchKernelGGL(kernel, dim3(hunits < slots ? hunits : slots), dim3(KCfg::NT), KCfg::LDS, s,
+                           static_cast<const uint16_t *>(packed), w, K, N, ms, out, ldo, nonfinite, head_rows, tiles_n,
+                           vec_store, epi, 1, (int64_t)0);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         GemmEpi et = epi;

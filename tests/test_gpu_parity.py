@@ -394,24 +394,28 @@ def test_callback_deferred_checking(torch, b1):
     W.free()
 
 
-@pytest.mark.parametrize("kind", ["plain", "scaled", "gate_residual", "swiglu", "gelu_packed"])
-def test_tail_rows_as_half_height_tiles(torch, b1, kind):
+@pytest.mark.parametrize("m,n,ms,kind", [(4608, 12288, 4096, kd) for kd in
+                                          ("plain", "scaled", "gate_residual", "swiglu", "gelu_packed")] +
+                         [(4096, 9216, 3584, kd) for kd in ("plain", "gate_residual", "gelu_packed")])
+def test_tail_rows_as_half_height_tiles(torch, b1, m, n, ms, kind):
     """M=4608 K=3072 N=12288 on 256 CUs runs its 768 full-round tiles of 128
-    rows, then rows 4096..4607 as 64-row tiles in a second launch.  Every
-    output is the same sum in the same order as in two separate calls over
-    rows [0, 4096) and [4096, 4608), which take no such split: bit for bit,
-    for each epilogue kind.  (The plain reference goes through the
+    rows, then rows 4096..4607 as 64-row tiles in a second launch (M=4096
+    N=9216: 504 tiles of rows [0, 3584) in two rounds, then the rest as
+    64-row tiles).  Every output is the same sum in the same order as in two
+    separate calls over rows [0, ms) and [ms, M), which take no such split:
+    bit for bit, for each epilogue kind.  (The plain reference goes through the
     epilogue entry with no epilogue: the plain entry would split the
     512-row call along K.)  With range-safe row scales, the scaled rows
     equal the unscaled ones times their scales."""
     from bonsai_b1 import synth
-    m, k, n, ms = 4608, 3072, 12288, 4096
-    say(f"tail rows as half-height tiles: {kind} ({torch.cuda.get_device_properties(0).multi_processor_count} CUs)")
+    k = 3072
+    say(f"tail rows as half-height tiles: ({m},{k},{n}) {kind} "
+        f"({torch.cuda.get_device_properties(0).multi_processor_count} CUs)")
     a = synth.device_activations(m, k, 61)
     w = synth.device_packed_weights(n, k, 62)
     if kind == "scaled":
         a[10] *= 3.0e5
-        a[4200] *= 2.0e6
+        a[ms + 104] *= 2.0e6
         pa, rsc = b1.pack_act_f16_scaled(a)
     else:
         pa = b1.pack_act_f16(a)
