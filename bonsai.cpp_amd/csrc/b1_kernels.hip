@@ -104,6 +104,21 @@ constexpr int kBufferFlags = 0x00020000;
 // non-temporal policy sends each quarter on its own (355 vs ~267 us at
 // M=4096 K=3072 N=12288).
 constexpr int kStoreNT = 0;
+// A 16-byte buffer store followed by 5 wait states before any instruction
+// may rewrite its data registers.  A store of more than 8 bytes reads its
+// data in the cycles after it issues; the compiler inserts that gap only
+// for stores whose soffset is not a register, and the epilogue stores carry
+// their row offset in an SGPR.  Without it, a VALU write issued right after
+// such a store changed the stored values of some lanes (the SwiGLU
+// epilogue: 2272 of 786,432 outputs, different on every launch).  The asm
+// takes the data as an input, so its registers stay live until the nops
+// have issued, and its memory clobber keeps it after the store.
+template <int AUX>
+__device__ __forceinline__ void store16_guarded(u32x4 v, __amdgpu_buffer_rsrc_t rsrc, int voff, int soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, voff, soff, AUX);
+    asm volatile("s_nop 4" ::"v"(v) : "memory");
+}
+
 // 16 bytes per lane from the buffer at byte offset voff, landing at
 // lds + 16 * lane (wave-uniform lds, through M0).
 __device__ __forceinline__ void dma_buf_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff) {
@@ -1222,7 +1237,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 #pragma unroll
                     for (int k = 0; k < 2; ++k) {
                         const int ro = (mt * 32 + 16 * half + 8 * k) * ldb + nt * 128;
-                        __builtin_amdgcn_raw_buffer_store_b128(vr[k], ors, lvoff, ro, kStoreNT);
+                        store16_guarded<kStoreNT>(vr[k], ors, lvoff, ro);
                     }
                 }
     };
@@ -1239,6 +1254,43 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
             const int H = epi.glu_h;
             const int jb = (n0 >> 1) + wave * 32;
             const bool fullg = vec_store && m0 + BM <= M && jb + 32 <= H;
+            if (fullg) {
+                // The wave's 32 outputs of a row are one 128-byte line: made
+                // by every lane, then through the transpose as whole lines
+                // (16 stores per lane).
+                if (cnt) {
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v)
+                            bad += !__builtin_isfinite(acc[mt][0][v]) + !__builtin_isfinite(acc[mt][1][v]);
+                }
+                const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+                    out + (size_t)m0 * ldo + jb, (short)0, (int)(BM * ldo * 4), kBufferFlags);
+                const int ldb = stride_bytes(ldo);
+                const int lvoff = rr0 * ldb + 16 * cc;
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt) {
+                    u32x4 v[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float o = mul_f32(silu_f32(acc[mt][0][4 * q + r]), acc[mt][1][4 * q + r]);
+                            v[q][r] = __builtin_bit_cast(uint32_t, o);
+                        }
+#pragma unroll
+                    for (int half = 0; half < 2; ++half) {
+                        u32x4 vr[2];
+                        transpose(v, half, vr);
+#pragma unroll
+                        for (int k = 0; k < 2; ++k)
+                            store16_guarded<kStoreNT>(vr[k], ors, lvoff, (mt * 32 + 16 * half + 8 * k) * ldb);
+                    }
+                }
+                count_nonfinite(nonfinite, bad);
+                return 3;
+            }
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt) {
                 const int m = m0 + mt * 32 + li;
@@ -1252,9 +1304,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                         o[r] = mul_f32(silu_f32(gt), vl);
                         if (cnt && m < M && j + r < H) bad += !__builtin_isfinite(gt) + !__builtin_isfinite(vl);
                     }
-                    if (fullg) {
-                        *reinterpret_cast<floatx4 *>(out + (size_t)m * ldo + j) = o;
-                    } else if (m < M) {
+                    if (m < M) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             if (j + r < H) out[(size_t)m * ldo + j + r] = o[r];
@@ -1315,7 +1365,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                             o[e] = __builtin_bit_cast(uint32_t, ov);
                         }
                         const int ro = (mt * 32 + 16 * half + 8 * k) * ldb + nt * 128;
-                        __builtin_amdgcn_raw_buffer_store_b128(o, ors, lvoff, ro, kStoreNT);
+                        store16_guarded<kStoreNT>(o, ors, lvoff, ro);
                     }
                 }
                 count_nonfinite(nonfinite, bad);
@@ -1396,7 +1446,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 #pragma unroll
                         for (int k = 0; k < 2; ++k) {
                             const int ro = (mt * 32 + 16 * half + 8 * k) * lpb;
-                            __builtin_amdgcn_raw_buffer_store_b128(vr[k], prs, lpoff, ro, 0);
+                            store16_guarded<0>(vr[k], prs, lpoff, ro);
                         }
                     }
                 }
