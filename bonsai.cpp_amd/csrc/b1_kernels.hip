@@ -90,7 +90,13 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // for the global and the buffer forms), leaving 4 bytes untouched per lane.
 // Kept as plain device functions: a kernel template that calls these
 // builtins directly loses its host-side launch stub.
-// global_load_lds_dword: lane i's 4 bytes land at lds + 4 i.
+// global_load_lds_dword: lane i's 4 bytes land at lds + 4 i.  The compiler
+// treats this global form as a FLAT access that may touch LDS, and with one
+// in a kernel it makes every LDS wait of that kernel a full lgkmcnt(0).  In
+// the GEMM (its row-scale copy) the buffer form instead gives waits that
+// count only the reads a step needs, and it measured no faster (252.9-253.4
+// vs 253.1 us at M=4096 K=3072 N=12288, 0.3-0.6 % slower on four other
+// shapes, bit-identical): the fragment reads' latency is already covered.
 __device__ __forceinline__ void dma_lds4(const void *src, void *lds) {
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 4, 0, 0);
 }
@@ -888,11 +894,11 @@ __global__ __launch_bounds__(256) void b1_fixup_rows_kernel(LinearArgs p) {
 // the activation rows, so no weight column is expanded twice).  K advances
 // in stages of 128 (4 blocks).  Both operands of a stage go global -> LDS
 // directly, with no VGPR staging, into three-slot rings fetched two stages
-// ahead: activations with global_load_lds_dwordx4 (rows of 256 bytes, 16-
+// ahead: activations with buffer_load_dwordx4 … lds (rows of 256 bytes, 16-
 // byte chunk c of row r at position c ^ (r & 15), so the 16 lanes one
 // ds_read_b128 phase serves hit 16 different bank groups of the 64), and
 // the 24 packed bytes per weight column and stage with two
-// global_load_lds_dwordx3 (12 bytes per lane, landing at a 16-byte lane
+// buffer_load_dwordx3 … lds (12 bytes per lane, landing at a 16-byte lane
 // stride).
 //
 // The grid is persistent (one work-group per CU, tiles strided by the grid
