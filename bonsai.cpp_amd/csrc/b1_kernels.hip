@@ -154,6 +154,39 @@ __device__ __forceinline__ uint32_t wpair(uint32_t w, int sh, uint32_t scale2) {
     return xnor_sel(kSignPair, w << sh, scale2);
 }
 
+// One v_lshlrev_b64 of the pair (w, w >> 8): its low dword is w << SH and
+// its high dword carries bits d + 8 and d + 24 of w at 15 and 31 (d = 15 -
+// SH < 8), so that one shift serves the weight dwords of pairs d and d + 8.
+// A 64-bit shift costs what a 32-bit one does on gfx950 (measured: both
+// about 2 ns per wave instruction per SIMD with the SIMDs saturated, a
+// v_bitop3 1.2 ns); the compiler splits a constant 64-bit shift into two
+// 32-bit ops, hence the asm.  Its result only feeds VALU bit ops (no MFMA
+// operand hazard).
+template <int SH>
+__device__ __forceinline__ uint64_t shl64(uint64_t v) {
+    static_assert(SH >= 8 && SH <= 15, "pairs d < 8");
+    uint64_t r;
+    asm("v_lshlrev_b64 %0, %1, %2" : "=v"(r) : "I"(SH), "v"(v));
+    return r;
+}
+// The weight dwords of pairs 4T + j (lo) and 4T + j + 8 (hi), j = 0..3,
+// T = 0 or 1, from the sign word w and w8 = w >> 8: the same values as
+// wpair(w, 15 - 4T - j, scale2) and wpair(w, 7 - 4T - j, scale2).
+template <int T>
+__device__ __forceinline__ void wpair_quads(uint32_t w, uint32_t w8, uint32_t scale2, u32x4 &lo, u32x4 &hi) {
+    const uint64_t v = (uint64_t)w8 << 32 | w;
+    const uint64_t v0 = shl64<15 - 4 * T>(v), v1 = shl64<14 - 4 * T>(v), v2 = shl64<13 - 4 * T>(v),
+                   v3 = shl64<12 - 4 * T>(v);
+    lo[0] = xnor_sel(kSignPair, (uint32_t)v0, scale2);
+    lo[1] = xnor_sel(kSignPair, (uint32_t)v1, scale2);
+    lo[2] = xnor_sel(kSignPair, (uint32_t)v2, scale2);
+    lo[3] = xnor_sel(kSignPair, (uint32_t)v3, scale2);
+    hi[0] = xnor_sel(kSignPair, (uint32_t)(v0 >> 32), scale2);
+    hi[1] = xnor_sel(kSignPair, (uint32_t)(v1 >> 32), scale2);
+    hi[2] = xnor_sel(kSignPair, (uint32_t)(v2 >> 32), scale2);
+    hi[3] = xnor_sel(kSignPair, (uint32_t)(v3 >> 32), scale2);
+}
+
 __device__ __forceinline__ void count_nonfinite(int32_t *ctr, int bad) {
     if (bad && ctr) atomicAdd(ctr, bad);
 }
@@ -1951,46 +1984,52 @@ __device__ __forceinline__ void g3_wait(int r) {
     }
 }
 
-// Decode and MFMA of row groups [0, nrg) of a pass, from a wave's staged
-// rows (wbuf, 80 bytes apart) and its activation fragments af.  The slice
-// of wave w starts 8 (w odd) bytes into its first chunk; block 4q + g sits
-// at 6 (4q + g) bytes into the slice, read as the aligned 8-byte window
-// that holds it (2 bytes earlier for odd g).  Each row group is decoded as
-// soon as its own DMAs have landed (AHEAD: DMAs issued after this chunk's).
-template <int AHEAD>
-__device__ __forceinline__ void g3_decode(const uint8_t *wbuf, int nrg, int wave, int lane, const u32x4 (&af)[kGvQuads][4],
-                                          floatx4 (&acc)[kGvMaxRG]) {
+// Decode and MFMA of row group r of a pass into its accumulator, from a
+// wave's staged rows (wbuf, 80 bytes apart) and its activation fragments af.
+// The slice of wave w starts 8 (w odd) bytes into its first chunk; block
+// 4q + g sits at 6 (4q + g) bytes into the slice, read as the aligned 8-byte
+// window that holds it (2 bytes earlier for odd g).
+__device__ __forceinline__ void g3_decode_rg(const uint8_t *wbuf, int r, int wave, int lane,
+                                             const u32x4 (&af)[kGvQuads][4], floatx4 &acc) {
     const int col = lane & 15, g = lane >> 4, odd = g & 1;
     const uint32_t sel_word = odd ? 0x07060504u : 0x05040302u;
     const uint32_t sel_scale = odd ? 0x03020302u : 0x01000100u;
     const int wshift = 8 * (wave & 1);
+    uint32_t wd[kGvQuads][2];
+#pragma unroll
+    for (int q = 0; q < kGvQuads; ++q) {
+        const __attribute__((address_space(3))) uint32_t *src =
+            reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
+                (__attribute__((address_space(3))) uint8_t *)wbuf + (r * 16 + col) * kG3RowB + (4 * q + g) * 6 +
+                wshift - 2 * odd);
+        wd[q][0] = src[0];
+        wd[q][1] = src[1];
+    }
+#pragma unroll
+    for (int q = 0; q < kGvQuads; ++q) {
+        const uint32_t s2 = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_scale);
+        const uint32_t w = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_word);
+        // MFMA t takes pairs 4t .. 4t + 3; one 64-bit shift serves t and t + 2
+        u32x4 bd[4];
+        wpair_quads<0>(w, w >> 8, s2, bd[0], bd[2]);
+        wpair_quads<1>(w, w >> 8, s2, bd[1], bd[3]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, af[q][t]),
+                                                         __builtin_bit_cast(half8, bd[t]), acc, 0, 0, 0);
+    }
+}
+
+// Row groups [0, nrg) of a pass, each decoded as soon as its own DMAs have
+// landed (AHEAD: DMAs issued after this pass's).
+template <int AHEAD>
+__device__ __forceinline__ void g3_decode(const uint8_t *wbuf, int nrg, int wave, int lane, const u32x4 (&af)[kGvQuads][4],
+                                          floatx4 (&acc)[kGvMaxRG]) {
 #pragma unroll
     for (int r = 0; r < kGvMaxRG; ++r) {
         if (r < nrg) {
             g3_wait<AHEAD>(r);
-            uint32_t wd[kGvQuads][2];
-#pragma unroll
-            for (int q = 0; q < kGvQuads; ++q) {
-                const __attribute__((address_space(3))) uint32_t *src =
-                    reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
-                        (__attribute__((address_space(3))) uint8_t *)wbuf + (r * 16 + col) * kG3RowB +
-                        (4 * q + g) * 6 + wshift - 2 * odd);
-                wd[q][0] = src[0];
-                wd[q][1] = src[1];
-            }
-#pragma unroll
-            for (int q = 0; q < kGvQuads; ++q) {
-                const uint32_t s2 = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_scale);
-                const uint32_t w = __builtin_amdgcn_perm(wd[q][1], wd[q][0], sel_word);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    u32x4 bd;
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) bd[jj] = wpair(w, 15 - 4 * t - jj, s2);
-                    acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, af[q][t]),
-                                                                    __builtin_bit_cast(half8, bd), acc[r], 0, 0, 0);
-                }
-            }
+            g3_decode_rg(wbuf, r, wave, lane, af, acc[r]);
         }
     }
 }
@@ -2256,98 +2295,200 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
 
 // Several small-M linears over one packed activation matrix in one launch
 // (the modulation projections of a step, q/k/v of the text stream at a few
-// tokens): persistent work-groups over the row groups of all the ops,
-// in chunks of at most kGvMaxRG row groups of one op; the activation
-// fragments (K <= 3072: one pass) are loaded once per work-group and held in
-// registers, and the weight DMAs of the next chunk are issued before the
-// current one is decoded, into the wave's other LDS buffer.  Each chunk is
-// reduced across the waves through the buffer it was decoded from.
+// tokens).  Each op has its own work-groups (wgstart), each taking at most
+// G4Cfg<S, WL>::P consecutive row groups of that op in one pass: every wave
+// DMAs its activation slice and then its K slice of those rows into its own
+// LDS area, keeping kG4Ahead row groups in flight behind the one it
+// decodes, with no work-group barrier until the end, where the waves'
+// partial tiles are summed once, in wave order.  The per-wave K slices,
+// MFMA order and reduction order are those of b1_gemv3_kernel, so each op's
+// outputs equal its own small-M call bit for bit.
 struct GemvGroup {
     const uint8_t *w[kGemvGroupMax];
     float *out[kGemvGroupMax];
     int64_t ldo[kGemvGroupMax];
     int N[kGemvGroupMax];
     int gstart[kGemvGroupMax + 1]; // first global row group of each op; gstart[nops..] = total
+    int wgstart[kGemvGroupMax + 1]; // first work-group of each op; wgstart[nops..] = the grid
     int nops, groups, K, M;
     const void *act;             // packed fp16 [M][K]
     const float *rsc;            // row scales of the packing, or nullptr
     int32_t *nonfinite;
 };
 
-template <int S>
-__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv_group_kernel(GemvGroup p) {
+// The first 8 entries of a kernel-argument array held in SGPRs: each is
+// read once with a constant index and passed through an empty asm, so that
+// a[i] for a wave-uniform i stays a chain of scalar selects.  (Without the
+// asm the compiler folds the selects back into an indexed read of argument
+// memory, a dependent scalar load of about 1 us before each weight DMA of
+// the grouped kernel; with an array member instead of named ones it moves
+// the entries to scratch.)
+template <class T>
+__device__ __forceinline__ T sgpr_opaque(T x) {
+    asm volatile("" : "+s"(x));
+    return x;
+}
+template <class T>
+struct Sgpr8 {
+    T a0, a1, a2, a3, a4, a5, a6, a7;
+    template <class U, int N>
+    __device__ __forceinline__ explicit Sgpr8(const U (&a)[N])
+        : a0(sgpr_opaque((T)a[0])), a1(sgpr_opaque((T)a[1])), a2(sgpr_opaque((T)a[2])), a3(sgpr_opaque((T)a[3])),
+          a4(sgpr_opaque((T)a[4])), a5(sgpr_opaque((T)a[5])), a6(sgpr_opaque((T)a[6])), a7(sgpr_opaque((T)a[7])) {
+        static_assert(N >= 8, "eight entries");
+    }
+    __device__ __forceinline__ T operator[](int i) const {
+        return i == 0 ? a0 : i == 1 ? a1 : i == 2 ? a2 : i == 3 ? a3 : i == 4 ? a4 : i == 5 ? a5 : i == 6 ? a6 : a7;
+    }
+};
+
+#ifndef B1_G4_AHEAD
+#define B1_G4_AHEAD 4
+#endif
+constexpr int kG4Ahead = B1_G4_AHEAD; // row groups in flight behind the one being decoded
+
+// Row groups of a one-pass work-group by token slots S and per-wave LDS
+// bytes WL: the activation slice (ABytes) and the weight slices of P row
+// groups (WInst DMAs of 1 KB) fill a wave's WL bytes.  WL = 10 KB (S <= 4)
+// puts two work-groups on a CU, so that one's reduction and tail overlap the
+// other's decode; S = 8 and 16 need the whole 20 KB.
+constexpr int g4_abytes(int S) { return S <= 8 ? (S - 1) * kG3ARow + 1024 : kGvBPW * 1024; }
+constexpr int g4_rows(int abytes, int wl) {
+    int p = 0;
+    while (abytes + ((16 * kG3RowCh * (p + 1) + 63) / 64) * 1024 <= wl) ++p;
+    return p;
+}
+template <int S, int WL>
+struct G4Cfg {
+    static constexpr int ABytes = g4_abytes(S);
+    static constexpr int P = g4_rows(ABytes, WL);
+    static constexpr int WInst = (P * 16 * kG3RowCh + 63) / 64;
+    static constexpr int Lds = kGvWaves * WL;
+    static_assert(P >= 1 && ABytes % 16 == 0 && ABytes + WInst * 1024 <= WL, "a wave's LDS area");
+    static_assert(P * 1024 <= WL, "the reduction fits");
+    static_assert(WInst + 2 * kGemvGroupMax < 64, "vmcnt range");
+};
+constexpr int kG4WL2 = 10 * 1024; // two work-groups per CU
+constexpr int kG4WL1 = kG3WaveLds; // one
+
+// Weight DMAs of a one-pass work-group that cover its row groups 0..r
+// (a row group's 16 rows x 5 chunks are 1.25 DMAs of 64 lanes).
+constexpr int g4_dmas(int r) { return (16 * kG3RowCh * (r + 1) + 63) / 64; }
+
+// Row groups R.. of the pass: issue the DMAs of row group R + D (keeping
+// D row groups in flight behind the one being decoded), wait for row group
+// R's (the DMAs issued after them: I - J; an extra DMA issued for a
+// straddling one only makes the wait stricter), decode it, go on while
+// R + 1 < nrg.
+template <int R, int P, int WI, int D>
+struct G4Decode {
+    template <class Issue>
+    static __device__ __forceinline__ void run(const uint8_t *wbuf, int nrg, int wave, int lane,
+                                               const u32x4 (&af)[kGvQuads][4], floatx4 (&acc)[P], Issue &issue) {
+        if (R < nrg) {
+            constexpr int lo = g4_dmas(R + D - 1) < WI ? g4_dmas(R + D - 1) : WI;
+            constexpr int hi = g4_dmas(R + D) < WI ? g4_dmas(R + D) : WI;
+#pragma unroll
+            for (int i = lo; i < hi; ++i) issue(i);
+            wait_vmcnt<hi - g4_dmas(R)>();
+            g3_decode_rg(wbuf, R, wave, lane, af, acc[R]);
+            G4Decode<R + 1, P, WI, D>::run(wbuf, nrg, wave, lane, af, acc, issue);
+        }
+    }
+};
+template <int P, int WI, int D>
+struct G4Decode<P, P, WI, D> {
+    template <class Issue>
+    static __device__ __forceinline__ void run(const uint8_t *, int, int, int, const u32x4 (&)[kGvQuads][4],
+                                               floatx4 (&)[P], Issue &) {}
+};
+
+template <int S, int WL>
+__global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 2 : 1) void b1_gemv_group_kernel(GemvGroup p) {
+    using C = G4Cfg<S, WL>;
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nb = p.K / 32;
+    const int K = sgpr_opaque(p.K), M = sgpr_opaque(p.M);
+    const void *const act = reinterpret_cast<const void *>(sgpr_opaque((uint64_t)p.act));
+    const float *const rsc = reinterpret_cast<const float *>(sgpr_opaque((uint64_t)p.rsc));
+    const int nb = K / 32;
     const uint32_t rs = (uint32_t)nb * 6;
-    uint8_t *bufA = gsm + wave * kG3WaveLds; // 8 KB
-    uint8_t *bufB = bufA + kG3WLds;          // 12 KB: the activations, then weights
+    uint8_t *abuf = gsm + wave * WL;
+    uint8_t *wbuf = abuf + C::ABytes;
     const uint32_t slice0 = (uint32_t)(72 * wave) & ~15u;
-    const int nwg = gridDim.x, bid = blockIdx.x;
-    int G0, G1;
-    wg_row_groups(p.groups, nwg, bid, G0, G1);
-    auto op_of = [&](int gg) {
-        int op = 0;
-#pragma unroll
-        for (int o = 1; o < kGemvGroupMax; ++o) op += gg >= p.gstart[o] ? 1 : 0;
-        return op;
-    };
-    auto chunk_len = [&](int cg0, int op) { return min(min(kGvMaxRG, G1 - cg0), p.gstart[op + 1] - cg0); };
-    auto issue_w = [&](int cg0, int cng, int op, uint8_t *buf) {
-        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t *>(p.w[op]), (short)0, (int)((uint32_t)p.N[op] * rs), kBufferFlags);
-        const int n0 = (cg0 - p.gstart[op]) * 16;
-#pragma unroll
-        for (int i = 0; i < kG3WInst; ++i) {
-            const int sl = i * 64 + lane;
-            const int row = sl / kG3RowCh, ch = sl - row * kG3RowCh;
-            const uint32_t inrow = slice0 + (uint32_t)ch * 16u;
-            dma_buf_lds16(wrs, buf + i * 1024,
-                          (row < cng * 16 && inrow < rs) ? (uint32_t)(n0 + row) * rs + inrow : 0xFFFFFFF0u);
-        }
-    };
+    // the per-op arguments, all read at the start (one round of scalar
+    // loads); this work-group's op and its row groups [R0, R0 + nrg)
+    static_assert(kGemvGroupMax == 8, "eight ops");
+    const Sgpr8<int> wgs(p.wgstart);
+    const Sgpr8<int> ns(p.N);
+    const Sgpr8<uint64_t> ws(p.w);
+    const Sgpr8<uint64_t> outs(p.out);
+    const Sgpr8<int64_t> ldos(p.ldo);
+    const int wg_end = sgpr_opaque(p.wgstart[kGemvGroupMax]);
+    const int bid = blockIdx.x;
+    const int op = (bid >= wgs.a1) + (bid >= wgs.a2) + (bid >= wgs.a3) + (bid >= wgs.a4) + (bid >= wgs.a5) +
+                   (bid >= wgs.a6) + (bid >= wgs.a7);
+    const int wg0 = wgs[op];
+    const int wg1 = op + 1 < kGemvGroupMax ? wgs[op + 1] : wg_end;
+    const int N = ns[op];
+    uint8_t *const wp = reinterpret_cast<uint8_t *>(ws[op]);
+    int R0, R1;
+    wg_row_groups((N + 15) / 16, wg1 - wg0, bid - wg0, R0, R1);
+    const int nrg = R1 - R0; // at most C::P (the launcher's grid)
+    // 1. the activation slice, then the weight slices, D row groups ahead
     const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void *>(p.act), (short)0, (int)((uint32_t)p.M * (uint32_t)p.K * 2u), kBufferFlags);
-    g3_issue_act<S>(ars, bufB, lane, wave * kGvBPW, nb, p.M, p.K);
-    int cg0 = G0;
-    int op = G0 < G1 ? op_of(G0) : 0;
-    int cng = G0 < G1 ? chunk_len(G0, op) : 0;
-    if (cng > 0) issue_w(cg0, cng, op, bufA);
-    wait_vmcnt<kG3WInst>();
+        const_cast<void *>(act), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), kBufferFlags);
+    g3_issue_act<S>(ars, abuf, lane, wave * kGvBPW, nb, M, K);
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(wp, (short)0, (int)((uint32_t)N * rs), kBufferFlags);
+    auto issue = [&](int i) {
+        const int sl = i * 64 + lane;
+        const int row = sl / kG3RowCh, ch = sl - row * kG3RowCh;
+        const uint32_t inrow = slice0 + (uint32_t)ch * 16u;
+        const int n = R0 * 16 + row;
+        const bool ok = row < nrg * 16 && n < N && inrow < rs;
+        dma_buf_lds16(wrs, wbuf + i * 1024, ok ? (uint32_t)n * rs + inrow : 0xFFFFFFF0u);
+    };
+    constexpr int D = kG4Ahead;
+    constexpr int first = g4_dmas(D - 1) < C::WInst ? g4_dmas(D - 1) : C::WInst;
+#pragma unroll
+    for (int i = 0; i < first; ++i) issue(i);
+    // 2. the activations (issued first) have landed when at most the weight
+    //    DMAs are outstanding
+    wait_vmcnt<first>();
     u32x4 af[kGvQuads][4];
-    g3_read_act<S>(bufB, lane, af);
-    __builtin_amdgcn_s_waitcnt(0xc07f); // the fragments are in registers before bufB takes weights
+    g3_read_act<S>(abuf, lane, af);
+    // 3. row group by row group, as this wave's own DMAs land
+    floatx4 acc[C::P];
+#pragma unroll
+    for (int r = 0; r < C::P; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+    G4Decode<0, C::P, C::WInst, D>::run(wbuf, nrg, wave, lane, af, acc, issue);
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
 
+    // 4. cross-wave reduction in wave order; waves 0-3 sum even and waves
+    //    4-7 odd row groups
+    __syncthreads();
+    floatx4 *red = reinterpret_cast<floatx4 *>(gsm); // [wave][P][lane]
+#pragma unroll
+    for (int r = 0; r < C::P; ++r)
+        if (r < nrg) red[(wave * C::P + r) * 64 + lane] = acc[r];
+    __syncthreads();
+    float *const out = reinterpret_cast<float *>(outs[op]);
+    const int64_t ldo = ldos[op];
     int bad = 0;
-    for (int c = 0; cg0 < G1; ++c) {
-        uint8_t *cur = (c & 1) ? bufB : bufA;
-        uint8_t *nxt = (c & 1) ? bufA : bufB;
-        const int ng0 = cg0 + cng;
-        const bool more = ng0 < G1;
-        const int nop = more ? op_of(ng0) : 0;
-        const int nng = more ? chunk_len(ng0, nop) : 0;
-        if (more) issue_w(ng0, nng, nop, nxt);
-        floatx4 acc[kGvMaxRG];
+    const int e = tid & 255, c = e & 15, tok = e >> 4;
+    const int ln = 16 * (tok >> 2) + c, v = tok & 3;
+    for (int r = wave >> 2; r < nrg; r += 2) {
+        float sum = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kGvMaxRG; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
-        // the next chunk's DMAs (and earlier chunks' output stores, which
-        // only make the wait stricter) were issued after the current chunk's
-        if (more)
-            g3_decode<kG3WInst>(cur, cng, wave, lane, af, acc);
-        else
-            g3_decode<0>(cur, cng, wave, lane, af, acc);
-        __builtin_amdgcn_s_waitcnt(0xc07f); // this wave's reads of `cur` are done
-        floatx4 *mine = reinterpret_cast<floatx4 *>(cur);
-#pragma unroll
-        for (int r = 0; r < kGvMaxRG; ++r)
-            if (r < cng) mine[r * 64 + lane] = acc[r];
-        __syncthreads();
-        bad += g3_reduce_store(gsm + ((c & 1) ? kG3WLds : 0), kG3WaveLds, cng, tid, p.M, p.N[op],
-                               (cg0 - p.gstart[op]) * 16, p.out[op], p.ldo[op], p.rsc);
-        __syncthreads(); // every wave's partials read before `cur` takes a later chunk
-        cg0 = ng0;
-        op = nop;
-        cng = nng;
+        for (int w = 0; w < kGvWaves; ++w) sum += red[(w * C::P + r) * 64 + ln][v];
+        const int n = (R0 + r) * 16 + c;
+        if (tok < M && n < N) {
+            if (rsc) sum *= rsc[tok];
+            bad += !__builtin_isfinite(sum);
+            out[(size_t)tok * ldo + n] = sum;
+        }
     }
     count_nonfinite(p.nonfinite, bad);
 }
@@ -2730,11 +2871,11 @@ static hipError_t gemv_attrs() {
             reinterpret_cast<const void *>(&b1_gemv3_kernel<4, true>),
             reinterpret_cast<const void *>(&b1_gemv3_kernel<8, true>),
             reinterpret_cast<const void *>(&b1_gemv3_kernel<16, true>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<1>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<2>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<4>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<8>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<16>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<1, kG4WL2>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<2, kG4WL2>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<4, kG4WL2>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<8, kG4WL1>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<16, kG4WL1>),
         };
         attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kGvLds);
@@ -2845,19 +2986,36 @@ hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M,
     p.act = packed;
     p.rsc = rsc;
     p.nonfinite = nonfinite;
-    int nwg = num_cus > 0 ? num_cus : 256;
-    if (nwg > gs) nwg = gs;
-    const dim3 grid(nwg), block(kGvWaves * 64);
+    // work-groups per op: in proportion to its row groups over the CUs'
+    // slots (two per CU where a work-group takes half the LDS), at least
+    // ceil(groups / P) so that one pass holds them, at most its row groups
+    const int cus = num_cus > 0 ? num_cus : 256;
+    auto launch = [&](auto kern, int P, int per_cu, int lds) {
+        const int64_t slots = (int64_t)per_cu * cus;
+        int nwg = 0;
+        for (int o = 0; o < kGemvGroupMax; ++o) {
+            p.wgstart[o] = nwg;
+            if (o >= nops) continue;
+            const int g = p.gstart[o + 1] - p.gstart[o];
+            int64_t k = (int64_t)g * slots / gs;
+            if (k < (g + P - 1) / P) k = (g + P - 1) / P;
+            if (k > g) k = g;
+            if (k < 1) k = 1;
+            nwg += (int)k;
+        }
+        p.wgstart[kGemvGroupMax] = nwg;
+        hipLaunchKernelGGL(kern, dim3(nwg), dim3(kGvWaves * 64), lds, s, p);
+    };
     if (M <= 1)
-        hipLaunchKernelGGL((b1_gemv_group_kernel<1>), grid, block, kG3Lds, s, p);
+        launch(b1_gemv_group_kernel<1, kG4WL2>, G4Cfg<1, kG4WL2>::P, 2, G4Cfg<1, kG4WL2>::Lds);
     else if (M <= 2)
-        hipLaunchKernelGGL((b1_gemv_group_kernel<2>), grid, block, kG3Lds, s, p);
+        launch(b1_gemv_group_kernel<2, kG4WL2>, G4Cfg<2, kG4WL2>::P, 2, G4Cfg<2, kG4WL2>::Lds);
     else if (M <= 4)
-        hipLaunchKernelGGL((b1_gemv_group_kernel<4>), grid, block, kG3Lds, s, p);
+        launch(b1_gemv_group_kernel<4, kG4WL2>, G4Cfg<4, kG4WL2>::P, 2, G4Cfg<4, kG4WL2>::Lds);
     else if (M <= 8)
-        hipLaunchKernelGGL((b1_gemv_group_kernel<8>), grid, block, kG3Lds, s, p);
+        launch(b1_gemv_group_kernel<8, kG4WL1>, G4Cfg<8, kG4WL1>::P, 1, G4Cfg<8, kG4WL1>::Lds);
     else
-        hipLaunchKernelGGL((b1_gemv_group_kernel<16>), grid, block, kG3Lds, s, p);
+        launch(b1_gemv_group_kernel<16, kG4WL1>, G4Cfg<16, kG4WL1>::P, 1, G4Cfg<16, kG4WL1>::Lds);
     return hipGetLastError();
 }
 

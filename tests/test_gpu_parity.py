@@ -771,6 +771,8 @@ GROUP_CASES = [  # (m, k, output widths): consecutive small-M ops on one input
     (1, 3072, [18432, 18432, 9216, 6144]),            # a step's modulation projections
     (5, 1536, [1000, 48, 4096, 16, 777, 1024, 3000, 2048, 500]),  # 8 grouped + 1 alone
     (16, 256, [64, 96]),
+    (1, 3072, [18432] * 8),                           # more row groups than one pass of the CUs holds
+    (8, 3072, [18432, 18432, 9216, 6144]),            # 8 token slots: fewer row groups per work-group
 ]
 
 
