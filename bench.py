@@ -58,6 +58,47 @@ def time_launches(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall
 
 
+_BENCH_LIB = None
+
+
+def read_floor(torch, bufs, nbytes, steps, warmup):
+    """The HBM read floor of a small-M leg: a kernel that only reads
+    `nbytes` of each buffer (16 bytes a lane, four loads in flight, the
+    result folded into a word that is never stored; lib/libb1bench.so),
+    replayed as a HIP graph over the same rotated copies as the leg.  The
+    best of three grid shapes; per-launch time, as the leg reports it."""
+    global _BENCH_LIB
+    import ctypes
+    if _BENCH_LIB is None:
+        _BENCH_LIB = ctypes.CDLL(str(ROOT / "bonsai.cpp_amd" / "lib" / "libb1bench.so"))
+        _BENCH_LIB.b1bench_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_void_p]
+        _BENCH_LIB.b1bench_read.restype = ctypes.c_int
+    best = None
+    for nwg, block in ((1024, 512), (2048, 256), (512, 1024)):
+        sink = torch.zeros(nwg, dtype=torch.int32, device="cuda")
+
+        def call(c):
+            st = torch.cuda.current_stream().cuda_stream
+            rc = _BENCH_LIB.b1bench_read(ctypes.c_void_p(bufs[c].data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()),
+                                         nwg, block, ctypes.c_void_p(st))
+            assert rc == 0, rc
+        call(0)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for c in range(len(bufs)):
+                call(c)
+        reps = max(1, steps // len(bufs))
+        ms, _ = time_launches(torch, lambda i: graph.replay(), reps, max(1, warmup // len(bufs)))
+        ms /= len(bufs)
+        if best is None or ms < best[0]:
+            best = (ms, nwg, block)
+    ms, nwg, block = best
+    return {"us": ms * 1e3, "GBps": nbytes / (ms * 1e-3) / 1e9, "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "grid": [nwg, block], "bytes": nbytes}
+
+
 def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto", inputs=None):
     """The whole op from fp32 activations, bonsai_b1_linear_f32 with the
     library's workspace: the range-safe pack pass, then the GEMM (split
@@ -570,14 +611,15 @@ def bench_weights_load(torch, b1, blocks=38):
         shutil.rmtree(d, ignore_errors=True)
 
 
-def bench_gemv(torch, b1, synth, m, k, n, steps, warmup, packed_input=False):
+def bench_gemv(torch, b1, synth, m, k, n, steps, warmup, packed_input=False, floor=False):
     """Small-M kernel, weight copies rotated past the MALL.  The launches are
     captured once into a HIP graph (one launch per weight copy) and the graph
     is replayed, so the GPU runs the kernels back to back with no host in the
     loop; the per-launch time is the event time over the replays / launches.
     packed_input: the activations arrive in the packed fp16 layout (from a
     producer) and bonsai_b1_linear_packed_f16 runs the same kernel without
-    the conversion."""
+    the conversion.  floor: also the plain read of the same copies
+    (read_floor)."""
     nbytes = n * (k // 32) * 6
     copies = max(2, (2 * MALL_BYTES) // nbytes + 1)      # rotate > 2x the MALL
     ws = [synth.device_packed_weights(n, k, 100 + c) for c in range(copies)]
@@ -601,9 +643,12 @@ def bench_gemv(torch, b1, synth, m, k, n, steps, warmup, packed_input=False):
     ms /= copies
     eager_ms, _ = time_launches(torch, lambda i: call(i % copies), steps, warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"shape": [m, k, n], "ms": ms, "us": ms * 1e3, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
-            "packed_bytes": nbytes, "weight_copies": copies, "launches": reps * copies,
-            "eager_us": eager_ms * 1e3, "wall_s": wall}
+    res = {"shape": [m, k, n], "ms": ms, "us": ms * 1e3, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
+           "packed_bytes": nbytes, "weight_copies": copies, "launches": reps * copies,
+           "eager_us": eager_ms * 1e3, "wall_s": wall}
+    if floor:
+        res["read_floor"] = read_floor(torch, ws, nbytes, steps, warmup)
+    return res
 
 
 MOD_GROUP = (1, 3072, [18432, 18432, 9216, 6144])   # a step's modulation projections over vec_silu
@@ -645,10 +690,14 @@ def bench_gemv_group(torch, b1, synth, m, k, ns, steps, warmup):
     grouped(copies - 1)
     torch.cuda.synchronize()
     same = all(torch.equal(o, r) for o, r in zip(outs, ref))
+    del wsets, views, ops
+    flat = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    floor = read_floor(torch, flat, nbytes, steps, warmup)
+    del flat
     return {"shape": [m, k, ns], "grouped_us": res["grouped"] * 1e3, "separate_us": res["separate"] * 1e3,
             "grouped_GBps": nbytes / (res["grouped"] * 1e-3) / 1e9,
             "separate_GBps": nbytes / (res["separate"] * 1e-3) / 1e9, "packed_bytes": nbytes,
-            "weight_sets": copies, "grouped_equals_separate": same}
+            "weight_sets": copies, "grouped_equals_separate": same, "read_floor": floor}
 
 
 def bench_dense_reference(torch, m, k, n, steps=1000, warmup=3000):
@@ -819,7 +868,7 @@ def main():
         return
     if args.only == "gemv":
         gm, gk, gn = GEMV
-        v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400))
+        v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400), floor=True)
         vp = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400),
                         packed_input=True)
         v1 = bench_gemv(torch, b1, synth, 1, gk, gn, max(args.steps, 200), min(args.warmup, 400))
@@ -852,9 +901,10 @@ def main():
 
     gm, gk, gn = GEMV
     log(f"[bench] GEMV M={gm} K={gk} N={gn}")
-    v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400))
+    v = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400), floor=True)
     log(f"[bench] GEMV {v['us']:.2f} us/launch (graph)  {v['gbs']:.0f} GB/s packed  "
-        f"{100*v['frac']:.1f}% of HBM peak; eager {v['eager_us']:.2f} us/call")
+        f"{100*v['frac']:.1f}% of HBM peak; eager {v['eager_us']:.2f} us/call; a plain read of the same "
+        f"bytes {v['read_floor']['us']:.2f} us/launch ({100 * v['read_floor']['frac_hbm']:.1f}% of HBM peak)")
     v1 = bench_gemv(torch, b1, synth, 1, gk, gn, max(args.steps, 200), min(args.warmup, 400))
     log(f"[bench] GEMV M=1 {v1['us']:.2f} us/call  {v1['gbs']:.0f} GB/s packed")
     vp = bench_gemv(torch, b1, synth, gm, gk, gn, max(args.steps, 200), min(args.warmup, 400), packed_input=True)
@@ -863,7 +913,8 @@ def main():
     vg = bench_gemv_group(torch, b1, synth, *MOD_GROUP, max(args.steps, 200), min(args.warmup, 400))
     log(f"[bench] modulation projections M={MOD_GROUP[0]} K={MOD_GROUP[1]} N={MOD_GROUP[2]}: one batch call "
         f"{vg['grouped_us']:.2f} us ({vg['grouped_GBps']:.0f} GB/s), separate calls {vg['separate_us']:.2f} us "
-        f"({vg['separate_GBps']:.0f} GB/s); equal {vg['grouped_equals_separate']}")
+        f"({vg['separate_GBps']:.0f} GB/s); equal {vg['grouped_equals_separate']}; a plain read of the same "
+        f"bytes {vg['read_floor']['us']:.2f} us/launch")
 
     configs = {}
     if not args.no_configs:
@@ -959,12 +1010,20 @@ def main():
                  "M1_us_per_call": round(v1["us"], 3), "M1_GBps_packed": round(v1["gbs"], 1),
                  "packed_input_us_per_call": round(vp["us"], 3), "packed_input_GBps": round(vp["gbs"], 1),
                  "packed_input_frac_hbm": round(vp["frac"], 4),
+                 "read_floor": {"us_per_call": round(v["read_floor"]["us"], 3),
+                                "GBps": round(v["read_floor"]["GBps"], 1),
+                                "frac_hbm": round(v["read_floor"]["frac_hbm"], 4),
+                                "grid": v["read_floor"]["grid"],
+                                "note": "a kernel that only reads the same packed bytes, same graph replay over the "
+                                        "same copies: what one launch of this size can reach on this GPU"},
                  "modulation_group": {"M": MOD_GROUP[0], "K": MOD_GROUP[1], "N": MOD_GROUP[2],
                                       "batch_call_us": round(vg["grouped_us"], 3),
                                       "batch_call_GBps": round(vg["grouped_GBps"], 1),
                                       "separate_calls_us": round(vg["separate_us"], 3),
                                       "separate_calls_GBps": round(vg["separate_GBps"], 1),
-                                      "equal": vg["grouped_equals_separate"]}},
+                                      "equal": vg["grouped_equals_separate"],
+                                      "read_floor_us": round(vg["read_floor"]["us"], 3),
+                                      "read_floor_GBps": round(vg["read_floor"]["GBps"], 1)}},
         "cpu_baseline": cpu,
     }
     if configs:
