@@ -1151,11 +1151,13 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
         // the expanded weights of a step: block b = step / 2 has its scale
         // and sign word at 6 (b % 2) bytes into its 12-byte pair; lane group
         // g takes dwords 8h + 4g .. +3 of the block (elements d, d + 16)
-        uint32_t s2[C::NTL], wg[C::NTL];
+        uint32_t s2[C::NTL];
         u32x4 bw[2][C::NTL];
 #if B1_GEMM_SHL64
         // step h = 1's shifted sign words, from step h = 0's 64-bit shifts
         u32x4 pend[C::NTL];
+#else
+        uint32_t wg_[C::NTL];
 #endif
         auto expand = [&](int step, u32x4 (&bo)[C::NTL]) {
             const int b = step >> 1, h = step & 1;
@@ -1187,6 +1189,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                     for (int j = 0; j < 4; ++j) bo[nt][j] = xnor_sel(kSignPair, pend[nt][j], s2[nt]);
                 }
 #else
+                uint32_t(&wg)[C::NTL] = wg_;
                 if (h == 0) {
                     const uint32_t *dd = d[nt][b >> 1];
                     if ((b & 1) == 0) {
@@ -2002,7 +2005,7 @@ constexpr int kG3ALds = kGvBPW * 1024;                         // 12 KB of fragm
 constexpr int kG3WaveLds = kG3WLds + kG3ALds;
 constexpr int kG3Lds = kGvWaves * kG3WaveLds;                  // 160 KB
 static_assert(kG3Lds <= 160 * 1024, "gfx950 LDS");
-static_assert(kGvWaves * kGvMaxRG * 64 * 16 <= kG3Lds, "the reduction fits");
+static_assert(kGvWaves * kGvMaxRG * 64 * 16 + kGvWaves * 4 <= kG3Lds, "the reduction and its flags fit");
 static_assert(kG3RowB >= 72 + 8, "a slice plus its alignment slack");
 
 // Row group R of the chunk being decoded has landed: all DMAs covering its
@@ -2285,49 +2288,55 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
         __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): LDS reads done before the next pass's DMAs
     }
 
-    // cross-wave reduction in a fixed order
+    // cross-wave reduction in a fixed order; the fp32 kernel's flags of
+    // tokens with an activation beyond the fp16 range (a word per wave) go
+    // with the partials, after them
     __syncthreads();
     floatx4 *red = reinterpret_cast<floatx4 *>(gsm); // [wave][rg][lane]
 #pragma unroll
     for (int r = 0; r < kGvMaxRG; ++r)
         if (r < nrg) red[(wave * kGvMaxRG + r) * 64 + lane] = acc[r];
+    uint32_t *flags = reinterpret_cast<uint32_t *>(gsm + kGvWaves * kGvMaxRG * 64 * 16);
+    if constexpr (!PACKED) {
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(ovf != 0);
+        const uint32_t toks = (uint32_t)((bal | (bal >> 16) | (bal >> 32) | (bal >> 48)) & 0xFFFFu);
+        if (lane == 0) flags[wave] = toks;
+    }
     __syncthreads();
     int bad = g3_reduce_store(gsm, kGvMaxRG * 64 * 16, nrg, tid, p.M, p.N, rg0 * 16, p.out, p.ldo,
                               PACKED ? p.rsc : nullptr);
     if constexpr (!PACKED) {
-        // tokens with an activation beyond the fp16 range: a flag word per
-        // wave, their OR, then this work-group's rows of those tokens again
-        const uint64_t bal = __builtin_amdgcn_ballot_w64(ovf != 0);
-        const uint32_t toks = (uint32_t)((bal | (bal >> 16) | (bal >> 32) | (bal >> 48)) & 0xFFFFu);
-        __syncthreads();
-        uint32_t *flags = reinterpret_cast<uint32_t *>(gsm);
-        if (lane == 0) flags[wave] = toks;
-        __syncthreads();
+        // this work-group's rows of the flagged tokens again, after every
+        // thread's stores above (a barrier only on this rare path; `all` is
+        // the same in every thread)
         uint32_t all = 0;
 #pragma unroll
         for (int w = 0; w < kGvWaves; ++w) all |= flags[w];
         if (all) {
+            __syncthreads();
+            {
 #pragma clang fp contract(off)
-            for (int e = tid; e < 16 * nrg * 16; e += kGvWaves * 64) {
-                const int tok = e / (nrg * 16), rr = e - tok * (nrg * 16);
-                const int n = rg0 * 16 + rr;
-                if (tok >= p.M || n >= p.N || !((all >> tok) & 1u)) continue;
-                const float *xr = p.act + (size_t)tok * p.lda;
-                const uint16_t *wr = reinterpret_cast<const uint16_t *>(p.w + (size_t)n * rs);
-                float sum = 0.0f;
-                for (int b = 0; b < nb; ++b) {
-                    const float scale = (float)__builtin_bit_cast(_Float16, wr[3 * b]);
-                    const uint32_t bits = (uint32_t)wr[3 * b + 1] | ((uint32_t)wr[3 * b + 2] << 16);
-                    float bs = 0.0f;
-                    for (int i = 0; i < 32; ++i) {
-                        const float a = xr[32 * b + i];
-                        bs = ((bits >> i) & 1u) ? bs + a : bs - a;
+                for (int e = tid; e < 16 * nrg * 16; e += kGvWaves * 64) {
+                    const int tok = e / (nrg * 16), rr = e - tok * (nrg * 16);
+                    const int n = rg0 * 16 + rr;
+                    if (tok >= p.M || n >= p.N || !((all >> tok) & 1u)) continue;
+                    const float *xr = p.act + (size_t)tok * p.lda;
+                    const uint16_t *wr = reinterpret_cast<const uint16_t *>(p.w + (size_t)n * rs);
+                    float sum = 0.0f;
+                    for (int b = 0; b < nb; ++b) {
+                        const float scale = (float)__builtin_bit_cast(_Float16, wr[3 * b]);
+                        const uint32_t bits = (uint32_t)wr[3 * b + 1] | ((uint32_t)wr[3 * b + 2] << 16);
+                        float bs = 0.0f;
+                        for (int i = 0; i < 32; ++i) {
+                            const float a = xr[32 * b + i];
+                            bs = ((bits >> i) & 1u) ? bs + a : bs - a;
+                        }
+                        sum = sum + scale * bs;
                     }
-                    sum = sum + scale * bs;
+                    float *o = p.out + (size_t)tok * p.ldo + n;
+                    bad += !__builtin_isfinite(sum) - !__builtin_isfinite(*o);
+                    *o = sum;
                 }
-                float *o = p.out + (size_t)tok * p.ldo + n;
-                bad += !__builtin_isfinite(sum) - !__builtin_isfinite(*o);
-                *o = sum;
             }
         }
     }
