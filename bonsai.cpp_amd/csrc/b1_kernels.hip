@@ -187,16 +187,6 @@ __device__ __forceinline__ void wpair_quads(uint32_t w, uint32_t w8, uint32_t sc
     hi[3] = xnor_sel(kSignPair, (uint32_t)(v3 >> 32), scale2);
 }
 
-// The GEMM's weight expansion with one 64-bit shift per two weight dwords
-// (a block's second step's shifted sign words kept from its first step):
-// 18 -> 15 VALU per block and 32-column group; bit-identical, 0.2-0.3 %
-// faster at M=4096 K=3072 N=12288 in an alternating A/B (285.8 -> 285.4 and
-// 285.0 -> 284.1 us, one box).  The MFMA pipe, not the expansion, bounds the
-// main loop.
-#ifndef B1_GEMM_SHL64
-#define B1_GEMM_SHL64 1
-#endif
-
 __device__ __forceinline__ void count_nonfinite(int32_t *ctr, int bad) {
     if (bad && ctr) atomicAdd(ctr, bad);
 }
@@ -1151,45 +1141,12 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
         // the expanded weights of a step: block b = step / 2 has its scale
         // and sign word at 6 (b % 2) bytes into its 12-byte pair; lane group
         // g takes dwords 8h + 4g .. +3 of the block (elements d, d + 16)
-        uint32_t s2[C::NTL];
+        uint32_t s2[C::NTL], wg[C::NTL];
         u32x4 bw[2][C::NTL];
-#if B1_GEMM_SHL64
-        // step h = 1's shifted sign words, from step h = 0's 64-bit shifts
-        u32x4 pend[C::NTL];
-#else
-        uint32_t wg_[C::NTL];
-#endif
         auto expand = [&](int step, u32x4 (&bo)[C::NTL]) {
             const int b = step >> 1, h = step & 1;
 #pragma unroll
             for (int nt = 0; nt < C::NTL; ++nt) {
-#if B1_GEMM_SHL64
-                if (h == 0) {
-                    const uint32_t *dd = d[nt][b >> 1];
-                    uint32_t w0, w8;
-                    if ((b & 1) == 0) {
-                        s2[nt] = dup_lo16(dd[0]);
-                        w0 = __builtin_amdgcn_alignbit(dd[1], dd[0], 16 + 4 * g);
-                        w8 = __builtin_amdgcn_alignbit(dd[1], dd[0], 24 + 4 * g);
-                    } else {
-                        s2[nt] = dup_hi16(dd[1]);
-                        w0 = dd[2] >> (4 * g);
-                        w8 = dd[2] >> (4 * g + 8);
-                    }
-                    const uint64_t v = (uint64_t)w8 << 32 | w0;
-                    const uint64_t v0 = shl64<15>(v), v1 = shl64<14>(v), v2 = shl64<13>(v), v3 = shl64<12>(v);
-                    bo[nt][0] = xnor_sel(kSignPair, (uint32_t)v0, s2[nt]);
-                    bo[nt][1] = xnor_sel(kSignPair, (uint32_t)v1, s2[nt]);
-                    bo[nt][2] = xnor_sel(kSignPair, (uint32_t)v2, s2[nt]);
-                    bo[nt][3] = xnor_sel(kSignPair, (uint32_t)v3, s2[nt]);
-                    pend[nt] = u32x4{(uint32_t)(v0 >> 32), (uint32_t)(v1 >> 32), (uint32_t)(v2 >> 32),
-                                     (uint32_t)(v3 >> 32)};
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) bo[nt][j] = xnor_sel(kSignPair, pend[nt][j], s2[nt]);
-                }
-#else
-                uint32_t(&wg)[C::NTL] = wg_;
                 if (h == 0) {
                     const uint32_t *dd = d[nt][b >> 1];
                     if ((b & 1) == 0) {
@@ -1206,7 +1163,6 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) bo[nt][j] = wpair(wg[nt], 15 - 8 * h - j, s2[nt]);
-#endif
             }
         };
         expand(0, bw[0]);
