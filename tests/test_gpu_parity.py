@@ -806,6 +806,36 @@ def test_linear_batch_groups_small_m_ops(torch, b1, oracle, m, k, ns):
         assert_fast_close(outs[i].cpu().numpy(), oracle.linear_f64(xh, raw, ns[i]), f"group op {i} vs fp64")
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_linear_batch_groups_random(torch, b1, oracle, seed):
+    """Seeded random groupings of small-M ops (1-8 ops, output widths 1 to
+    5000 rows, M 1-16, K a multiple of 256 up to 3072): each op's output bit
+    for bit its own small-M call, the padding after each output row
+    untouched, the last op within the FAST bar of the float64 oracle.  Op
+    widths that are not multiples of 16 put partial row groups at every op
+    boundary, and the op count and widths vary the work-groups per op."""
+    from bonsai_b1 import synth
+    rng = np.random.default_rng(1000 + seed)
+    m = int(rng.integers(1, 17))
+    k = 256 * int(rng.integers(1, 13))
+    nops = int(rng.integers(1, 9))
+    ns = [int(rng.choice([rng.integers(1, 64), rng.integers(64, 5001)])) for _ in range(nops)]
+    say(f"random group seed={seed} m={m} k={k} ns={ns}")
+    x = synth.device_activations(m, k, 700 + seed)
+    ws = [synth.device_packed_weights(n, k, 710 + 10 * seed + i) for i, n in enumerate(ns)]
+    outs = [torch.full((m, n + 3), 5.0, device="cuda")[:, :n] for n in ns]
+    b1.linear_batch([(x, b1.device_weights(w, k, n), o) for w, n, o in zip(ws, ns, outs)])
+    torch.cuda.synchronize()
+    for i, (w, n, o) in enumerate(zip(ws, ns, outs)):
+        ref = b1.linear(x, w, n)
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref), f"op {i} (n={n})"
+        pad = o.as_strided((m, 3), (o.stride(0), 1), o.storage_offset() + n)
+        assert bool((pad == 5.0).all()), f"op {i} pad"
+    assert_fast_close(outs[-1].cpu().numpy(), oracle.linear_f64(x.cpu().numpy(), ws[-1].cpu().numpy(), ns[-1]),
+                      f"random group last op vs fp64 (seed {seed})")
+
+
 def test_linear_batch_group_order_and_range(torch, b1):
     """Small-M ops whose outputs overlap one another or the shared input are
     not grouped (the batch keeps their order); a row beyond the fp16 range
