@@ -2313,22 +2313,21 @@ struct GemvGroup {
     const uint8_t *w[kGemvGroupMax];
     float *out[kGemvGroupMax];
     int64_t ldo[kGemvGroupMax];
-    int N[kGemvGroupMax];
-    int gstart[kGemvGroupMax + 1]; // first global row group of each op; gstart[nops..] = total
+    int N[kGemvGroupMax];           // 0 for the entries past the ops
     int wgstart[kGemvGroupMax + 1]; // first work-group of each op; wgstart[nops..] = the grid
-    int nops, groups, K, M;
-    const void *act;             // packed fp16 [M][K]
-    const float *rsc;            // row scales of the packing, or nullptr
+    int K, M;
+    const void *act;  // packed fp16 [M][K]
+    const float *rsc; // row scales of the packing, or nullptr
     int32_t *nonfinite;
 };
 
 // The first 8 entries of a kernel-argument array held in SGPRs: each is
 // read once with a constant index and passed through an empty asm, so that
-// a[i] for a wave-uniform i stays a chain of scalar selects.  (Without the
-// asm the compiler folds the selects back into an indexed read of argument
-// memory, a dependent scalar load of about 1 us before each weight DMA of
-// the grouped kernel; with an array member instead of named ones it moves
-// the entries to scratch.)
+// a[i] for a wave-uniform i stays a chain of scalar selects and every
+// argument arrives in the kernel's first round of scalar loads.  (Without
+// the asm the compiler folds the selects back into an indexed read of
+// argument memory, a dependent scalar load of about 1 us; with an array
+// member instead of named ones it moves the entries to scratch.)
 template <class T>
 __device__ __forceinline__ T sgpr_opaque(T x) {
     asm volatile("" : "+s"(x));
@@ -2348,10 +2347,10 @@ struct Sgpr8 {
     }
 };
 
-#ifndef B1_G4_AHEAD
-#define B1_G4_AHEAD 4
-#endif
-constexpr int kG4Ahead = B1_G4_AHEAD; // row groups in flight behind the one being decoded
+// Row groups whose DMAs are in flight behind the one being decoded (2, 3, 4
+// and 6 measured alike: 22.7-23.4 us for the modulation projections in an
+// earlier one-work-group-per-CU form).
+constexpr int kG4Ahead = 4;
 
 // Row groups of a one-pass work-group by token slots S and per-wave LDS
 // bytes WL: the activation slice (ABytes) and the weight slices of P row
@@ -2383,9 +2382,8 @@ constexpr int g4_dmas(int r) { return (16 * kG3RowCh * (r + 1) + 63) / 64; }
 
 // Row groups R.. of the pass: issue the DMAs of row group R + D (keeping
 // D row groups in flight behind the one being decoded), wait for row group
-// R's (the DMAs issued after them: I - J; an extra DMA issued for a
-// straddling one only makes the wait stricter), decode it, go on while
-// R + 1 < nrg.
+// R's (DMAs retire in issue order: at most the hi - g4_dmas(R) issued after
+// them may be outstanding), decode it, go on while R + 1 < nrg.
 template <int R, int P, int WI, int D>
 struct G4Decode {
     template <class Issue>
@@ -2973,20 +2971,17 @@ hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M,
     const hipError_t attr_err = gemv_attrs();
     if (attr_err != hipSuccess) return attr_err;
     GemvGroup p{};
-    int gs = 0;
+    int groups[kGemvGroupMax] = {};
+    int gs = 0; // row groups of all the ops
     for (int o = 0; o < kGemvGroupMax; ++o) {
-        p.gstart[o] = gs;
         const GemvGroupOp &op = ops[o < nops ? o : 0];
         p.w[o] = op.w;
         p.out[o] = op.out;
         p.ldo[o] = o < nops ? op.ldo : 0;
         p.N[o] = o < nops ? op.N : 0;
-        if (o < nops) gs += (op.N + 15) / 16;
+        groups[o] = o < nops ? (op.N + 15) / 16 : 0;
+        gs += groups[o];
     }
-    // ops past nops start at the end: no row group maps to them
-    for (int o = nops; o <= kGemvGroupMax; ++o) p.gstart[o] = gs;
-    p.nops = nops;
-    p.groups = gs;
     p.K = K;
     p.M = M;
     p.act = packed;
@@ -3002,7 +2997,7 @@ hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M,
         for (int o = 0; o < kGemvGroupMax; ++o) {
             p.wgstart[o] = nwg;
             if (o >= nops) continue;
-            const int g = p.gstart[o + 1] - p.gstart[o];
+            const int g = groups[o];
             int64_t k = (int64_t)g * slots / gs;
             if (k < (g + P - 1) / P) k = (g + P - 1) / P;
             if (k > g) k = g;
