@@ -2347,10 +2347,11 @@ struct Sgpr8 {
     }
 };
 
-// Row groups whose DMAs are in flight behind the one being decoded (2, 3, 4
-// and 6 measured alike: 22.7-23.4 us for the modulation projections in an
-// earlier one-work-group-per-CU form).
-constexpr int kG4Ahead = 4;
+// Row groups whose DMAs are in flight behind the one being decoded.  With
+// two work-groups per CU (16 waves), 2 measured best for the modulation
+// projections: 13.9 us per launch against 14.2-14.5 us with 1 and 14.4-14.6
+// us with 4 (a timing copy, two alternating passes).
+constexpr int kG4Ahead = 2;
 
 // Row groups of a one-pass work-group by token slots S and per-wave LDS
 // bytes WL: the activation slice (ABytes) and the weight slices of P row
