@@ -864,19 +864,26 @@ static int fuse_span(int n_ops, int mode, int num_cus, OpAt at, int i, int *n_su
     return last;
 }
 
-// The ops from i on that run as one grouped small-M launch with op i over
-// one range-safe packing of their input: consecutive plain small-M ops on
-// the same input (the modulation projections of src/diffuser_graph.cpp:308-311,
-// 470-471 and 548 all read vec_silu at one token), at most kGemvGroupMax,
-// whose outputs lie apart from that input and from one another (the group
-// writes them in no particular order).  Returns the last op of the run, i
-// when op i runs alone; fills ops[0 .. last - i].
+// A grouped small-M run of at most kGemvGroupF32MaxM tokens reads their fp32
+// rows itself (no packing, outputs equal to the single calls bit for bit,
+// out-of-range tokens included); a larger one reads a range-safe packing.
+static bool gemv_group_direct(const b1::LinearArgs &a) {
+    return a.M <= b1::kGemvGroupF32MaxM && b1::gemv_group_f32_ok(a.act, a.lda, a.M, a.K);
+}
+
+// The ops from i on that run as one grouped small-M launch with op i:
+// consecutive plain small-M ops on the same input (the modulation
+// projections of src/diffuser_graph.cpp:308-311, 470-471 and 548 all read
+// vec_silu at one token), at most kGemvGroupMax, whose outputs lie apart
+// from that input and from one another (the group writes them in no
+// particular order).  Returns the last op of the run, i when op i runs
+// alone; fills ops[0 .. last - i].
 template <class OpAt>
 static int gemv_span(int n_ops, int mode, OpAt at, int i, b1::GemvGroupOp *ops) {
     const BatchOp bi = at(i);
     const b1::LinearArgs a = batch_args(*bi.op);
     if (epi_kind(bi.epi) != BONSAI_B1_EPI_NONE || batch_path(a, mode) != BatchPath::Gemv ||
-        !b1::pack_supported(a.act, a.lda, a.M, a.K))
+        !(gemv_group_direct(a) || b1::pack_supported(a.act, a.lda, a.M, a.K)))
         return i;
     auto range = [](const void *p, int rows, int64_t ld, int cols, size_t elt, uintptr_t *r0, uintptr_t *r1) {
         *r0 = reinterpret_cast<uintptr_t>(p);
@@ -908,7 +915,7 @@ static int gemv_span(int n_ops, int mode, OpAt at, int i, b1::GemvGroupOp *ops) 
 
 // Workspace areas of a batch, laid out [pack][split][y], each 256-byte
 // aligned: the largest range-safe packing among its packed GEMMs and
-// grouped small-M runs, the largest split-K partial area among its plain packed GEMMs
+// grouped small-M runs of more than kGemvGroupF32MaxM tokens, the largest split-K partial area among its plain packed GEMMs
 // (fused runs included), and the largest fp32 linear output among its ops
 // whose epilogue runs as a separate pass (the other paths).
 struct BatchAreas {
@@ -930,7 +937,7 @@ static BatchAreas batch_areas(int n_ops, int mode, int num_cus, OpAt at) {
             b1::GemvGroupOp ops[b1::kGemvGroupMax];
             const int last = gemv_span(n_ops, mode, at, i, ops);
             if (last > i) {
-                r.pack = std::max(r.pack, b1::pack_area_bytes(a.M, a.K));
+                if (!gemv_group_direct(a)) r.pack = std::max(r.pack, b1::pack_area_bytes(a.M, a.K));
                 i = last;
                 continue;
             }
@@ -1041,11 +1048,12 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
         const BatchPath path = batch_path(a, mode);
         b1::GemvGroupOp gops[b1::kGemvGroupMax];
         const int glast = path == BatchPath::Gemv ? gemv_span(n_ops, mode, at, i, gops) : i;
+        const bool direct = glast > i && gemv_group_direct(a);
         hipError_t e = hipSuccess;
         // the range-safe packing of this op's input, unless the workspace
         // holds it already
         const float *rsc = nullptr;
-        if (path == BatchPath::Packed || glast > i) {
+        if (path == BatchPath::Packed || (glast > i && !direct)) {
             if (!(packed_act == a.act && packed_lda == a.lda && packed_m == a.M && packed_k == a.K)) {
                 e = b1::launch_pack_rows(a.act, a.lda, a.M, a.K, workspace, stream);
                 packed_act = a.act;
@@ -1056,8 +1064,11 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
             rsc = b1::pack_area_rsc(workspace, a.M, a.K);
         }
         if (glast > i) {
-            // the run's outputs lie apart from the packed input (gemv_span)
-            if (e == hipSuccess)
+            // the run's outputs lie apart from its input (gemv_span)
+            if (direct)
+                e = b1::launch_gemv_group_f32(a.act, a.lda, a.K, a.M, gops, glast - i + 1, nonfinite, dev->num_cus,
+                                              stream);
+            else if (e == hipSuccess)
                 e = b1::launch_gemv_group(workspace, rsc, a.K, a.M, gops, glast - i + 1, nonfinite, dev->num_cus,
                                           stream);
             i = glast;

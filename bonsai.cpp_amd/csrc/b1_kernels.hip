@@ -2299,16 +2299,18 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
     count_nonfinite(p.nonfinite, bad);
 }
 
-// Several small-M linears over one packed activation matrix in one launch
-// (the modulation projections of a step, q/k/v of the text stream at a few
-// tokens).  Each op has its own work-groups (wgstart), each taking at most
-// G4Cfg<S, WL>::P consecutive row groups of that op in one pass: every wave
-// DMAs its activation slice and then its K slice of those rows into its own
-// LDS area, keeping kG4Ahead row groups in flight behind the one it
-// decodes, with no work-group barrier until the end, where the waves'
-// partial tiles are summed once, in wave order.  The per-wave K slices,
-// MFMA order and reduction order are those of b1_gemv3_kernel, so each op's
-// outputs equal its own small-M call bit for bit.
+// Several small-M linears over one activation matrix in one launch (the
+// modulation projections of a step, q/k/v of the text stream at a few
+// tokens): packed fp16, or at most 2 tokens of fp32 rows (F32: converted by
+// each wave as it stages them, tokens beyond the fp16 range recomputed in
+// EXACT arithmetic).  Each op has its own work-groups (wgstart), each
+// taking at most G4Cfg::P consecutive row groups of that op in one pass:
+// every wave stages its activation slice and then DMAs its K slice of those
+// rows into its own LDS area, keeping kG4Ahead row groups in flight behind
+// the one it decodes, with no work-group barrier until the end, where the
+// waves' partial tiles are summed once, in wave order.  The per-wave K
+// slices, MFMA order and reduction order are those of b1_gemv3_kernel, so
+// each op's outputs equal its own small-M call bit for bit.
 struct GemvGroup {
     const uint8_t *w[kGemvGroupMax];
     float *out[kGemvGroupMax];
@@ -2316,7 +2318,8 @@ struct GemvGroup {
     int N[kGemvGroupMax];           // 0 for the entries past the ops
     int wgstart[kGemvGroupMax + 1]; // first work-group of each op; wgstart[nops..] = the grid
     int K, M;
-    const void *act;  // packed fp16 [M][K]
+    const void *act;  // packed fp16 [M][K], or fp32 [M][lda] (the F32 kernels)
+    int64_t lda;      // fp32 row stride (elements)
     const float *rsc; // row scales of the packing, or nullptr
     int32_t *nonfinite;
 };
@@ -2364,7 +2367,7 @@ constexpr int g4_rows(int abytes, int wl) {
     while (abytes + ((16 * kG3RowCh * (p + 1) + 63) / 64) * 1024 <= wl) ++p;
     return p;
 }
-template <int S, int WL>
+template <int S, int WL, bool F32 = false>
 struct G4Cfg {
     static constexpr int ABytes = g4_abytes(S);
     static constexpr int P = g4_rows(ABytes, WL);
@@ -2373,6 +2376,7 @@ struct G4Cfg {
     static_assert(P >= 1 && ABytes % 16 == 0 && ABytes + WInst * 1024 <= WL, "a wave's LDS area");
     static_assert(P * 1024 <= WL, "the reduction fits");
     static_assert(WInst + 2 * kGemvGroupMax < 64, "vmcnt range");
+    static_assert(P * 1024 * kGvWaves + kGvWaves * 4 <= kGvWaves * WL, "the reduction and its flags fit");
 };
 constexpr int kG4WL2 = 10 * 1024; // two work-groups per CU
 constexpr int kG4WL1 = kG3WaveLds; // one
@@ -2408,9 +2412,62 @@ struct G4Decode<P, P, WI, D> {
                                                floatx4 (&)[P], Issue &) {}
 };
 
-template <int S, int WL>
-__global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 2 : 1) void b1_gemv_group_kernel(GemvGroup p) {
-    using C = G4Cfg<S, WL>;
+// fp32 activations of the grouped kernel, S <= 2 token slots, through
+// registers into the packed layout g3_read_act<S> reads: token t at abuf +
+// kG3ARow t, block b's 16 dwords at 64 b, dword d the fp16 pair (element d,
+// element d + 16), rounded as the single call rounds.  Job j = (t, b, q) of
+// the S * 48 loads elements 32 b + 4 q .. + 3 and 16 later of token t's
+// slice (the wave's 12 blocks from block wb0) and stores them packed at
+// kG3ARow t + 64 b + 16 q.  Blocks past K and tokens past M read zeros.
+// (Staging the fp32 slice in LDS instead takes a second KB of the wave's
+// area, a row group fewer per work-group and, for a step's modulation
+// projections, more work-groups than two a CU hold.)
+template <int S>
+struct G4ActF32 {
+    static_assert(S <= 2, "at most 2 token slots");
+    static constexpr int J = S * 48, R = (J + 63) / 64;
+    floatx4 x[R][2];
+    // frs: the rows, (M - 1) lda + K floats; rowb = lda * 4
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t frs, int lane, int wb0, int nb, int M,
+                                         uint32_t rowb) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int j = r * 64 + lane, t = j / 48, bq = j - 48 * t, b = bq >> 2;
+            const uint32_t off = (uint32_t)t * rowb + (uint32_t)(wb0 + b) * 128u + (uint32_t)(bq & 3) * 16u;
+            const bool ok = j < J && t < M && wb0 + b < nb;
+            x[r][0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(frs, ok ? off : 0xFFFFFFF0u, 0, 0));
+            x[r][1] = __builtin_bit_cast(floatx4,
+                                         __builtin_amdgcn_raw_buffer_load_b128(frs, ok ? off + 64u : 0xFFFFFFF0u, 0, 0));
+        }
+    }
+    // Returns the tokens (bit t) this lane found an element beyond the fp16
+    // range in.
+    __device__ __forceinline__ uint32_t store(uint8_t *abuf, int lane) const {
+        uint32_t ovf = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int j = r * 64 + lane, t = j / 48, bq = j - 48 * t;
+            if (j < J) {
+                u32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ovf |= (uint32_t)((__builtin_fabsf(x[r][0][e]) >= 65520.0f) |
+                                      (__builtin_fabsf(x[r][1][e]) >= 65520.0f))
+                           << t;
+                    v[e] = pack_f16(x[r][0][e], x[r][1][e]);
+                }
+                *reinterpret_cast<u32x4 *>(abuf + t * kG3ARow + 64 * (bq >> 2) + 16 * (bq & 3)) = v;
+            }
+        }
+        return ovf;
+    }
+};
+
+// (__launch_bounds__' second argument is the minimum of waves per SIMD: two
+// work-groups of 8 waves on a CU need 4, so at most 128 registers a wave.)
+template <int S, int WL, bool F32>
+__global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_group_kernel(GemvGroup p) {
+    using C = G4Cfg<S, WL, F32>;
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = sgpr_opaque(p.K), M = sgpr_opaque(p.M);
@@ -2441,9 +2498,17 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 2 : 1) void b1_gemv_g
     wg_row_groups((N + 15) / 16, wg1 - wg0, bid - wg0, R0, R1);
     const int nrg = R1 - R0; // at most C::P (the launcher's grid)
     // 1. the activation slice, then the weight slices, D row groups ahead
-    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void *>(act), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), kBufferFlags);
-    g3_issue_act<S>(ars, abuf, lane, wave * kGvBPW, nb, M, K);
+    G4ActF32<F32 ? S : 1> xf; // fp32: this lane's activation chunks
+    if constexpr (F32) {
+        const uint32_t rowb = (uint32_t)sgpr_opaque(p.lda) * 4u;
+        const __amdgpu_buffer_rsrc_t frs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<void *>(act), (short)0, (int)((uint32_t)(M - 1) * rowb + (uint32_t)K * 4u), kBufferFlags);
+        xf.load(frs, lane, wave * kGvBPW, nb, M, rowb);
+    } else {
+        const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<void *>(act), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), kBufferFlags);
+        g3_issue_act<S>(ars, abuf, lane, wave * kGvBPW, nb, M, K);
+    }
     const __amdgpu_buffer_rsrc_t wrs =
         __builtin_amdgcn_make_buffer_rsrc(wp, (short)0, (int)((uint32_t)N * rs), kBufferFlags);
     auto issue = [&](int i) {
@@ -2459,9 +2524,12 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 2 : 1) void b1_gemv_g
 #pragma unroll
     for (int i = 0; i < first; ++i) issue(i);
     // 2. the activations (issued first) have landed when at most the weight
-    //    DMAs are outstanding
+    //    DMAs are outstanding; the fp32 ones go to LDS packed (read back
+    //    by this wave only: its LDS operations complete in order)
     wait_vmcnt<first>();
     u32x4 af[kGvQuads][4];
+    uint32_t ovf = 0; // fp32: tokens (bit t) this lane found beyond the fp16 range
+    if constexpr (F32) ovf = xf.store(abuf, lane);
     g3_read_act<S>(abuf, lane, af);
     // 3. row group by row group, as this wave's own DMAs land
     floatx4 acc[C::P];
@@ -2472,12 +2540,21 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 2 : 1) void b1_gemv_g
     __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
 
     // 4. cross-wave reduction in wave order; waves 0-3 sum even and waves
-    //    4-7 odd row groups
+    //    4-7 odd row groups; the fp32 kernel's out-of-range token flags (a
+    //    word per wave) go with the partials
     __syncthreads();
     floatx4 *red = reinterpret_cast<floatx4 *>(gsm); // [wave][P][lane]
 #pragma unroll
     for (int r = 0; r < C::P; ++r)
         if (r < nrg) red[(wave * C::P + r) * 64 + lane] = acc[r];
+    uint32_t *flags = reinterpret_cast<uint32_t *>(gsm + kGvWaves * C::P * 1024);
+    if constexpr (F32) {
+        uint32_t toks = 0;
+#pragma unroll
+        for (int t = 0; t < S; ++t)
+            if (__builtin_amdgcn_ballot_w64(((ovf >> t) & 1u) != 0)) toks |= 1u << t;
+        if (lane == 0) flags[wave] = toks;
+    }
     __syncthreads();
     float *const out = reinterpret_cast<float *>(outs[op]);
     const int64_t ldo = ldos[op];
@@ -2493,6 +2570,44 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 2 : 1) void b1_gemv_g
             if (rsc) sum *= rsc[tok];
             bad += !__builtin_isfinite(sum);
             out[(size_t)tok * ldo + n] = sum;
+        }
+    }
+    if constexpr (F32) {
+        // this work-group's rows of the flagged tokens again in the
+        // reference's scalar arithmetic (the single call's EXACT rows),
+        // after every thread's stores above (a barrier only on this rare
+        // path; `all` is the same in every thread)
+        uint32_t all = 0;
+#pragma unroll
+        for (int w = 0; w < kGvWaves; ++w) all |= flags[w];
+        if (all) {
+            __syncthreads();
+            const float *xa = static_cast<const float *>(act);
+            const int64_t lda = p.lda;
+            {
+#pragma clang fp contract(off)
+                for (int e2 = tid; e2 < S * nrg * 16; e2 += kGvWaves * 64) {
+                    const int t2 = e2 / (nrg * 16), rr = e2 - t2 * (nrg * 16);
+                    const int n = R0 * 16 + rr;
+                    if (t2 >= M || n >= N || !((all >> t2) & 1u)) continue;
+                    const float *xr = xa + (size_t)t2 * lda;
+                    const uint16_t *wr = reinterpret_cast<const uint16_t *>(wp + (size_t)n * rs);
+                    float sum = 0.0f;
+                    for (int b = 0; b < nb; ++b) {
+                        const float scale = (float)__builtin_bit_cast(_Float16, wr[3 * b]);
+                        const uint32_t bits = (uint32_t)wr[3 * b + 1] | ((uint32_t)wr[3 * b + 2] << 16);
+                        float bs = 0.0f;
+                        for (int i = 0; i < 32; ++i) {
+                            const float a = xr[32 * b + i];
+                            bs = ((bits >> i) & 1u) ? bs + a : bs - a;
+                        }
+                        sum = sum + scale * bs;
+                    }
+                    float *o = out + (size_t)t2 * ldo + n;
+                    bad += !__builtin_isfinite(sum) - !__builtin_isfinite(*o);
+                    *o = sum;
+                }
+            }
         }
     }
     count_nonfinite(p.nonfinite, bad);
@@ -2876,11 +2991,13 @@ static hipError_t gemv_attrs() {
             reinterpret_cast<const void *>(&b1_gemv3_kernel<4, true>),
             reinterpret_cast<const void *>(&b1_gemv3_kernel<8, true>),
             reinterpret_cast<const void *>(&b1_gemv3_kernel<16, true>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<1, kG4WL2>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<2, kG4WL2>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<4, kG4WL2>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<8, kG4WL1>),
-            reinterpret_cast<const void *>(&b1_gemv_group_kernel<16, kG4WL1>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<1, kG4WL2, false>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<2, kG4WL2, false>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<4, kG4WL2, false>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<8, kG4WL1, false>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<16, kG4WL1, false>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<1, kG4WL2, true>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<2, kG4WL2, true>),
         };
         attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kGvLds);
@@ -2967,8 +3084,10 @@ bool gemv_group_ok(int M, int K, const GemvGroupOp *ops, int nops) {
     return groups <= INT32_MAX;
 }
 
-hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M, const GemvGroupOp *ops, int nops,
-                             int32_t *nonfinite, int num_cus, hipStream_t s) {
+// Both forms of the grouped launch: packed fp16 activations (with the row
+// scales of a range-safe packing) or, at most 2 tokens, fp32 rows.
+static hipError_t gemv_group_run(const void *act, int64_t lda, const float *rsc, bool f32, int K, int M,
+                                 const GemvGroupOp *ops, int nops, int32_t *nonfinite, int num_cus, hipStream_t s) {
     const hipError_t attr_err = gemv_attrs();
     if (attr_err != hipSuccess) return attr_err;
     GemvGroup p{};
@@ -2985,7 +3104,8 @@ hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M,
     }
     p.K = K;
     p.M = M;
-    p.act = packed;
+    p.act = act;
+    p.lda = lda;
     p.rsc = rsc;
     p.nonfinite = nonfinite;
     // work-groups per op: in proportion to its row groups over the CUs'
@@ -3008,17 +3128,38 @@ hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M,
         p.wgstart[kGemvGroupMax] = nwg;
         hipLaunchKernelGGL(kern, dim3(nwg), dim3(kGvWaves * 64), lds, s, p);
     };
-    if (M <= 1)
-        launch(b1_gemv_group_kernel<1, kG4WL2>, G4Cfg<1, kG4WL2>::P, 2, G4Cfg<1, kG4WL2>::Lds);
-    else if (M <= 2)
-        launch(b1_gemv_group_kernel<2, kG4WL2>, G4Cfg<2, kG4WL2>::P, 2, G4Cfg<2, kG4WL2>::Lds);
-    else if (M <= 4)
-        launch(b1_gemv_group_kernel<4, kG4WL2>, G4Cfg<4, kG4WL2>::P, 2, G4Cfg<4, kG4WL2>::Lds);
-    else if (M <= 8)
-        launch(b1_gemv_group_kernel<8, kG4WL1>, G4Cfg<8, kG4WL1>::P, 1, G4Cfg<8, kG4WL1>::Lds);
-    else
-        launch(b1_gemv_group_kernel<16, kG4WL1>, G4Cfg<16, kG4WL1>::P, 1, G4Cfg<16, kG4WL1>::Lds);
+    if (f32) {
+        if (M <= 1)
+            launch(b1_gemv_group_kernel<1, kG4WL2, true>, G4Cfg<1, kG4WL2, true>::P, 2, G4Cfg<1, kG4WL2, true>::Lds);
+        else
+            launch(b1_gemv_group_kernel<2, kG4WL2, true>, G4Cfg<2, kG4WL2, true>::P, 2, G4Cfg<2, kG4WL2, true>::Lds);
+    } else if (M <= 1) {
+        launch(b1_gemv_group_kernel<1, kG4WL2, false>, G4Cfg<1, kG4WL2>::P, 2, G4Cfg<1, kG4WL2>::Lds);
+    } else if (M <= 2) {
+        launch(b1_gemv_group_kernel<2, kG4WL2, false>, G4Cfg<2, kG4WL2>::P, 2, G4Cfg<2, kG4WL2>::Lds);
+    } else if (M <= 4) {
+        launch(b1_gemv_group_kernel<4, kG4WL2, false>, G4Cfg<4, kG4WL2>::P, 2, G4Cfg<4, kG4WL2>::Lds);
+    } else if (M <= 8) {
+        launch(b1_gemv_group_kernel<8, kG4WL1, false>, G4Cfg<8, kG4WL1>::P, 1, G4Cfg<8, kG4WL1>::Lds);
+    } else {
+        launch(b1_gemv_group_kernel<16, kG4WL1, false>, G4Cfg<16, kG4WL1>::P, 1, G4Cfg<16, kG4WL1>::Lds);
+    }
     return hipGetLastError();
+}
+
+hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M, const GemvGroupOp *ops, int nops,
+                             int32_t *nonfinite, int num_cus, hipStream_t s) {
+    return gemv_group_run(packed, K, rsc, false, K, M, ops, nops, nonfinite, num_cus, s);
+}
+
+bool gemv_group_f32_ok(const float *act, int64_t lda, int M, int K) {
+    return M >= 1 && M <= kGemvGroupF32MaxM && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(act) & 15) == 0 &&
+           ((uint64_t)(M - 1) * (uint64_t)lda + (uint64_t)K) * 4u < (1ull << 31);
+}
+
+hipError_t launch_gemv_group_f32(const float *act, int64_t lda, int K, int M, const GemvGroupOp *ops, int nops,
+                                 int32_t *nonfinite, int num_cus, hipStream_t s) {
+    return gemv_group_run(act, lda, nullptr, true, K, M, ops, nops, nonfinite, num_cus, s);
 }
 
 } // namespace b1

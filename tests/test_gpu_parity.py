@@ -778,10 +778,11 @@ GROUP_CASES = [  # (m, k, output widths): consecutive small-M ops on one input
 
 @pytest.mark.parametrize("m,k,ns", GROUP_CASES)
 def test_linear_batch_groups_small_m_ops(torch, b1, oracle, m, k, ns):
-    """Consecutive small-M ops on the same input run as one launch over one
-    range-safe packing (up to 8): each output bit for bit the op's own
-    small-M call, the counter of non-finite outputs unchanged, the workspace
-    the packing; within the FAST bar of the float64 oracle."""
+    """Consecutive small-M ops on the same input run as one launch (up to
+    8), from the fp32 rows at M <= 2 (no workspace) and over one range-safe
+    packing above (the workspace that packing): each output bit for bit the
+    op's own small-M call, the counter of non-finite outputs unchanged;
+    within the FAST bar of the float64 oracle."""
     from bonsai_b1 import capi, synth
     say(f"group m={m} k={k} ns={ns}")
     x = synth.device_activations(m, k, 300 + m)
@@ -789,7 +790,7 @@ def test_linear_batch_groups_small_m_ops(torch, b1, oracle, m, k, ns):
     outs = [torch.full((m, n + 8), 7.0, device="cuda")[:, :n] for n in ns]
     ops = [(x, b1.device_weights(w, k, n), o) for w, n, o in zip(ws, ns, outs)]
     pack = (m * k * 2 + 255) // 256 * 256 + (m * 4 + 255) // 256 * 256
-    assert capi.linear_batch_workspace_bytes(ops) == pack
+    assert capi.linear_batch_workspace_bytes(ops) == (pack if m > 2 else 0)
     assert capi.linear_batch_workspace_bytes(ops[:1]) == 0       # alone: converts itself
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     b1.linear_batch(ops, nonfinite=nf)
@@ -834,6 +835,50 @@ def test_linear_batch_groups_random(torch, b1, oracle, seed):
         assert bool((pad == 5.0).all()), f"op {i} pad"
     assert_fast_close(outs[-1].cpu().numpy(), oracle.linear_f64(x.cpu().numpy(), ws[-1].cpu().numpy(), ns[-1]),
                       f"random group last op vs fp64 (seed {seed})")
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_linear_batch_group_fp32_rows(torch, b1, m):
+    """A grouped run of at most 2 tokens reads the fp32 rows itself: with
+    rows beyond the fp16 range (x 1e5, and 3e38 whose outputs overflow fp32)
+    each op's outputs equal its own fp32 call bit for bit (those rows again
+    in EXACT arithmetic) and the non-finite outputs are counted once; a row
+    stride other than K (16-byte aligned) takes the same path, an unaligned
+    view runs each op alone, both with no workspace."""
+    from bonsai_b1 import capi, synth
+    k, ns = 3072, [1024, 77, 2048]
+    say(f"fp32 group m={m} k={k} ns={ns}")
+    x = synth.device_activations(m, k, 450 + m)
+    ws = [synth.device_packed_weights(n, k, 460 + i) for i, n in enumerate(ns)]
+    dws = [b1.device_weights(w, k, n) for w, n in zip(ws, ns)]
+
+    def run(xv):
+        outs = [torch.full((m, n), 3.0, device="cuda") for n in ns]
+        nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+        b1.linear_batch([(xv, dw, o) for dw, o in zip(dws, outs)], nonfinite=nf)
+        refs = [b1.linear(xv, w, n) for w, n in zip(ws, ns)]
+        torch.cuda.synchronize()
+        for i, (o, r) in enumerate(zip(outs, refs)):   # equal, NaN where the call gives NaN
+            assert torch.allclose(o, r, rtol=0.0, atol=0.0, equal_nan=True), f"op {i}"
+        return outs, int(nf.item())
+
+    xb = x.clone()
+    xb[0] *= 1e5
+    _, nf = run(xb)
+    assert nf == 0
+    if m == 2:
+        xb[1] = 3.0e38
+        outs, nf = run(xb)
+        bad = sum(int((~torch.isfinite(o)).sum()) for o in outs)
+        say(f"  non-finite outputs {bad}, counted {nf}")
+        assert bad > 0 and nf == bad and all(bool(torch.isfinite(o[0]).all()) for o in outs)
+    big = torch.zeros((m, k + 12), device="cuda")
+    for off in (4, 1):
+        xv = big[:, off:off + k]
+        xv.copy_(x)
+        ops = [(xv, dw, torch.empty((m, n), device="cuda")) for dw, n in zip(dws, ns)]
+        assert capi.linear_batch_workspace_bytes(ops) == 0, f"offset {off}"
+        run(xv)
 
 
 def test_linear_batch_group_order_and_range(torch, b1):
