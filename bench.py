@@ -656,9 +656,9 @@ MOD_GROUP = (1, 3072, [18432, 18432, 9216, 6144])   # a step's modulation projec
 
 def bench_gemv_group(torch, b1, synth, m, k, ns, steps, warmup):
     """Consecutive small-M linears on one input (a diffusion step's
-    modulation projections): one bonsai_b1_linear_batch call, which packs the
-    input once and runs them as one launch, against the same linears as
-    separate calls.  Weight sets rotated past the MALL, launches captured in
+    modulation projections): one bonsai_b1_linear_batch call, which runs them
+    as one launch (over the fp32 input itself at m <= 8, else over one
+    packing of it), against the same linears as separate calls.  Weight sets rotated past the MALL, launches captured in
     a HIP graph as in bench_gemv."""
     nbytes = sum(n * (k // 32) * 6 for n in ns)
     copies = max(2, (2 * MALL_BYTES) // nbytes + 1)

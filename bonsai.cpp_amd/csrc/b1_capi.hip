@@ -864,9 +864,10 @@ static int fuse_span(int n_ops, int mode, int num_cus, OpAt at, int i, int *n_su
     return last;
 }
 
-// A grouped small-M run of at most kGemvGroupF32MaxM tokens reads their fp32
-// rows itself (no packing, outputs equal to the single calls bit for bit,
-// out-of-range tokens included); a larger one reads a range-safe packing.
+// A grouped small-M run of at most kGemvGroupF32MaxM (8) tokens reads their
+// fp32 rows itself (no packing, outputs equal to the single calls bit for
+// bit, out-of-range tokens included); a larger one reads a range-safe
+// packing.
 static bool gemv_group_direct(const b1::LinearArgs &a) {
     return a.M <= b1::kGemvGroupF32MaxM && b1::gemv_group_f32_ok(a.act, a.lda, a.M, a.K);
 }

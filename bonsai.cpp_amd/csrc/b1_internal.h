@@ -158,7 +158,8 @@ hipError_t launch_gemv_group(const void *packed, const float *rsc, int K, int M,
 // (rows 16-byte aligned, lda % 4 == 0, under 2^31 bytes): no packing pass,
 // each op's outputs bit for bit those of its own small-M call, rows of
 // tokens beyond the fp16 range included (EXACT rows, as the single call).
-constexpr int kGemvGroupF32MaxM = 2;
+// launch_gemv runs a single op of at most 4 tokens this way.
+constexpr int kGemvGroupF32MaxM = 8;
 bool gemv_group_f32_ok(const float *act, int64_t lda, int M, int K);
 hipError_t launch_gemv_group_f32(const float *act, int64_t lda, int K, int M, const GemvGroupOp *ops, int nops,
                                  int32_t *nonfinite, int num_cus, hipStream_t s);

@@ -2301,7 +2301,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
 
 // Several small-M linears over one activation matrix in one launch (the
 // modulation projections of a step, q/k/v of the text stream at a few
-// tokens): packed fp16, or at most 2 tokens of fp32 rows (F32: converted by
+// tokens): packed fp16, or at most 8 tokens of fp32 rows (F32: converted by
 // each wave as it stages them, tokens beyond the fp16 range recomputed in
 // EXACT arithmetic).  Each op has its own work-groups (wgstart), each
 // taking at most G4Cfg::P consecutive row groups of that op in one pass:
@@ -2424,7 +2424,7 @@ struct G4Decode<P, P, WI, D> {
 // projections, more work-groups than two a CU hold.)
 template <int S>
 struct G4ActF32 {
-    static_assert(S <= 2, "at most 2 token slots");
+    static_assert(S <= 8, "at most 8 token slots");
     static constexpr int J = S * 48, R = (J + 63) / 64;
     floatx4 x[R][2];
     // frs: the rows, (M - 1) lda + K floats; rowb = lda * 4
@@ -2998,6 +2998,8 @@ static hipError_t gemv_attrs() {
             reinterpret_cast<const void *>(&b1_gemv_group_kernel<16, kG4WL1, false>),
             reinterpret_cast<const void *>(&b1_gemv_group_kernel<1, kG4WL2, true>),
             reinterpret_cast<const void *>(&b1_gemv_group_kernel<2, kG4WL2, true>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<4, kG4WL2, true>),
+            reinterpret_cast<const void *>(&b1_gemv_group_kernel<8, kG4WL1, true>),
         };
         attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&b1_gemv_kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kGvLds);
@@ -3025,9 +3027,21 @@ static void gemv_grid(int N, int num_cus, int *nwg_out, int *groups_out) {
     *groups_out = groups;
 }
 
+static hipError_t gemv_group_run(const void *act, int64_t lda, const float *rsc, bool f32, int K, int M,
+                                 const GemvGroupOp *ops, int nops, int32_t *nonfinite, int num_cus, hipStream_t s);
+
 hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
     const hipError_t attr_err = gemv_attrs();
     if (attr_err != hipSuccess) return attr_err;
+    // up to 4 tokens at K <= 3072: the grouped kernel with one op (the same
+    // bits; 7.6 against 8.3 us at M = 1, 8.2 against 8.4 at M = 4, K = 3072,
+    // N = 18432, graph replay; from 5 tokens on b1_gemv3_kernel<8, false>
+    // is as fast or faster: 8.8 against 9.05 us at M = 8)
+    {
+        const GemvGroupOp op{a.w, a.N, a.out, a.ldo};
+        if (a.M <= 4 && gemv_group_ok(a.M, a.K, &op, 1) && gemv_group_f32_ok(a.act, a.lda, a.M, a.K))
+            return gemv_group_run(a.act, a.lda, nullptr, true, a.K, a.M, &op, 1, a.nonfinite, num_cus, s);
+    }
     int nwg, groups;
     gemv_grid(a.N, num_cus, &nwg, &groups);
     if (gemv_staged(a.K, a.N)) {
@@ -3085,7 +3099,7 @@ bool gemv_group_ok(int M, int K, const GemvGroupOp *ops, int nops) {
 }
 
 // Both forms of the grouped launch: packed fp16 activations (with the row
-// scales of a range-safe packing) or, at most 2 tokens, fp32 rows.
+// scales of a range-safe packing) or, at most 8 tokens, fp32 rows.
 static hipError_t gemv_group_run(const void *act, int64_t lda, const float *rsc, bool f32, int K, int M,
                                  const GemvGroupOp *ops, int nops, int32_t *nonfinite, int num_cus, hipStream_t s) {
     const hipError_t attr_err = gemv_attrs();
@@ -3131,8 +3145,12 @@ static hipError_t gemv_group_run(const void *act, int64_t lda, const float *rsc,
     if (f32) {
         if (M <= 1)
             launch(b1_gemv_group_kernel<1, kG4WL2, true>, G4Cfg<1, kG4WL2, true>::P, 2, G4Cfg<1, kG4WL2, true>::Lds);
-        else
+        else if (M <= 2)
             launch(b1_gemv_group_kernel<2, kG4WL2, true>, G4Cfg<2, kG4WL2, true>::P, 2, G4Cfg<2, kG4WL2, true>::Lds);
+        else if (M <= 4)
+            launch(b1_gemv_group_kernel<4, kG4WL2, true>, G4Cfg<4, kG4WL2, true>::P, 2, G4Cfg<4, kG4WL2, true>::Lds);
+        else
+            launch(b1_gemv_group_kernel<8, kG4WL1, true>, G4Cfg<8, kG4WL1, true>::P, 1, G4Cfg<8, kG4WL1, true>::Lds);
     } else if (M <= 1) {
         launch(b1_gemv_group_kernel<1, kG4WL2, false>, G4Cfg<1, kG4WL2>::P, 2, G4Cfg<1, kG4WL2>::Lds);
     } else if (M <= 2) {

@@ -263,9 +263,9 @@ int bonsai_b1_linear_packed_f16_scaled(const void *packed_act,
  * in_dim <= 3072, no epilogue) on the same activations -- the modulation
  * projections of a step, all over vec_silu at one token (:308-311,
  * 470-471,548) -- run as one launch when their outputs lie apart from
- * those activations and from one another: from the fp32 rows at batch <= 2
+ * those activations and from one another: from the fp32 rows at batch <= 8
  * (no workspace), over one packing above; each op's outputs are those of
- * its own small-batch call, bit for bit (above batch 2 for activations
+ * its own small-batch call, bit for bit (above batch 8 for activations
  * within the fp16 range).  workspace: device buffer of
  * bonsai_b1_linear_batch_workspace_bytes bytes, or NULL for the library's
  * per-stream workspace.  On an invalid op

@@ -779,7 +779,7 @@ GROUP_CASES = [  # (m, k, output widths): consecutive small-M ops on one input
 @pytest.mark.parametrize("m,k,ns", GROUP_CASES)
 def test_linear_batch_groups_small_m_ops(torch, b1, oracle, m, k, ns):
     """Consecutive small-M ops on the same input run as one launch (up to
-    8), from the fp32 rows at M <= 2 (no workspace) and over one range-safe
+    8), from the fp32 rows at M <= 8 (no workspace) and over one range-safe
     packing above (the workspace that packing): each output bit for bit the
     op's own small-M call, the counter of non-finite outputs unchanged;
     within the FAST bar of the float64 oracle."""
@@ -790,7 +790,7 @@ def test_linear_batch_groups_small_m_ops(torch, b1, oracle, m, k, ns):
     outs = [torch.full((m, n + 8), 7.0, device="cuda")[:, :n] for n in ns]
     ops = [(x, b1.device_weights(w, k, n), o) for w, n, o in zip(ws, ns, outs)]
     pack = (m * k * 2 + 255) // 256 * 256 + (m * 4 + 255) // 256 * 256
-    assert capi.linear_batch_workspace_bytes(ops) == (pack if m > 2 else 0)
+    assert capi.linear_batch_workspace_bytes(ops) == (pack if m > 8 else 0)
     assert capi.linear_batch_workspace_bytes(ops[:1]) == 0       # alone: converts itself
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     b1.linear_batch(ops, nonfinite=nf)
@@ -837,9 +837,9 @@ def test_linear_batch_groups_random(torch, b1, oracle, seed):
                       f"random group last op vs fp64 (seed {seed})")
 
 
-@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 4, 5, 8])
 def test_linear_batch_group_fp32_rows(torch, b1, m):
-    """A grouped run of at most 2 tokens reads the fp32 rows itself: with
+    """A grouped run of at most 8 tokens reads the fp32 rows itself: with
     rows beyond the fp16 range (x 1e5, and 3e38 whose outputs overflow fp32)
     each op's outputs equal its own fp32 call bit for bit (those rows again
     in EXACT arithmetic) and the non-finite outputs are counted once; a row
@@ -866,12 +866,12 @@ def test_linear_batch_group_fp32_rows(torch, b1, m):
     xb[0] *= 1e5
     _, nf = run(xb)
     assert nf == 0
-    if m == 2:
-        xb[1] = 3.0e38
+    if m >= 2:
+        xb[m - 1] = 3.0e38
         outs, nf = run(xb)
         bad = sum(int((~torch.isfinite(o)).sum()) for o in outs)
         say(f"  non-finite outputs {bad}, counted {nf}")
-        assert bad > 0 and nf == bad and all(bool(torch.isfinite(o[0]).all()) for o in outs)
+        assert bad > 0 and nf == bad and all(bool(torch.isfinite(o[:m - 1]).all()) for o in outs)
     big = torch.zeros((m, k + 12), device="cuda")
     for off in (4, 1):
         xv = big[:, off:off + k]
@@ -884,10 +884,11 @@ def test_linear_batch_group_fp32_rows(torch, b1, m):
 def test_linear_batch_group_order_and_range(torch, b1):
     """Small-M ops whose outputs overlap one another or the shared input are
     not grouped (the batch keeps their order); a row beyond the fp16 range
-    in a group gives the scaled packing's results (the fp32 entry computes
-    it in EXACT arithmetic instead), and a non-finite output is counted."""
+    in a group over a packing (more than 8 tokens) gives the scaled
+    packing's results (the fp32 entry computes it in EXACT arithmetic
+    instead), and a non-finite output is counted."""
     from bonsai_b1 import synth
-    m, k, n = 4, 3072, 1024
+    m, k, n = 12, 3072, 1024
     x = synth.device_activations(m, k, 401)
     wa, wb, wc = (synth.device_packed_weights(n, k, 402 + i) for i in range(3))
     # two ops into one output: the second wins
@@ -923,7 +924,7 @@ def test_linear_batch_group_order_and_range(torch, b1):
     bad = int((~torch.isfinite(ga)).sum() + (~torch.isfinite(gb)).sum())
     say(f"  non-finite outputs {bad}, counted {int(nf.item())}")
     assert bad > 0 and int(nf.item()) == bad
-    assert bool(torch.isfinite(ga[[0, 1, 3]]).all())
+    assert bool(torch.isfinite(ga[[0, 1, 3, 11]]).all())
 
 
 # ---------------------------------------------------------------- split-K --
