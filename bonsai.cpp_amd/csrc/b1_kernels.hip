@@ -65,6 +65,17 @@ __device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
+// max(m, |a|, |b|) in one v_max3_f32: the running largest magnitude of the
+// activations a lane converts, against fp16's range (a quiet NaN operand is
+// passed over, as IEEE maxNum does: a NaN does not count as out of range).
+__device__ __forceinline__ float absmax3(float m, float a, float b) {
+    float r;
+    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+    return r;
+}
+// fp32 magnitudes from this on round to fp16 infinity
+constexpr float kF16Overflow = 65520.0f;
+
 // s_waitcnt vmcnt(N) leaving expcnt and lgkmcnt alone (gfx9 encoding:
 // vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 template <int N>
@@ -2165,7 +2176,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
     floatx4 acc[kGvMaxRG];
 #pragma unroll
     for (int r = 0; r < kGvMaxRG; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
-    int ovf = 0; // fp32: this lane converted an activation beyond the fp16 range
+    float amax = 0.0f; // fp32: the largest magnitude this lane converted
 
     for (int kb0 = 0; kb0 < nb; kb0 += kG3Chunk) {
         const int wb0 = kb0 + wave * kGvBPW;
@@ -2225,7 +2236,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    ovf |= (__builtin_fabsf(x0[j]) >= 65520.0f) | (__builtin_fabsf(x1[j]) >= 65520.0f);
+                    amax = absmax3(amax, x0[j], x1[j]);
                     af[f >> 2][f & 3][j] = pack_f16(x0[j], x1[j]);
                 }
             }
@@ -2234,7 +2245,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
             for (int f = 0; f < kGvBPW; ++f)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    ovf |= (__builtin_fabsf(xa[f][0][j]) >= 65520.0f) | (__builtin_fabsf(xa[f][1][j]) >= 65520.0f);
+                    amax = absmax3(amax, xa[f][0][j], xa[f][1][j]);
                     af[f >> 2][f & 3][j] = pack_f16(xa[f][0][j], xa[f][1][j]);
                 }
         }
@@ -2254,7 +2265,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
         if (r < nrg) red[(wave * kGvMaxRG + r) * 64 + lane] = acc[r];
     uint32_t *flags = reinterpret_cast<uint32_t *>(gsm + kGvWaves * kGvMaxRG * 64 * 16);
     if constexpr (!PACKED) {
-        const uint64_t bal = __builtin_amdgcn_ballot_w64(ovf != 0);
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(amax >= kF16Overflow);
         const uint32_t toks = (uint32_t)((bal | (bal >> 16) | (bal >> 32) | (bal >> 48)) & 0xFFFFu);
         if (lane == 0) flags[wave] = toks;
     }
@@ -2449,13 +2460,13 @@ struct G4ActF32 {
             const int j = r * 64 + lane, t = j / 48, bq = j - 48 * t;
             if (j < J) {
                 u32x4 v;
+                float amax = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    ovf |= (uint32_t)((__builtin_fabsf(x[r][0][e]) >= 65520.0f) |
-                                      (__builtin_fabsf(x[r][1][e]) >= 65520.0f))
-                           << t;
+                    amax = absmax3(amax, x[r][0][e], x[r][1][e]);
                     v[e] = pack_f16(x[r][0][e], x[r][1][e]);
                 }
+                ovf |= (uint32_t)(amax >= kF16Overflow) << t;
                 *reinterpret_cast<u32x4 *>(abuf + t * kG3ARow + 64 * (bq >> 2) + 16 * (bq & 3)) = v;
             }
         }
