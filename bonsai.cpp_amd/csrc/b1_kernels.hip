@@ -2182,6 +2182,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
         const int wb0 = kb0 + wave * kGvBPW;
         // 1. activations
         constexpr bool F32LDS = !PACKED && S <= 8;
+        static_assert((S & (S - 1)) == 0, "token slots a power of two");
         floatx4 xa[PACKED || F32LDS ? 1 : kGvBPW][2];
         if constexpr (PACKED) {
             const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
@@ -2225,15 +2226,16 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
         } else if constexpr (F32LDS) {
             // lane (g, col), fragment (q, t): chunks 8 blk + t and + 4 of its
             // slot's slice, blk = 4 q + g (elements 32 blk + 4 t .. +3 and 16
-            // later)
+            // later).  Chunks past K hold the DMA's zeros.  Every lane reads:
+            // one whose column is a slot past M, or past S (it reads slot
+            // col mod S), gets another token's or stale values, which reach
+            // only output columns that are never stored (MFMA columns are
+            // independent), and its range flag is masked below.
 #pragma unroll
             for (int f = 0; f < kGvBPW; ++f) {
                 const int bl = 4 * (f >> 2) + g, c = 8 * bl + (f & 3);
-                floatx4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = x0;
-                if (col < p.M && wb0 + bl < nb) {
-                    x0 = g3_act_f32(abuf, col, c);
-                    x1 = g3_act_f32(abuf, col, c + 4);
-                }
+                const floatx4 x0 = g3_act_f32(abuf, col & (S - 1), c);
+                const floatx4 x1 = g3_act_f32(abuf, col & (S - 1), c + 4);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     amax = absmax3(amax, x0[j], x1[j]);
@@ -2266,7 +2268,8 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
     uint32_t *flags = reinterpret_cast<uint32_t *>(gsm + kGvWaves * kGvMaxRG * 64 * 16);
     if constexpr (!PACKED) {
         const uint64_t bal = __builtin_amdgcn_ballot_w64(amax >= kF16Overflow);
-        const uint32_t toks = (uint32_t)((bal | (bal >> 16) | (bal >> 32) | (bal >> 48)) & 0xFFFFu);
+        const uint32_t toks = (uint32_t)((bal | (bal >> 16) | (bal >> 32) | (bal >> 48)) & 0xFFFFu) &
+                              (p.M >= 16 ? 0xFFFFu : (1u << p.M) - 1u);
         if (lane == 0) flags[wave] = toks;
     }
     __syncthreads();
