@@ -2000,6 +2000,8 @@ __device__ __forceinline__ void g3_wait(int r) {
 // The slice of wave w starts 8 (w odd) bytes into its first chunk; block
 // 4q + g sits at 6 (4q + g) bytes into the slice, read as the aligned 8-byte
 // window that holds it (2 bytes earlier for odd g).
+// FRESH: acc holds nothing yet; the first MFMA adds to a constant zero.
+template <bool FRESH = false>
 __device__ __forceinline__ void g3_decode_rg(const uint8_t *wbuf, int r, int wave, int lane,
                                              const u32x4 (&af)[kGvQuads][4], floatx4 &acc) {
     const int col = lane & 15, g = lane >> 4, odd = g & 1;
@@ -2027,7 +2029,9 @@ __device__ __forceinline__ void g3_decode_rg(const uint8_t *wbuf, int r, int wav
 #pragma unroll
         for (int t = 0; t < 4; ++t)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, af[q][t]),
-                                                         __builtin_bit_cast(half8, bd[t]), acc, 0, 0, 0);
+                                                         __builtin_bit_cast(half8, bd[t]),
+                                                         FRESH && q == 0 && t == 0 ? floatx4{0.f, 0.f, 0.f, 0.f} : acc,
+                                                         0, 0, 0);
     }
 }
 
@@ -2414,7 +2418,7 @@ struct G4Decode {
 #pragma unroll
             for (int i = lo; i < hi; ++i) issue(i);
             wait_vmcnt<hi - g4_dmas(R)>();
-            g3_decode_rg(wbuf, R, wave, lane, af, acc[R]);
+            g3_decode_rg<true>(wbuf, R, wave, lane, af, acc[R]);
             G4Decode<R + 1, P, WI, D>::run(wbuf, nrg, wave, lane, af, acc, issue);
         }
     }
@@ -2426,7 +2430,7 @@ struct G4Decode<P, P, WI, D> {
                                                floatx4 (&)[P], Issue &) {}
 };
 
-// fp32 activations of the grouped kernel, S <= 2 token slots, through
+// fp32 activations of the grouped kernel, S <= 8 token slots, through
 // registers into the packed layout g3_read_act<S> reads: token t at abuf +
 // kG3ARow t, block b's 16 dwords at 64 b, dword d the fp16 pair (element d,
 // element d + 16), rounded as the single call rounds.  Job j = (t, b, q) of
@@ -2546,9 +2550,7 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
     if constexpr (F32) ovf = xf.store(abuf, lane);
     g3_read_act<S>(abuf, lane, af);
     // 3. row group by row group, as this wave's own DMAs land
-    floatx4 acc[C::P];
-#pragma unroll
-    for (int r = 0; r < C::P; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 acc[C::P]; // each set by its row group's decode; [nrg, P) never read
     G4Decode<0, C::P, C::WInst, D>::run(wbuf, nrg, wave, lane, af, acc, issue);
     wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
