@@ -2371,7 +2371,9 @@ struct Sgpr8 {
 // Row groups whose DMAs are in flight behind the one being decoded.  With
 // two work-groups per CU (16 waves), 2 measured best for the modulation
 // projections: 13.9 us per launch against 14.2-14.5 us with 1 and 14.4-14.6
-// us with 4 (a timing copy, two alternating passes).
+// us with 4 (a timing copy, two alternating passes).  With one work-group
+// per CU (8 tokens) 2 is best too: the four projections at M = 8 took
+// 18.6 us against 20.3-20.4 us with 4 or 8.
 constexpr int kG4Ahead = 2;
 
 // Row groups of a one-pass work-group by token slots S and per-wave LDS
