@@ -807,7 +807,7 @@ def test_linear_batch_groups_small_m_ops(torch, b1, oracle, m, k, ns):
         assert_fast_close(outs[i].cpu().numpy(), oracle.linear_f64(xh, raw, ns[i]), f"group op {i} vs fp64")
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", range(10))
 def test_linear_batch_groups_random(torch, b1, oracle, seed):
     """Seeded random groupings of small-M ops (1-8 ops, output widths 1 to
     5000 rows, M 1-16, K a multiple of 256 up to 3072): each op's output bit
