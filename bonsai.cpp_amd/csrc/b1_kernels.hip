@@ -2344,11 +2344,11 @@ struct GemvGroup {
 
 // The first 8 entries of a kernel-argument array held in SGPRs: each is
 // read once with a constant index and passed through an empty asm, so that
-// a[i] for a wave-uniform i stays a chain of scalar selects and every
-// argument arrives in the kernel's first round of scalar loads.  (Without
-// the asm the compiler folds the selects back into an indexed read of
-// argument memory, a dependent scalar load of about 1 us; with an array
-// member instead of named ones it moves the entries to scratch.)
+// a choice among them by a wave-uniform condition stays scalar selects and
+// the entries arrive in one round of scalar loads.  (Without the asm the
+// compiler folds the selects back into an indexed read of argument memory,
+// a dependent scalar load of about 1 us; with an array member instead of
+// named ones it moves the entries to scratch.)
 template <class T>
 __device__ __forceinline__ T sgpr_opaque(T x) {
     asm volatile("" : "+s"(x));
@@ -2362,9 +2362,6 @@ struct Sgpr8 {
         : a0(sgpr_opaque((T)a[0])), a1(sgpr_opaque((T)a[1])), a2(sgpr_opaque((T)a[2])), a3(sgpr_opaque((T)a[3])),
           a4(sgpr_opaque((T)a[4])), a5(sgpr_opaque((T)a[5])), a6(sgpr_opaque((T)a[6])), a7(sgpr_opaque((T)a[7])) {
         static_assert(N >= 8, "eight entries");
-    }
-    __device__ __forceinline__ T operator[](int i) const {
-        return i == 0 ? a0 : i == 1 ? a1 : i == 2 ? a2 : i == 3 ? a3 : i == 4 ? a4 : i == 5 ? a5 : i == 6 ? a6 : a7;
     }
 };
 
@@ -2504,16 +2501,27 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
     const Sgpr8<int> wgs(p.wgstart);
     const Sgpr8<int> ns(p.N);
     const Sgpr8<uint64_t> ws(p.w);
-    const Sgpr8<uint64_t> outs(p.out);
-    const Sgpr8<int64_t> ldos(p.ldo);
     const int wg_end = sgpr_opaque(p.wgstart[kGemvGroupMax]);
     const int bid = blockIdx.x;
-    const int op = (bid >= wgs.a1) + (bid >= wgs.a2) + (bid >= wgs.a3) + (bid >= wgs.a4) + (bid >= wgs.a5) +
-                   (bid >= wgs.a6) + (bid >= wgs.a7);
-    const int wg0 = wgs[op];
-    const int wg1 = op + 1 < kGemvGroupMax ? wgs[op + 1] : wg_end;
-    const int N = ns[op];
-    uint8_t *const wp = reinterpret_cast<uint8_t *>(ws[op]);
+    // the op is the last whose first work-group is at or before bid: a scan
+    // of scalar compares and selects (indexing the entries by a computed op
+    // made a tree of branches, ~270 scalar instructions before the first
+    // DMA, in every wave)
+    const int wgv[kGemvGroupMax + 1] = {wgs.a0, wgs.a1, wgs.a2, wgs.a3, wgs.a4, wgs.a5, wgs.a6, wgs.a7, wg_end};
+    const int nv[kGemvGroupMax] = {ns.a0, ns.a1, ns.a2, ns.a3, ns.a4, ns.a5, ns.a6, ns.a7};
+    const uint64_t wv[kGemvGroupMax] = {ws.a0, ws.a1, ws.a2, ws.a3, ws.a4, ws.a5, ws.a6, ws.a7};
+    int op = 0, wg0 = wgv[0], wg1 = wgv[1], N = nv[0];
+    uint64_t wq = wv[0];
+#pragma unroll
+    for (int k = 1; k < kGemvGroupMax; ++k) {
+        const bool c = bid >= wgv[k];
+        op = c ? k : op;
+        wg0 = c ? wgv[k] : wg0;
+        wg1 = c ? wgv[k + 1] : wg1;
+        N = c ? nv[k] : N;
+        wq = c ? wv[k] : wq;
+    }
+    uint8_t *const wp = reinterpret_cast<uint8_t *>(wq);
     int R0, R1;
     wg_row_groups((N + 15) / 16, wg1 - wg0, bid - wg0, R0, R1);
     const int nrg = R1 - R0; // at most C::P (the launcher's grid)
@@ -2543,6 +2551,10 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
     constexpr int first = g4_dmas(D - 1) < C::WInst ? g4_dmas(D - 1) : C::WInst;
 #pragma unroll
     for (int i = 0; i < first; ++i) issue(i);
+    // the outputs' arguments only now, so that their scalar loads do not
+    // hold back the first DMAs
+    const Sgpr8<uint64_t> outs(p.out);
+    const Sgpr8<int64_t> ldos(p.ldo);
     // 2. the activations (issued first) have landed when at most the weight
     //    DMAs are outstanding; the fp32 ones go to LDS packed (read back
     //    by this wave only: its LDS operations complete in order)
@@ -2574,8 +2586,16 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
         if (lane == 0) flags[wave] = toks;
     }
     __syncthreads();
-    float *const out = reinterpret_cast<float *>(outs[op]);
-    const int64_t ldo = ldos[op];
+    const uint64_t ov[kGemvGroupMax] = {outs.a0, outs.a1, outs.a2, outs.a3, outs.a4, outs.a5, outs.a6, outs.a7};
+    const int64_t lv[kGemvGroupMax] = {ldos.a0, ldos.a1, ldos.a2, ldos.a3, ldos.a4, ldos.a5, ldos.a6, ldos.a7};
+    uint64_t oq = ov[0];
+    int64_t ldo = lv[0];
+#pragma unroll
+    for (int k = 1; k < kGemvGroupMax; ++k) {
+        oq = k <= op ? ov[k] : oq;
+        ldo = k <= op ? lv[k] : ldo;
+    }
+    float *const out = reinterpret_cast<float *>(oq);
     int bad = 0;
     const int e = tid & 255, c = e & 15, tok = e >> 4;
     const int ln = 16 * (tok >> 2) + c, v = tok & 3;
