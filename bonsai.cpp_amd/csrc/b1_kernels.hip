@@ -2335,6 +2335,7 @@ struct GemvGroup {
     int64_t ldo[kGemvGroupMax];
     int N[kGemvGroupMax];           // 0 for the entries past the ops
     int wgstart[kGemvGroupMax + 1]; // first work-group of each op; wgstart[nops..] = the grid
+    int rgqr[kGemvGroupMax];        // an op's row groups over its work-groups: q | r << 4
     int K, M;
     const void *act;  // packed fp16 [M][K], or fp32 [M][lda] (the F32 kernels)
     int64_t lda;      // fp32 row stride (elements)
@@ -2391,6 +2392,7 @@ struct G4Cfg {
     static constexpr int WInst = (P * 16 * kG3RowCh + 63) / 64;
     static constexpr int Lds = kGvWaves * WL;
     static_assert(P >= 1 && ABytes % 16 == 0 && ABytes + WInst * 1024 <= WL, "a wave's LDS area");
+    static_assert(P < 16, "row groups per work-group in 4 bits (GemvGroup::rgqr)");
     static_assert(P * 1024 <= WL, "the reduction fits");
     static_assert(WInst + 2 * kGemvGroupMax < 64, "vmcnt range");
     static_assert(P * 1024 * kGvWaves + kGvWaves * 4 <= kGvWaves * WL, "the reduction and its flags fit");
@@ -2501,30 +2503,33 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
     const Sgpr8<int> wgs(p.wgstart);
     const Sgpr8<int> ns(p.N);
     const Sgpr8<uint64_t> ws(p.w);
-    const int wg_end = sgpr_opaque(p.wgstart[kGemvGroupMax]);
+    const Sgpr8<int> qrs(p.rgqr);
     const int bid = blockIdx.x;
     // the op is the last whose first work-group is at or before bid: a scan
     // of scalar compares and selects (indexing the entries by a computed op
     // made a tree of branches, ~270 scalar instructions before the first
     // DMA, in every wave)
-    const int wgv[kGemvGroupMax + 1] = {wgs.a0, wgs.a1, wgs.a2, wgs.a3, wgs.a4, wgs.a5, wgs.a6, wgs.a7, wg_end};
+    const int wgv[kGemvGroupMax] = {wgs.a0, wgs.a1, wgs.a2, wgs.a3, wgs.a4, wgs.a5, wgs.a6, wgs.a7};
     const int nv[kGemvGroupMax] = {ns.a0, ns.a1, ns.a2, ns.a3, ns.a4, ns.a5, ns.a6, ns.a7};
     const uint64_t wv[kGemvGroupMax] = {ws.a0, ws.a1, ws.a2, ws.a3, ws.a4, ws.a5, ws.a6, ws.a7};
-    int op = 0, wg0 = wgv[0], wg1 = wgv[1], N = nv[0];
+    const int qrv[kGemvGroupMax] = {qrs.a0, qrs.a1, qrs.a2, qrs.a3, qrs.a4, qrs.a5, qrs.a6, qrs.a7};
+    int op = 0, wg0 = wgv[0], N = nv[0], qr = qrv[0];
     uint64_t wq = wv[0];
 #pragma unroll
     for (int k = 1; k < kGemvGroupMax; ++k) {
         const bool c = bid >= wgv[k];
         op = c ? k : op;
         wg0 = c ? wgv[k] : wg0;
-        wg1 = c ? wgv[k + 1] : wg1;
         N = c ? nv[k] : N;
         wq = c ? wv[k] : wq;
+        qr = c ? qrv[k] : qr;
     }
     uint8_t *const wp = reinterpret_cast<uint8_t *>(wq);
-    int R0, R1;
-    wg_row_groups((N + 15) / 16, wg1 - wg0, bid - wg0, R0, R1);
-    const int nrg = R1 - R0; // at most C::P (the launcher's grid)
+    // the op's row groups split as wg_row_groups would, from the host's
+    // quotient and remainder (no division here)
+    const int q = qr & 15, r = qr >> 4, local = bid - wg0;
+    const int R0 = local * q + min(local, r);
+    const int nrg = q + (local < r ? 1 : 0); // at most C::P (the launcher's grid)
     // 1. the activation slice, then the weight slices, D row groups ahead
     G4ActF32<F32 ? S : 1> xf; // fp32: this lane's activation chunks
     if constexpr (F32) {
@@ -2539,13 +2544,24 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
     }
     const __amdgpu_buffer_rsrc_t wrs =
         __builtin_amdgcn_make_buffer_rsrc(wp, (short)0, (int)((uint32_t)N * rs), kBufferFlags);
+    // DMA i's lane takes slot 64 i + lane of the work-group's rows x
+    // kG3RowCh chunks: with 64 = 12 kG3RowCh + 4, its row is row0 + 12 i +
+    // (4 i + ch0) / 5 and its chunk (4 i + ch0) % 5, so each offset is the
+    // lane's base plus a uniform term and one select (no division or
+    // 64-bit multiply per DMA)
+    static_assert(kG3RowCh == 5, "slot arithmetic for 5 chunks a row");
+    const int row0 = lane / kG3RowCh, ch0 = lane - row0 * kG3RowCh;
+    const int lim = min(nrg * 16, N - R0 * 16); // rows of the work-group's row groups that exist
+    const uint32_t base = (uint32_t)(R0 * 16 + row0) * rs + slice0 + (uint32_t)ch0 * 16u;
+    const uint32_t inrow0 = slice0 + (uint32_t)ch0 * 16u;
     auto issue = [&](int i) {
-        const int sl = i * 64 + lane;
-        const int row = sl / kG3RowCh, ch = sl - row * kG3RowCh;
-        const uint32_t inrow = slice0 + (uint32_t)ch * 16u;
-        const int n = R0 * 16 + row;
-        const bool ok = row < nrg * 16 && n < N && inrow < rs;
-        dma_buf_lds16(wrs, wbuf + i * 1024, ok ? (uint32_t)n * rs + inrow : 0xFFFFFFF0u);
+        const int m = (4 * i) % 5, qi = (4 * i) / 5;
+        const bool carry = ch0 + m >= 5;
+        const int row = row0 + 12 * i + qi + (carry ? 1 : 0);
+        const uint32_t inrow = inrow0 + 16u * (uint32_t)m - (carry ? 80u : 0u);
+        const uint32_t off = base + (uint32_t)(12 * i + qi) * rs + 16u * (uint32_t)m + (carry ? rs - 80u : 0u);
+        const bool ok = (row < lim) & (inrow < rs);
+        dma_buf_lds16(wrs, wbuf + i * 1024, ok ? off : 0xFFFFFFF0u);
     };
     constexpr int D = kG4Ahead;
     constexpr int first = g4_dmas(D - 1) < C::WInst ? g4_dmas(D - 1) : C::WInst;
@@ -3175,6 +3191,8 @@ static hipError_t gemv_group_run(const void *act, int64_t lda, const float *rsc,
             if (k < (g + P - 1) / P) k = (g + P - 1) / P;
             if (k > g) k = g;
             if (k < 1) k = 1;
+            const int q = g / (int)k; // 1 .. P
+            p.rgqr[o] = q | (g - q * (int)k) << 4;
             nwg += (int)k;
         }
         p.wgstart[kGemvGroupMax] = nwg;
