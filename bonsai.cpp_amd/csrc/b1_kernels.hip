@@ -1967,6 +1967,35 @@ constexpr int kG3Chunk = kGvWaves * kGvBPW;                    // 96 blocks per 
 constexpr int kG3RowCh = 5;                                    // 16-byte chunks per row per wave
 constexpr int kG3RowB = kG3RowCh * 16;                         // 80: wave-private row stride
 constexpr int kG3WInst = (kGvMaxRG * 16 * kG3RowCh + 63) / 64; // 8 weight DMAs per wave
+
+// The weight DMAs of a wave's slices: DMA i's lane takes slot 64 i + lane of
+// the rows x kG3RowCh chunks, and with 64 = 12 kG3RowCh + 4 that slot is row
+// row0 + 12 i + (4 i + ch0) / 5, chunk (4 i + ch0) % 5 (row0, ch0: slot
+// lane's).  So each DMA's offset is the lane's base plus a uniform term and
+// one select: no division or wide multiply per DMA.
+static_assert(kG3RowCh == 5, "slot arithmetic for 5 chunks a row");
+struct SliceDmas {
+    int row0, ch0;
+    uint32_t base, inrow0; // offset and in-row byte of slot lane at K offset 0
+    // rows from global row `first`, rs bytes a row; slice0: the wave's first
+    // byte in a row
+    __device__ __forceinline__ SliceDmas(int lane, int first, uint32_t rs, uint32_t slice0) {
+        row0 = lane / kG3RowCh;
+        ch0 = lane - row0 * kG3RowCh;
+        inrow0 = slice0 + (uint32_t)ch0 * 16u;
+        base = (uint32_t)(first + row0) * rs + inrow0;
+    }
+    // DMA i's offset kofs bytes into the rows, or an out-of-range one for a
+    // slot past `rows` rows or past a row's rs bytes
+    __device__ __forceinline__ uint32_t off(int i, int rows, uint32_t rs, uint32_t kofs) const {
+        const int m = (4 * i) % 5, qi = (4 * i) / 5;
+        const bool carry = ch0 + m >= 5;
+        const int row = row0 + 12 * i + qi + (carry ? 1 : 0);
+        const uint32_t inrow = kofs + inrow0 + 16u * (uint32_t)m - (carry ? 80u : 0u);
+        const uint32_t o = base + kofs + (uint32_t)(12 * i + qi) * rs + 16u * (uint32_t)m + (carry ? rs - 80u : 0u);
+        return ((row < rows) & (inrow < rs)) ? o : 0xFFFFFFF0u;
+    }
+};
 constexpr int kG3WLds = kG3WInst * 1024;                       // 8 KB of weights per wave
 constexpr int kG3ALds = kGvBPW * 1024;                         // 12 KB of fragments per wave
 constexpr int kG3WaveLds = kG3WLds + kG3ALds;
@@ -2176,6 +2205,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
     // this wave's slice: bytes [72 w, 72 w + 72) of a pass's row part,
     // fetched from the aligned 72 w - 8 (w odd) as kG3RowCh chunks
     const uint32_t slice0 = (uint32_t)(72 * wave) & ~15u;
+    const SliceDmas wd(lane, rg0 * 16, rs, slice0);
 
     floatx4 acc[kGvMaxRG];
 #pragma unroll
@@ -2214,13 +2244,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
         }
         // 2. this wave's slice of every row of the work-group's row groups
 #pragma unroll
-        for (int i = 0; i < kG3WInst; ++i) {
-            const int sl = i * 64 + lane;
-            const int row = sl / kG3RowCh, ch = sl - row * kG3RowCh;
-            const uint32_t inrow = (uint32_t)kb0 * 6u + slice0 + (uint32_t)ch * 16u;
-            dma_buf_lds16(wrs, wbuf + i * 1024,
-                          (row < nrg * 16 && inrow < rs) ? (uint32_t)(rg0 * 16 + row) * rs + inrow : 0xFFFFFFF0u);
-        }
+        for (int i = 0; i < kG3WInst; ++i) dma_buf_lds16(wrs, wbuf + i * 1024, wd.off(i, nrg * 16, rs, (uint32_t)kb0 * 6u));
         // 3. the activations (issued first) have landed when at most the
         //    weight DMAs are outstanding
         wait_vmcnt<kG3WInst>();
@@ -2544,25 +2568,9 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
     }
     const __amdgpu_buffer_rsrc_t wrs =
         __builtin_amdgcn_make_buffer_rsrc(wp, (short)0, (int)((uint32_t)N * rs), kBufferFlags);
-    // DMA i's lane takes slot 64 i + lane of the work-group's rows x
-    // kG3RowCh chunks: with 64 = 12 kG3RowCh + 4, its row is row0 + 12 i +
-    // (4 i + ch0) / 5 and its chunk (4 i + ch0) % 5, so each offset is the
-    // lane's base plus a uniform term and one select (no division or
-    // 64-bit multiply per DMA)
-    static_assert(kG3RowCh == 5, "slot arithmetic for 5 chunks a row");
-    const int row0 = lane / kG3RowCh, ch0 = lane - row0 * kG3RowCh;
+    const SliceDmas wd(lane, R0 * 16, rs, slice0);
     const int lim = min(nrg * 16, N - R0 * 16); // rows of the work-group's row groups that exist
-    const uint32_t base = (uint32_t)(R0 * 16 + row0) * rs + slice0 + (uint32_t)ch0 * 16u;
-    const uint32_t inrow0 = slice0 + (uint32_t)ch0 * 16u;
-    auto issue = [&](int i) {
-        const int m = (4 * i) % 5, qi = (4 * i) / 5;
-        const bool carry = ch0 + m >= 5;
-        const int row = row0 + 12 * i + qi + (carry ? 1 : 0);
-        const uint32_t inrow = inrow0 + 16u * (uint32_t)m - (carry ? 80u : 0u);
-        const uint32_t off = base + (uint32_t)(12 * i + qi) * rs + 16u * (uint32_t)m + (carry ? rs - 80u : 0u);
-        const bool ok = (row < lim) & (inrow < rs);
-        dma_buf_lds16(wrs, wbuf + i * 1024, ok ? off : 0xFFFFFFF0u);
-    };
+    auto issue = [&](int i) { dma_buf_lds16(wrs, wbuf + i * 1024, wd.off(i, lim, rs, 0u)); };
     constexpr int D = kG4Ahead;
     constexpr int first = g4_dmas(D - 1) < C::WInst ? g4_dmas(D - 1) : C::WInst;
 #pragma unroll
