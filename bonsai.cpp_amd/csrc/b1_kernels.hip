@@ -2188,14 +2188,16 @@ __device__ __forceinline__ floatx4 g3_act_f32(const uint8_t *abuf, int t, int c)
 }
 
 template <int S, bool PACKED>
-__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, int groups) {
+// qr: the row groups over the work-groups as wg_row_groups splits them,
+// quotient | remainder << 4, from the host (no division in the kernel).
+__global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, int qr) {
     extern __shared__ __attribute__((aligned(16))) uint8_t gsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
-    const int nwg = gridDim.x, bid = blockIdx.x;
-    int rg0, rg1;
-    wg_row_groups(groups, nwg, bid, rg0, rg1);
-    const int nrg = rg1 - rg0;
+    const int bid = blockIdx.x;
+    const int q = qr & 15, r = qr >> 4;
+    const int rg0 = bid * q + min(bid, r);
+    const int nrg = q + (bid < r ? 1 : 0);
     const int nb = p.K / 32;
     const uint32_t rs = (uint32_t)nb * 6;
     uint8_t *wbuf = gsm + wave * kG3WaveLds;
@@ -3079,7 +3081,8 @@ static bool gemv_staged(int K, int N) {
 }
 
 // One work-group per CU, at most kGvMaxRG row groups each, at least one.
-static void gemv_grid(int N, int num_cus, int *nwg_out, int *groups_out) {
+static_assert(kGvMaxRG < 16, "row groups per work-group in 4 bits");
+static void gemv_grid(int N, int num_cus, int *nwg_out, int *groups_out, int *qr_out = nullptr) {
     const int groups = (N + 15) / 16;
     int nwg = num_cus > 0 ? num_cus : 256;
     const int need = (groups + kGvMaxRG - 1) / kGvMaxRG;
@@ -3087,6 +3090,10 @@ static void gemv_grid(int N, int num_cus, int *nwg_out, int *groups_out) {
     if (nwg > groups) nwg = groups;
     *nwg_out = nwg;
     *groups_out = groups;
+    if (qr_out) {
+        const int q = groups / nwg; // 1 .. kGvMaxRG
+        *qr_out = q | (groups - q * nwg) << 4;
+    }
 }
 
 static hipError_t gemv_group_run(const void *act, int64_t lda, const float *rsc, bool f32, int K, int M,
@@ -3104,17 +3111,17 @@ hipError_t launch_gemv(const LinearArgs &a, int num_cus, hipStream_t s) {
         if (a.M <= 4 && gemv_group_ok(a.M, a.K, &op, 1) && gemv_group_f32_ok(a.act, a.lda, a.M, a.K))
             return gemv_group_run(a.act, a.lda, nullptr, true, a.K, a.M, &op, 1, a.nonfinite, num_cus, s);
     }
-    int nwg, groups;
-    gemv_grid(a.N, num_cus, &nwg, &groups);
+    int nwg, groups, qr;
+    gemv_grid(a.N, num_cus, &nwg, &groups, &qr);
     if (gemv_staged(a.K, a.N)) {
         // converts and repairs out-of-range tokens itself
         LinearArgs b = a;
         b.rsc = nullptr;
         // up to 8 tokens whose rows lie in a buffer resource: through LDS
         if (a.M <= 8 && ((uint64_t)(a.M - 1) * (uint64_t)a.lda + (uint64_t)a.K) * 4u < (1ull << 31))
-            hipLaunchKernelGGL((b1_gemv3_kernel<8, false>), dim3(nwg), dim3(kGvWaves * 64), kG3Lds, s, b, groups);
+            hipLaunchKernelGGL((b1_gemv3_kernel<8, false>), dim3(nwg), dim3(kGvWaves * 64), kG3Lds, s, b, qr);
         else
-            hipLaunchKernelGGL((b1_gemv3_kernel<16, false>), dim3(nwg), dim3(kGvWaves * 64), kG3Lds, s, b, groups);
+            hipLaunchKernelGGL((b1_gemv3_kernel<16, false>), dim3(nwg), dim3(kGvWaves * 64), kG3Lds, s, b, qr);
         return hipGetLastError();
     }
     int mp_log2 = 0;
@@ -3134,19 +3141,19 @@ hipError_t launch_gemv_packed(const void *packed, const uint8_t *w, int K, int N
     const hipError_t attr_err = gemv_attrs();
     if (attr_err != hipSuccess) return attr_err;
     const LinearArgs a{static_cast<const float *>(packed), K, w, K, N, M, out, ldo, nonfinite, rsc};
-    int nwg, groups;
-    gemv_grid(N, num_cus, &nwg, &groups);
+    int nwg, groups, qr;
+    gemv_grid(N, num_cus, &nwg, &groups, &qr);
     const dim3 grid(nwg), block(kGvWaves * 64);
     if (M <= 1)
-        hipLaunchKernelGGL((b1_gemv3_kernel<1, true>), grid, block, kG3Lds, s, a, groups);
+        hipLaunchKernelGGL((b1_gemv3_kernel<1, true>), grid, block, kG3Lds, s, a, qr);
     else if (M <= 2)
-        hipLaunchKernelGGL((b1_gemv3_kernel<2, true>), grid, block, kG3Lds, s, a, groups);
+        hipLaunchKernelGGL((b1_gemv3_kernel<2, true>), grid, block, kG3Lds, s, a, qr);
     else if (M <= 4)
-        hipLaunchKernelGGL((b1_gemv3_kernel<4, true>), grid, block, kG3Lds, s, a, groups);
+        hipLaunchKernelGGL((b1_gemv3_kernel<4, true>), grid, block, kG3Lds, s, a, qr);
     else if (M <= 8)
-        hipLaunchKernelGGL((b1_gemv3_kernel<8, true>), grid, block, kG3Lds, s, a, groups);
+        hipLaunchKernelGGL((b1_gemv3_kernel<8, true>), grid, block, kG3Lds, s, a, qr);
     else
-        hipLaunchKernelGGL((b1_gemv3_kernel<16, true>), grid, block, kG3Lds, s, a, groups);
+        hipLaunchKernelGGL((b1_gemv3_kernel<16, true>), grid, block, kG3Lds, s, a, qr);
     return hipGetLastError();
 }
 
