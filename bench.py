@@ -848,7 +848,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the B1_0 linear is built and timed on a single "
-              "MI355X; multi-GPU sharding is design-only (see DESIGN.md).", file=sys.stderr)
+              "MI355X; sharding across GPUs is designed but not built.", file=sys.stderr)
         sys.exit(2)
 
     import torch
