@@ -2595,9 +2595,8 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
     wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
 
-    // 4. cross-wave reduction in wave order; waves 0-3 sum even and waves
-    //    4-7 odd row groups; the fp32 kernel's out-of-range token flags (a
-    //    word per wave) go with the partials
+    // 4. cross-wave reduction in wave order; the fp32 kernel's out-of-range
+    //    token flags (a word per wave) go with the partials
     __syncthreads();
     floatx4 *red = reinterpret_cast<floatx4 *>(gsm); // [wave][P][lane]
 #pragma unroll
@@ -2622,10 +2621,14 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
         ldo = k <= op ? lv[k] : ldo;
     }
     float *const out = reinterpret_cast<float *>(oq);
+    // the (row, token slot) elements of all nrg row groups spread over the
+    // work-group's threads (one pass at S <= 4); each element summed over
+    // the waves in wave order
     int bad = 0;
-    const int e = tid & 255, c = e & 15, tok = e >> 4;
-    const int ln = 16 * (tok >> 2) + c, v = tok & 3;
-    for (int r = wave >> 2; r < nrg; r += 2) {
+    constexpr int SE = 16 * S; // elements of a row group, a power of two
+    for (int idx = tid; idx < nrg * SE; idx += kGvWaves * 64) {
+        const int r = idx / SE, tok = (idx % SE) >> 4, c = idx & 15;
+        const int ln = 16 * (tok >> 2) + c, v = tok & 3;
         float sum = 0.0f;
 #pragma unroll
         for (int w = 0; w < kGvWaves; ++w) sum += red[(w * C::P + r) * 64 + ln][v];
