@@ -2138,12 +2138,15 @@ __device__ __forceinline__ void g3_read_act(const uint8_t *abuf, int lane, u32x4
 // Cross-wave reduction of a chunk's partial tiles (waves' partials at
 // `red` + wave * wstride, [rg][lane] floatx4) in wave order, then the
 // outputs of row groups [0, nrg) starting at row n0 of out, times the row
-// scales rsc when given.  Returns the non-finite count.
+// scales rsc when given; the (row, token slot) elements of S slots spread
+// over the threads.  Returns the non-finite count.
+template <int S>
 __device__ __forceinline__ int g3_reduce_store(const uint8_t *red, int wstride, int nrg, int tid, int M, int N, int n0,
                                                float *out, int64_t ldo, const float *rsc) {
+    constexpr int SE = 16 * S; // elements of a row group, a power of two
     int bad = 0;
-    for (int e = tid; e < nrg * 256; e += kGvWaves * 64) {
-        const int c = e & 15, tok = (e >> 4) & 15, r = e >> 8;
+    for (int e = tid; e < nrg * SE; e += kGvWaves * 64) {
+        const int c = e & 15, tok = (e % SE) >> 4, r = e / SE;
         const int ln = 16 * (tok >> 2) + c, v = tok & 3;
         float sum = 0.0f;
 #pragma unroll
@@ -2303,7 +2306,7 @@ __global__ __launch_bounds__(kGvWaves * 64) void b1_gemv3_kernel(LinearArgs p, i
         if (lane == 0) flags[wave] = toks;
     }
     __syncthreads();
-    int bad = g3_reduce_store(gsm, kGvMaxRG * 64 * 16, nrg, tid, p.M, p.N, rg0 * 16, p.out, p.ldo,
+    int bad = g3_reduce_store<S>(gsm, kGvMaxRG * 64 * 16, nrg, tid, p.M, p.N, rg0 * 16, p.out, p.ldo,
                               PACKED ? p.rsc : nullptr);
     if constexpr (!PACKED) {
         // this work-group's rows of the flagged tokens again, after every
