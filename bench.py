@@ -30,6 +30,7 @@ sys.path[:0] = [str(ROOT), str(ROOT / "bonsai.cpp_amd")]
 
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 (vector and matrix)
 HEADLINE = (4096, 3072, 12288)
 GEMV = (8, 3072, 18432)
 MALL_BYTES = 256 << 20
@@ -439,7 +440,34 @@ def bench_configs(torch, b1, synth, steps, warmup):
     log(f"[bench] c5 step (38 blocks): {c5['ms_per_step']:.2f} ms ({c5['gemm_tflops']:.0f} TFLOP/s of GEMM work, "
         f"{100*c5['frac']:.1f}% of peak); the 76 GEMMs alone {c5['ms_per_step_gemms_only']:.2f} ms")
     torch.cuda.empty_cache()
+    kl = bench_klein_step(torch, b1, synth)
+    out["klein_step"] = {x: round(v_, 4) if isinstance(v_, float) else v_ for x, v_ in kl.items()}
+    log(f"[bench] Klein step (100 linears): {kl['ms_per_step']:.2f} ms ({kl['tflops']:.0f} TFLOP/s, "
+        f"{100 * kl['frac']:.1f}% of peak); over producer-packed fp16 inputs {kl['ms_per_step_packed_inputs']:.2f} ms; "
+        f"with FF-in and linear1 writing SwiGLU as the next packed input {kl['ms_per_step_swiglu_epilogues']:.2f} ms")
+    torch.cuda.empty_cache()
     return out
+
+
+def bench_exact(torch, b1, synth):
+    """EXACT mode (b1_exact_kernel: fp32 VALU in the reference's scalar
+    summation order, src/b1_0_kernel.h:240-287, bit-identical to it) at C1
+    and at the headline shape, from fp32 activations; a few launches each
+    after one warm-up (the headline takes milliseconds per launch)."""
+    res = {}
+    for name, (m, k, n), reps in (("c1", (256, 3072, 3072), 20), ("headline", HEADLINE, 3)):
+        a = synth.device_activations(m, k, 31)
+        w = synth.device_packed_weights(n, k, 32)
+        y = torch.empty((m, n), device="cuda")
+        ms, _ = time_launches(torch, lambda i: b1.linear(a, w, n, out=y, mode="exact"), reps, 1)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        res[name] = {"shape": [m, k, n], "us": round(ms * 1e3, 1), "tflops": round(tf, 2),
+                     "frac_fp32_valu": round(tf / PEAK_FP32_TFLOPS, 4), "launches": reps}
+        log(f"[bench] EXACT mode {name} {(m, k, n)}: {ms * 1e3:.1f} us ({tf:.2f} TFLOP/s, "
+            f"{100 * tf / PEAK_FP32_TFLOPS:.1f}% of the fp32 peak)")
+        del a, w, y
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_klein_step(torch, b1, synth):
@@ -542,6 +570,7 @@ def bench_klein_step(torch, b1, synth):
     nbytes = sum(v.numel() for per in d for st in per.values() for v in st.values()) + \
         sum(a.numel() + b.numel() for a, b in s)
     return {"linears": 100, "ms_per_step": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
+            "frac": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
             "ms_per_step_separate_qkv": ms_sep, "packed_weight_bytes": nbytes,
             "ms_per_step_packed_inputs": ms_packed, "tflops_packed_inputs": flop / (ms_packed * 1e-3) / 1e12,
             "ms_per_step_swiglu_epilogues": ms_epi, "tflops_swiglu_epilogues": flop / (ms_epi * 1e-3) / 1e12,
@@ -827,9 +856,30 @@ def cpu_baselines(a_dev, w_dev, n, threads_share):
     nbytes = gn * (gk // 32) * 6
     gemv = {}
     for th in (threads_share, 4):
-        dt = cpu_time(run(ga, graw, gn, th), 3)
-        gemv[th] = {"us": dt * 1e6, "GBps_packed": nbytes / dt / 1e9}
+        # a call takes milliseconds, most of it thread start-up and the
+        # first touch of 10.6 MB: the median of many is the stable figure
+        dt = cpu_time(run(ga, graw, gn, th), 25)
+        gemv[th] = {"us": dt * 1e6, "GBps_packed": nbytes / dt / 1e9, "reps": 25}
     return res, gemv
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo, else lscpu), or None."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return None
 
 
 def main():
@@ -947,12 +997,7 @@ def main():
             f".safetensors: pinned pipeline {wl['pinned_s'] * 1e3:.0f} ms ({wl['pinned_GBps']:.1f} GB/s), "
             f"per-tensor upload from the mapping {wl['pageable_s'] * 1e3:.0f} ms ({wl['pageable_GBps']:.1f} GB/s)")
         torch.cuda.empty_cache()
-        kl = bench_klein_step(torch, b1, synth)
-        configs["klein_step"] = {x: round(v_, 4) if isinstance(v_, float) else v_ for x, v_ in kl.items()}
-        log(f"[bench] Klein step (100 linears): {kl['ms_per_step']:.2f} ms ({kl['tflops']:.0f} TFLOP/s); "
-            f"over producer-packed fp16 inputs {kl['ms_per_step_packed_inputs']:.2f} ms; with FF-in and "
-            f"linear1 writing SwiGLU as the next packed input {kl['ms_per_step_swiglu_epilogues']:.2f} ms")
-        torch.cuda.empty_cache()
+    exact = None if args.no_configs else bench_exact(torch, b1, synth)
 
     cpu = None
     if not args.no_cpu:
@@ -961,7 +1006,7 @@ def main():
         res, gemv_cpu = cpu_baselines(a, w, n, share)
         top = res[share]
         cpu = {"value": round(top["tflops"], 5), "unit": "TFLOP/s", "cores": share, "kind": "port",
-               "host_cpus": os.cpu_count(),
+               "host_cpus": os.cpu_count(), "cpu_model": cpu_model(),
                "sample": f"M={top['rows']} of {m} rows, K={k}, N={n}; AVX2 restatement of "
                          f"src/b1_0_kernel.h:79-239, gcc -O3 -mavx2 -mfma -mf16c -ffp-contract=off, "
                          f"ggml row split nth={share}; median of 3 ({top['s']:.2f} s)",
@@ -1026,6 +1071,8 @@ def main():
                                       "read_floor_GBps": round(vg["read_floor"]["GBps"], 1)}},
         "cpu_baseline": cpu,
     }
+    if exact:
+        line["exact"] = exact
     if configs:
         line["configs"] = configs
     print(json.dumps(line), flush=True)

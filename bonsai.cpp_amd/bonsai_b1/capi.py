@@ -2,12 +2,16 @@
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 from pathlib import Path
 
 _PKG = Path(__file__).resolve().parent.parent          # bonsai.cpp_amd/
 _REPO = _PKG.parent
-_LIB = _PKG / "lib" / "libbonsai_b1.so"
+# BONSAI_B1_LIB names another build of the same library (the host-sanitized
+# one of `make -C bonsai.cpp_amd sanitize`); by default the in-tree build.
+_LIB = Path(os.environ["BONSAI_B1_LIB"]).resolve() if os.environ.get("BONSAI_B1_LIB") else \
+    _PKG / "lib" / "libbonsai_b1.so"
 _HDR = _REPO / "include" / "bonsai_b1.h"
 
 BLOCK_SIZE = 32

@@ -87,9 +87,12 @@ DeviceInfo *current_device(int *dev_out) {
     return d.state == 1 ? &d : nullptr;
 }
 
-// This device's address of `scratch` (nullptr if its lookup failed).
+// This device's address of `scratch` (nullptr if its lookup fails), with
+// that device current.  A lookup that failed at the probe (say, while
+// another stream of the process was being captured) is tried again here.
 void *device_scratch(DeviceInfo *d) {
     std::lock_guard<std::mutex> lk(g_mu);
+    if (d->scratch_state != 1) lookup_scratch(d);
     return d->scratch_state == 1 ? d->scratch : nullptr;
 }
 
@@ -207,6 +210,30 @@ const char *bonsai_b1_status_string(int status) {
     }
 }
 
+static b1::LinearArgs linear_args(const float *act, int64_t lda, const void *w, int in_dim, int out_dim, int batch,
+                                  float *out, int64_t ldo, int32_t *nonfinite) {
+    b1::LinearArgs a;
+    a.act = act;
+    a.lda = lda;
+    a.w = static_cast<const uint8_t *>(w);
+    a.K = in_dim;
+    a.N = out_dim;
+    a.M = batch;
+    a.out = out;
+    a.ldo = ldo;
+    a.nonfinite = nonfinite;
+    return a;
+}
+
+// The workspace the kernel linear_impl picks for these arguments can use:
+// the FAST GEMM's range-safe packing and split-K partials; none for the
+// small-M kernel and EXACT mode.
+static size_t linear_need(const b1::LinearArgs &a, int mode, int num_cus) {
+    if (mode == BONSAI_B1_MODE_EXACT || mode == BONSAI_B1_MODE_GEMV) return 0;
+    if (mode != BONSAI_B1_MODE_GEMM && b1::gemv_supported(a)) return 0;
+    return b1::gemm_supported(a) ? b1::gemm_workspace_bytes_total(a, num_cus) : 0;
+}
+
 // Shared body of the two linear entry points.  ws_mode: 0 = library-owned
 // workspace, 1 = caller's (ws, ws_bytes; may be NULL / too small).
 static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim, int out_dim, int batch,
@@ -219,16 +246,7 @@ static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim,
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     if (batch == 0) return BONSAI_B1_OK;
 
-    b1::LinearArgs a;
-    a.act = act;
-    a.lda = lda;
-    a.w = static_cast<const uint8_t *>(w);
-    a.K = in_dim;
-    a.N = out_dim;
-    a.M = batch;
-    a.out = out;
-    a.ldo = ldo;
-    a.nonfinite = nonfinite;
+    const b1::LinearArgs a = linear_args(act, lda, w, in_dim, out_dim, batch, out, ldo, nonfinite);
 
     // the library's workspace for this stream (ws_mode 0), or the caller's
     WsLease lease;
@@ -240,7 +258,7 @@ static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim,
         }
     };
     auto gemm = [&]() {
-        workspace(b1::gemm_workspace_bytes_total(a, dev->num_cus));
+        workspace(linear_need(a, mode, dev->num_cus));
         return b1::launch_gemm(a, dev->num_cus, ws, ws_bytes, stream);
     };
     auto gemv = [&]() { return b1::launch_gemv(a, dev->num_cus, stream); };
@@ -315,8 +333,10 @@ int bonsai_b1_linear_f32_noalloc(const float *act, int64_t lda, const void *w, i
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     if (batch == 0) return BONSAI_B1_OK;
-    if (bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) > BONSAI_B1_NOALLOC_SCRATCH_BYTES)
-        return BONSAI_B1_ERR_SCRATCH;
+    // what the kernel this call runs would use (an unaligned call runs EXACT
+    // mode and needs none)
+    const b1::LinearArgs a = linear_args(act, lda, w, in_dim, out_dim, batch, out, ldo, nonfinite);
+    if (linear_need(a, mode, dev->num_cus) > BONSAI_B1_NOALLOC_SCRATCH_BYTES) return BONSAI_B1_ERR_SCRATCH;
     void *ws = device_scratch(dev);
     if (!ws) return BONSAI_B1_ERR_HIP;
     return linear_impl(act, lda, w, in_dim, out_dim, batch, out, ldo, mode, nonfinite, 1, ws,
@@ -674,13 +694,11 @@ static bool packed_path(const b1::LinearArgs &a, int mode) {
 size_t bonsai_b1_linear_epi_workspace_bytes(int batch, int in_dim, int out_dim, int kind, int mode) {
     if (batch <= 0 || in_dim <= 0 || out_dim <= 0 || in_dim % BONSAI_B1_BLOCK_SIZE) return 0;
     if (kind == BONSAI_B1_EPI_NONE) return bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode);
-    // either the range-safe packing (fused path) or the linear's output
-    // (separate pass) followed by the small-M kernel's packing
+    // either the range-safe packing (fused path) or the linear's fp32 output
+    // (separate pass; the linear then runs a kernel that needs no workspace
+    // of its own)
     const size_t pack = b1::gemm_packed_ok(batch, in_dim, out_dim) ? b1::pack_area_bytes(batch, in_dim) : 0;
-    const size_t y = epi_y_bytes(batch, out_dim) + bonsai_b1_workspace_bytes(batch, in_dim, out_dim,
-                                                                             mode == BONSAI_B1_MODE_EXACT
-                                                                                 ? mode
-                                                                                 : BONSAI_B1_MODE_GEMV);
+    const size_t y = epi_y_bytes(batch, out_dim);
     return pack > y ? pack : y;
 }
 
@@ -702,16 +720,7 @@ int bonsai_b1_linear_epi_f32(const float *act, int64_t lda, const void *w, int i
     DeviceInfo *dev = current_device(nullptr);
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     if (batch == 0) return BONSAI_B1_OK;
-    b1::LinearArgs a;
-    a.act = act;
-    a.lda = lda;
-    a.w = static_cast<const uint8_t *>(w);
-    a.K = in_dim;
-    a.N = out_dim;
-    a.M = batch;
-    a.out = out;
-    a.ldo = ldo;
-    a.nonfinite = nonfinite;
+    const b1::LinearArgs a = linear_args(act, lda, w, in_dim, out_dim, batch, out, ldo, nonfinite);
     const bool fused = packed_path(a, mode);
     // separate pass: y, then what the linear's own kernel can use
     const size_t y_bytes = epi_y_bytes(batch, out_dim);
@@ -878,13 +887,15 @@ static bool gemv_group_direct(const b1::LinearArgs &a) {
 // vec_silu at one token), at most kGemvGroupMax, whose outputs lie apart
 // from that input and from one another (the group writes them in no
 // particular order).  Returns the last op of the run, i when op i runs
-// alone; fills ops[0 .. last - i].
+// alone; fills ops[0 .. last - i].  pack_groups: a run that would read a
+// packing (more than kGemvGroupF32MaxM tokens) may form; when false (no
+// workspace to be had) its ops run one by one.
 template <class OpAt>
-static int gemv_span(int n_ops, int mode, OpAt at, int i, b1::GemvGroupOp *ops) {
+static int gemv_span(int n_ops, int mode, OpAt at, int i, b1::GemvGroupOp *ops, bool pack_groups) {
     const BatchOp bi = at(i);
     const b1::LinearArgs a = batch_args(*bi.op);
     if (epi_kind(bi.epi) != BONSAI_B1_EPI_NONE || batch_path(a, mode) != BatchPath::Gemv ||
-        !(gemv_group_direct(a) || b1::pack_supported(a.act, a.lda, a.M, a.K)))
+        !(gemv_group_direct(a) || (pack_groups && b1::pack_supported(a.act, a.lda, a.M, a.K))))
         return i;
     auto range = [](const void *p, int rows, int64_t ld, int cols, size_t elt, uintptr_t *r0, uintptr_t *r1) {
         *r0 = reinterpret_cast<uintptr_t>(p);
@@ -927,7 +938,7 @@ struct BatchAreas {
 };
 
 template <class OpAt>
-static BatchAreas batch_areas(int n_ops, int mode, int num_cus, OpAt at) {
+static BatchAreas batch_areas(int n_ops, int mode, int num_cus, OpAt at, bool pack_groups = true) {
     BatchAreas r;
     for (int i = 0; i < n_ops; ++i) {
         const BatchOp b = at(i);
@@ -936,7 +947,7 @@ static BatchAreas batch_areas(int n_ops, int mode, int num_cus, OpAt at) {
         const BatchPath path = batch_path(a, mode);
         if (path == BatchPath::Gemv) {
             b1::GemvGroupOp ops[b1::kGemvGroupMax];
-            const int last = gemv_span(n_ops, mode, at, i, ops);
+            const int last = gemv_span(n_ops, mode, at, i, ops, pack_groups);
             if (last > i) {
                 if (!gemv_group_direct(a)) r.pack = std::max(r.pack, b1::pack_area_bytes(a.M, a.K));
                 i = last;
@@ -985,12 +996,25 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
     if (!dev) return BONSAI_B1_ERR_DEVICE;
     BatchAreas areas = batch_areas(n_ops, mode, dev->num_cus, at);
     WsLease lease;
+    bool pack_groups = true;
     if (areas.need() > 0) {
         if (!workspace) {
             lease.acquire(dev, stream, areas.need());
             workspace = lease.ptr();
             workspace_bytes = workspace ? areas.need() : 0;
+            if (!workspace) {
+                // No library workspace to be had (a capture with no large
+                // enough buffer): grouped small-M runs that would read a
+                // packing run their ops one by one instead, which needs none.
+                const BatchAreas alone = batch_areas(n_ops, mode, dev->num_cus, at, false);
+                if (alone.need() == 0) {
+                    areas = alone;
+                    pack_groups = false;
+                }
+            }
         }
+    }
+    if (areas.need() > 0) {
         // a workspace without room for the split-K partials runs every GEMM
         // unsplit (the same outputs up to the order of the K summation)
         if (workspace && workspace_bytes < areas.need()) areas.split = 0;
@@ -1048,7 +1072,8 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
         int out_cols = kind == BONSAI_B1_EPI_SWIGLU ? a.N / 2 : a.N;
         const BatchPath path = batch_path(a, mode);
         b1::GemvGroupOp gops[b1::kGemvGroupMax];
-        const int glast = path == BatchPath::Gemv ? gemv_span(n_ops, mode, at, i, gops) : i;
+        const int first = i;
+        const int glast = path == BatchPath::Gemv ? gemv_span(n_ops, mode, at, i, gops, pack_groups) : i;
         const bool direct = glast > i && gemv_group_direct(a);
         hipError_t e = hipSuccess;
         // the range-safe packing of this op's input, unless the workspace
@@ -1112,7 +1137,8 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
             return BONSAI_B1_ERR_HIP;
         }
         // An output written over the packed activations' source invalidates
-        // the packing.
+        // the packing: every output of a grouped small-M run (all its ops
+        // share op i's batch), else op i's (or its fused run's) own.
         if (packed_act) {
             const uintptr_t p0 = reinterpret_cast<uintptr_t>(packed_act);
             const uintptr_t p1 = p0 + ((size_t)(packed_m - 1) * (size_t)packed_lda + (size_t)packed_k) * sizeof(float);
@@ -1121,7 +1147,10 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
                 const uintptr_t o1 = o0 + (size_t)(a.M - 1) * (size_t)ld_bytes + (size_t)row_bytes;
                 return o0 < p1 && p0 < o1;
             };
-            if (kind == BONSAI_B1_EPI_PACKED) {
+            if (glast > first) {
+                for (int j = 0; j <= glast - first; ++j)
+                    if (hits(gops[j].out, gops[j].ldo * 4, (int64_t)gops[j].N * 4)) packed_act = nullptr;
+            } else if (kind == BONSAI_B1_EPI_PACKED) {
                 // the fp32 columns and the packed fp16 columns
                 const int pcols = g.glu_h ? g.glu_h : a.N - g.split;
                 if ((g.split > 0 && hits(a.out, a.ldo * 4, (int64_t)g.split * 4)) ||

@@ -643,6 +643,31 @@ def test_gelu_tanh_matches_float64(torch, b1):
     assert bool((big[:, 1028:] == 0).all()), "padding untouched"
 
 
+def test_gelu_tanh_c4_size_matches_float64(torch, b1):
+    """The standalone GELU at the size the C4 MLP runs it (4608 x 12288, the
+    up-projection's output): 64 sampled rows, every element, within
+    GELU_TOL * max(1, |x|) of the float64 GELU; the rest of the matrix
+    finite and odd-symmetric in the sense gelu(x) - gelu(-x) = x (checked
+    on one more sampled block by a second launch over -x)."""
+    m, n = 4608, 12288
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    x = torch.randn((m, n), device="cuda", generator=g) * 3
+    y = b1.gelu_tanh(x)
+    yn = b1.gelu_tanh(-x)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all())
+    rows = np.random.default_rng(78).choice(m, 64, replace=False)
+    xs = x[rows].cpu().numpy()
+    err = np.abs(y[rows].cpu().numpy().astype(np.float64) - gelu64(xs)) / np.maximum(1.0, np.abs(xs))
+    say(f"  C4-size gelu, 64 sampled rows: max scaled err {err.max():.2e}")
+    assert err.max() <= GELU_TOL
+    # gelu(x) - gelu(-x) = x exactly in real arithmetic; in fp32 within the
+    # two evaluations' error bounds
+    d = (y - yn - x).abs() / torch.clamp(x.abs(), min=1.0)
+    assert float(d.max()) <= 2 * GELU_TOL + 2 ** -23
+
+
 def test_gelu_pack_matches_pack_of_gelu(torch, b1, oracle):
     """gelu_tanh_pack_f16 == the pack_act_f16 layout of fp16(gelu(x)): each
     fp16 is within half an fp16 ulp (its rounding) plus the fp32 GELU bound
@@ -696,6 +721,16 @@ def test_linear_batch_matches_single_calls(torch, b1, mode):
     # 9: reads x_over again: the stale packing must not be reused
     o8 = torch.empty((200, 600), device="cuda")
     ops.append((x_over, b1.device_weights(spec[0][1], 768, 600), o8))
+    # 10, 11: a grouped small-M run on z (8 tokens, read as fp32: no packing)
+    # whose SECOND op writes rows 8..15 of x_over; 12 reads x_over again, so
+    # the packing made for op 9 must be dropped for every op of the group
+    w_side = w(256, 3072, 18)
+    side = torch.empty((8, 256), device="cuda")
+    ops.append((z, b1.device_weights(w_side, 3072, 256), side))
+    w_over2 = w(768, 3072, 19)
+    ops.append((z, b1.device_weights(w_over2, 3072, 768), x_over[8:16]))
+    o12 = torch.empty((200, 600), device="cuda")
+    ops.append((x_over, b1.device_weights(spec[0][1], 768, 600), o12))
     b1.linear_batch(ops, mode=mode)
     torch.cuda.synchronize()
     for i, ((a, wt, n), o) in enumerate(zip(spec, outs)):
@@ -706,10 +741,15 @@ def test_linear_batch_matches_single_calls(torch, b1, mode):
     new_x = x.clone()
     b1.linear(z, w_over, 768, out=new_x[:8], mode=mode)
     ref8 = b1.linear(new_x, spec[0][1], 600, mode=mode)
+    ref_side = b1.linear(z, w_side, 256, mode=mode)
+    b1.linear(z, w_over2, 768, out=new_x[8:16], mode=mode)
+    ref12 = b1.linear(new_x, spec[0][1], 600, mode=mode)
     torch.cuda.synchronize()
     assert torch.equal(x_before, ref_before)
     assert torch.equal(x_over, new_x)
     assert torch.equal(o8, ref8)
+    assert torch.equal(side, ref_side)
+    assert torch.equal(o12, ref12), "a grouped op's output left a stale packing in use"
 
 
 def test_linear_batch_fuses_concatenated_qkv(torch, b1):

@@ -240,6 +240,40 @@ def test_pinned_workspace_survives_growth(torch, b1):
     torch.cuda.synchronize()
 
 
+def test_packed_small_m_group_under_capture_without_workspace(torch, b1):
+    """A batch of small-M ops on one 12-token input (a grouped run would read
+    a range-safe packing) captured on a stream the library has never seen
+    and with no caller workspace: a capture allocates nothing, so the ops
+    run one by one instead of failing.  Every replay equals the single
+    calls, with eager calls between the replays."""
+    from bonsai_b1 import synth
+    m, k = 12, 3072
+    ns = (1024, 640, 384)
+    x = synth.device_activations(m, k, 84)
+    ws = [synth.device_packed_weights(n, k, 85 + i) for i, n in enumerate(ns)]
+    refs = [b1.linear(x, w, n) for w, n in zip(ws, ns)]
+    outs = [torch.empty((m, n), device="cuda") for n in ns]
+    ops = [(x, b1.device_weights(w, k, n), o) for w, n, o in zip(ws, ns, outs)]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            b1.linear_batch(ops)
+    torch.cuda.synchronize()
+    other = synth.device_activations(300, k, 88)
+    for i in range(3):
+        for o in outs:
+            o.fill_(float(i + 1))
+        b1.linear(other, ws[0], ns[0])
+        g.replay()
+        torch.cuda.synchronize()
+        for j, (o, r) in enumerate(zip(outs, refs)):
+            assert torch.equal(o, r), f"replay {i}, op {j}"
+    del g
+    torch.cuda.synchronize()
+
+
 # ----------------------------------------------- one entry, one answer ---
 
 @pytest.mark.parametrize("m,k,n", [(256, 3072, 3072), (512, 9216, 3072), (37, 15360, 384)])

@@ -83,6 +83,26 @@ def test_noalloc_refuses_oversized_call(torch, lib):
                                             0, None, None) == capi.ERR_ARG
 
 
+def test_noalloc_takes_unaligned_call_of_any_size(torch, lib):
+    """The same oversized shape over activations that are not 16-byte
+    aligned (row stride K + 1): such a call runs EXACT mode, which needs no
+    workspace, so it is accepted and equals bonsai_b1_linear_f32 bit for
+    bit."""
+    from bonsai_b1 import capi, synth
+    m, k, n = 4608, 12288, 64
+    buf = torch.empty((m, k + 1), device="cuda")
+    buf[:, 1:] = synth.device_activations(m, k, 8)
+    a = buf[:, 1:]
+    w = synth.device_packed_weights(n, k, 9)
+    ref = torch.full((m, n), 3.0, device="cuda")
+    got = torch.full((m, n), 5.0, device="cuda")
+    say("no-alloc unaligned call")
+    assert _call(lib, torch, "bonsai_b1_linear_f32", a, w, n, ref, "auto") == capi.OK
+    assert _call(lib, torch, "bonsai_b1_linear_f32_noalloc", a, w, n, got, "auto") == capi.OK
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
 def test_noalloc_under_graph_capture(torch, lib):
     """Captured on a stream the library has never seen (so it owns no
     workspace for it, and a capture cannot allocate one), the no-alloc entry
