@@ -61,6 +61,12 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
 // area it needs (splits x M x N rounded up to 4 columns).
 int gemm_splits(int M, int K, int N, int num_cus);
 size_t gemm_split_bytes(int M, int N, int splits);
+// Whether the packed GEMM of this shape runs 144 x 384 tiles (16x16x32
+// MFMAs; plain and gate-residual epilogues) instead of 128 x 512: full
+// tiles, no split, and clearly fewer rounds on num_cus CUs.  A function of
+// the shape and CU count only, so every entry point picks alike; the two
+// tile kernels sum K in different orders (the same to ~1e-6 relative).
+bool gemm16_shape(int M, int K, int N, int num_cus);
 
 // The two halves of the workspace path.  Packed activations: u32 word
 // (row m, 16 j + d) = fp16(a[m][32 j + d]) | fp16(a[m][32 j + d + 16]) << 16,

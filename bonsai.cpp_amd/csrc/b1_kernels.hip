@@ -154,6 +154,10 @@ __device__ __forceinline__ void dma_buf_lds16s(__amdgpu_buffer_rsrc_t rsrc, void
 __device__ __forceinline__ void dma_buf_lds12s(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds, 12, voff, soff, 0, 0);
 }
+// 4 bytes per lane, landing at lds + 4 * lane.
+__device__ __forceinline__ void dma_buf_lds4(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds, 4, voff, 0, 0, 0);
+}
 
 __device__ __forceinline__ uint32_t dup_lo16(uint32_t d) {
     return __builtin_amdgcn_perm(d, d, 0x01000100u);
@@ -1718,6 +1722,439 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
     }
 }
 
+// ---------------------------------------------------------------- gemm16 --
+//
+// The same GEMM over 144 x 384 tiles with 16x16x32 MFMAs, for shapes whose
+// 128 x 512 tiles quantise badly on 256 CUs: at M = 4608 (Flux image +
+// text tokens) N = 3072 gives 216 tiles of 128 x 512 (one round at 84 % of
+// the CUs) but exactly 256 of 144 x 384, and N = 9216 gives 648 (2.53
+// rounds, run as 3) but exactly 768 (3 full rounds).  A 144 x 384 tile is
+// 0.84 of a 128 x 512 one.
+//
+// Eight waves side by side along N, each 144 tokens x 48 columns: 9 x 3
+// tiles of 16x16, weights as the MFMA's A operand (16 output columns x 32
+// K), tokens as B.  Lane (li, g) of a 16x16x32 operand holds K indices
+// 8g .. 8g + 7 of row li: with the K-slot pairing, dword t of them is
+// packed word 4g + t of the 32-element block (elements 4g + t and
+// 4g + t + 16), i.e. 16-byte chunk g of the block's 64 bytes of packed
+// activations, and on the weight side the sign bits 4g + t and 4g + t + 16:
+// the sign word shifted right by 4g, then one shift by 15 - t and one bit
+// op per dword, as in the 32x32 kernel.  The accumulator's lane (li, g)
+// holds output columns 4g .. 4g + 3 of token li: one 16-byte store.
+//
+// Pipeline and LDS as in b1_gemm_kernel: K in stages of 128 (4 blocks), a
+// three-slot ring fetched two stages ahead with buffer loads straight into
+// LDS, one barrier per stage with counted vmcnt waits.  A stage is 144 rows
+// x 256 bytes of activations (36 loads of 1 KB) and 384 columns x 24 bytes
+// of weights (six 64-column groups, two 12-byte loads each): waves 0-5 load
+// 4 activation kilobytes and weight group w, waves 6-7 six activation
+// kilobytes, so every wave issues 6 loads a stage and the waits are
+// uniform.  Activation row r's chunk c sits at position c ^ (r & 15), so the
+// 16 lanes of a fragment read (rows li, one chunk) hit distinct banks.
+// Full tiles only (M % 144, N % 384, K % 384 == 0); EPI 0 plain, 1
+// gate-residual (GemmEpi); row scales of range-safe packing as in the
+// 32x32 kernel.
+template <int BM_, int BN_>
+struct Gemm16Cfg {
+    static constexpr int BM = BM_, BN = BN_, NW = 8, NT = NW * 64;
+    static constexpr int WN = BN / NW, MT = BM / 16, NTL = WN / 16;
+    static constexpr int STAGES = 3, KC = 128, ROWB = 256;
+    static constexpr int ASTAGE = BM * ROWB;            // activation bytes per slot
+    static constexpr int NWG = BN / 64;                 // 64-column weight load groups
+    static constexpr int BSTAGE = NWG * 2048;           // weight bytes per slot
+    static constexpr int ABASE = STAGES * BSTAGE;       // weights first
+    static constexpr int RSC = ABASE + STAGES * ASTAGE;
+    static constexpr int RSCN = (BM + 63) / 64 * 64;    // row scales per parity (64 per copying wave)
+    static constexpr int LDS = RSC + 2 * RSCN * 4;
+    static constexpr int GROUP_M = 4;
+    // loads per wave per stage, the same for every wave: waves 0 .. NWG - 1
+    // load a weight group (2 loads) and AW activation kilobytes, the others
+    // LOADS activation kilobytes
+    static constexpr int ALOADS = ASTAGE / 1024;
+    static constexpr int LOADS = (ALOADS + 2 * NWG) / NW;
+    static constexpr int AW = LOADS - 2;
+    static constexpr int AHEAD = (STAGES - 2) * LOADS;
+    static constexpr int EPI_STORES = MT * NTL;         // 16-byte stores per lane, full tile
+    static_assert(BM % 16 == 0 && WN % 16 == 0 && BN % 64 == 0 && NWG <= NW, "tile shape");
+    static_assert(LOADS * NW == ALOADS + 2 * NWG && AW * NWG + LOADS * (NW - NWG) == ALOADS, "uniform loads");
+    static_assert(LDS <= 160 * 1024, "gfx950 LDS");
+    static_assert(EPI_STORES + AHEAD <= 63, "vmcnt holds 6 bits");
+    static_assert((MT - 1) * 16 * ROWB + 16 * ROWB <= 65536, "fragment immediates");
+};
+
+template <int BM, int BN, int EPI>
+__global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(const uint16_t *__restrict__ ah,
+                                                                     const uint8_t *__restrict__ w, int K, int N, int M,
+                                                                     float *__restrict__ out, int64_t ldo,
+                                                                     int32_t *nonfinite, int tiles_m, int tiles_n,
+                                                                     int vec_store, GemmEpi epi) {
+    using C = Gemm16Cfg<BM, BN>;
+    static_assert(EPI == 0 || EPI == 1, "plain and gate-residual epilogues");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15, g = lane >> 4;
+    const int nstage = K / C::KC; // a multiple of STAGES
+    const int ntiles = tiles_m * tiles_n;
+    const uint32_t rs = (uint32_t)(K / 32) * 6;
+
+    auto tile_origin = [&](int t, int &m0, int &n0) {
+        const int group = t / (C::GROUP_M * tiles_n);
+        const int first_m = group * C::GROUP_M;
+        const int gsize = min(C::GROUP_M, tiles_m - first_m);
+        const int tin = t - first_m * tiles_n;
+        m0 = (first_m + tin % gsize) * C::BM;
+        n0 = (tin / gsize) * C::BN;
+    };
+
+    // Loads of a stage.  Activation load j (0..35) fills LDS bytes
+    // [1024 j, +1024) of the slot: rows 4j .. 4j + 3, lane L at position
+    // L % 16 of row 4j + L / 16, holding chunk (L % 16) ^ (row & 15).  Waves
+    // 0-5 issue loads 4w .. 4w + 3, waves 6-7 24 + 6 (w - 6) .. + 5.  Weight
+    // group q (waves 0-5, q = w): lane L fetches 12 bytes (blocks 0-1, then
+    // 2-3 of the stage) of column n0 + 64 q + L.  Rows and columns past the
+    // matrix cannot occur (full tiles).
+    const bool wload = wave < C::NWG;
+    const int a_first = wload ? C::AW * wave : C::AW * C::NWG + C::LOADS * (wave - C::NWG);
+    uint32_t aoff[C::LOADS];
+    uint32_t boff = 0;
+    auto setup = [&](int m0, int n0) {
+#pragma unroll
+        for (int i = 0; i < C::LOADS; ++i) {
+            const int row = 4 * (a_first + i) + (lane >> 4);
+            const int c = (lane & 15) ^ (row & 15);
+            aoff[i] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)c * 8) * 2;
+        }
+        boff = (uint32_t)(n0 + 64 * (wload ? wave : 0) + lane) * rs;
+    };
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(ah), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(w), (short)0, (int)((uint32_t)N * rs), kBufferFlags);
+    auto issue = [&](int ks, int slot) {
+        uint8_t *sa = smem + C::ABASE + slot * C::ASTAGE + a_first * 1024;
+        const uint32_t aso = (uint32_t)ks * C::ROWB, wso = (uint32_t)ks * 24;
+        if (wload) {
+#pragma unroll
+            for (int i = 0; i < C::AW; ++i) dma_buf_lds16s(ars, sa + i * 1024, aoff[i], aso);
+            uint8_t *sw = smem + slot * C::BSTAGE + wave * 2048;
+            dma_buf_lds12s(wrs, sw, boff, wso);
+            dma_buf_lds12s(wrs, sw + 1024, boff, wso + 12);
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::LOADS; ++i) dma_buf_lds16s(ars, sa + i * 1024, aoff[i], aso);
+        }
+    };
+
+    // Fragment addresses.  Activations: lane (li, g), block j of the stage,
+    // row tile mt: row 16 mt + li, chunk 4 j + g at position (4 j + g) ^ li,
+    // 256-byte rows; one LDS pointer per (slot, j), the row tile an
+    // immediate.  Weights: the wave's 16-column chunk q = 3 wave + nt of the
+    // tile lies in load group q / 4 at column (q % 4) 16 + li, 16 bytes a
+    // column in each 1 KB half.
+    typedef const __attribute__((address_space(3))) uint8_t lds_u8;
+    lds_u8 *const lbase = (lds_u8 *)smem;
+    // Slots 0 and 1 share one pointer set (slot 1 an immediate away) when
+    // their offsets stay below the 64 KiB immediate range; slot 2 has its own.
+    constexpr bool SHARE01 = C::ASTAGE + (C::MT - 1) * 16 * C::ROWB < 65536;
+    lds_u8 *fa[2][4];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            fa[sl][j] = lbase + C::ABASE + (sl ? 2 : 0) * C::ASTAGE + li * C::ROWB + (((4 * j + g) ^ li) * 16);
+    auto frag_ptr = [&](int slot, int j) -> lds_u8 * {
+        if constexpr (SHARE01) return slot == 2 ? fa[1][j] : fa[0][j] + slot * C::ASTAGE;
+        return fa[0][j] + slot * C::ASTAGE;
+    };
+    // Weights: with 4 column tiles a wave (NTL % 4 == 0) they are one load
+    // group's consecutive 256-byte quarters, an immediate apart.
+    lds_u8 *qw[C::NTL % 4 == 0 ? 1 : C::NTL];
+    if constexpr (C::NTL % 4 == 0) {
+        qw[0] = lbase + (C::NTL * wave >> 2) * 2048 + li * 16;
+    } else {
+#pragma unroll
+        for (int nt = 0; nt < C::NTL; ++nt) {
+            const int q = C::NTL * wave + nt;
+            qw[nt] = lbase + (q >> 2) * 2048 + ((q & 3) * 16 + li) * 16;
+        }
+    }
+    auto wcol_ptr = [&](int nt) -> lds_u8 * {
+        if constexpr (C::NTL % 4 == 0) return qw[0] + (nt >> 2) * 2048 + (nt & 3) * 256;
+        return qw[nt];
+    };
+
+    floatx4 acc[C::MT][C::NTL];
+
+    // One stage: 4 steps (blocks) x MT row tiles.  The wave's weight dwords
+    // of blocks 0-1 are read at the stage top and those of blocks 2-3, into
+    // the same registers, once step 1's weights have been expanded (during
+    // step 0); activation fragments stream through a ring of 4, three row
+    // tiles ahead (across steps); the weights of step j + 1 are expanded one
+    // 16-column tile per row tile at the start of step j, while its MFMAs
+    // run.  A scheduling fence per row tile keeps the compiler from hoisting
+    // every read of the stage.
+    static_assert(C::NTL + 1 < C::MT, "weight reads of blocks 2-3 inside step 0");
+    auto compute = [&](int slot, auto &&after_first_reads) {
+        uint32_t d[C::NTL][3];
+        auto read_w = [&](int bp) {
+#pragma unroll
+            for (int nt = 0; nt < C::NTL; ++nt) {
+                const __attribute__((address_space(3))) uint32_t *q =
+                    reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
+                        wcol_ptr(nt) + slot * C::BSTAGE + bp * 1024);
+                d[nt][0] = q[0];
+                d[nt][1] = q[1];
+                d[nt][2] = q[2];
+            }
+        };
+        read_w(0);
+        constexpr int R = 4, DIST = 3, NF = 4 * C::MT;
+        half8 af[R];
+        auto read_frag = [&](int f) {
+            const int j = f / C::MT, mt = f % C::MT;
+            af[f % R] = *reinterpret_cast<const __attribute__((address_space(3))) half8 *>(frag_ptr(slot, j) +
+                                                                                            mt * 16 * C::ROWB);
+        };
+#pragma unroll
+        for (int f = 0; f < DIST; ++f) read_frag(f);
+        after_first_reads();
+        // LATE: with 4 column tiles a wave, one buffer of expanded weights:
+        // tile nt of step j + 1 is expanded into tile nt's registers right
+        // after step j's last MFMA with them (two buffers would not fit
+        // beside 128 accumulators without spills)
+        constexpr bool LATE = C::NTL >= 4;
+        u32x4 bw[LATE ? 1 : 2][C::NTL];
+        // block j's scale and sign word sit at 6 (j % 2) bytes into the
+        // 12-byte pair held in d
+        auto expand = [&](int j, int nt, u32x4 &bo) {
+            const uint32_t *dd = d[nt];
+            uint32_t s2, wg;
+            if ((j & 1) == 0) {
+                s2 = dup_lo16(dd[0]);
+                // the sign word of block j, shifted right by 4g (bits above
+                // 27 are not those of the plain shift; only bits t and
+                // 16 + t, t < 4, reach the mask)
+                wg = __builtin_amdgcn_alignbit(dd[1], dd[0], 16 + 4 * g);
+            } else {
+                s2 = dup_hi16(dd[1]);
+                wg = dd[2] >> (4 * g);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) bo[t] = wpair(wg, 15 - t, s2);
+        };
+#pragma unroll
+        for (int nt = 0; nt < C::NTL; ++nt) expand(0, nt, bw[0][nt]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const int j = f / C::MT, mt = f % C::MT;
+            if (f + DIST < NF) read_frag(f + DIST);
+            if constexpr (LATE) {
+                if (j == 1 && mt == 0) read_w(1);
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt) {
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, bw[0][nt]),
+                                                                         af[f % R], acc[mt][nt], 0, 0, 0);
+                    if (j + 1 < 4 && mt == C::MT - 1) expand(j + 1, nt, bw[0][nt]);
+                }
+            } else {
+                if (j + 1 < 4 && mt < C::NTL) expand(j + 1, mt, bw[(j + 1) & 1][mt]);
+                if (j == 0 && mt == C::NTL) read_w(1);
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, bw[j & 1][nt]),
+                                                                         af[f % R], acc[mt][nt], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    auto count_tile = [&](int &bad) {
+        if (nonfinite != nullptr) {
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) bad += !__builtin_isfinite(acc[mt][nt][v]);
+        }
+    };
+    auto stride_bytes = [](int64_t ld) {
+        int b = (int)ld * 4;
+        asm volatile("" : "+s"(b));
+        return b;
+    };
+    // Lane (li, g) of tile (mt, nt): token m0 + 16 mt + li, columns
+    // n0 + 48 wave + 16 nt + 4 g .. + 3: one 16-byte store each (27 per
+    // lane), half a line per 4 lanes.  Without vec_store (out, or the
+    // residual and gate, not 16-byte aligned rows) the same values go out
+    // as scalar stores.  Returns whether EPI_STORES vector stores are in
+    // flight.
+    auto epilogue = [&](int m0, int n0) -> bool {
+        int bad = 0;
+        count_tile(bad);
+        if (!vec_store) {
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const size_t m = (size_t)(m0 + 16 * mt + li);
+                        const int n = n0 + C::WN * wave + 16 * nt + 4 * g + e;
+                        float y = acc[mt][nt][e];
+                        if constexpr (EPI == 1) y = gate_residual(epi.res[m * epi.ldr + n], epi.gate[n], y);
+                        out[m * ldo + n] = y;
+                    }
+            count_nonfinite(nonfinite, bad);
+            return false;
+        }
+        const int ldb = stride_bytes(ldo);
+        const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+            out + (size_t)m0 * ldo + n0 + C::WN * wave, (short)0, (int)(C::BM * ldo * 4), kBufferFlags);
+        const int lvoff = li * ldb + 16 * g;
+        if constexpr (EPI == 0) {
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt) {
+                    u32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x = acc[mt][nt][e];
+                        v[e] = __builtin_bit_cast(uint32_t, x);
+                    }
+                    store16_guarded<kStoreNT>(v, ors, lvoff, mt * 16 * ldb + nt * 64);
+                }
+        } else {
+            // out = residual + gate[n] * y, the residual read at the same
+            // places P tiles ahead; it may be `out` itself: each element is
+            // read by the lane that writes it, before that write
+            const int lrb = stride_bytes(epi.ldr);
+            const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(epi.res) + (size_t)m0 * epi.ldr + n0 + C::WN * wave, (short)0,
+                (int)(C::BM * epi.ldr * 4), kBufferFlags);
+            const int lroff = li * lrb + 16 * g;
+            floatx4 gq[C::NTL];
+#pragma unroll
+            for (int nt = 0; nt < C::NTL; ++nt)
+                gq[nt] = *reinterpret_cast<const floatx4 *>(epi.gate + n0 + C::WN * wave + 16 * nt + 4 * g);
+            constexpr int NP = C::MT * C::NTL, P = 6;
+            u32x4 rv[NP];
+            auto load_res = [&](int p) {
+                const int mt = p / C::NTL, nt = p % C::NTL;
+                rv[p] = __builtin_amdgcn_raw_buffer_load_b128(rrs, lroff, mt * 16 * lrb + nt * 64, 0);
+            };
+#pragma unroll
+            for (int p = 0; p < P; ++p) load_res(p);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                if (p + P < NP) load_res(p + P);
+                const int mt = p / C::NTL, nt = p % C::NTL;
+                u32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // elements copied out before any bit cast (a bit cast of
+                    // a vector element reads element 0 in this clang)
+                    const float y = acc[mt][nt][e];
+                    const uint32_t ru = rv[p][e];
+                    const float ov = gate_residual(__builtin_bit_cast(float, ru), gq[nt][e], y);
+                    o[e] = __builtin_bit_cast(uint32_t, ov);
+                }
+                store16_guarded<kStoreNT>(o, ors, lvoff, mt * 16 * ldb + nt * 64);
+            }
+        }
+        count_nonfinite(nonfinite, bad);
+        return true;
+    };
+
+    int unit = xcd_tile(blockIdx.x, gridDim.x);
+    int m0, n0;
+    const bool rows_scaled = epi.rsc != nullptr;
+    int parity = 0;
+    // Row scales of the tile: waves 0 .. RSCN / 64 - 1 copy 64 each (entries
+    // past BM are never read), ahead of the tile's first stage.  The
+    // buffer form of the copy: with a global-form LDS copy in the kernel the
+    // compiler makes every LDS wait a full lgkmcnt(0), which here would also
+    // wait for the fragment reads issued ahead.
+    const __amdgpu_buffer_rsrc_t rsrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(epi.rsc), (short)0, rows_scaled ? M * 4 : 0, kBufferFlags);
+    auto issue_rsc = [&](int par) {
+        if (rows_scaled && wave < C::RSCN / 64)
+            dma_buf_lds4(rsrs, smem + C::RSC + par * C::RSCN * 4 + wave * 256,
+                         (uint32_t)min(m0 + 64 * wave + lane, M - 1) * 4u);
+    };
+    tile_origin(unit, m0, n0);
+    setup(m0, n0);
+    issue_rsc(parity);
+#pragma unroll
+    for (int t = 0; t < C::STAGES - 1; ++t) issue(t, t);
+    bool prev_stores = false; // the previous epilogue's EPI_STORES stores are in flight
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+            for (int j = 0; j < C::NTL; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // At the top of stage s the wave waits for its own loads of stage s
+        // (at most stage s + 1's LOADS newer, plus in the first two stages of
+        // a tile the previous tile's stores, issued after this tile's stages
+        // 0 and 1; a gate-residual epilogue also issued its loads before
+        // those stores, which only adds older operations), then the barrier
+        // publishes every wave's part and retires all reads of the slot
+        // that stage s + 2 then refills.
+        for (int s = 0; s < nstage; s += C::STAGES) {
+#pragma unroll
+            for (int u = 0; u < C::STAGES; ++u) {
+                if (s + u + 1 >= nstage)
+                    wait_vmcnt<0>();
+                else if (s == 0 && u < C::STAGES - 1 && prev_stores)
+                    wait_vmcnt<C::EPI_STORES + C::AHEAD>();
+                else if (s == 0 && u == 0)
+                    wait_vmcnt<0>(); // after scalar stores (or the first tile)
+                else
+                    wait_vmcnt<C::AHEAD>();
+                lds_barrier();
+                compute(u, [&] {
+                    if (s + u + C::STAGES - 1 < nstage) issue(s + u + C::STAGES - 1, (u + C::STAGES - 1) % C::STAGES);
+                });
+            }
+        }
+        // Slots 0 and 1 were last read before the final barrier: fetch the
+        // next tile's first two stages now, then store this tile.
+        const int cm0 = m0, cn0 = n0, cpar = parity;
+        unit += gridDim.x;
+        const bool more = unit < ntiles;
+        if (more) {
+            tile_origin(unit, m0, n0);
+            setup(m0, n0);
+            parity ^= 1;
+            issue_rsc(parity);
+#pragma unroll
+            for (int t = 0; t < C::STAGES - 1; ++t) issue(t, t);
+        }
+        if (rows_scaled) {
+            const float *rsp = reinterpret_cast<const float *>(smem + C::RSC + cpar * C::RSCN * 4);
+            float sc[C::MT];
+            int any = 0;
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt) {
+                sc[mt] = rsp[16 * mt + li];
+                any |= sc[mt] != 1.0f;
+            }
+            if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[mt][nt][v] *= sc[mt];
+            }
+        }
+        prev_stores = epilogue(cm0, cn0);
+        if (!more) break;
+    }
+}
+
 // Split-K reduction: out[m][n] = sum over s = 0..S-1, in that order, of
 // part[s][m][n] (slices pstride apart, rows ldp apart, ldp % 4 == 0), with
 // the non-finite count of the sums.
@@ -2821,12 +3258,73 @@ size_t gemm_split_bytes(int M, int N, int splits) {
     return splits > 1 ? (size_t)splits * (size_t)M * (size_t)((N + 3) & ~3) * sizeof(float) : 0;
 }
 
+// Rounds of the 128 x 512 kernel's persistent grid, in units of one round
+// of full tiles: ceil(tiles / slots), or, where launch_gemm_packed_t runs
+// the last partial round as 64-row tiles, the full rounds plus ~0.6.
+static double gemm_rounds128(int M, int N, int num_cus) {
+    const int tiles_n = (N + kBN - 1) / kBN, tiles = ((M + kBM - 1) / kBM) * tiles_n;
+    const int slots = num_cus * kWgPerCu;
+    const int full = tiles / slots * slots, head_rows = full / tiles_n;
+    const int tail_tiles = ((M - head_rows * kBM + kBMH - 1) / kBMH) * tiles_n;
+    if (full > 0 && full < tiles && tiles_n < slots && head_rows > 0 && tail_tiles <= slots)
+        return full / slots + 0.6;
+    return (double)((tiles + slots - 1) / slots);
+}
+
+bool gemm16_shape(int M, int K, int N, int num_cus) {
+    using C = Gemm16Cfg<144, 384>;
+    if (num_cus <= 0 || !gemm_packed_ok(M, K, N) || M % C::BM || N % C::BN || K % (C::KC * C::STAGES)) return false;
+    if (gemm_splits(M, K, N, num_cus) > 1) return false;
+    const int tiles = (M / C::BM) * (N / C::BN);
+    // a 144 x 384 tile is 0.84 of a 128 x 512 one; take it when its rounds
+    // are clearly fewer (at M = 4608 on 256 CUs: N = 3072 and 9216, not
+    // 12288, whose partial round the 128 x 512 kernel runs as 64-row tiles)
+#ifdef B1_NO_GEMM16
+    return false;
+#endif
+    const double r16 = (double)((tiles + num_cus - 1) / num_cus) * (double)(C::BM * C::BN) / (kBM * kBN);
+    return r16 < 0.9 * gemm_rounds128(M, N, num_cus);
+}
+
+template <int BM, int BN, int EPI>
+static hipError_t launch_gemm16_t(const void *packed, const uint8_t *w, int K, int N, int M, float *out, int64_t ldo,
+                                  int32_t *nonfinite, int num_cus, const GemmEpi &epi, hipStream_t s) {
+    using C = Gemm16Cfg<BM, BN>;
+    auto kernel = &b1_gemm16_kernel<BM, BN, EPI>;
+    static std::once_flag attr_once;
+    static hipError_t attr_err = hipSuccess;
+    std::call_once(attr_once, [kernel] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+    });
+    if (attr_err != hipSuccess) return attr_err;
+    auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    // 16-byte rows, and BM rows of a buffer resource under 2^31 bytes
+    int vec_store = al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 21);
+    if (EPI == 1)
+        vec_store = vec_store && al16(epi.res) && al16(epi.gate) && epi.ldr % 4 == 0 && epi.ldr < (int64_t(1) << 21);
+    const int tiles_m = M / C::BM, tiles_n = N / C::BN, tiles = tiles_m * tiles_n;
+    const int grid = tiles < num_cus ? tiles : num_cus; // persistent
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(C::NT), C::LDS, s, static_cast<const uint16_t *>(packed), w, K, N, M,
+                       out, ldo, nonfinite, tiles_m, tiles_n, vec_store, epi);
+    return hipGetLastError();
+}
+
 template <int EPI>
 static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int K, int N, int M, float *out,
                                        int64_t ldo, int32_t *nonfinite, int num_cus, const GemmEpi &epi,
                                        hipStream_t s, int ksplit = 1, float *partials = nullptr) {
     // (with ksplit > 1 the row scales epi.rsc go to the reduction, not the
     // GEMM, which writes plain partial products)
+    if constexpr (EPI == 0 || EPI == 1) {
+        if (!(ksplit > 1 && partials != nullptr) && gemm16_shape(M, K, N, num_cus))
+            return launch_gemm16_t<144, 384, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
+#ifdef B1_GEMM16_128
+        if (!(ksplit > 1 && partials != nullptr) && gemm_packed_ok(M, K, N) && M % 128 == 0 && N % 512 == 0 &&
+            gemm_splits(M, K, N, num_cus) == 1)
+            return launch_gemm16_t<128, 512, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
+#endif
+    }
     auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages, EPI>;
     static std::once_flag attr_once;
     static hipError_t attr_err = hipSuccess;
