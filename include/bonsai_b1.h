@@ -155,9 +155,12 @@ void bonsai_b1_release_workspaces(void);
  * of the activations and the split-K partials) is a static device array of
  * BONSAI_B1_NOALLOC_SCRATCH_BYTES that the library holds on each device it
  * runs on until the process ends.  Never calls hipMalloc or hipFree.
- * Returns BONSAI_B1_ERR_SCRATCH, launching nothing, when the call needs
- * more than that (bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) >
- * BONSAI_B1_NOALLOC_SCRATCH_BYTES).  Every call on a device shares that
+ * Returns BONSAI_B1_ERR_SCRATCH, launching nothing, when the kernel the
+ * call runs needs more than that (for aligned activations,
+ * bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) >
+ * BONSAI_B1_NOALLOC_SCRATCH_BYTES; activations that are not 16-byte
+ * aligned, or lda % 4 != 0, run EXACT mode, which needs none, at any
+ * size).  Every call on a device shares that
  * device's array and leaves its contents behind: calls that overlap in time
  * on one device (other streams, other threads) race and must be serialised
  * by the caller; calls on one stream are ordered.
