@@ -114,6 +114,37 @@ def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto", inputs=Non
             "frac": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "wall_s": wall, "inputs": (a, w)}
 
 
+TILES16_SHAPES = [("c3_qkv", (4608, 3072, 9216), "none"), ("c3_out", (4608, 3072, 3072), "none"),
+                  ("c4_down", (4608, 12288, 3072), "none"), ("c5_linear2", (4608, 15360, 3072), "gate_residual")]
+
+
+def bench_tiles16(torch, b1, synth, steps, warmup):
+    """The 144 x 384 tile GEMM (b1_gemm16_kernel) alone at the M = 4608
+    shapes it runs: packed activations made once, then the packed entry
+    (range-safe row scales, or the gate-residual epilogue for C5's linear2)
+    timed with HIP events on its launch stream."""
+    out = {}
+    for name, (m, k, n), epi in TILES16_SHAPES:
+        a = synth.device_activations(m, k, 21)
+        w = synth.device_packed_weights(n, k, 22)
+        pa, rs = b1.pack_act_f16_scaled(a)
+        y = torch.empty((m, n), device="cuda")
+        if epi == "gate_residual":
+            g = 0.1 * torch.randn(n, device="cuda")
+            r = torch.randn((m, n), device="cuda")
+            fn = lambda i: b1.linear_packed_f16_epi(pa, w, k, n, m, "gate_residual", gate=g, residual=r, out=y)
+        else:
+            fn = lambda i: b1.linear_packed_f16_scaled(pa, rs, w, k, n, m, out=y)
+        ms, _ = time_launches(torch, fn, steps, warmup)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out[name] = {"shape": [m, k, n], "epilogue": epi, "kernel_us": round(ms * 1e3, 2), "tflops": round(tf, 1),
+                     "frac": round(tf / PEAK_FP16_TFLOPS, 4)}
+        log(f"[bench] 144 x 384 tiles {name} {(m, k, n)} {epi}: {ms * 1e3:.1f} us {tf:.1f} TFLOP/s "
+            f"({100 * tf / PEAK_FP16_TFLOPS:.1f}% of peak)")
+        del a, w, pa, rs, y
+    return out
+
+
 def bench_step_kernels(torch, b1, a, w, n, steps, warmup):
     """The two kernels of the step, each timed alone with HIP events on its
     launch stream: the GEMM kernel over packed activations
@@ -893,7 +924,7 @@ def main():
     ap.add_argument("--all", action="store_true", help="also time the secondary legs (stderr and JSON)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1/C3/C4/C5 config legs")
-    ap.add_argument("--only", choices=["gemm", "gemv", "copy", "c5chain"], default=None,
+    ap.add_argument("--only", choices=["gemm", "gemv", "copy", "c5chain", "tiles16"], default=None,
                     help="run one leg only (profiler runs); prints that leg's numbers")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -911,6 +942,14 @@ def main():
     if args.only == "copy":
         c = bench_copy(torch, 256 << 20, args.steps, args.warmup)
         print(json.dumps({"copy": c}), flush=True)
+        return
+    if args.only == "tiles16":
+        a = synth.device_activations(4608, 3072, 1)
+        w = synth.device_packed_weights(3072, 3072, 2)
+        settle_s, sclk = settle_clock(torch, lambda i: b1.linear(a, w, 3072), args.settle_s)
+        del a, w
+        t16 = bench_tiles16(torch, b1, synth, args.steps, args.warmup)
+        print(json.dumps({"tiles16": t16, "sclk_mhz": sclk}), flush=True)
         return
     if args.only == "c5chain":
         ch = bench_c5_block_chain(torch, b1, synth, producer_form=True)
