@@ -965,7 +965,7 @@ template <int BM, int BN, int WN, int STAGES_>
 struct GemmLdsCfg {
     static constexpr int NW = BN / WN, NT = NW * 64;
     static constexpr int MT = BM / 32, NTL = WN / 32;
-    static constexpr int STAGES = STAGES_;            // ring slots, fetched STAGES-1 ahead
+    static constexpr int STAGES = STAGES_;            // ring slots, fetched one stage ahead
     static constexpr int KC = 128;                    // K per stage (4 blocks)
     static constexpr int ROWB = KC * 2;               // LDS bytes per activation row
     static constexpr int ASTAGE = BM * ROWB;          // activation bytes per slot
@@ -984,18 +984,13 @@ struct GemmLdsCfg {
     static_assert(ASTAGE % (1024 * NW) == 0, "activation loads must split evenly");
     static_assert(WN % 64 == 0, "weight loads cover 64 columns, one per lane");
     static_assert(LDS <= 160 * 1024, "gfx950 LDS");
-    // vector memory operations that may be newer than stage s at its top:
-    // the STAGES-2 stages fetched after it, plus at a tile's start the
-    // previous tile's stores
-    static constexpr int AHEAD = (STAGES - 2) * (LPW + 2 * CG);
     // The previous tile's stores are counted in vmcnt waits when the count
     // fits its 6 bits; otherwise a tile starts by draining them.
-    static constexpr bool COUNT_STORES = EPI_STORES + AHEAD <= 63;
+    static constexpr bool COUNT_STORES = EPI_STORES <= 63;
     // 8 waves: 2 per SIMD, 256 registers each.  4 waves (128-column wave
     // tiles, 256 accumulators): 1 per SIMD with 512.
     static constexpr int WAVES_PER_SIMD = NW >= 8 ? 2 : 1;
     static_assert(STAGES == 3, "the three-slot ring is the verified configuration");
-    static_assert(AHEAD <= 63, "vmcnt holds 6 bits");
 };
 
 // Two waves per SIMD (8 waves, one work-group per CU): 256 registers a wave.
@@ -1632,8 +1627,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
     unit_origin(unit);
     setup(m0, n0);
     issue_rsc(parity);
-#pragma unroll
-    for (int t = 0; t < STAGES - 1; ++t) issue(kst0 + t, t);
+    issue(kst0, 0);
     int prev_stores = 0; // what the previous epilogue left in flight (its return value)
     for (;;) {
 #pragma unroll
@@ -1643,47 +1637,45 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-        // Pipeline (stage s in slot s % 3).  At the top of stage s the wave
-        // waits for its own loads of stage s, then the barrier publishes
-        // every wave's part of stage s and retires all reads of slot
-        // (s+2) % 3 (stage s-1's), which stage s+2's loads then refill.
-        // Vector memory operations retire in issue order and loads and
-        // stores share vmcnt, so "stage s has landed" is "at most the
-        // operations issued after it are outstanding": stage s+1's LPW + 2
-        // loads, plus, in the first two stages of a tile, the previous
-        // tile's 32 (or 16) vector stores per lane, issued after stages 0
-        // and 1 of this tile (a gate-residual epilogue also issued loads
-        // there, which only adds to the operations after those stages).
-        // Those stores thus drain under two stages of MFMA work instead of
-        // stalling the tile change.  A ragged previous tile stored a
-        // variable count with scalar stores: wait for everything.
-        // Unrolled by three so that slots are compile-time; the stage count
-        // is a multiple of three, so the loop has no exit mid-body.
+        // Pipeline (stage s in slot s % 3), loads one stage ahead.  At the
+        // top of stage s the wave waits for its own loads of stage s, then
+        // the barrier publishes every wave's part of stage s and retires all
+        // reads of stage s-1, and stage s+1's loads go to slot (s+1) % 3 (its
+        // last reader was stage s-2).  Vector memory operations retire in
+        // issue order and loads and stores share vmcnt, so "stage s has
+        // landed" is "at most the operations issued after it are
+        // outstanding": none within a tile; at a tile's first stage the
+        // previous tile's 32 (or 16) vector stores per lane, issued after
+        // this tile's stage 0 (a gate-residual epilogue also issued loads
+        // there, which only adds to the operations after that stage).  Those
+        // stores thus drain under the tile's first stage of MFMA work.  A
+        // ragged previous tile stored a variable count with scalar stores:
+        // wait for everything.  (Loads two stages ahead, the third slot
+        // refilled as soon as it is read, measured 0.7-1.1 % slower on the
+        // shapes that run this kernel, and so did the next tile's first two
+        // stages fetched before the stores.)  Unrolled by three so that
+        // slots are compile-time; the stage count is a multiple of three, so
+        // the loop has no exit mid-body.
         for (int s = 0; s < nstage; s += STAGES) {
 #pragma unroll
             for (int u = 0; u < STAGES; ++u) {
-                if (s + u + 1 >= nstage)
-                    wait_vmcnt<0>();
-                else if (C::COUNT_STORES && s == 0 && u < STAGES - 1 && prev_stores == 2)
-                    wait_vmcnt<(C::COUNT_STORES ? C::EPI_STORES + C::AHEAD : 0)>();
-                else if (C::COUNT_STORES && s == 0 && u < STAGES - 1 && prev_stores == 3)
-                    wait_vmcnt<(C::COUNT_STORES ? C::EPI_STORES / 2 + C::AHEAD : 0)>();
-                else if (s == 0 && u == 0 && prev_stores != 0)
-                    wait_vmcnt<0>();
+                if (C::COUNT_STORES && s == 0 && u == 0 && prev_stores == 2)
+                    wait_vmcnt<(C::COUNT_STORES ? C::EPI_STORES : 0)>();
+                else if (C::COUNT_STORES && s == 0 && u == 0 && prev_stores == 3)
+                    wait_vmcnt<(C::COUNT_STORES ? C::EPI_STORES / 2 : 0)>();
                 else
-                    wait_vmcnt<C::AHEAD>();
+                    wait_vmcnt<0>();
                 lds_barrier();
                 // the stage's first fragment reads go out before the next
                 // stage's loads, so the loads issue under their latency
                 compute(u, [&] {
-                    if (s + u + STAGES - 1 < nstage)
-                        issue(kst0 + s + u + STAGES - 1, (u + STAGES - 1) % STAGES);
+                    if (s + u + 1 < nstage) issue(kst0 + s + u + 1, (u + 1) % STAGES);
                 });
             }
         }
 
-        // Slots 0..STAGES-2 were last read before the final barrier: fetch
-        // the next tile's first STAGES-1 stages now, then store this tile.
+        // Slots 0 and 1 were last read before the final barrier: fetch the
+        // next tile's first stage now, then store this tile.
         const int cm0 = m0, cn0 = n0, cpar = parity;
         float *const cout = uout;
         unit += gridDim.x;
@@ -1693,8 +1685,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
             setup(m0, n0);
             parity ^= 1;
             issue_rsc(parity);
-#pragma unroll
-            for (int t = 0; t < STAGES - 1; ++t) issue(kst0 + t, t);
+            issue(kst0, 0);
         }
         if (rows_scaled) {
             // this tile's rows: token m0 + 32 mt + li in every accumulator
@@ -1743,7 +1734,7 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 // holds output columns 4g .. 4g + 3 of token li: one 16-byte store.
 //
 // Pipeline and LDS as in b1_gemm_kernel: K in stages of 128 (4 blocks), a
-// three-slot ring fetched two stages ahead with buffer loads straight into
+// three-slot ring fetched one stage ahead with buffer loads straight into
 // LDS, one barrier per stage with counted vmcnt waits.  A stage is 144 rows
 // x 256 bytes of activations (36 loads of 1 KB) and 384 columns x 24 bytes
 // of weights (six 64-column groups, two 12-byte loads each): waves 0-5 load
@@ -1773,12 +1764,11 @@ struct Gemm16Cfg {
     static constexpr int ALOADS = ASTAGE / 1024;
     static constexpr int LOADS = (ALOADS + 2 * NWG) / NW;
     static constexpr int AW = LOADS - 2;
-    static constexpr int AHEAD = (STAGES - 2) * LOADS;
     static constexpr int EPI_STORES = MT * NTL;         // 16-byte stores per lane, full tile
     static_assert(BM % 16 == 0 && WN % 16 == 0 && BN % 64 == 0 && NWG <= NW, "tile shape");
     static_assert(LOADS * NW == ALOADS + 2 * NWG && AW * NWG + LOADS * (NW - NWG) == ALOADS, "uniform loads");
     static_assert(LDS <= 160 * 1024, "gfx950 LDS");
-    static_assert(EPI_STORES + AHEAD <= 63, "vmcnt holds 6 bits");
+    static_assert(EPI_STORES <= 63, "vmcnt holds 6 bits");
     static_assert((MT - 1) * 16 * ROWB + 16 * ROWB <= 65536, "fragment immediates");
 };
 
@@ -2087,40 +2077,36 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
     tile_origin(unit, m0, n0);
     setup(m0, n0);
     issue_rsc(parity);
-#pragma unroll
-    for (int t = 0; t < C::STAGES - 1; ++t) issue(t, t);
+    issue(0, 0);
     bool prev_stores = false; // the previous epilogue's EPI_STORES stores are in flight
     for (;;) {
 #pragma unroll
         for (int i = 0; i < C::MT; ++i)
 #pragma unroll
             for (int j = 0; j < C::NTL; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        // At the top of stage s the wave waits for its own loads of stage s
-        // (at most stage s + 1's LOADS newer, plus in the first two stages of
-        // a tile the previous tile's stores, issued after this tile's stages
-        // 0 and 1; a gate-residual epilogue also issued its loads before
-        // those stores, which only adds older operations), then the barrier
-        // publishes every wave's part and retires all reads of the slot
-        // that stage s + 2 then refills.
+        // Loads one stage ahead, as in b1_gemm_kernel.  At the top of stage s
+        // the wave waits for its own loads of stage s (nothing newer, except
+        // at a tile's first stage the previous tile's stores, issued after
+        // this tile's stage 0; a gate-residual epilogue also issued its loads
+        // there, which only adds to the newer operations), then the barrier
+        // publishes every wave's part and retires all reads of stage s - 1,
+        // and stage s + 1 goes to the slot stage s - 2 held.  (Two stages
+        // ahead measured 0.5-1.8 % slower at the M = 4608 shapes.)
         for (int s = 0; s < nstage; s += C::STAGES) {
 #pragma unroll
             for (int u = 0; u < C::STAGES; ++u) {
-                if (s + u + 1 >= nstage)
-                    wait_vmcnt<0>();
-                else if (s == 0 && u < C::STAGES - 1 && prev_stores)
-                    wait_vmcnt<C::EPI_STORES + C::AHEAD>();
-                else if (s == 0 && u == 0)
-                    wait_vmcnt<0>(); // after scalar stores (or the first tile)
+                if (s == 0 && u == 0 && prev_stores)
+                    wait_vmcnt<C::EPI_STORES>();
                 else
-                    wait_vmcnt<C::AHEAD>();
+                    wait_vmcnt<0>(); // (after scalar stores, or in the first tile, everything)
                 lds_barrier();
                 compute(u, [&] {
-                    if (s + u + C::STAGES - 1 < nstage) issue(s + u + C::STAGES - 1, (u + C::STAGES - 1) % C::STAGES);
+                    if (s + u + 1 < nstage) issue(s + u + 1, (u + 1) % C::STAGES);
                 });
             }
         }
-        // Slots 0 and 1 were last read before the final barrier: fetch the
-        // next tile's first two stages now, then store this tile.
+        // Slot 0 was last read before the final barrier: fetch the next
+        // tile's first stage now, then store this tile.
         const int cm0 = m0, cn0 = n0, cpar = parity;
         unit += gridDim.x;
         const bool more = unit < ntiles;
@@ -2129,8 +2115,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             setup(m0, n0);
             parity ^= 1;
             issue_rsc(parity);
-#pragma unroll
-            for (int t = 0; t < C::STAGES - 1; ++t) issue(t, t);
+            issue(0, 0);
         }
         if (rows_scaled) {
             const float *rsp = reinterpret_cast<const float *>(smem + C::RSC + cpar * C::RSCN * 4);
