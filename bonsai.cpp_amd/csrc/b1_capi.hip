@@ -859,9 +859,9 @@ static int fuse_span(int n_ops, int mode, int num_cus, OpAt at, int i, int *n_su
         if (batch_path(qa, mode) != BatchPath::Packed || b1::gemm_splits(qa.M, qa.K, qa.N, num_cus) != splits) break;
         // the concatenated GEMM runs the tile kernel each part would (the
         // two sum K in different orders)
-        const bool t16 = b1::gemm16_shape(a.M, a.K, a.N, num_cus);
-        if (b1::gemm16_shape(qa.M, qa.K, qa.N, num_cus) != t16 ||
-            b1::gemm16_shape(a.M, a.K, *n_sum + q.w->out_dim, num_cus) != t16)
+        const int tk = b1::gemm_tiles(a.M, a.K, a.N, num_cus);
+        if (b1::gemm_tiles(qa.M, qa.K, qa.N, num_cus) != tk ||
+            b1::gemm_tiles(a.M, a.K, *n_sum + q.w->out_dim, num_cus) != tk)
             break;
         *n_sum += q.w->out_dim;
         ++last;

@@ -61,12 +61,16 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
 // area it needs (splits x M x N rounded up to 4 columns).
 int gemm_splits(int M, int K, int N, int num_cus);
 size_t gemm_split_bytes(int M, int N, int splits);
-// Whether the packed GEMM of this shape runs 144 x 384 tiles (16x16x32
-// MFMAs; plain and gate-residual epilogues) instead of 128 x 512: full
-// tiles, no split, and clearly fewer rounds on num_cus CUs.  A function of
-// the shape and CU count only, so every entry point picks alike; the two
-// tile kernels sum K in different orders (the same to ~1e-6 relative).
-bool gemm16_shape(int M, int K, int N, int num_cus);
+// The tile kernel of the packed GEMM with the plain or gate-residual
+// epilogue: 0 b1_gemm_kernel, 128 x 512 tiles (any shape; 64-row tiles for a
+// short last round, split-K for few tiles); 1 b1_gemm16_kernel 144 x 384 and
+// 2 b1_gemm16_kernel 128 x 384 (16x16x32 MFMAs; full tiles, K % 384 == 0, no
+// split), whichever needs the fewest rounds on num_cus CUs, counting a
+// BM x BN tile as BM BN / 65536 of a 128 x 512 round; ties stay on 0.  A
+// function of the shape and CU count only, so every entry point picks alike.
+// The SwiGLU and packed-output epilogues always run kernel 0.  The kernels
+// sum K in different orders (the same to ~1e-6 relative).
+int gemm_tiles(int M, int K, int N, int num_cus);
 
 // The two halves of the workspace path.  Packed activations: u32 word
 // (row m, 16 j + d) = fp16(a[m][32 j + d]) | fp16(a[m][32 j + d + 16]) << 16,

@@ -1715,16 +1715,19 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 
 // ---------------------------------------------------------------- gemm16 --
 //
-// The same GEMM over 144 x 384 tiles with 16x16x32 MFMAs, for shapes whose
-// 128 x 512 tiles quantise badly on 256 CUs: at M = 4608 (Flux image +
-// text tokens) N = 3072 gives 216 tiles of 128 x 512 (one round at 84 % of
-// the CUs) but exactly 256 of 144 x 384, and N = 9216 gives 648 (2.53
-// rounds, run as 3) but exactly 768 (3 full rounds).  A 144 x 384 tile is
-// 0.84 of a 128 x 512 one.
+// The same GEMM over 144 x 384 or 128 x 384 tiles with 16x16x32 MFMAs, for
+// shapes whose 128 x 512 tiles quantise badly on 256 CUs (gemm_tiles picks):
+// at M = 4608 (Flux image + text tokens) N = 3072 gives 216 tiles of
+// 128 x 512 (one round at 84 % of the CUs) but exactly 256 of 144 x 384, and
+// N = 9216 gives 648 (2.53 rounds, run as 3) but exactly 768 (3 full
+// rounds); at M = 4096 (Klein image tokens) N = 3072 gives 192 tiles of
+// 128 x 512 but 256 of 128 x 384, N = 9216 2.25 rounds of 128 x 512 (run
+// as 2 plus a round of 64-row tiles) but 3 full rounds of 128 x 384.  A
+// 144 x 384 tile is 0.84 of a 128 x 512 one, a 128 x 384 tile 0.75.
 //
-// Eight waves side by side along N, each 144 tokens x 48 columns: 9 x 3
-// tiles of 16x16, weights as the MFMA's A operand (16 output columns x 32
-// K), tokens as B.  Lane (li, g) of a 16x16x32 operand holds K indices
+// Eight waves side by side along N, each BM tokens x BN / 8 columns (144 x 48:
+// 9 x 3 tiles of 16x16), weights as the MFMA's A operand (16 output columns
+// x 32 K), tokens as B.  Lane (li, g) of a 16x16x32 operand holds K indices
 // 8g .. 8g + 7 of row li: with the K-slot pairing, dword t of them is
 // packed word 4g + t of the 32-element block (elements 4g + t and
 // 4g + t + 16), i.e. 16-byte chunk g of the block's 64 bytes of packed
@@ -1735,14 +1738,14 @@ __global__ __launch_bounds__((BN / WN) * 64, (BN / WN) >= 8 ? 2 : 1) void b1_gem
 //
 // Pipeline and LDS as in b1_gemm_kernel: K in stages of 128 (4 blocks), a
 // three-slot ring fetched one stage ahead with buffer loads straight into
-// LDS, one barrier per stage with counted vmcnt waits.  A stage is 144 rows
-// x 256 bytes of activations (36 loads of 1 KB) and 384 columns x 24 bytes
-// of weights (six 64-column groups, two 12-byte loads each): waves 0-5 load
-// 4 activation kilobytes and weight group w, waves 6-7 six activation
-// kilobytes, so every wave issues 6 loads a stage and the waits are
-// uniform.  Activation row r's chunk c sits at position c ^ (r & 15), so the
-// 16 lanes of a fragment read (rows li, one chunk) hit distinct banks.
-// Full tiles only (M % 144, N % 384, K % 384 == 0); EPI 0 plain, 1
+// LDS, one barrier per stage with counted vmcnt waits.  A stage is BM rows
+// x 256 bytes of activations (BM / 4 loads of 1 KB) and BN columns x 24
+// bytes of weights (BN / 64 column groups, two 12-byte loads each): the
+// first BN / 64 waves load a weight group and some activation kilobytes,
+// the others only activation kilobytes (144 x 384: 6 loads a wave; 128 x
+// 384: 6 and 4).  Activation row r's chunk c sits at position c ^ (r & 15),
+// so the 16 lanes of a fragment read (rows li, one chunk) hit distinct
+// banks.  Full tiles only (M % BM, N % BN, K % 384 == 0); EPI 0 plain, 1
 // gate-residual (GemmEpi); row scales of range-safe packing as in the
 // 32x32 kernel.
 template <int BM_, int BN_>
@@ -1758,15 +1761,30 @@ struct Gemm16Cfg {
     static constexpr int RSCN = (BM + 63) / 64 * 64;    // row scales per parity (64 per copying wave)
     static constexpr int LDS = RSC + 2 * RSCN * 4;
     static constexpr int GROUP_M = 4;
-    // loads per wave per stage, the same for every wave: waves 0 .. NWG - 1
-    // load a weight group (2 loads) and AW activation kilobytes, the others
-    // LOADS activation kilobytes
+    // Loads per wave per stage: waves 0 .. NWG - 1 load a weight group (2
+    // loads) and AW activation kilobytes, the others AO activation
+    // kilobytes; AW is the split with the fewest loads on the busiest wave
+    // (144 x 384: 4 + 2 and 6; 128 x 384: 4 + 2 and 4).  The waits count no
+    // loads (every wait inside a tile is for everything), so the counts need
+    // not be equal.
     static constexpr int ALOADS = ASTAGE / 1024;
-    static constexpr int LOADS = (ALOADS + 2 * NWG) / NW;
-    static constexpr int AW = LOADS - 2;
+    static constexpr int split_aw() {
+        int best = -1, cost = 1 << 30;
+        for (int aw = 0; aw * NWG <= ALOADS; ++aw) {
+            const int rest = ALOADS - aw * NWG;
+            if (NW == NWG ? rest != 0 : rest % (NW - NWG) != 0) continue;
+            const int ao = NW == NWG ? 0 : rest / (NW - NWG);
+            const int c = aw + 2 > ao ? aw + 2 : ao;
+            if (c < cost) cost = c, best = aw;
+        }
+        return best;
+    }
+    static constexpr int AW = split_aw();
+    static constexpr int AO = NW == NWG ? 0 : (ALOADS - AW * NWG) / (NW - NWG);
+    static constexpr int LOADS = AW > AO ? AW : AO;    // activation offsets a wave keeps
     static constexpr int EPI_STORES = MT * NTL;         // 16-byte stores per lane, full tile
     static_assert(BM % 16 == 0 && WN % 16 == 0 && BN % 64 == 0 && NWG <= NW, "tile shape");
-    static_assert(LOADS * NW == ALOADS + 2 * NWG && AW * NWG + LOADS * (NW - NWG) == ALOADS, "uniform loads");
+    static_assert(AW >= 0 && AW * NWG + AO * (NW - NWG) == ALOADS, "the loads cover the stage");
     static_assert(LDS <= 160 * 1024, "gfx950 LDS");
     static_assert(EPI_STORES <= 63, "vmcnt holds 6 bits");
     static_assert((MT - 1) * 16 * ROWB + 16 * ROWB <= 65536, "fragment immediates");
@@ -1796,15 +1814,15 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
         n0 = (tin / gsize) * C::BN;
     };
 
-    // Loads of a stage.  Activation load j (0..35) fills LDS bytes
+    // Loads of a stage.  Activation load j (0 .. BM / 4 - 1) fills LDS bytes
     // [1024 j, +1024) of the slot: rows 4j .. 4j + 3, lane L at position
     // L % 16 of row 4j + L / 16, holding chunk (L % 16) ^ (row & 15).  Waves
-    // 0-5 issue loads 4w .. 4w + 3, waves 6-7 24 + 6 (w - 6) .. + 5.  Weight
-    // group q (waves 0-5, q = w): lane L fetches 12 bytes (blocks 0-1, then
-    // 2-3 of the stage) of column n0 + 64 q + L.  Rows and columns past the
-    // matrix cannot occur (full tiles).
+    // w < NWG issue loads AW w .. + AW - 1, the others AW NWG + AO (w - NWG)
+    // .. + AO - 1.  Weight group q (waves q < NWG): lane L fetches 12 bytes
+    // (blocks 0-1, then 2-3 of the stage) of column n0 + 64 q + L.  Rows and
+    // columns past the matrix cannot occur (full tiles).
     const bool wload = wave < C::NWG;
-    const int a_first = wload ? C::AW * wave : C::AW * C::NWG + C::LOADS * (wave - C::NWG);
+    const int a_first = wload ? C::AW * wave : C::AW * C::NWG + C::AO * (wave - C::NWG);
     uint32_t aoff[C::LOADS];
     uint32_t boff = 0;
     auto setup = [&](int m0, int n0) {
@@ -1831,7 +1849,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             dma_buf_lds12s(wrs, sw + 1024, boff, wso + 12);
         } else {
 #pragma unroll
-            for (int i = 0; i < C::LOADS; ++i) dma_buf_lds16s(ars, sa + i * 1024, aoff[i], aso);
+            for (int i = 0; i < C::AO; ++i) dma_buf_lds16s(ars, sa + i * 1024, aoff[i], aso);
         }
     };
 
@@ -3256,19 +3274,27 @@ static double gemm_rounds128(int M, int N, int num_cus) {
     return (double)((tiles + slots - 1) / slots);
 }
 
-bool gemm16_shape(int M, int K, int N, int num_cus) {
-    using C = Gemm16Cfg<144, 384>;
-    if (num_cus <= 0 || !gemm_packed_ok(M, K, N) || M % C::BM || N % C::BN || K % (C::KC * C::STAGES)) return false;
-    if (gemm_splits(M, K, N, num_cus) > 1) return false;
-    const int tiles = (M / C::BM) * (N / C::BN);
-    // a 144 x 384 tile is 0.84 of a 128 x 512 one; take it when its rounds
-    // are clearly fewer (at M = 4608 on 256 CUs: N = 3072 and 9216, not
-    // 12288, whose partial round the 128 x 512 kernel runs as 64-row tiles)
-#ifdef B1_NO_GEMM16
-    return false;
-#endif
-    const double r16 = (double)((tiles + num_cus - 1) / num_cus) * (double)(C::BM * C::BN) / (kBM * kBN);
-    return r16 < 0.9 * gemm_rounds128(M, N, num_cus);
+int gemm_tiles(int M, int K, int N, int num_cus) {
+    if (num_cus <= 0 || !gemm_packed_ok(M, K, N) || K % (Gemm16Cfg<128, 384>::KC * Gemm16Cfg<128, 384>::STAGES))
+        return 0;
+    if (gemm_splits(M, K, N, num_cus) > 1) return 0;
+    // rounds of the persistent grid in units of a 128 x 512 round (a BM x BN
+    // tile counts BM BN / 65536 of one); strictly fewer to leave the
+    // 128 x 512 kernel
+    double best = gemm_rounds128(M, N, num_cus);
+    int kind = 0;
+    auto consider = [&](int id, int bm, int bn) {
+        if (M % bm || N % bn) return;
+        const int tiles = (M / bm) * (N / bn);
+        const double r = (double)((tiles + num_cus - 1) / num_cus) * (double)(bm * bn) / (double)(kBM * kBN);
+        if (r < best) {
+            best = r;
+            kind = id;
+        }
+    };
+    consider(1, 144, 384);
+    consider(2, 128, 384);
+    return kind;
 }
 
 template <int BM, int BN, int EPI>
@@ -3302,13 +3328,11 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
     // (with ksplit > 1 the row scales epi.rsc go to the reduction, not the
     // GEMM, which writes plain partial products)
     if constexpr (EPI == 0 || EPI == 1) {
-        if (!(ksplit > 1 && partials != nullptr) && gemm16_shape(M, K, N, num_cus))
-            return launch_gemm16_t<144, 384, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
-#ifdef B1_GEMM16_128
-        if (!(ksplit > 1 && partials != nullptr) && gemm_packed_ok(M, K, N) && M % 128 == 0 && N % 512 == 0 &&
-            gemm_splits(M, K, N, num_cus) == 1)
-            return launch_gemm16_t<128, 512, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
-#endif
+        if (!(ksplit > 1 && partials != nullptr)) {
+            const int t = gemm_tiles(M, K, N, num_cus);
+            if (t == 1) return launch_gemm16_t<144, 384, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
+            if (t == 2) return launch_gemm16_t<128, 384, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
+        }
     }
     auto kernel = &b1_gemm_kernel<kBM, kBN, kWN, kStages, EPI>;
     static std::once_flag attr_once;

@@ -82,7 +82,7 @@ def assert_rows_close(y, ref, what):
 # (m, k, n, mode, workspace): "lib" = the library's own, None = a too-small
 # caller workspace (the kernels that convert activations themselves)
 PATHS = [
-    (2048, 768, 4608, "auto", "lib"),     # packed GEMM (144 tiles, unsplit)
+    (2048, 768, 4608, "auto", "lib"),     # packed GEMM, unsplit (192 tiles of 128 x 384)
     (256, 3072, 3072, "auto", "lib"),     # packed GEMM split along K (C1)
     (8, 3072, 4096, "auto", "lib"),       # small-M kernel: exact rows inside it
     (16, 768, 640, "gemm", "lib"),        # GEMM tile for a few rows

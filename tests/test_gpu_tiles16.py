@@ -1,10 +1,13 @@
-"""The 144 x 384 tile GEMM (b1_gemm16_kernel, 16x16x32 MFMAs).
+"""The 16x16x32-MFMA tile GEMMs (b1_gemm16_kernel, 144 x 384 and 128 x 384).
 
-The packed GEMM runs it for full-tile shapes whose 128 x 512 tiles would
-quantise badly on the CUs (M % 144 == 0, N % 384 == 0, K % 384 == 0, no
-split along K, clearly fewer rounds: on 256 CUs e.g. 288 x 384 -> 768,
-1440 x 1152 -> 3072 and the Flux shapes M = 4608 with N = 3072 or 9216).
-Checked here on such shapes, through the fp32, packed and epilogue entries:
+The packed GEMM runs one of them for full-tile shapes whose 128 x 512 tiles
+would quantise worse on the CUs (M % 144 or M % 128 == 0, N % 384 == 0,
+K % 384 == 0, no split along K, fewer rounds counted in 128 x 512 tiles:
+on 256 CUs e.g. 288 x 384 -> 768, 1440 x 1152 -> 3072 and the Flux shapes
+M = 4608 with N = 3072, 9216, 12288 or 21504 take 144 x 384 tiles; 512 x
+384 -> 768, 2048 x 768 -> 4608 and the Klein image shapes M = 4096 with
+N = 3072, 9216 or 18432 take 128 x 384 tiles).  Checked here on such
+shapes, through the fp32, packed and epilogue entries:
 
   * the FAST bar against the float64 oracle (per element
     |y - ref| / max(|ref|, rms(ref)) <= 1e-2 and cosine >= 0.9999);
@@ -26,7 +29,9 @@ pytestmark = pytest.mark.gpu
 
 TOL_REL = 1e-2
 TOL_COS = 0.9999
-SHAPES = [(288, 384, 768), (1440, 1152, 3072), (4608, 3072, 3072)]
+SHAPES144 = [(288, 384, 768), (1440, 1152, 3072), (4608, 3072, 3072)]
+SHAPES128 = [(512, 384, 768), (2048, 768, 4608), (4096, 3072, 9216)]
+SHAPES = SHAPES144 + SHAPES128
 
 
 def say(msg):
@@ -98,7 +103,7 @@ def test_tiles16_against_oracle_and_entries(torch, b1, oracle, m, k, n):
     assert bool((big[:, n] == 7.0).all())
 
 
-@pytest.mark.parametrize("m,k,n", SHAPES[:2])
+@pytest.mark.parametrize("m,k,n", SHAPES144[:2] + SHAPES128[:2])
 def test_tiles16_gate_residual(torch, b1, m, k, n):
     """out = residual + gate * y, fused, equals the fp32 multiply then add on
     the plain y; in place (residual = out) too."""
@@ -125,9 +130,9 @@ def test_tiles16_gate_residual(torch, b1, m, k, n):
     assert torch.equal(got2, want), "fp32 epilogue entry"
 
 
-def test_tiles16_rows_beyond_fp16_and_nonfinite(torch, b1, oracle):
+@pytest.mark.parametrize("m,k,n", [(1440, 1152, 3072), (2048, 768, 4608)])
+def test_tiles16_rows_beyond_fp16_and_nonfinite(torch, b1, oracle, m, k, n):
     from bonsai_b1 import synth
-    m, k, n = 1440, 1152, 3072
     a = synth.device_activations(m, k, 206)
     a[5] *= 3.0e5
     a[777] *= -2.0e6
