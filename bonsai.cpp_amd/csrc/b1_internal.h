@@ -61,15 +61,16 @@ hipError_t launch_gemm(const LinearArgs &a, int num_cus, void *workspace, size_t
 // area it needs (splits x M x N rounded up to 4 columns).
 int gemm_splits(int M, int K, int N, int num_cus);
 size_t gemm_split_bytes(int M, int N, int splits);
-// The tile kernel of the packed GEMM with the plain or gate-residual
-// epilogue: 0 b1_gemm_kernel, 128 x 512 tiles (any shape; 64-row tiles for a
-// short last round, split-K for few tiles); 1 b1_gemm16_kernel 144 x 384 and
-// 2 b1_gemm16_kernel 128 x 384 (16x16x32 MFMAs; full tiles, K % 384 == 0, no
-// split), whichever needs the fewest rounds on num_cus CUs, counting a
-// BM x BN tile as BM BN / 65536 of a 128 x 512 round; ties stay on 0.  A
-// function of the shape and CU count only, so every entry point picks alike.
-// The SwiGLU and packed-output epilogues always run kernel 0.  The kernels
-// sum K in different orders (the same to ~1e-6 relative).
+// The tile kernel of the packed GEMM with the plain, gate-residual or
+// packed-output (GELU or none) epilogue: 0 b1_gemm_kernel, 128 x 512 tiles
+// (any shape; 64-row tiles for a short last round, split-K for few tiles);
+// 1 b1_gemm16_kernel 144 x 384 and 2 b1_gemm16_kernel 128 x 384 (16x16x32
+// MFMAs; full tiles, K % 384 == 0, no split), whichever needs the fewest
+// rounds on num_cus CUs, counting a BM x BN tile as BM BN / 65536 of a
+// 128 x 512 round; ties stay on 0.  A function of the shape and CU count
+// only, so every entry point picks alike.  The SwiGLU epilogues (fp32 or
+// packed) always run kernel 0.  The kernels sum K in different orders (the
+// same to ~1e-6 relative).
 int gemm_tiles(int M, int K, int N, int num_cus);
 
 // The two halves of the workspace path.  Packed activations: u32 word

@@ -1797,7 +1797,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                                                                      int32_t *nonfinite, int tiles_m, int tiles_n,
                                                                      int vec_store, GemmEpi epi) {
     using C = Gemm16Cfg<BM, BN>;
-    static_assert(EPI == 0 || EPI == 1, "plain and gate-residual epilogues");
+    static_assert(EPI == 0 || EPI == 1 || EPI == 3, "plain, gate-residual and packed-output epilogues");
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, g = lane >> 4;
@@ -1993,14 +1993,106 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
         return b;
     };
     // Lane (li, g) of tile (mt, nt): token m0 + 16 mt + li, columns
-    // n0 + 48 wave + 16 nt + 4 g .. + 3: one 16-byte store each (27 per
+    // n0 + WN wave + 16 nt + 4 g .. + 3: one 16-byte store each (MT NTL per
     // lane), half a line per 4 lanes.  Without vec_store (out, or the
-    // residual and gate, not 16-byte aligned rows) the same values go out
-    // as scalar stores.  Returns whether EPI_STORES vector stores are in
-    // flight.
+    // residual and gate, or the packed rows, not 16-byte aligned) the same
+    // values go out as scalar stores.  Returns whether at least EPI_STORES
+    // vector stores per lane are in flight.
     auto epilogue = [&](int m0, int n0) -> bool {
         int bad = 0;
         count_tile(bad);
+        if constexpr (EPI == 3) {
+            // Columns below epi.split: fp32 into out.  From split on: fp16
+            // (of GELU-tanh when epi.act) into the packed rows of epi.pk
+            // (ldpw dwords apart), as the next linear reads them: column
+            // split + 32 b + e of a row is half e / 16 of dword 16 b + e % 16.
+            // split % 32 == 0 and tiles are 16-column aligned, so a tile is
+            // one half of one block, and lane (li, g) holds that half of
+            // dwords 16 b + 4 g .. + 3.  When the block's other half is in
+            // the same wave the low tile writes the four dwords as one
+            // 16-byte store; a half whose partner lies in the next or the
+            // previous wave (a wave has 3 tiles) goes out as four 2-byte
+            // stores, the two halves meeting in L2.
+            const int wb = n0 + C::WN * wave; // wave-uniform
+            auto act = [&](float y) { return epi.act ? gelu_tanh(y) : y; };
+            if (!vec_store) {
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < C::NTL; ++nt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const size_t m = (size_t)(m0 + 16 * mt + li);
+                            const int n = wb + 16 * nt + 4 * g + e;
+                            const float y = acc[mt][nt][e];
+                            if (n < epi.split) {
+                                out[m * ldo + n] = y;
+                            } else {
+                                const int c = n - epi.split;
+                                const uint32_t h = pack_f16(act(y), 0.0f);
+                                reinterpret_cast<uint16_t *>(epi.pk + m * epi.ldpw + (c >> 5) * 16 + (c & 15))[(c >> 4) & 1] =
+                                    (uint16_t)h;
+                            }
+                        }
+                count_nonfinite(nonfinite, bad);
+                return false;
+            }
+            const int ldb = stride_bytes(ldo), lpb = stride_bytes(epi.ldpw);
+            const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+                out + (size_t)m0 * ldo, (short)0, (int)(C::BM * ldo * 4), kBufferFlags);
+            const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+                epi.pk + (size_t)m0 * epi.ldpw, (short)0, (int)(C::BM * epi.ldpw * 4), kBufferFlags);
+            const int lvoff = li * ldb + 16 * g, lpoff = li * lpb + 16 * g;
+            int nst = 0; // vector stores per lane (wave-uniform)
+#pragma unroll
+            for (int nt = 0; nt < C::NTL; ++nt) {
+                const int cb = wb + 16 * nt; // the tile's first column
+                if (cb < epi.split) {
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt) {
+                        u32x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float x = acc[mt][nt][e];
+                            v[e] = __builtin_bit_cast(uint32_t, x);
+                        }
+                        store16_guarded<kStoreNT>(v, ors, lvoff, mt * 16 * ldb + cb * 4);
+                    }
+                    nst += C::MT;
+                    continue;
+                }
+                const int c = cb - epi.split, hi = (c >> 4) & 1;
+                const int dw = (c >> 5) * 16; // the block's first dword
+                if (hi == 0 && nt + 1 < C::NTL) {
+                    // this tile and the next: the whole block
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt) {
+                        u32x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float y0 = acc[mt][nt][e], y1 = acc[mt][nt + 1][e];
+                            v[e] = pack_f16(act(y0), act(y1));
+                        }
+                        store16_guarded<0>(v, prs, lpoff, mt * 16 * lpb + dw * 4);
+                    }
+                    nst += C::MT;
+                    continue;
+                }
+                if (hi == 1 && nt > 0) continue; // written with the tile before
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float y = acc[mt][nt][e];
+                        const uint32_t h = pack_f16(act(y), 0.0f);
+                        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)h, prs, lpoff,
+                                                              mt * 16 * lpb + (dw + e) * 4 + 2 * hi, 0);
+                    }
+                nst += 4 * C::MT;
+            }
+            count_nonfinite(nonfinite, bad);
+            return nst >= C::EPI_STORES;
+        }
         if (!vec_store) {
 #pragma unroll
             for (int mt = 0; mt < C::MT; ++mt)
@@ -3314,6 +3406,9 @@ static hipError_t launch_gemm16_t(const void *packed, const uint8_t *w, int K, i
     int vec_store = al16(out) && ldo % 4 == 0 && ldo < (int64_t(1) << 21);
     if (EPI == 1)
         vec_store = vec_store && al16(epi.res) && al16(epi.gate) && epi.ldr % 4 == 0 && epi.ldr < (int64_t(1) << 21);
+    if (EPI == 3)
+        vec_store = (epi.split == 0 || vec_store) && al16(epi.pk) && epi.ldpw % 4 == 0 &&
+                    epi.ldpw < (int64_t(1) << 21);
     const int tiles_m = M / C::BM, tiles_n = N / C::BN, tiles = tiles_m * tiles_n;
     const int grid = tiles < num_cus ? tiles : num_cus; // persistent
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(C::NT), C::LDS, s, static_cast<const uint16_t *>(packed), w, K, N, M,
@@ -3327,8 +3422,10 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
                                        hipStream_t s, int ksplit = 1, float *partials = nullptr) {
     // (with ksplit > 1 the row scales epi.rsc go to the reduction, not the
     // GEMM, which writes plain partial products)
-    if constexpr (EPI == 0 || EPI == 1) {
-        if (!(ksplit > 1 && partials != nullptr)) {
+    // (the SwiGLU epilogues pair a gate and a value 32-column tile in each
+    // wave of the 128 x 512 kernel and always run it)
+    if constexpr (EPI == 0 || EPI == 1 || EPI == 3) {
+        if (!(ksplit > 1 && partials != nullptr) && !(EPI == 3 && epi.act == 2)) {
             const int t = gemm_tiles(M, K, N, num_cus);
             if (t == 1) return launch_gemm16_t<144, 384, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
             if (t == 2) return launch_gemm16_t<128, 384, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);

@@ -2,7 +2,7 @@
 activations (bonsai_b1_linear_packed_f16_to_packed).
 
 Bar (bit for bit): the fp32 columns equal the plain GEMM's output (the same
-128-row tile, the same K order), and the packed columns equal the packing
+tile kernel, the same K order), and the packed columns equal the packing
 the separate producers write from that output -- bonsai_b1_pack_act_f16_ld,
 bonsai_b1_gelu_tanh_pack_f16_ld or bonsai_b1_swiglu_pack_f16_ld -- which
 the producer tests pin against the oracle's layout.  Bytes outside the
@@ -59,6 +59,19 @@ CASES = [
     (256, 768, 2048, 192, "swiglu", 64, 1216),       # SwiGLU split inside a tile, into a column range
     (600, 3072, 21504, 9216, "gelu_tanh", 3072, 15360),  # C5 linear1 -> linear2's input
     (600, 3072, 27648, 9216, "swiglu", 3072, 12288),     # reference single block linear1 -> to_out's input
+    # 16x16 tile kernels (GELU and none; the plain reference runs the same
+    # kernel): 144 x 384 and 128 x 384 tiles, every column packed; split
+    # inside a wave (a block's halves in two waves: 2-byte half stores);
+    # a wave with one fp32 tile and one packed block (fewer stores than a
+    # full tile's: the next tile waits for everything); several tiles a
+    # work-group
+    (288, 384, 768, 0, "gelu_tanh", 0, None),
+    (288, 384, 768, 416, "gelu_tanh", 0, None),
+    (288, 384, 768, 448, "none", 32, 400),
+    (512, 384, 768, 0, "gelu_tanh", 0, None),
+    (512, 384, 768, 160, "gelu_tanh", 96, 800),
+    (2048, 384, 9216, 4096, "gelu_tanh", 0, None),
+    (4608, 384, 9216, 3072, "gelu_tanh", 0, None),
 ]
 
 
