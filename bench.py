@@ -114,17 +114,26 @@ def bench_gemm(torch, b1, synth, m, k, n, steps, warmup, mode="auto", inputs=Non
             "frac": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "wall_s": wall, "inputs": (a, w)}
 
 
-TILES16_SHAPES = [("c3_qkv", (4608, 3072, 9216), "none"), ("c3_out", (4608, 3072, 3072), "none"),
-                  ("c4_down", (4608, 12288, 3072), "none"), ("c5_linear2", (4608, 15360, 3072), "gate_residual")]
+# (name, (M, K, N), epilogue, tile): the shapes the 16x16 tile kernels run,
+# 144 x 384 at M = 4608 and 128 x 384 at the Klein image stream's M = 4096
+TILES16_SHAPES = [("c3_qkv", (4608, 3072, 9216), "none", "144x384"), ("c3_out", (4608, 3072, 3072), "none", "144x384"),
+                  ("c4_up", (4608, 3072, 12288), "none", "144x384"), ("c4_down", (4608, 12288, 3072), "none", "144x384"),
+                  ("c5_linear2", (4608, 15360, 3072), "gate_residual", "144x384"),
+                  ("klein_single_linear1", (4608, 3072, 27648), "none", "144x384"),
+                  ("klein_img_qkv", (4096, 3072, 9216), "none", "128x384"),
+                  ("klein_img_out", (4096, 3072, 3072), "none", "128x384"),
+                  ("klein_img_ff_in", (4096, 3072, 18432), "none", "128x384"),
+                  ("klein_img_ff_out", (4096, 9216, 3072), "none", "128x384")]
 
 
 def bench_tiles16(torch, b1, synth, steps, warmup):
-    """The 144 x 384 tile GEMM (b1_gemm16_kernel) alone at the M = 4608
-    shapes it runs: packed activations made once, then the packed entry
-    (range-safe row scales, or the gate-residual epilogue for C5's linear2)
-    timed with HIP events on its launch stream."""
+    """The 16x16 tile GEMMs (b1_gemm16_kernel, 144 x 384 and 128 x 384) alone
+    at the Flux and Klein shapes they run: packed activations made once,
+    then the packed entry (range-safe row scales, or the gate-residual
+    epilogue for C5's linear2) timed with HIP events on its launch
+    stream."""
     out = {}
-    for name, (m, k, n), epi in TILES16_SHAPES:
+    for name, (m, k, n), epi, tile in TILES16_SHAPES:
         a = synth.device_activations(m, k, 21)
         w = synth.device_packed_weights(n, k, 22)
         pa, rs = b1.pack_act_f16_scaled(a)
@@ -137,9 +146,9 @@ def bench_tiles16(torch, b1, synth, steps, warmup):
             fn = lambda i: b1.linear_packed_f16_scaled(pa, rs, w, k, n, m, out=y)
         ms, _ = time_launches(torch, fn, steps, warmup)
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        out[name] = {"shape": [m, k, n], "epilogue": epi, "kernel_us": round(ms * 1e3, 2), "tflops": round(tf, 1),
-                     "frac": round(tf / PEAK_FP16_TFLOPS, 4)}
-        log(f"[bench] 144 x 384 tiles {name} {(m, k, n)} {epi}: {ms * 1e3:.1f} us {tf:.1f} TFLOP/s "
+        out[name] = {"shape": [m, k, n], "epilogue": epi, "tile": tile, "kernel_us": round(ms * 1e3, 2),
+                     "tflops": round(tf, 1), "frac": round(tf / PEAK_FP16_TFLOPS, 4)}
+        log(f"[bench] {tile} tiles {name} {(m, k, n)} {epi}: {ms * 1e3:.1f} us {tf:.1f} TFLOP/s "
             f"({100 * tf / PEAK_FP16_TFLOPS:.1f}% of peak)")
         del a, w, pa, rs, y
     return out
