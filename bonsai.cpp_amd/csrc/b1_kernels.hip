@@ -2043,53 +2043,67 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
                 epi.pk + (size_t)m0 * epi.ldpw, (short)0, (int)(C::BM * epi.ldpw * 4), kBufferFlags);
             const int lvoff = li * ldb + 16 * g, lpoff = li * lpb + 16 * g;
+            // Each tile's part, decided once (wave-uniform): 0 fp32, 1 the low
+            // half of a block whose high half is the next tile (one 16-byte
+            // store for both), 2 that high half (nothing more), 3 a lone
+            // half (2-byte stores).  The stores go out row tile by row tile,
+            // so the two halves of a 128-byte line leave within a few
+            // instructions of each other, in this wave or in its neighbour:
+            // ordered tile by tile, 30 % more bytes reached memory (lines
+            // written in parts).
+            int kind[C::NTL], off[C::NTL];
             int nst = 0; // vector stores per lane (wave-uniform)
 #pragma unroll
             for (int nt = 0; nt < C::NTL; ++nt) {
                 const int cb = wb + 16 * nt; // the tile's first column
+                const int c = cb - epi.split, hi = (c >> 4) & 1;
                 if (cb < epi.split) {
+                    kind[nt] = 0;
+                    off[nt] = cb * 4;
+                    nst += C::MT;
+                } else if (hi == 0 && nt + 1 < C::NTL) {
+                    kind[nt] = 1;
+                    off[nt] = (c >> 5) * 64; // the block's first dword, in bytes
+                    nst += C::MT;
+                } else if (hi == 1 && nt > 0) {
+                    kind[nt] = 2;
+                    off[nt] = 0;
+                } else {
+                    kind[nt] = 3;
+                    off[nt] = (c >> 5) * 64 + 2 * hi;
+                    nst += 4 * C::MT;
+                }
+            }
 #pragma unroll
-                    for (int mt = 0; mt < C::MT; ++mt) {
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < C::NTL; ++nt) {
+                    if (kind[nt] == 0) {
                         u32x4 v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float x = acc[mt][nt][e];
                             v[e] = __builtin_bit_cast(uint32_t, x);
                         }
-                        store16_guarded<kStoreNT>(v, ors, lvoff, mt * 16 * ldb + cb * 4);
-                    }
-                    nst += C::MT;
-                    continue;
-                }
-                const int c = cb - epi.split, hi = (c >> 4) & 1;
-                const int dw = (c >> 5) * 16; // the block's first dword
-                if (hi == 0 && nt + 1 < C::NTL) {
-                    // this tile and the next: the whole block
-#pragma unroll
-                    for (int mt = 0; mt < C::MT; ++mt) {
+                        store16_guarded<kStoreNT>(v, ors, lvoff, mt * 16 * ldb + off[nt]);
+                    } else if (kind[nt] == 1) {
                         u32x4 v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const float y0 = acc[mt][nt][e], y1 = acc[mt][nt + 1][e];
+                            const float y0 = acc[mt][nt][e], y1 = acc[mt][(nt + 1) % C::NTL][e];
                             v[e] = pack_f16(act(y0), act(y1));
                         }
-                        store16_guarded<0>(v, prs, lpoff, mt * 16 * lpb + dw * 4);
+                        store16_guarded<0>(v, prs, lpoff, mt * 16 * lpb + off[nt]);
+                    } else if (kind[nt] == 3) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float y = acc[mt][nt][e];
+                            const uint32_t h = pack_f16(act(y), 0.0f);
+                            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)h, prs, lpoff, mt * 16 * lpb + off[nt] + 4 * e,
+                                                                  0);
+                        }
                     }
-                    nst += C::MT;
-                    continue;
                 }
-                if (hi == 1 && nt > 0) continue; // written with the tile before
-#pragma unroll
-                for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float y = acc[mt][nt][e];
-                        const uint32_t h = pack_f16(act(y), 0.0f);
-                        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)h, prs, lpoff,
-                                                              mt * 16 * lpb + (dw + e) * 4 + 2 * hi, 0);
-                    }
-                nst += 4 * C::MT;
-            }
             count_nonfinite(nonfinite, bad);
             return nst >= C::EPI_STORES;
         }
