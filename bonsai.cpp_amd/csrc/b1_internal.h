@@ -68,9 +68,10 @@ size_t gemm_split_bytes(int M, int N, int splits);
 // MFMAs; full tiles, K % 384 == 0, no split), whichever needs the fewest
 // rounds on num_cus CUs, counting a BM x BN tile as BM BN / 65536 of a
 // 128 x 512 round; ties stay on 0.  A function of the shape and CU count
-// only, so every entry point picks alike.  The SwiGLU epilogues (fp32 or
-// packed) always run kernel 0.  The kernels sum K in different orders (the
-// same to ~1e-6 relative).
+// only, so every entry point picks alike, for every epilogue (the packed
+// output's SwiGLU columns need split % 384 == 0 for the 16x16 kernels;
+// otherwise kernel 0).  The kernels sum K in different orders (the same to
+// ~1e-6 relative).
 int gemm_tiles(int M, int K, int N, int num_cus);
 
 // The two halves of the workspace path.  Packed activations: u32 word

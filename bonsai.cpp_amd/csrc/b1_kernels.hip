@@ -65,6 +65,16 @@ __device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
+// fp32 -> fp16 bits of one value, rounded once from the fp32 value: the
+// empty asm keeps the compiler from folding the multiply that produced x
+// into the conversion (v_fma_mixlo_f16 rounds the exact product to fp16
+// once, which differs from the producer passes' fp32-then-fp16 rounding in
+// the rare products an fp32 rounding puts on an fp16 midpoint).
+__device__ __forceinline__ uint16_t half_bits(float x) {
+    asm("" : "+v"(x));
+    return (uint16_t)pack_f16(x, 0.0f);
+}
+
 // max(m, |a|, |b|) in one v_max3_f32: the running largest magnitude of the
 // activations a lane converts, against fp16's range (a quiet NaN operand is
 // passed over, as IEEE maxNum does: a NaN does not count as out of range).
@@ -82,6 +92,11 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Waits for this wave's LDS operations only (vmcnt and expcnt left open).
+__device__ __forceinline__ void wait_lgkmcnt0() {
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));
 }
 
 // Work-group barrier that does not drain outstanding global->LDS loads
@@ -1797,7 +1812,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                                                                      int32_t *nonfinite, int tiles_m, int tiles_n,
                                                                      int vec_store, GemmEpi epi) {
     using C = Gemm16Cfg<BM, BN>;
-    static_assert(EPI == 0 || EPI == 1 || EPI == 3, "plain, gate-residual and packed-output epilogues");
+    static_assert(EPI >= 0 && EPI <= 3, "plain, gate-residual, SwiGLU and packed-output epilogues");
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, g = lane >> 4;
@@ -1821,6 +1836,9 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
     // .. + AO - 1.  Weight group q (waves q < NWG): lane L fetches 12 bytes
     // (blocks 0-1, then 2-3 of the stage) of column n0 + 64 q + L.  Rows and
     // columns past the matrix cannot occur (full tiles).
+    // whether tile column n0's columns are SwiGLU [gate | value] pairs (EPI 2,
+    // or EPI 3 with act 2 from split on; split % BN == 0 there)
+    auto swiglu_tile = [&](int n0) { return EPI == 2 || (EPI == 3 && epi.act == 2 && n0 >= epi.split); };
     const bool wload = wave < C::NWG;
     const int a_first = wload ? C::AW * wave : C::AW * C::NWG + C::AO * (wave - C::NWG);
     uint32_t aoff[C::LOADS];
@@ -1832,7 +1850,24 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             const int c = (lane & 15) ^ (row & 15);
             aoff[i] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)c * 8) * 2;
         }
-        boff = (uint32_t)(n0 + 64 * (wload ? wave : 0) + lane) * rs;
+        int row = n0 + 64 * (wload ? wave : 0) + lane;
+        if (swiglu_tile(n0)) {
+            // SwiGLU: the tile's 24 16-column tiles are the gates and the
+            // values of its 192 outputs in 12 groups of 16; waves 2p and
+            // 2p + 1 hold groups 3p .. 3p + 2 as [gate 3p, value 3p, gate
+            // 3p + 1] and [value 3p + 1, gate 3p + 2, value 3p + 2].  Every
+            // weight row keeps the place in its 16x16 MFMA tile it has in
+            // the plain GEMM of the same rows (the MFMA's last bits depend
+            // on the place), so the outputs are those of the plain GEMM.
+            const int base = EPI == 3 ? epi.split : 0;
+            const int tc = row - n0, sub = tc >> 4, pos = tc & 15;
+            const int w = sub / 3, t = sub - 3 * w, pr = w >> 1, odd = w & 1;
+            // group and kind of sub-tile t of wave w
+            const int grp = 3 * pr + (odd ? (t == 0 ? 1 : 2) : (t == 2 ? 1 : 0));
+            const bool value = odd ? (t != 1) : (t == 1);
+            row = base + (value ? epi.glu_h : 0) + (n0 - base) / 2 + 16 * grp + pos;
+        }
+        boff = (uint32_t)row * rs;
     };
     const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(ah), (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), kBufferFlags);
@@ -1996,11 +2031,124 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
     // n0 + WN wave + 16 nt + 4 g .. + 3: one 16-byte store each (MT NTL per
     // lane), half a line per 4 lanes.  Without vec_store (out, or the
     // residual and gate, or the packed rows, not 16-byte aligned) the same
-    // values go out as scalar stores.  Returns whether at least EPI_STORES
-    // vector stores per lane are in flight.
-    auto epilogue = [&](int m0, int n0) -> bool {
+    // values go out as scalar stores.  Returns the vector stores per lane it
+    // left in flight (0 after scalar stores).
+    auto epilogue = [&](int m0, int n0) -> int {
         int bad = 0;
         count_tile(bad);
+        if constexpr (EPI == 2 || EPI == 3) {
+            if (swiglu_tile(n0)) {
+                // SwiGLU (the layout of setup): the even wave of a pair
+                // holds gate 3p and value 3p in tiles 0 and 1 (each lane
+                // both of its outputs' operands) and gate 3p + 1 in tile 2,
+                // whose values the odd wave holds in its tile 0 and passes
+                // through LDS; the odd wave holds gate and value 3p + 2 in
+                // tiles 1 and 2.  The exchange area is slot 1's activation
+                // area, idle from the last stage's barrier to the next
+                // tile's first.  silu(gate) * value as the producer pass
+                // computes it.
+                static_assert(C::NTL == 3 && C::NW % 2 == 0 && C::NW / 2 * C::MT * 1024 <= C::ASTAGE,
+                              "the SwiGLU exchange");
+                typedef __attribute__((address_space(3))) uint8_t lds8;
+                typedef __attribute__((address_space(3))) floatx4 lds_f4;
+                const bool odd = wave & 1;
+                const int pr = wave >> 1;
+                lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + pr * (C::MT * 1024) + (li * 16 + 4 * g) * 4;
+                if (odd) {
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt) *(lds_f4 *)(xa + mt * 1024) = acc[mt][0];
+                }
+                wait_lgkmcnt0();
+                lds_barrier();
+                const int ob = (n0 - (EPI == 3 ? epi.split : 0)) / 2 + 48 * pr; // the pair's first output
+                // group q of the wave (0 or 1): its first output and, for
+                // lane (li, g) and element e, its value
+                auto swiglu = [&](float gt, float vl) { return mul_f32(silu_f32(gt), vl); };
+                auto group_out = [&](int mt, int q, int e) {
+                    if (!odd) {
+                        if (q == 0) return swiglu(acc[mt][0][e], acc[mt][1][e]);
+                        const floatx4 v = *(const lds_f4 *)(xa + mt * 1024);
+                        const float ve = v[e];
+                        return swiglu(acc[mt][2][e], ve);
+                    }
+                    return swiglu(acc[mt][1][e], acc[mt][2][e]);
+                };
+                const int nq = odd ? 1 : 2;
+                auto group_first = [&](int q) { return ob + 16 * (odd ? 2 : q); };
+                if constexpr (EPI == 2) {
+                    if (!vec_store) {
+#pragma unroll
+                        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e)
+                                    if (q < nq) {
+                                        const size_t m = (size_t)(m0 + 16 * mt + li);
+                                        out[m * ldo + group_first(q) + 4 * g + e] = group_out(mt, q, e);
+                                    }
+                        count_nonfinite(nonfinite, bad);
+                        return 0;
+                    }
+                    const int ldb = stride_bytes(ldo);
+                    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+                        out + (size_t)m0 * ldo, (short)0, (int)(C::BM * ldo * 4), kBufferFlags);
+                    const int lvoff = li * ldb + 16 * g;
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                        for (int q = 0; q < 2; ++q)
+                            if (q < nq) {
+                                u32x4 v;
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) {
+                                    const float o = group_out(mt, q, e);
+                                    v[e] = __builtin_bit_cast(uint32_t, o);
+                                }
+                                store16_guarded<kStoreNT>(v, ors, lvoff, mt * 16 * ldb + group_first(q) * 4);
+                            }
+                    count_nonfinite(nonfinite, bad);
+                    return nq * C::MT;
+                } else {
+                    // packed: output column c of a row is half (c / 16) % 2 of
+                    // dword 16 (c / 32) + c % 16; a 16-output group is one
+                    // half of 16 dwords, 2-byte stores, row tile by row tile
+                    auto half_at = [&](int c) { return ((c >> 5) * 16 + (c & 15)) * 4 + 2 * ((c >> 4) & 1); };
+                    if (!vec_store) {
+#pragma unroll
+                        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e)
+                                    if (q < nq) {
+                                        const size_t m = (size_t)(m0 + 16 * mt + li);
+                                        uint8_t *rowp = reinterpret_cast<uint8_t *>(epi.pk + m * epi.ldpw);
+                                        *reinterpret_cast<uint16_t *>(rowp + half_at(group_first(q) + 4 * g + e)) =
+                                            half_bits(group_out(mt, q, e));
+                                    }
+                        count_nonfinite(nonfinite, bad);
+                        return 0;
+                    }
+                    const int lpb = stride_bytes(epi.ldpw);
+                    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+                        epi.pk + (size_t)m0 * epi.ldpw, (short)0, (int)(C::BM * epi.ldpw * 4), kBufferFlags);
+                    const int lroff = li * lpb;
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                        for (int q = 0; q < 2; ++q)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (q < nq)
+                                    __builtin_amdgcn_raw_buffer_store_b16(half_bits(group_out(mt, q, e)),
+                                                                          prs, lroff + half_at(group_first(q) + 4 * g + e),
+                                                                          mt * 16 * lpb, 0);
+                    count_nonfinite(nonfinite, bad);
+                    return 4 * nq * C::MT;
+                }
+            }
+        }
         if constexpr (EPI == 3) {
             // Columns below epi.split: fp32 into out.  From split on: fp16
             // (of GELU-tanh when epi.act) into the packed rows of epi.pk
@@ -2029,13 +2177,12 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                                 out[m * ldo + n] = y;
                             } else {
                                 const int c = n - epi.split;
-                                const uint32_t h = pack_f16(act(y), 0.0f);
-                                reinterpret_cast<uint16_t *>(epi.pk + m * epi.ldpw + (c >> 5) * 16 + (c & 15))[(c >> 4) & 1] =
-                                    (uint16_t)h;
+                                const uint16_t h = half_bits(act(y));
+                                reinterpret_cast<uint16_t *>(epi.pk + m * epi.ldpw + (c >> 5) * 16 + (c & 15))[(c >> 4) & 1] = h;
                             }
                         }
                 count_nonfinite(nonfinite, bad);
-                return false;
+                return 0;
             }
             const int ldb = stride_bytes(ldo), lpb = stride_bytes(epi.ldpw);
             const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
@@ -2098,14 +2245,14 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float y = acc[mt][nt][e];
-                            const uint32_t h = pack_f16(act(y), 0.0f);
-                            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)h, prs, lpoff, mt * 16 * lpb + off[nt] + 4 * e,
+                            const uint16_t h = half_bits(act(y));
+                            __builtin_amdgcn_raw_buffer_store_b16(h, prs, lpoff, mt * 16 * lpb + off[nt] + 4 * e,
                                                                   0);
                         }
                     }
                 }
             count_nonfinite(nonfinite, bad);
-            return nst >= C::EPI_STORES;
+            return nst;
         }
         if (!vec_store) {
 #pragma unroll
@@ -2121,7 +2268,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                         out[m * ldo + n] = y;
                     }
             count_nonfinite(nonfinite, bad);
-            return false;
+            return 0;
         }
         const int ldb = stride_bytes(ldo);
         const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
@@ -2179,7 +2326,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             }
         }
         count_nonfinite(nonfinite, bad);
-        return true;
+        return C::EPI_STORES;
     };
 
     int unit = xcd_tile(blockIdx.x, gridDim.x);
@@ -2202,7 +2349,10 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
     setup(m0, n0);
     issue_rsc(parity);
     issue(0, 0);
-    bool prev_stores = false; // the previous epilogue's EPI_STORES stores are in flight
+    // what the previous epilogue left in flight: EPI_STORES vector stores per
+    // lane, or (a SwiGLU tile, or a packed-output wave that wrote one or two
+    // blocks) MT
+    bool prev_stores = false, prev_part = false;
     for (;;) {
 #pragma unroll
         for (int i = 0; i < C::MT; ++i)
@@ -2221,6 +2371,8 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             for (int u = 0; u < C::STAGES; ++u) {
                 if (s == 0 && u == 0 && prev_stores)
                     wait_vmcnt<C::EPI_STORES>();
+                else if ((EPI == 2 || EPI == 3) && s == 0 && u == 0 && prev_part)
+                    wait_vmcnt<C::MT>();
                 else
                     wait_vmcnt<0>(); // (after scalar stores, or in the first tile, everything)
                 lds_barrier();
@@ -2259,7 +2411,9 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                         for (int v = 0; v < 4; ++v) acc[mt][nt][v] *= sc[mt];
             }
         }
-        prev_stores = epilogue(cm0, cn0);
+        const int ns = epilogue(cm0, cn0);
+        prev_stores = ns >= C::EPI_STORES;
+        prev_part = (EPI == 2 || EPI == 3) && ns >= C::MT;
         if (!more) break;
     }
 }
@@ -3436,10 +3590,12 @@ static hipError_t launch_gemm_packed_t(const void *packed, const uint8_t *w, int
                                        hipStream_t s, int ksplit = 1, float *partials = nullptr) {
     // (with ksplit > 1 the row scales epi.rsc go to the reduction, not the
     // GEMM, which writes plain partial products)
-    // (the SwiGLU epilogues pair a gate and a value 32-column tile in each
-    // wave of the 128 x 512 kernel and always run it)
-    if constexpr (EPI == 0 || EPI == 1 || EPI == 3) {
-        if (!(ksplit > 1 && partials != nullptr) && !(EPI == 3 && epi.act == 2)) {
+    // (a packed SwiGLU output on 16x16 tiles needs the split point on a
+    // tile boundary, every tile wholly fp32 or wholly SwiGLU pairs; otherwise
+    // it runs the 128 x 512 kernel)
+    {
+        const bool tiles_ok = !(EPI == 3 && epi.act == 2 && epi.split % 384 != 0);
+        if (!(ksplit > 1 && partials != nullptr) && tiles_ok) {
             const int t = gemm_tiles(M, K, N, num_cus);
             if (t == 1) return launch_gemm16_t<144, 384, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);
             if (t == 2) return launch_gemm16_t<128, 384, EPI>(packed, w, K, N, M, out, ldo, nonfinite, num_cus, epi, s);

@@ -72,6 +72,12 @@ CASES = [
     (512, 384, 768, 160, "gelu_tanh", 96, 800),
     (2048, 384, 9216, 4096, "gelu_tanh", 0, None),
     (4608, 384, 9216, 3072, "gelu_tanh", 0, None),
+    # SwiGLU on 16x16 tiles (split on a 384-column tile boundary): every
+    # wave's 24 gates paired with their values, written as fp16 halves
+    (512, 384, 768, 0, "swiglu", 0, None),
+    (288, 384, 1152, 384, "swiglu", 0, None),
+    (512, 384, 1536, 768, "swiglu", 32, 432),
+    (4608, 384, 18432, 9216, "swiglu", 0, None),
 ]
 
 
