@@ -165,7 +165,9 @@ def test_epilogue_counts_linear_outputs(torch, b1):
 
 # ---------------------------------------------- LayerNorm + modulation (A) --
 
-@pytest.mark.parametrize("rows,h", [(4096, 3072), (37, 3072), (5, 12288), (3, 96)])
+# (4608 rows: more work-groups than one round of the grid holds; 2051 x
+# 1536: a ragged row count at a shorter row)
+@pytest.mark.parametrize("rows,h", [(4096, 3072), (4608, 3072), (2051, 1536), (37, 3072), (5, 12288), (3, 96)])
 def test_norm_mod_matches_oracle(torch, b1, oracle, rows, h):
     """bonsai_b1_norm_mod_f32 against the oracle's restatement of ggml_norm
     + modulation, bit for bit; the _pack form against the oracle's fp16 pack
