@@ -75,6 +75,13 @@ __device__ __forceinline__ uint16_t half_bits(float x) {
     return (uint16_t)pack_f16(x, 0.0f);
 }
 
+// (lo, hi) -> packed fp16 pair, each rounded once from its fp32 value (the
+// fold half_bits keeps out, for two values).
+__device__ __forceinline__ uint32_t pack_f16_rounded(float lo, float hi) {
+    asm("" : "+v"(lo), "+v"(hi));
+    return pack_f16(lo, hi);
+}
+
 // max(m, |a|, |b|) in one v_max3_f32: the running largest magnitude of the
 // activations a lane converts, against fp16's range (a quiet NaN operand is
 // passed over, as IEEE maxNum does: a NaN does not count as out of range).
@@ -1853,18 +1860,17 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
         int row = n0 + 64 * (wload ? wave : 0) + lane;
         if (swiglu_tile(n0)) {
             // SwiGLU: the tile's 24 16-column tiles are the gates and the
-            // values of its 192 outputs in 12 groups of 16; waves 2p and
-            // 2p + 1 hold groups 3p .. 3p + 2 as [gate 3p, value 3p, gate
-            // 3p + 1] and [value 3p + 1, gate 3p + 2, value 3p + 2].  Every
-            // weight row keeps the place in its 16x16 MFMA tile it has in
-            // the plain GEMM of the same rows (the MFMA's last bits depend
-            // on the place), so the outputs are those of the plain GEMM.
+            // values of its 192 outputs in 12 groups of 16.  Waves 4h + r,
+            // r < 3, hold [gate 6h + 2r, its value, gate 6h + 2r + 1]
+            // (groups 6h + 2r and 6h + 2r + 1 are packed block 3h + r);
+            // wave 4h + 3 holds the values of groups 6h + 1, 6h + 3 and
+            // 6h + 5 (the epilogue passes them to the block's wave).  Each
+            // weight row keeps its place within its 16-column MFMA tile.
             const int base = EPI == 3 ? epi.split : 0;
             const int tc = row - n0, sub = tc >> 4, pos = tc & 15;
-            const int w = sub / 3, t = sub - 3 * w, pr = w >> 1, odd = w & 1;
-            // group and kind of sub-tile t of wave w
-            const int grp = 3 * pr + (odd ? (t == 0 ? 1 : 2) : (t == 2 ? 1 : 0));
-            const bool value = odd ? (t != 1) : (t == 1);
+            const int w = sub / 3, t = sub - 3 * w, h = w >> 2, r = w & 3;
+            const int grp = r < 3 ? 6 * h + 2 * r + (t == 2) : 6 * h + 2 * t + 1;
+            const bool value = r < 3 ? t == 1 : true;
             row = base + (value ? epi.glu_h : 0) + (n0 - base) / 2 + 16 * grp + pos;
         }
         boff = (uint32_t)row * rs;
@@ -2038,55 +2044,58 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
         count_tile(bad);
         if constexpr (EPI == 2 || EPI == 3) {
             if (swiglu_tile(n0)) {
-                // SwiGLU (the layout of setup): the even wave of a pair
-                // holds gate 3p and value 3p in tiles 0 and 1 (each lane
-                // both of its outputs' operands) and gate 3p + 1 in tile 2,
-                // whose values the odd wave holds in its tile 0 and passes
-                // through LDS; the odd wave holds gate and value 3p + 2 in
-                // tiles 1 and 2.  The exchange area is slot 1's activation
-                // area, idle from the last stage's barrier to the next
-                // tile's first.  silu(gate) * value as the producer pass
-                // computes it.
-                static_assert(C::NTL == 3 && C::NW % 2 == 0 && C::NW / 2 * C::MT * 1024 <= C::ASTAGE,
-                              "the SwiGLU exchange");
+                // SwiGLU (the layout of setup): wave 4h + 3 passes its three
+                // value tiles through LDS (slots 1 and 2's activation area,
+                // idle from the last stage's barrier to the next tile's
+                // first); wave 4h + r, r < 3, then holds block 3h + r: low
+                // group silu(tile 0) * tile 1, high group silu(tile 2) *
+                // the passed values, silu(gate) * value as the producer pass
+                // computes it, and stores it row tile by row tile (fp32: two
+                // 16-byte stores, the line's halves; packed: one, dwords
+                // 4g .. 4g + 3 of the block's row).
+                static_assert(C::NTL == 3 && C::NW == 8 && 6 * C::MT * 1024 <= 2 * C::ASTAGE, "the SwiGLU exchange");
                 typedef __attribute__((address_space(3))) uint8_t lds8;
                 typedef __attribute__((address_space(3))) floatx4 lds_f4;
-                const bool odd = wave & 1;
-                const int pr = wave >> 1;
-                lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + pr * (C::MT * 1024) + (li * 16 + 4 * g) * 4;
-                if (odd) {
+                const int h = wave >> 2, r = wave & 3;
+                lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + h * (3 * C::MT * 1024) + (li * 16 + 4 * g) * 4;
+                if (r == 3) {
 #pragma unroll
-                    for (int mt = 0; mt < C::MT; ++mt) *(lds_f4 *)(xa + mt * 1024) = acc[mt][0];
+                    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                        for (int t = 0; t < 3; ++t) *(lds_f4 *)(xa + (t * C::MT + mt) * 1024) = acc[mt][t];
                 }
                 wait_lgkmcnt0();
                 lds_barrier();
-                const int ob = (n0 - (EPI == 3 ? epi.split : 0)) / 2 + 48 * pr; // the pair's first output
-                // group q of the wave (0 or 1): its first output and, for
-                // lane (li, g) and element e, its value
+                if (r == 3) {
+                    count_nonfinite(nonfinite, bad);
+                    return 0;
+                }
+                // the block's first output
+                const int ob = (n0 - (EPI == 3 ? epi.split : 0)) / 2 + 32 * (3 * h + r);
                 auto swiglu = [&](float gt, float vl) { return mul_f32(silu_f32(gt), vl); };
-                auto group_out = [&](int mt, int q, int e) {
-                    if (!odd) {
-                        if (q == 0) return swiglu(acc[mt][0][e], acc[mt][1][e]);
-                        const floatx4 v = *(const lds_f4 *)(xa + mt * 1024);
+                // the block's low and high outputs of row tile mt, element e
+                auto block_out = [&](int mt, floatx4 &lo, floatx4 &hi) {
+                    const floatx4 v = *(const lds_f4 *)(xa + (r * C::MT + mt) * 1024);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        lo[e] = swiglu(acc[mt][0][e], acc[mt][1][e]);
                         const float ve = v[e];
-                        return swiglu(acc[mt][2][e], ve);
+                        hi[e] = swiglu(acc[mt][2][e], ve);
                     }
-                    return swiglu(acc[mt][1][e], acc[mt][2][e]);
                 };
-                const int nq = odd ? 1 : 2;
-                auto group_first = [&](int q) { return ob + 16 * (odd ? 2 : q); };
                 if constexpr (EPI == 2) {
                     if (!vec_store) {
 #pragma unroll
-                        for (int mt = 0; mt < C::MT; ++mt)
+                        for (int mt = 0; mt < C::MT; ++mt) {
+                            floatx4 lo, hi;
+                            block_out(mt, lo, hi);
+                            const size_t m = (size_t)(m0 + 16 * mt + li);
 #pragma unroll
-                            for (int q = 0; q < 2; ++q)
-#pragma unroll
-                                for (int e = 0; e < 4; ++e)
-                                    if (q < nq) {
-                                        const size_t m = (size_t)(m0 + 16 * mt + li);
-                                        out[m * ldo + group_first(q) + 4 * g + e] = group_out(mt, q, e);
-                                    }
+                            for (int e = 0; e < 4; ++e) {
+                                out[m * ldo + ob + 4 * g + e] = lo[e];
+                                out[m * ldo + ob + 16 + 4 * g + e] = hi[e];
+                            }
+                        }
                         count_nonfinite(nonfinite, bad);
                         return 0;
                     }
@@ -2095,57 +2104,53 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                         out + (size_t)m0 * ldo, (short)0, (int)(C::BM * ldo * 4), kBufferFlags);
                     const int lvoff = li * ldb + 16 * g;
 #pragma unroll
-                    for (int mt = 0; mt < C::MT; ++mt)
+                    for (int mt = 0; mt < C::MT; ++mt) {
+                        floatx4 lo, hi;
+                        block_out(mt, lo, hi);
+                        u32x4 a, b;
 #pragma unroll
-                        for (int q = 0; q < 2; ++q)
-                            if (q < nq) {
-                                u32x4 v;
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) {
-                                    const float o = group_out(mt, q, e);
-                                    v[e] = __builtin_bit_cast(uint32_t, o);
-                                }
-                                store16_guarded<kStoreNT>(v, ors, lvoff, mt * 16 * ldb + group_first(q) * 4);
-                            }
+                        for (int e = 0; e < 4; ++e) {
+                            const float x0 = lo[e], x1 = hi[e];
+                            a[e] = __builtin_bit_cast(uint32_t, x0);
+                            b[e] = __builtin_bit_cast(uint32_t, x1);
+                        }
+                        store16_guarded<kStoreNT>(a, ors, lvoff, mt * 16 * ldb + ob * 4);
+                        store16_guarded<kStoreNT>(b, ors, lvoff, mt * 16 * ldb + ob * 4 + 64);
+                    }
                     count_nonfinite(nonfinite, bad);
-                    return nq * C::MT;
+                    return 2 * C::MT;
                 } else {
                     // packed: output column c of a row is half (c / 16) % 2 of
-                    // dword 16 (c / 32) + c % 16; a 16-output group is one
-                    // half of 16 dwords, 2-byte stores, row tile by row tile
-                    auto half_at = [&](int c) { return ((c >> 5) * 16 + (c & 15)) * 4 + 2 * ((c >> 4) & 1); };
+                    // dword 16 (c / 32) + c % 16: the block is dwords ob / 2 ..
+                    // + 15 of the row
                     if (!vec_store) {
 #pragma unroll
-                        for (int mt = 0; mt < C::MT; ++mt)
+                        for (int mt = 0; mt < C::MT; ++mt) {
+                            floatx4 lo, hi;
+                            block_out(mt, lo, hi);
+                            const size_t m = (size_t)(m0 + 16 * mt + li);
 #pragma unroll
-                            for (int q = 0; q < 2; ++q)
-#pragma unroll
-                                for (int e = 0; e < 4; ++e)
-                                    if (q < nq) {
-                                        const size_t m = (size_t)(m0 + 16 * mt + li);
-                                        uint8_t *rowp = reinterpret_cast<uint8_t *>(epi.pk + m * epi.ldpw);
-                                        *reinterpret_cast<uint16_t *>(rowp + half_at(group_first(q) + 4 * g + e)) =
-                                            half_bits(group_out(mt, q, e));
-                                    }
+                            for (int e = 0; e < 4; ++e)
+                                epi.pk[m * epi.ldpw + ob / 2 + 4 * g + e] = pack_f16_rounded(lo[e], hi[e]);
+                        }
                         count_nonfinite(nonfinite, bad);
                         return 0;
                     }
                     const int lpb = stride_bytes(epi.ldpw);
                     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
                         epi.pk + (size_t)m0 * epi.ldpw, (short)0, (int)(C::BM * epi.ldpw * 4), kBufferFlags);
-                    const int lroff = li * lpb;
+                    const int lpoff = li * lpb + 16 * g;
 #pragma unroll
-                    for (int mt = 0; mt < C::MT; ++mt)
+                    for (int mt = 0; mt < C::MT; ++mt) {
+                        floatx4 lo, hi;
+                        block_out(mt, lo, hi);
+                        u32x4 v;
 #pragma unroll
-                        for (int q = 0; q < 2; ++q)
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (q < nq)
-                                    __builtin_amdgcn_raw_buffer_store_b16(half_bits(group_out(mt, q, e)),
-                                                                          prs, lroff + half_at(group_first(q) + 4 * g + e),
-                                                                          mt * 16 * lpb, 0);
+                        for (int e = 0; e < 4; ++e) v[e] = pack_f16_rounded(lo[e], hi[e]);
+                        store16_guarded<0>(v, prs, lpoff, mt * 16 * lpb + ob * 2);
+                    }
                     count_nonfinite(nonfinite, bad);
-                    return 4 * nq * C::MT;
+                    return C::MT;
                 }
             }
         }
