@@ -1846,6 +1846,9 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
     // whether tile column n0's columns are SwiGLU [gate | value] pairs (EPI 2,
     // or EPI 3 with act 2 from split on; split % BN == 0 there)
     auto swiglu_tile = [&](int n0) { return EPI == 2 || (EPI == 3 && epi.act == 2 && n0 >= epi.split); };
+    // whether tile column n0 is wholly packed GELU or plain (EPI 3, act 0 or
+    // 1, from split on)
+    auto packed_tile = [&](int n0) { return EPI == 3 && epi.act != 2 && n0 >= epi.split; };
     const bool wload = wave < C::NWG;
     const int a_first = wload ? C::AW * wave : C::AW * C::NWG + C::AO * (wave - C::NWG);
     uint32_t aoff[C::LOADS];
@@ -1872,6 +1875,18 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             const int grp = r < 3 ? 6 * h + 2 * r + (t == 2) : 6 * h + 2 * t + 1;
             const bool value = r < 3 ? t == 1 : true;
             row = base + (value ? epi.glu_h : 0) + (n0 - base) / 2 + 16 * grp + pos;
+        } else if (packed_tile(n0)) {
+            // Packed columns: the tile's 12 blocks of 32 columns, each a low
+            // and a high 16-column half.  Waves 4h + r, r < 3, hold [low and
+            // high half of block 6h + 2r, low half of block 6h + 2r + 1];
+            // wave 4h + 3 holds the high halves of blocks 6h + 1, 6h + 3 and
+            // 6h + 5 (the epilogue passes them on).  Each weight row keeps
+            // its place within its 16-column MFMA tile.
+            const int tc = row - n0, sub = tc >> 4, pos = tc & 15;
+            const int w = sub / 3, t = sub - 3 * w, h = w >> 2, r = w & 3;
+            const int blk = 6 * h + (r < 3 ? 2 * r + (t == 2) : 2 * t + 1);
+            const int half = r < 3 ? t == 1 : 1;
+            row = n0 + 32 * blk + 16 * half + pos;
         }
         boff = (uint32_t)row * rs;
     };
@@ -2155,8 +2170,81 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             }
         }
         if constexpr (EPI == 3) {
-            // Columns below epi.split: fp32 into out.  From split on: fp16
-            // (of GELU-tanh when epi.act) into the packed rows of epi.pk
+            if (packed_tile(n0)) {
+                // A wholly packed tile (the layout of setup): wave 4h + 3
+                // applies the activation to its three high halves and passes
+                // them through LDS (slots 1 and 2's activation area, free
+                // from the last stage's barrier to the next tile's first);
+                // wave 4h + r, r < 3, then holds blocks 6h + 2r and 6h + 2r +
+                // 1, a 128-byte line of each row, and stores it row tile by
+                // row tile as two 16-byte stores (dwords 4g .. 4g + 3 of each
+                // block).
+                static_assert(C::NTL == 3 && C::NW == 8 && 6 * C::MT * 1024 <= 2 * C::ASTAGE, "the block exchange");
+                typedef __attribute__((address_space(3))) uint8_t lds8;
+                typedef __attribute__((address_space(3))) floatx4 lds_f4;
+                auto act = [&](float y) { return epi.act ? gelu_tanh(y) : y; };
+                const int h = wave >> 2, r = wave & 3;
+                lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + h * (3 * C::MT * 1024) + (li * 16 + 4 * g) * 4;
+                if (r == 3) {
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                        for (int t = 0; t < 3; ++t) {
+                            floatx4 v;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = act(acc[mt][t][e]);
+                            *(lds_f4 *)(xa + (t * C::MT + mt) * 1024) = v;
+                        }
+                }
+                wait_lgkmcnt0();
+                lds_barrier();
+                if (r == 3) {
+                    count_nonfinite(nonfinite, bad);
+                    return 0;
+                }
+                // the line's first byte in the packed row: block 6h + 2r
+                const int cb = (n0 - epi.split) * 2 + 64 * (6 * h + 2 * r);
+                auto line = [&](int mt, u32x4 &a, u32x4 &b) {
+                    const floatx4 v = *(const lds_f4 *)(xa + (r * C::MT + mt) * 1024);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float ve = v[e];
+                        a[e] = pack_f16_rounded(act(acc[mt][0][e]), act(acc[mt][1][e]));
+                        b[e] = pack_f16_rounded(act(acc[mt][2][e]), ve);
+                    }
+                };
+                if (!vec_store) {
+#pragma unroll
+                    for (int mt = 0; mt < C::MT; ++mt) {
+                        u32x4 a, b;
+                        line(mt, a, b);
+                        uint32_t *rowp = epi.pk + (size_t)(m0 + 16 * mt + li) * epi.ldpw + cb / 4 + 4 * g;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            rowp[e] = a[e];
+                            rowp[16 + e] = b[e];
+                        }
+                    }
+                    count_nonfinite(nonfinite, bad);
+                    return 0;
+                }
+                const int lpb = stride_bytes(epi.ldpw);
+                const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+                    epi.pk + (size_t)m0 * epi.ldpw, (short)0, (int)(C::BM * epi.ldpw * 4), kBufferFlags);
+                const int lpoff = li * lpb + 16 * g;
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt) {
+                    u32x4 a, b;
+                    line(mt, a, b);
+                    store16_guarded<0>(a, prs, lpoff, mt * 16 * lpb + cb);
+                    store16_guarded<0>(b, prs, lpoff, mt * 16 * lpb + cb + 64);
+                }
+                count_nonfinite(nonfinite, bad);
+                return 2 * C::MT;
+            }
+            // A tile of fp32 columns, or one the split point crosses (the
+            // plain layout).  Columns below epi.split: fp32 into out.  From
+            // split on: fp16 (of GELU-tanh when epi.act) into the packed rows of epi.pk
             // (ldpw dwords apart), as the next linear reads them: column
             // split + 32 b + e of a row is half e / 16 of dword 16 b + e % 16.
             // split % 32 == 0 and tiles are 16-column aligned, so a tile is

@@ -78,6 +78,10 @@ CASES = [
     (288, 384, 1152, 384, "swiglu", 0, None),
     (512, 384, 1536, 768, "swiglu", 32, 432),
     (4608, 384, 18432, 9216, "swiglu", 0, None),
+    # packed rows of 2^22 + 32 fp16 elements, past the range of a buffer
+    # resource over a tile's rows: the element-by-element stores
+    (288, 384, 768, 0, "gelu_tanh", 0, 2**22 + 32),
+    (512, 384, 1536, 0, "swiglu", 0, 2**22 + 32),
 ]
 
 
