@@ -2074,7 +2074,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                 typedef __attribute__((address_space(3))) uint8_t lds8;
                 typedef __attribute__((address_space(3))) floatx4 lds_f4;
                 const int h = wave >> 2, r = wave & 3;
-                lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + h * (3 * C::MT * 1024) + (li * 16 + 4 * g) * 4;
+                lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + h * (3 * C::MT * 1024) + lane * 16;
                 if (r == 3) {
 #pragma unroll
                     for (int mt = 0; mt < C::MT; ++mt)
@@ -2186,7 +2186,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                 typedef __attribute__((address_space(3))) floatx4 lds_f4;
                 auto act = [&](float y) { return epi.act ? gelu_tanh(y) : y; };
                 const int h = wave >> 2, r = wave & 3;
-                lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + h * (3 * C::MT * 1024) + (li * 16 + 4 * g) * 4;
+                lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + h * (3 * C::MT * 1024) + lane * 16;
                 if (r == 3) {
 #pragma unroll
                     for (int mt = 0; mt < C::MT; ++mt)
