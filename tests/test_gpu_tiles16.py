@@ -104,6 +104,26 @@ def test_tiles16_against_oracle_and_entries(torch, b1, oracle, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES144[:2] + SHAPES128[:2])
+def test_tiles16_swiglu_scalar_store(torch, b1, m, k, n):
+    """The fused SwiGLU epilogue into rows whose stride is not a multiple
+    of 4 (element stores, the owner waves' block layout) gives the bits of
+    the aligned call, which equal silu(gate) * value over the plain GEMM's
+    columns as the separate epilogue pass computes them."""
+    from bonsai_b1 import synth
+    say(f"tiles16 swiglu scalar stores ({m},{k},{n})")
+    h = n // 2
+    a = synth.device_activations(m, k, 211)
+    w = synth.device_packed_weights(n, k, 212)
+    pa = b1.pack_act_f16(a)
+    want = b1.linear_packed_f16_epi(pa, w, k, n, m, "swiglu")
+    odd = torch.full((m, h + 1), 7.0, device="cuda")
+    b1.linear_packed_f16_epi(pa, w, k, n, m, "swiglu", out=odd[:, :h])
+    torch.cuda.synchronize()
+    assert torch.equal(odd[:, :h], want), "scalar-store path"
+    assert bool((odd[:, h] == 7.0).all())
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES144[:2] + SHAPES128[:2])
 def test_tiles16_gate_residual(torch, b1, m, k, n):
     """out = residual + gate * y, fused, equals the fp32 multiply then add on
     the plain y; in place (residual = out) too."""
