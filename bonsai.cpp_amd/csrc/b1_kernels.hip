@@ -2062,9 +2062,11 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
         if constexpr (EPI == 2 || EPI == 3) {
             if (swiglu_tile(n0)) {
                 // SwiGLU (the layout of setup): wave 4h + 3 passes its three
-                // value tiles through LDS (slots 1 and 2's activation area,
-                // idle from the last stage's barrier to the next tile's
-                // first); wave 4h + r, r < 3, then holds block 3h + r: low
+                // value tiles through LDS (slots 1 and 2's activation area:
+                // slot 1's is idle from the last stage's barrier to the next
+                // tile's first, slot 2's once every wave has finished the
+                // last stage, hence the barrier before the writes); wave
+                // 4h + r, r < 3, then holds block 3h + r: low
                 // group silu(tile 0) * tile 1, high group silu(tile 2) *
                 // the passed values, silu(gate) * value as the producer pass
                 // computes it, and stores it row tile by row tile (fp32: two
@@ -2075,6 +2077,9 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                 typedef __attribute__((address_space(3))) floatx4 lds_f4;
                 const int h = wave >> 2, r = wave & 3;
                 lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + h * (3 * C::MT * 1024) + lane * 16;
+                // the area runs into slot 2's, which slower waves may still
+                // be reading for the tile's last stage
+                lds_barrier();
                 if (r == 3) {
 #pragma unroll
                     for (int mt = 0; mt < C::MT; ++mt)
@@ -2175,8 +2180,8 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
             if (packed_tile(n0)) {
                 // A wholly packed tile (the layout of setup): wave 4h + 3
                 // applies the activation to its three high halves and passes
-                // them through LDS (slots 1 and 2's activation area, free
-                // from the last stage's barrier to the next tile's first);
+                // them through LDS (slots 1 and 2's activation area, after a
+                // barrier: slot 2 holds the last stage);
                 // wave 4h + r, r < 3, then holds blocks 6h + 2r and 6h + 2r +
                 // 1, a 128-byte line of each row, and stores it row tile by
                 // row tile as two 16-byte stores (dwords 4g .. 4g + 3 of each
@@ -2187,6 +2192,7 @@ __global__ __launch_bounds__((Gemm16Cfg<BM, BN>::NT), 2) void b1_gemm16_kernel(c
                 auto act = [&](float y) { return epi.act ? gelu_tanh(y) : y; };
                 const int h = wave >> 2, r = wave & 3;
                 lds8 *const xa = (lds8 *)smem + C::ABASE + C::ASTAGE + h * (3 * C::MT * 1024) + lane * 16;
+                lds_barrier(); // (as in the SwiGLU exchange: slot 2's area)
                 if (r == 3) {
 #pragma unroll
                     for (int mt = 0; mt < C::MT; ++mt)
