@@ -478,6 +478,14 @@ __device__ __forceinline__ floatx4 load_f4(const float *p) {
 // Producer inputs from this size on are streamed with non-temporal loads.
 constexpr uint64_t kNtInputBytes = 128ull << 20;
 
+template <bool NT>
+__device__ __forceinline__ void store_f4(float *p, const floatx4 &v) {
+    if constexpr (NT)
+        __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(p));
+    else
+        *reinterpret_cast<floatx4 *>(p) = v;
+}
+
 // ------------------------------------------------------------- GELU-tanh --
 //
 // 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), elementwise in
@@ -500,18 +508,44 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
-__global__ __launch_bounds__(256) void b1_gelu_kernel(const float *__restrict__ x, int64_t ldx,
-                                                      float *__restrict__ y, int64_t ldy, int cols, int rows) {
+// Four float4 units in flight per thread (loads first), non-temporal past
+// 128 MB: a grid of at most 8192 blocks walking one unit at a time ran
+// 81.2 us at 4608 x 12288 (2.8 TB/s read), this form 72.0 us.  In place
+// (x == y) too: a thread writes only the units it has read.
+template <bool NT>
+__global__ __launch_bounds__(256) void b1_gelu_kernel(const float *x, int64_t ldx, float *y, int64_t ldy, int cols,
+                                                      int rows) {
     const int q = cols / 4; // float4 units per row (cols % 4 == 0)
     const int64_t units = (int64_t)rows * q;
-    for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; u + 3 * stride < units; u += 4 * stride) {
+        int64_t r[4];
+        int c[4];
+        floatx4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t uk = u + k * stride;
+            r[k] = uk / q;
+            c[k] = (int)(uk - r[k] * q) * 4;
+            v[k] = load_f4<NT>(x + r[k] * ldx + c[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            floatx4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = gelu_tanh(v[k][j]);
+            store_f4<NT>(y + r[k] * ldy + c[k], o);
+        }
+    }
+    for (; u < units; u += stride) {
         const int64_t r = u / q;
         const int c = (int)(u - r * q) * 4;
-        const floatx4 v = *reinterpret_cast<const floatx4 *>(x + r * ldx + c);
+        const floatx4 v = load_f4<NT>(x + r * ldx + c);
         floatx4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = gelu_tanh(v[j]);
-        *reinterpret_cast<floatx4 *>(y + r * ldy + c) = o;
+        store_f4<NT>(y + r * ldy + c, o);
     }
 }
 
@@ -3899,9 +3933,11 @@ hipError_t launch_epi_packed(const float *y, int64_t ldy, int M, int N, const Ge
 
 hipError_t launch_gelu(const float *x, int64_t ldx, float *y, int64_t ldy, int cols, int rows, hipStream_t s) {
     const int64_t units = (int64_t)rows * (cols / 4);
-    const int64_t want = (units + 255) / 256;
-    const int grid = (int)(want < 8192 ? want : 8192);
-    hipLaunchKernelGGL(b1_gelu_kernel, dim3(grid), dim3(256), 0, s, x, ldx, y, ldy, cols, rows);
+    const int64_t want = (units + 1023) / 1024; // 4 units a thread
+    const int grid = (int)(want < 65535 ? want : 65535);
+    const bool nt = (uint64_t)rows * (uint64_t)cols * 4 > kNtInputBytes;
+    hipLaunchKernelGGL(nt ? b1_gelu_kernel<true> : b1_gelu_kernel<false>, dim3(grid), dim3(256), 0, s, x, ldx, y, ldy,
+                       cols, rows);
     return hipGetLastError();
 }
 
