@@ -72,6 +72,9 @@ CASES = [
     (512, 384, 768, 160, "gelu_tanh", 96, 800),
     (2048, 384, 9216, 4096, "gelu_tanh", 0, None),
     (4608, 384, 9216, 3072, "gelu_tanh", 0, None),
+    # no activation, tiles wholly past the split point (the owner layout)
+    (512, 384, 768, 0, "none", 0, None),
+    (288, 384, 1152, 384, "none", 0, None),
     # SwiGLU on 16x16 tiles (split on a 384-column tile boundary): every
     # wave's 24 gates paired with their values, written as fp16 halves
     (512, 384, 768, 0, "swiglu", 0, None),
