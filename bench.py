@@ -429,22 +429,13 @@ def bench_c5_block_chain(torch, b1, synth, blocks=38, producer_form=False):
     return r
 
 
-def bench_configs(torch, b1, synth, steps, warmup):
-    """The other config shapes, each from fp32 activations through
-    bonsai_b1_linear_f32 (pack pass + GEMM; split along K where the shape
-    asks for it): C1 (256 x 3072 -> 3072), C3 q/k/v and out-projection,
-    C4 up- and down-projection, GELU-tanh between them, and the C4 chain in
-    its fused form (GELU in the up-projection's epilogue, written as the
-    down-projection's packed input); then the C5 38-block step."""
+def bench_c4_mlp(torch, b1, synth, reps=4):
+    """C4 between its GEMMs: the standalone GELU-tanh over the up-projection's
+    fp32 output (4608 x 12288, into a separate buffer), and the C4
+    chain in its fused form (pack, up-projection with GELU in its epilogue
+    written as the down-projection's packed input, down-projection), each
+    captured into a HIP graph and replayed."""
     out = {}
-    for name, shp in [("c1_parity", (256, 3072, 3072)), ("c3_qkv", (4608, 3072, 9216)),
-                      ("c3_out", (4608, 3072, 3072)), ("c4_up", (4608, 3072, 12288)),
-                      ("c4_down", (4608, 12288, 3072))]:
-        r = bench_gemm(torch, b1, synth, *shp, steps, warmup)
-        out[name] = {"shape": list(shp), "us": round(r["ms"] * 1e3, 2), "tflops": round(r["tflops"], 1),
-                     "frac": round(r["frac"], 4)}
-        log(f"[bench] {name} {shp}: {r['ms']*1e3:.1f} us {r['tflops']:.1f} TFLOP/s ({100*r['frac']:.1f}% of peak)")
-        del r
     m, k, hid = 4608, 3072, 12288
     a = synth.device_activations(m, k, 11)
     wu = synth.device_packed_weights(hid, k, 12)
@@ -456,7 +447,7 @@ def bench_configs(torch, b1, synth, steps, warmup):
     ph = torch.empty(m * hid * 2, dtype=torch.uint8, device="cuda")
     y2 = torch.empty((m, k), device="cuda")
     b1.linear(a, wu, hid, out=y1)
-    gelu_ms = graph_ms(torch, lambda: [b1.gelu_tanh(y1, out=g) for _ in range(4)]) / 4
+    gelu_ms = graph_ms(torch, lambda: [b1.gelu_tanh(y1, out=g) for _ in range(reps)]) / reps
 
     def chain():
         b1.pack_act_f16_scaled(a, packed=pa, row_scale=rs)
@@ -474,6 +465,26 @@ def bench_configs(torch, b1, synth, steps, warmup):
     log(f"[bench] c4 GELU {gelu_ms*1e3:.1f} us; c4 chain {chain_ms*1e3:.1f} us "
         f"({out['c4_chain']['tflops']:.0f} TFLOP/s)")
     del a, wu, wd, y1, g, pa, ph, y2
+    return out
+
+
+def bench_configs(torch, b1, synth, steps, warmup):
+    """The other config shapes, each from fp32 activations through
+    bonsai_b1_linear_f32 (pack pass + GEMM; split along K where the shape
+    asks for it): C1 (256 x 3072 -> 3072), C3 q/k/v and out-projection,
+    C4 up- and down-projection, GELU-tanh between them, and the C4 chain in
+    its fused form (GELU in the up-projection's epilogue, written as the
+    down-projection's packed input); then the C5 38-block step."""
+    out = {}
+    for name, shp in [("c1_parity", (256, 3072, 3072)), ("c3_qkv", (4608, 3072, 9216)),
+                      ("c3_out", (4608, 3072, 3072)), ("c4_up", (4608, 3072, 12288)),
+                      ("c4_down", (4608, 12288, 3072))]:
+        r = bench_gemm(torch, b1, synth, *shp, steps, warmup)
+        out[name] = {"shape": list(shp), "us": round(r["ms"] * 1e3, 2), "tflops": round(r["tflops"], 1),
+                     "frac": round(r["frac"], 4)}
+        log(f"[bench] {name} {shp}: {r['ms']*1e3:.1f} us {r['tflops']:.1f} TFLOP/s ({100*r['frac']:.1f}% of peak)")
+        del r
+    out.update(bench_c4_mlp(torch, b1, synth))
     torch.cuda.empty_cache()
     c5 = bench_c5_block_chain(torch, b1, synth)
     out["c5_step"] = {x: (round(v, 4) if isinstance(v, float) else v) for x, v in c5.items()}
@@ -933,7 +944,7 @@ def main():
     ap.add_argument("--all", action="store_true", help="also time the secondary legs (stderr and JSON)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1/C3/C4/C5 config legs")
-    ap.add_argument("--only", choices=["gemm", "gemv", "copy", "c5chain", "tiles16"], default=None,
+    ap.add_argument("--only", choices=["gemm", "gemv", "copy", "c5chain", "tiles16", "c4"], default=None,
                     help="run one leg only (profiler runs); prints that leg's numbers")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -959,6 +970,10 @@ def main():
         del a, w
         t16 = bench_tiles16(torch, b1, synth, args.steps, args.warmup)
         print(json.dumps({"tiles16": t16, "sclk_mhz": sclk}), flush=True)
+        return
+    if args.only == "c4":
+        c4 = bench_c4_mlp(torch, b1, synth, reps=max(4, args.steps // 10))
+        print(json.dumps({"c4": c4}), flush=True)
         return
     if args.only == "c5chain":
         ch = bench_c5_block_chain(torch, b1, synth, producer_form=True)
