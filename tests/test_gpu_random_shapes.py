@@ -1,0 +1,126 @@
+"""Seeded random shapes through the fp32 entry point in every mode, and
+through its gate-residual epilogue, against the CPU oracle.
+
+Bars (those of tests/test_gpu_parity.py and tests/test_gpu_epilogue.py):
+  EXACT mode    : bit-identical to the oracle's scalar path
+                  (src/b1_0_kernel.h:240-287).
+  FAST modes    : auto, gemm and gemv against the oracle's AVX2 path
+                  (src/b1_0_kernel.h:79-239): per element
+                  |y - ref| / max(|ref|, rms(ref)) <= 1e-2, cosine >= 0.9999.
+  gate-residual : bit for bit numpy's float32 residual + gate * y, y the
+                  library's own linear in the same mode over a workspace
+                  that holds the packing only (the GEMM then runs unsplit
+                  along K, as the fused epilogue does).
+  Columns past out_dim keep their sentinel in every mode.
+The shapes are drawn so that every kernel choice of the library meets
+ragged edges: M from 1 to 1300 (the small-M kernels up to several rounds of
+tiles), K any multiple of 64 up to 4608 (K % 384 != 0 takes the
+fused-conversion GEMM, K % 256 != 0 the fallback small-M kernel), N from 1
+to 2600 (partial tiles, split-K and half-height tails where they apply),
+and padded row strides.
+"""
+import random
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL_REL = 1e-2
+TOL_COS = 0.9999
+EXACT_MAX_MACS = 5e8   # the scalar oracle's share of the test's time
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "GPU tests need the MI355X"
+    return t
+
+
+@pytest.fixture(scope="module")
+def b1(torch):
+    import bonsai_b1
+    bonsai_b1.load()
+    return bonsai_b1
+
+
+def _draw(count, seed):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        band = rng.choice(["small", "mid", "large"])
+        m = {"small": (1, 16), "mid": (17, 400), "large": (401, 1300)}[band]
+        m = rng.randint(*m)
+        k = 64 * rng.randint(1, 72)
+        n = rng.randint(1, 2600)
+        mode = rng.choice(["auto", "exact", "gemm"] + (["gemv"] if m <= 16 else []))
+        if mode == "exact" and m * k * n > EXACT_MAX_MACS:
+            mode = "auto"
+        lda = k + 4 * rng.randint(1, 8) if rng.random() < 0.3 else None
+        ldo = n + rng.randint(1, 16) if rng.random() < 0.3 else None
+        cases.append((m, k, n, mode, lda, ldo))
+    return cases
+
+
+CASES = _draw(40, 20261202)
+
+
+def _fast_close(y, ref):
+    ref = np.asarray(ref, np.float64)
+    y = np.asarray(y, np.float64)
+    den = np.maximum(np.abs(ref), np.sqrt(np.mean(ref * ref)))
+    rel = float(np.max(np.abs(y - ref) / den))
+    cos = float((y.ravel() @ ref.ravel()) / (np.linalg.norm(y) * np.linalg.norm(ref)))
+    return rel, cos
+
+
+@pytest.mark.parametrize("m,k,n,mode,lda,ldo", CASES)
+def test_random_shape(torch, b1, oracle, m, k, n, mode, lda, ldo):
+    from bonsai_b1 import synth
+    say(f"random shape ({m},{k},{n}) {mode} lda={lda} ldo={ldo}")
+    act = synth.activations(m, k, m + 7 * k + 13 * n)
+    raw = synth.packed_weights(n, k, m + k + n)
+    if lda is None:
+        a = torch.from_numpy(act).cuda()
+    else:
+        a = torch.zeros((m, lda), dtype=torch.float32)
+        a[:, :k] = torch.from_numpy(act)
+        a = a.cuda()[:, :k]
+    w = torch.from_numpy(raw.ravel()).cuda()
+    out = torch.full((m, ldo if ldo else n), 7.0, device="cuda")
+    b1.linear(a, w, n, out=out[:, :n], mode=mode)
+    torch.cuda.synchronize()
+    y = out.cpu().numpy()
+    if ldo:
+        assert np.all(y[:, n:] == 7.0), "columns past out_dim untouched"
+    y = y[:, :n]
+    if mode == "exact":
+        ref, _ = oracle.linear(act, raw, n, variant="scalar", nth=16, nthreads=16)
+        say(f"  mismatching elements: {int((y.view(np.uint32) != ref.view(np.uint32)).sum())}")
+        assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    else:
+        ref, _ = oracle.linear(act, raw, n, variant="avx2", nth=16, nthreads=16)
+        rel, cos = _fast_close(y, ref)
+        say(f"  rel_to_rms={rel:.3e} cos={cos:.8f}")
+        assert rel <= TOL_REL and cos >= TOL_COS
+
+    # the gate-residual epilogue over the same linear
+    ws = torch.empty((m * k * 2 + 255) // 256 * 256 + (m * 4 + 255) // 256 * 256, dtype=torch.uint8,
+                     device="cuda")
+    yp = b1.linear(a, w, n, mode=mode, workspace=ws)
+    g = torch.from_numpy(synth.activations(1, n, n + 5)[0]).cuda()
+    pad = 3 if (m + n) % 2 else 0      # row stride of the residual: aligned or not
+    res = torch.from_numpy(synth.activations(m, n + pad, m + 11)).cuda()[:, :n]
+    got = b1.linear_epi(a, w, n, "gate_residual", gate=g, residual=res, mode=mode)
+    torch.cuda.synchronize()
+    want = res.cpu().numpy() + g.cpu().numpy()[None, :] * yp.cpu().numpy()   # float32 ops
+    got = got.cpu().numpy()
+    say(f"  gate-residual mismatching elements: {int((got.view(np.uint32) != want.view(np.uint32)).sum())}")
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
