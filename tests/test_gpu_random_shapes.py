@@ -124,3 +124,51 @@ def test_random_shape(torch, b1, oracle, m, k, n, mode, lda, ldo):
     got = got.cpu().numpy()
     say(f"  gate-residual mismatching elements: {int((got.view(np.uint32) != want.view(np.uint32)).sum())}")
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+SWIGLU_TOL = 1e-6   # silu through the device exp and divide, a few fp32 ulp
+
+
+def _draw_swiglu(count, seed):
+    """Shapes for the SwiGLU epilogue: out_dim a multiple of 64 (gates and
+    values, H = out_dim / 2 a multiple of 32)."""
+    rng = random.Random(seed)
+    cases = []
+    for m, k, _, mode, lda, _ in _draw(count, seed):
+        n = 64 * rng.randint(1, 40)
+        if mode == "exact" and m * k * n > EXACT_MAX_MACS:
+            mode = "auto"
+        cases.append((m, k, n, mode, lda))
+    return cases
+
+
+@pytest.mark.parametrize("m,k,n,mode,lda", _draw_swiglu(16, 7))
+def test_random_shape_swiglu(torch, b1, m, k, n, mode, lda):
+    """out[:, j] = silu(y[:, j]) * y[:, H + j] against that formula in
+    float64 on the library's own unsplit linear y, per element within
+    1e-6 of the result; columns past H untouched."""
+    from bonsai_b1 import synth
+    say(f"random SwiGLU ({m},{k},{n}) {mode} lda={lda}")
+    h = n // 2
+    act = synth.activations(m, k, 3 * m + k + n)
+    raw = synth.packed_weights(n, k, m + 5 * k + n)
+    if lda is None:
+        a = torch.from_numpy(act).cuda()
+    else:
+        a = torch.zeros((m, lda), dtype=torch.float32)
+        a[:, :k] = torch.from_numpy(act)
+        a = a.cuda()[:, :k]
+    w = torch.from_numpy(raw.ravel()).cuda()
+    ws = torch.empty((m * k * 2 + 255) // 256 * 256 + (m * 4 + 255) // 256 * 256, dtype=torch.uint8,
+                     device="cuda")
+    y = b1.linear(a, w, n, mode=mode, workspace=ws)
+    out = torch.full((m, h + 4), 7.0, device="cuda")
+    b1.linear_epi(a, w, n, "swiglu", out=out[:, :h], mode=mode)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert bool((got[:, h:] == 7.0).all()), "columns past H untouched"
+    yy = y.cpu().numpy().astype(np.float64)
+    ref = yy[:, :h] / (1.0 + np.exp(-yy[:, :h])) * yy[:, h:]
+    bad = np.abs(got[:, :h] - ref) > SWIGLU_TOL * np.maximum(np.abs(ref), 1e-30) + 1e-30
+    say(f"  {int(bad.sum())} elements beyond the bar")
+    assert not bad.any()
