@@ -172,3 +172,97 @@ def test_random_shape_swiglu(torch, b1, m, k, n, mode, lda):
     bad = np.abs(got[:, :h] - ref) > SWIGLU_TOL * np.maximum(np.abs(ref), 1e-30) + 1e-30
     say(f"  {int(bad.sum())} elements beyond the bar")
     assert not bad.any()
+
+
+def _batch_plan(seed):
+    """A random sequence of linears over a pool of three fp32 activation
+    matrices: some ops read a matrix that an earlier op of the same call
+    wrote rows of (the cached packing must not outlive that write), some
+    run back to back on one input with weights that are adjacent row
+    ranges of one buffer and outputs adjacent column ranges of one matrix
+    (q/k/v, run as one GEMM), small-M ops in a row on one input (grouped
+    into one launch), K a multiple of 64 (the packed GEMM, the
+    fused-conversion GEMM and the small-M kernels)."""
+    rng = random.Random(seed)
+    pool = []
+    for _ in range(3):
+        m = rng.choice([rng.randint(1, 16), rng.randint(17, 600)])
+        k = rng.choice([384 * rng.randint(1, 8), 64 * rng.randint(1, 48)])
+        pool.append((m, k))
+    ops = []      # (input, [widths], out): out ("fresh",) or ("pool", q)
+    last_in, last_written = None, None
+    for _ in range(rng.randint(3, 9)):
+        u = rng.random()
+        if last_written is not None and u < 0.4:
+            p = last_written            # read what an earlier op wrote
+        elif last_in is not None and u < 0.7:
+            p = last_in                 # the same input again (its packing reused)
+        else:
+            p = rng.randrange(3)
+        last_in = p
+        m, k = pool[p]
+        widths = [rng.randint(1, 1500)]
+        if rng.random() < 0.3:
+            widths = [rng.randint(1, 700) for _ in range(3)]          # q/k/v
+        elif m <= 16 and rng.random() < 0.5:
+            widths = [rng.randint(1, 2000) for _ in range(rng.randint(2, 4))]   # a grouped run
+        q = rng.randrange(3)
+        if len(widths) == 1 and q != p and pool[q][0] >= m and pool[q][1] >= widths[0] and rng.random() < 0.5:
+            ops.append((p, widths, ("pool", q)))
+            last_written = q
+        else:
+            ops.append((p, widths, ("fresh",)))
+    return pool, ops
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batch(torch, b1, seed):
+    """bonsai_b1_linear_batch over a random plan equals the same linears
+    issued one by one in the same order, bit for bit: every output, and the
+    pool matrices that ops wrote into."""
+    from bonsai_b1 import synth
+    pool, plan = _batch_plan(9000 + seed)
+    mode = "exact" if seed % 4 == 3 else "auto"
+    say(f"random batch seed={seed} mode={mode} pool={pool} ops={plan}")
+    base = [synth.device_activations(m, k, 900 + 10 * seed + i) for i, (m, k) in enumerate(pool)]
+    weights = []
+    for j, (p, widths, _) in enumerate(plan):
+        k = pool[p][1]
+        big = synth.device_packed_weights(sum(widths), k, 950 + 20 * seed + j)
+        weights.append(big.reshape(-1))     # rows of k / 32 * 6 bytes, sliced below
+
+    def run(batched):
+        mats = [x.clone() for x in base]
+        outs, ops = [], []
+        for (p, widths, dst), big in zip(plan, weights):
+            m, k = pool[p]
+            rs = k // 32 * 6
+            if dst[0] == "pool":
+                o = mats[dst[1]][:m, :widths[0]]
+                parts = [o]
+            else:
+                o = torch.full((m, sum(widths) + 5), 7.0, device="cuda")
+                outs.append(o)
+                parts, c = [], 0
+                for wd in widths:
+                    parts.append(o[:, c:c + wd])
+                    c += wd
+            r = 0
+            for wd, part in zip(widths, parts):
+                wv = big[r * rs:(r + wd) * rs]
+                if batched:
+                    ops.append((mats[p], b1.device_weights(wv, k, wd), part))
+                else:
+                    b1.linear(mats[p], wv, wd, out=part, mode=mode)
+                r += wd
+        if batched:
+            b1.linear_batch(ops, mode=mode)
+        torch.cuda.synchronize()
+        return mats, outs
+
+    mats_b, outs_b = run(True)
+    mats_s, outs_s = run(False)
+    for i, (x, y) in enumerate(zip(outs_b, outs_s)):
+        assert torch.equal(x, y), f"output {i}"
+    for i, (x, y) in enumerate(zip(mats_b, mats_s)):
+        assert torch.equal(x, y), f"pool matrix {i}"
