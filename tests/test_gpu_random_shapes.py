@@ -266,3 +266,41 @@ def test_random_batch(torch, b1, seed):
         assert torch.equal(x, y), f"output {i}"
     for i, (x, y) in enumerate(zip(mats_b, mats_s)):
         assert torch.equal(x, y), f"pool matrix {i}"
+
+
+def _draw_norm(count, seed):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        rows = rng.choice([rng.randint(1, 40), rng.randint(41, 3000)])
+        h = 32 * rng.choice([rng.randint(1, 96), rng.randint(97, 384), rng.randint(385, 640)])
+        pad = 4 * rng.randint(1, 8) if rng.random() < 0.4 else 0
+        cases.append((rows, h, pad))
+    return cases
+
+
+@pytest.mark.parametrize("rows,h,pad", _draw_norm(14, 31))
+def test_random_norm_mod(torch, b1, oracle, rows, h, pad):
+    """LayerNorm + modulation over random row counts and lengths (rows held
+    in registers up to 3072 and 12288 elements, read three times beyond),
+    row strides padded or not: the fp32 form bit for bit the oracle's
+    restatement of ggml_norm + modulation, the packed form its fp16
+    packing."""
+    say(f"random norm_mod rows={rows} h={h} pad={pad}")
+    rng = np.random.default_rng(rows * 7 + h)
+    x = (rng.standard_normal((rows, h + pad)) * 2 + 0.5).astype(np.float32)
+    x[rows // 2, :] = -0.625                      # a constant row: var = 0
+    sc = (rng.standard_normal(h) * 0.2).astype(np.float32)
+    sh = (rng.standard_normal(h) * 0.2).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()[:, :h]
+    scd, shd = torch.from_numpy(sc).cuda(), torch.from_numpy(sh).cuda()
+    y = b1.norm_mod(xd, scd, shd, eps=1e-6)
+    packed = b1.norm_mod(xd, scd, shd, eps=1e-6, packed=True)
+    torch.cuda.synchronize()
+    want = oracle.norm_mod(np.ascontiguousarray(x[:, :h]), sc, sh, eps=1e-6)
+    got = y.cpu().numpy()
+    nbad = int((got.view(np.uint32) != want.view(np.uint32)).sum())
+    say(f"  {nbad} mismatching")
+    assert nbad == 0
+    words = packed.cpu().numpy().view(np.uint32).reshape(rows, h // 2)
+    assert np.array_equal(words, oracle.pack_act_words(want))
