@@ -304,3 +304,29 @@ def test_random_norm_mod(torch, b1, oracle, rows, h, pad):
     assert nbad == 0
     words = packed.cpu().numpy().view(np.uint32).reshape(rows, h // 2)
     assert np.array_equal(words, oracle.pack_act_words(want))
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 16512, 640), (37, 24576, 520), (130, 16128, 700)])
+def test_long_rows(torch, b1, oracle, m, k, n):
+    """K past 16384 (the range-safe pack reads such rows twice instead of
+    holding them in registers) and K just below it (four waves a row, eight
+    units a lane), through the fp32 entry, one row scaled past the fp16
+    range (it is packed scaled down by a power of two, its outputs scaled
+    back): within the FAST bar of the oracle's AVX2 path, row by row."""
+    from bonsai_b1 import synth
+    say(f"long rows ({m},{k},{n})")
+    act = synth.activations(m, k, k + n)
+    act[m // 3] *= 1.0e5
+    raw = synth.packed_weights(n, k, m + n)
+    y = b1.linear(torch.from_numpy(act).cuda(), torch.from_numpy(raw.ravel()).cuda(), n)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    ref, _ = oracle.linear(act, raw, n, variant="avx2", nth=16, nthreads=16)
+    for r in (m // 3, (m // 3 + 1) % m):
+        rel, cos = _fast_close(y[r], ref[r])
+        say(f"  row {r}: rel_to_rms={rel:.3e} cos={cos:.8f}")
+        assert rel <= TOL_REL and cos >= TOL_COS
+    keep = np.arange(m) != m // 3
+    rel, cos = _fast_close(y[keep], ref[keep])
+    say(f"  other rows: rel_to_rms={rel:.3e} cos={cos:.8f}")
+    assert rel <= TOL_REL and cos >= TOL_COS
