@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <list>
 #include <mutex>
 #include <utility>
@@ -27,14 +28,19 @@ constexpr int kMaxDevices = 64;
 
 constexpr int kWsFree = 8; // unpinned workspaces kept per device (about one per stream)
 
-// A library-owned workspace of one stream.  `pins`: handed out while the
-// stream was being captured, so a graph may hold its address; a pinned
-// buffer is never freed or evicted (growing allocates a new one), only
-// bonsai_b1_release_workspaces frees it.  `users`: entry-point calls that
-// hold it between the hand-out and their last launch; never evicted then
-// (another thread may not free it under a call that has not launched yet).
+// A library-owned workspace of one stream.  `owner`: 0, or for the
+// per-thread default stream (hipStreamPerThread, one handle value that names
+// a different stream in every thread) the calling thread's id, so that two
+// threads never share a buffer their streams do not order.  `pins`: handed
+// out while the stream was being captured, so a graph may hold its address;
+// a pinned buffer is never freed or evicted (growing allocates a new one),
+// only bonsai_b1_release_workspaces frees it.  `users`: entry-point calls
+// that hold it between the hand-out and their last launch; never evicted
+// then (another thread may not free it under a call that has not launched
+// yet).
 struct Workspace {
     hipStream_t stream = nullptr;
+    uint64_t owner = 0;
     void *ptr = nullptr;
     size_t bytes = 0;
     uint64_t last_use = 0;
@@ -121,6 +127,16 @@ class WsLease {
     Workspace *w_ = nullptr;
 };
 
+// The workspace owner of a stream handle: the calling thread's id (from 1,
+// never reused) for hipStreamPerThread, 0 for every other handle.
+std::atomic<uint64_t> g_next_thread_id{0};
+uint64_t stream_owner(hipStream_t stream) {
+    if (stream != hipStreamPerThread) return 0;
+    thread_local uint64_t id = 0;
+    if (!id) id = g_next_thread_id.fetch_add(1) + 1;
+    return id;
+}
+
 // Hands out this stream's most recently used buffer of at least `need`
 // bytes (pinning it when the stream is being captured), or, outside a
 // capture, a new one.  A new buffer takes the place of an unpinned buffer
@@ -131,10 +147,12 @@ void WsLease::acquire(DeviceInfo *d, hipStream_t stream, size_t need) {
     drop();
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     const bool capturing = hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+    const uint64_t owner = stream_owner(stream);
     std::lock_guard<std::mutex> lk(g_mu);
     Workspace *hit = nullptr;
     for (Workspace &w : d->ws)
-        if (w.stream == stream && w.bytes >= need && (!hit || w.last_use > hit->last_use)) hit = &w;
+        if (w.stream == stream && w.owner == owner && w.bytes >= need && (!hit || w.last_use > hit->last_use))
+            hit = &w;
     if (hit) {
         hit->last_use = ++d->tick;
         ++hit->users;
@@ -149,7 +167,7 @@ void WsLease::acquire(DeviceInfo *d, hipStream_t stream, size_t need) {
         if (w.pins) continue;
         ++unpinned;
         if (w.users) continue;
-        if (w.stream == stream) own = &w;
+        if (w.stream == stream && w.owner == owner) own = &w;
         if (!lru || w.last_use < lru->last_use) lru = &w;
     }
     Workspace *slot = own ? own : unpinned >= kWsFree ? lru : nullptr;
@@ -169,6 +187,7 @@ void WsLease::acquire(DeviceInfo *d, hipStream_t stream, size_t need) {
         slot = &d->ws.back();
     }
     slot->stream = stream;
+    slot->owner = owner;
     slot->ptr = p;
     slot->bytes = bytes;
     slot->last_use = ++d->tick;

@@ -118,7 +118,9 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
  * bonsai_b1_workspace_bytes(batch, in_dim, out_dim, mode) bytes (0 when the
  * call needs none: EXACT, and small batches, whose kernel converts the
  * activations itself).  bonsai_b1_linear_f32 keeps library-owned workspaces
- * per (device, stream), grown on demand with hipMalloc; while a stream is
+ * per (device, stream) -- per calling thread for hipStreamPerThread, whose
+ * one handle value names each thread's own stream -- grown on demand with
+ * hipMalloc; while a stream is
  * being captured it never allocates and, lacking a large enough buffer,
  * runs the kernel variant that converts activations tile by tile.  A buffer
  * handed out during a capture is pinned, since the graph holds its address:

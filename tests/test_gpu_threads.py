@@ -10,7 +10,11 @@ buffers are replaced and evicted while other threads' calls are in flight.
 Bar: every output equals the same call made alone on one stream
 beforehand, bit for bit (same kernels, same split along K).
 The per-thread non-finite counter of the deferred callback is checked the
-same way: each thread's count is its own.
+same way: each thread's count is its own.  The callback queues on
+hipStreamPerThread, one handle value that names each thread's own stream:
+its workspace must be kept per calling thread, or one thread's GEMM reads
+another's packing (both tests below fail on a library that keyed it by the
+handle alone).
 """
 import sys
 import threading
@@ -94,12 +98,12 @@ def test_concurrent_callers_on_own_streams(torch, b1):
 
 def test_concurrent_deferred_callbacks(torch, b1):
     """Each thread defers its callback checks (the callback then enqueues on
-    the thread's own stream, hipStreamPerThread), runs two ops whose inputs
-    hold t + 1 tokens with a NaN, and reads back exactly its own count: 2 (t
+    the thread's own stream, hipStreamPerThread), runs three ops whose inputs
+    hold t + 1 tokens with a NaN, and reads back exactly its own count: 3 (t
     + 1) out_dim; the outputs equal the library's AUTO linear."""
     import ctypes
     from bonsai_b1 import capi, synth
-    k, n, m = 768, 256, 48
+    k, n, m = 3072, 1024, 600
     W = b1.Weights(synth.packed_weights(n, k, 4001), k, n)
     acts = []
     for t in range(THREADS):
@@ -132,7 +136,7 @@ def test_concurrent_deferred_callbacks(torch, b1):
         return td
 
     counts = [None] * THREADS
-    outs = [[torch.full((m, n), 7.0, device="cuda") for _ in range(2)] for _ in range(THREADS)]
+    outs = [[torch.full((m, n), 7.0, device="cuda") for _ in range(3)] for _ in range(THREADS)]
     torch.cuda.synchronize()
 
     def work(t):
@@ -150,9 +154,39 @@ def test_concurrent_deferred_callbacks(torch, b1):
     _run_threads(work)
     torch.cuda.synchronize()
     for t in range(THREADS):
-        assert counts[t] == (capi.ERR_NONFINITE, 2 * (t + 1) * n), (t, counts[t])
+        assert counts[t] == (capi.ERR_NONFINITE, 3 * (t + 1) * n), (t, counts[t])
         for o in outs[t]:
             assert torch.equal(o.isnan(), refs[t].isnan()), t
             keep = ~refs[t].isnan()
             assert torch.equal(o[keep], refs[t][keep]), t
     W.free()
+
+
+def test_per_thread_default_stream(torch, b1):
+    """hipStreamPerThread, one handle value naming a different stream in
+    each thread, passed to the fp32 entry by ten threads at once, four calls
+    each with no synchronisation between them (each call packs its input
+    into the library's workspace and splits the GEMM along K into partials
+    there): every output bit for bit the same call made alone.  The library
+    keeps such a stream's workspace per calling thread; shared by handle
+    value, one thread's packing would be read by another's GEMM."""
+    from bonsai_b1 import capi, synth
+    m, k, n = 1024, 3072, 2048
+    per_thread_stream = 2          # hipStreamPerThread
+    w = synth.device_packed_weights(n, k, 4201)
+    acts = [synth.device_activations(m, k, 4210 + t) for t in range(THREADS)]
+    refs = [b1.linear(a, w, n) for a in acts]
+    outs = [[torch.full((m, n), 7.0, device="cuda") for _ in range(4)] for _ in range(THREADS)]
+    torch.cuda.synchronize()
+
+    def work(t):
+        for o in outs[t]:
+            st = capi.linear_raw(acts[t].data_ptr(), k, w.data_ptr(), k, n, m, o.data_ptr(), n, "auto", 0,
+                                 per_thread_stream)
+            assert st == capi.OK, st
+
+    _run_threads(work)
+    torch.cuda.synchronize()
+    for t in range(THREADS):
+        for i, o in enumerate(outs[t]):
+            assert torch.equal(o, refs[t]), f"thread {t} call {i}"
