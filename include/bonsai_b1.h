@@ -133,7 +133,9 @@ int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
  * unsplit (the same values up to the order of the K summation), and (b) for
  * rows beyond the fp16 range, which the converting variant computes in
  * EXACT arithmetic.  Concurrent calls on one stream are ordered; calls on
- * different streams use different workspaces.
+ * different streams use different workspaces.  A workspace is found by the
+ * stream's handle, so synchronize a stream before destroying it while calls
+ * on it may still run: a stream created later can get the same handle.
  */
 size_t bonsai_b1_workspace_bytes(int batch, int in_dim, int out_dim, int mode);
 
