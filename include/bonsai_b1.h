@@ -103,7 +103,10 @@ enum {
  *   nonfinite  optional device int32 counter; every non-finite output adds 1
  *            (NULL: not counted).  Replaces the reference's abort().
  * Preconditions checked on the host: in_dim % 32 == 0, in_dim, out_dim > 0,
- * batch >= 0, lda >= in_dim, ldo >= out_dim, non-NULL pointers.
+ * batch >= 0, lda >= in_dim, ldo >= out_dim, non-NULL pointers.  Not
+ * checked (as in the reference, whose graph never aliases them): out must
+ * not overlap act or w; the small-M and EXACT kernels read act while other
+ * work-groups write out.
  * Returns BONSAI_B1_OK or an error code; never blocks the host.
  */
 int bonsai_b1_linear_f32(const float *act, int64_t lda, const void *w,
