@@ -330,3 +330,38 @@ def test_long_rows(torch, b1, oracle, m, k, n):
     rel, cos = _fast_close(y[keep], ref[keep])
     say(f"  other rows: rel_to_rms={rel:.3e} cos={cos:.8f}")
     assert rel <= TOL_REL and cos >= TOL_COS
+
+
+def _draw_producers(count, seed):
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        m = rng.choice([rng.randint(1, 40), rng.randint(41, 3000)])
+        k1 = 32 * rng.randint(1, 128)
+        k2 = 32 * rng.randint(1, 256)
+        spad = 4 * rng.randint(0, 8)            # source row padding (16-byte rows)
+        dpad = 32 * rng.randint(0, 3)           # packed row padding
+        cases.append((m, k1, k2, spad, dpad))
+    return cases
+
+
+@pytest.mark.parametrize("m,k1,k2,spad,dpad", _draw_producers(12, 77))
+def test_random_column_range_producers(torch, b1, m, k1, k2, spad, dpad):
+    """The plain pack and the GELU pack writing adjacent column ranges of one
+    packed matrix (row length k1 + k2 + dpad fp16 elements) from sources with
+    padded rows: the range equals the packing of the fp32 concatenation
+    [a1 | gelu_tanh(a2)] bit for bit, and the row padding keeps its
+    sentinel."""
+    from bonsai_b1 import synth
+    say(f"random producers m={m} k1={k1} k2={k2} spad={spad} dpad={dpad}")
+    a1 = synth.device_activations(m, k1 + spad, 5100 + m)[:, :k1]
+    a2 = synth.device_activations(m, k2 + spad, 5200 + m)[:, :k2]
+    ldp = k1 + k2 + dpad
+    buf = torch.full((m * ldp * 2,), 0xAB, dtype=torch.uint8, device="cuda")
+    b1.pack_act_f16(a1, packed=buf, ldp=ldp)
+    b1.gelu_tanh_pack_f16(a2, packed=buf[k1 * 2:], ldp=ldp)
+    want = b1.pack_act_f16(torch.cat([a1, b1.gelu_tanh(a2.contiguous())], 1))
+    torch.cuda.synchronize()
+    rows = buf.view(m, ldp * 2)
+    assert torch.equal(rows[:, :(k1 + k2) * 2], want.view(m, (k1 + k2) * 2))
+    assert bool((rows[:, (k1 + k2) * 2:] == 0xAB).all()), "row padding untouched"
