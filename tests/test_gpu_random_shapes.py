@@ -365,3 +365,29 @@ def test_random_column_range_producers(torch, b1, m, k1, k2, spad, dpad):
     rows = buf.view(m, ldp * 2)
     assert torch.equal(rows[:, :(k1 + k2) * 2], want.view(m, (k1 + k2) * 2))
     assert bool((rows[:, (k1 + k2) * 2:] == 0xAB).all()), "row padding untouched"
+
+
+def _draw_packed(count, seed):
+    rng = random.Random(seed)
+    return [(rng.choice([rng.randint(1, 16), rng.randint(17, 1300)]), 384 * rng.randint(1, 12),
+             rng.randint(1, 2600)) for _ in range(count)]
+
+
+@pytest.mark.parametrize("m,k,n", _draw_packed(16, 55))
+def test_random_packed_entry(torch, b1, m, k, n):
+    """bonsai_b1_linear_packed_f16 over pack_act_f16 of the activations gives
+    the fp32 entry's outputs bit for bit: its FAST mode (M > 16 or K % 256
+    == 0, the small-M kernel at M <= 16) or its GEMM mode (M <= 16 with K %
+    256 != 0, where the packed entry keeps the GEMM tile), split along K
+    alike."""
+    from bonsai_b1 import synth
+    mode = "auto" if (m > 16 or k % 256 == 0) else "gemm"
+    say(f"random packed entry ({m},{k},{n}) vs fp32 {mode}")
+    a = synth.device_activations(m, k, 5300 + m)
+    w = synth.device_packed_weights(n, k, 5400 + n)
+    ref = b1.linear(a, w, n, mode=mode)
+    out = torch.full((m, n + 3), 7.0, device="cuda")
+    b1.linear_packed_f16(b1.pack_act_f16(a), w, k, n, m, out=out[:, :n])
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :n], ref)
+    assert bool((out[:, n:] == 7.0).all()), "columns past out_dim untouched"
