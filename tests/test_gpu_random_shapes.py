@@ -391,3 +391,27 @@ def test_random_packed_entry(torch, b1, m, k, n):
     torch.cuda.synchronize()
     assert torch.equal(out[:, :n], ref)
     assert bool((out[:, n:] == 7.0).all()), "columns past out_dim untouched"
+
+
+@pytest.mark.parametrize("m", [1, 8, 24])
+def test_weights_past_2gib(torch, b1, oracle, m):
+    """3.8 M weight rows at K = 3072: 2.19 GB of packed weights, past the
+    31-bit range of a buffer resource.  M <= 16 then takes the small-M
+    fallback kernel (64-bit addressing, no LDS staging), M = 24 the packed
+    GEMM (32-bit weight offsets, below 4 GiB): within the FAST bar of the
+    oracle's AVX2 path."""
+    from bonsai_b1 import synth
+    k, n = 3072, 3_800_000
+    say(f"weights past 2 GiB m={m} n={n}")
+    act = synth.activations(m, k, 5500 + m)
+    w = synth.device_packed_weights(n, k, 5501)
+    assert w.numel() > 2 ** 31
+    y = b1.linear(torch.from_numpy(act).cuda(), w, n)
+    torch.cuda.synchronize()
+    raw = w.cpu().numpy()
+    del w
+    torch.cuda.empty_cache()
+    ref, _ = oracle.linear(act, raw, n, variant="avx2", nth=16, nthreads=16)
+    rel, cos = _fast_close(y.cpu().numpy(), ref)
+    say(f"  rel_to_rms={rel:.3e} cos={cos:.8f}")
+    assert rel <= TOL_REL and cos >= TOL_COS
