@@ -415,3 +415,33 @@ def test_weights_past_2gib(torch, b1, oracle, m):
     rel, cos = _fast_close(y.cpu().numpy(), ref)
     say(f"  rel_to_rms={rel:.3e} cos={cos:.8f}")
     assert rel <= TOL_REL and cos >= TOL_COS
+
+
+def test_activations_past_2gib(torch, b1, oracle):
+    """180,000 tokens at K = 3072: 2.21 GB of fp32 activations (the
+    range-safe pack reads them with 64-bit offsets; the packing, 1.1 GB,
+    stays within the GEMM's 32-bit offsets), within the FAST bar of the
+    oracle's AVX2 path; one token scaled past the fp16 range."""
+    from bonsai_b1 import synth
+    m, k, n = 180_000, 3072, 512
+    say(f"activations past 2 GiB m={m}")
+    act = synth.activations(m, k, 5600)
+    act[m - 7] *= 1.0e5
+    assert act.nbytes > 2 ** 31
+    raw = synth.packed_weights(n, k, 5601)
+    a = torch.from_numpy(act).cuda()
+    y = b1.linear(a, torch.from_numpy(raw.ravel()).cuda(), n)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    del a
+    torch.cuda.empty_cache()
+    ref, _ = oracle.linear(act, raw, n, variant="avx2", nth=16, nthreads=16)
+    # the scaled token against its own row (its outputs are 1e5 times the
+    # others'), the other tokens together
+    keep = np.arange(m) != m - 7
+    rel, cos = _fast_close(y[keep], ref[keep])
+    say(f"  other tokens: rel_to_rms={rel:.3e} cos={cos:.8f}")
+    assert rel <= TOL_REL and cos >= TOL_COS
+    rel, cos = _fast_close(y[m - 7], ref[m - 7])
+    say(f"  scaled token: rel_to_rms={rel:.3e} cos={cos:.8f}")
+    assert rel <= TOL_REL and cos >= TOL_COS
