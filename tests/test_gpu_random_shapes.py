@@ -393,15 +393,16 @@ def test_random_packed_entry(torch, b1, m, k, n):
     assert bool((out[:, n:] == 7.0).all()), "columns past out_dim untouched"
 
 
-@pytest.mark.parametrize("m", [1, 8, 24])
-def test_weights_past_2gib(torch, b1, oracle, m):
+@pytest.mark.parametrize("m,n", [(1, 3_800_000), (8, 3_800_000), (24, 3_800_000), (24, 7_600_000)])
+def test_weights_past_2gib(torch, b1, oracle, m, n):
     """3.8 M weight rows at K = 3072: 2.19 GB of packed weights, past the
     31-bit range of a buffer resource.  M <= 16 then takes the small-M
     fallback kernel (64-bit addressing, no LDS staging), M = 24 the packed
-    GEMM (32-bit weight offsets, below 4 GiB): within the FAST bar of the
-    oracle's AVX2 path."""
+    GEMM (32-bit weight offsets, below 4 GiB); 7.6 M rows (4.38 GB, past 32
+    bits) take the GEMM that converts its activations tile by tile (64-bit
+    addressing): within the FAST bar of the oracle's AVX2 path."""
     from bonsai_b1 import synth
-    k, n = 3072, 3_800_000
+    k = 3072
     say(f"weights past 2 GiB m={m} n={n}")
     act = synth.activations(m, k, 5500 + m)
     w = synth.device_packed_weights(n, k, 5501)
