@@ -446,3 +446,56 @@ def test_activations_past_2gib(torch, b1, oracle):
     rel, cos = _fast_close(y[m - 7], ref[m - 7])
     say(f"  scaled token: rel_to_rms={rel:.3e} cos={cos:.8f}")
     assert rel <= TOL_REL and cos >= TOL_COS
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_batch_epilogues(torch, b1, seed):
+    """bonsai_b1_linear_batch_epi over a random sequence of plain,
+    gate-residual and SwiGLU linears on two inputs (the packed GEMM, the
+    small-M kernel or EXACT mode by shape and mode) equals the same linears
+    issued one by one through the fp32 and epilogue entries, bit for bit."""
+    from bonsai_b1 import synth
+    rng = random.Random(9500 + seed)
+    mode = "exact" if seed % 4 == 3 else "auto"
+    inputs = []
+    for i in range(2):
+        m = rng.choice([rng.randint(1, 16), rng.randint(17, 700)])
+        k = 384 * rng.randint(1, 8)
+        inputs.append(synth.device_activations(m, k, 9600 + 10 * seed + i))
+    plan = []
+    for j in range(rng.randint(3, 8)):
+        p = rng.randrange(2)
+        kind = rng.choice(["none", "gate_residual", "swiglu"])
+        n = 64 * rng.randint(1, 24) if kind == "swiglu" else rng.randint(1, 1500)
+        plan.append((p, kind, n))
+    say(f"random batch with epilogues seed={seed} mode={mode} "
+        f"inputs={[tuple(x.shape) for x in inputs]} plan={plan}")
+    ops, singles = [], []
+    for j, (p, kind, n) in enumerate(plan):
+        a = inputs[p]
+        m, k = a.shape
+        w = synth.device_packed_weights(n, k, 9700 + 20 * seed + j)
+        cols = n // 2 if kind == "swiglu" else n
+        out = torch.full((m, cols + 3), 7.0, device="cuda")[:, :cols]
+        ref = torch.full((m, cols + 3), 7.0, device="cuda")[:, :cols]
+        if kind == "gate_residual":
+            g = synth.device_activations(1, n, 9800 + j)[0]
+            r = synth.device_activations(m, n, 9900 + j)
+            ops.append((a, b1.device_weights(w, k, n), out, ("gate_residual", g, r)))
+            singles.append(lambda a=a, w=w, n=n, g=g, r=r, ref=ref:
+                           b1.linear_epi(a, w, n, "gate_residual", gate=g, residual=r, out=ref, mode=mode))
+        elif kind == "swiglu":
+            ops.append((a, b1.device_weights(w, k, n), out, "swiglu"))
+            singles.append(lambda a=a, w=w, n=n, ref=ref: b1.linear_epi(a, w, n, "swiglu", out=ref, mode=mode))
+        else:
+            ops.append((a, b1.device_weights(w, k, n), out))
+            singles.append(lambda a=a, w=w, n=n, ref=ref: b1.linear(a, w, n, out=ref, mode=mode))
+        plan[j] = (out, ref, w)
+    b1.linear_batch(ops, mode=mode)
+    for f in singles:
+        f()
+    torch.cuda.synchronize()
+    for j, (out, ref, _) in enumerate(plan):
+        full_o = out.as_strided((out.shape[0], out.shape[1] + 3), out.stride())
+        full_r = ref.as_strided((ref.shape[0], ref.shape[1] + 3), ref.stride())
+        assert torch.equal(full_o, full_r), f"op {j}"
