@@ -499,3 +499,28 @@ def test_random_batch_epilogues(torch, b1, seed):
         full_o = out.as_strided((out.shape[0], out.shape[1] + 3), out.stride())
         full_r = ref.as_strided((ref.shape[0], ref.shape[1] + 3), ref.stride())
         assert torch.equal(full_o, full_r), f"op {j}"
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_quantize(torch, b1, oracle, seed):
+    """The GPU writer over random shapes and magnitudes (per-row scales from
+    1e-30 to 1e30, so fp16 scales that round to 0, to subnormals and to
+    inf, blocks of one repeated magnitude, signed zeros): both reference
+    writers' bytes (numpy's mean order and the left-to-right order), bit for
+    bit."""
+    rng = np.random.default_rng(9900 + seed)
+    n = int(rng.integers(1, 2000))
+    k = 32 * int(rng.integers(1, 200))
+    say(f"random quantize seed={seed} n={n} k={k}")
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    w *= (10.0 ** rng.uniform(-30, 30, (n, 1))).astype(np.float32)
+    w[n // 2, :32] = np.float32(0.375) * np.sign(rng.standard_normal(32)).astype(np.float32)
+    w[n // 3, :32] = -0.0
+    dw = torch.from_numpy(w).cuda()
+    for order in ("numpy", "sequential"):
+        got = b1.quantize_f32(dw, order=order)
+        torch.cuda.synchronize()
+        want = oracle.pack(w, order=order)
+        nbad = int((got.cpu().numpy() != want).sum())
+        say(f"  {order}: {nbad} differing bytes")
+        assert nbad == 0
