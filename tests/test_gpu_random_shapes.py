@@ -524,3 +524,35 @@ def test_random_quantize(torch, b1, oracle, seed):
         nbad = int((got.cpu().numpy() != want).sum())
         say(f"  {order}: {nbad} differing bytes")
         assert nbad == 0
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_gelu(torch, b1, seed):
+    """GELU-tanh over random shapes (up to 3000 x 12000; the non-temporal
+    form past 128 MB is checked at the C4 size in test_gpu_parity.py),
+    padded row strides, out of place and in place: within 1e-6 max(1, |x|)
+    of the float64 function, in place equal to out of place bit for bit,
+    row padding untouched."""
+    from oracle import b1_oracle
+    rng = np.random.default_rng(9950 + seed)
+    rows = int(rng.choice([rng.integers(1, 64), rng.integers(64, 3000)]))
+    cols = 4 * int(rng.integers(1, 3000))
+    px, py = 4 * int(rng.integers(0, 4)), 4 * int(rng.integers(0, 4))
+    say(f"random GELU seed={seed} rows={rows} cols={cols} pads={px},{py}")
+    x = (rng.standard_normal((rows, cols + px)) * 3).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()[:, :cols]
+    yd = torch.full((rows, cols + py), 7.0, device="cuda")
+    b1.gelu_tanh(xd, out=yd[:, :cols])
+    inplace = torch.from_numpy(x).cuda()
+    b1.gelu_tanh(inplace[:, :cols], out=inplace[:, :cols])
+    torch.cuda.synchronize()
+    y = yd.cpu().numpy()
+    assert bool((y[:, cols:] == 7.0).all()), "row padding untouched"
+    y = y[:, :cols]
+    ref = b1_oracle.gelu_tanh_f64(x[:, :cols].astype(np.float64))
+    err = float(np.max(np.abs(y - ref) / np.maximum(1.0, np.abs(x[:, :cols]))))
+    say(f"  max err {err:.3e}")
+    assert err <= 1e-6
+    ip = inplace.cpu().numpy()
+    assert np.array_equal(ip[:, :cols].view(np.uint32), y.view(np.uint32))
+    assert np.array_equal(ip[:, cols:], x[:, cols:]), "padding of the in-place rows untouched"
