@@ -285,7 +285,7 @@ static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim,
     hipError_t e;
     switch (mode) {
     case BONSAI_B1_MODE_EXACT:
-        e = b1::launch_exact(a, stream);
+        e = b1::launch_exact(a, dev->num_cus, stream);
         break;
     case BONSAI_B1_MODE_GEMM:
         if (!b1::gemm_supported(a)) return BONSAI_B1_ERR_ARG;
@@ -301,7 +301,7 @@ static int linear_impl(const float *act, int64_t lda, const void *w, int in_dim,
         else if (b1::gemm_supported(a))
             e = gemm();
         else
-            e = b1::launch_exact(a, stream); // unaligned / K % 64 != 0
+            e = b1::launch_exact(a, dev->num_cus, stream); // unaligned / K % 64 != 0
         break;
     }
     return e == hipSuccess ? BONSAI_B1_OK : BONSAI_B1_ERR_HIP;
@@ -1132,7 +1132,7 @@ static int batch_run(int n_ops, int mode, int32_t *nonfinite, void *workspace, s
             }
             if (e == hipSuccess) {
                 switch (path) {
-                case BatchPath::Exact: e = b1::launch_exact(la, stream); break;
+                case BatchPath::Exact: e = b1::launch_exact(la, dev->num_cus, stream); break;
                 case BatchPath::Gemv: e = b1::launch_gemv(la, dev->num_cus, stream); break;
                 default: e = b1::launch_gemm(la, dev->num_cus, nullptr, 0, stream); break;
                 }

@@ -41,7 +41,7 @@ struct LinearArgs {
 };
 
 // fp32 VALU kernel in the reference scalar order; any K % 32 == 0.
-hipError_t launch_exact(const LinearArgs &a, hipStream_t s);
+hipError_t launch_exact(const LinearArgs &a, int num_cus, hipStream_t s);
 
 // fp16 MFMA GEMM; requires K % 64 == 0, lda % 4 == 0, act 16-byte aligned.
 // With a workspace of gemm_workspace_bytes(a) bytes (> 0 when K % 384 == 0)

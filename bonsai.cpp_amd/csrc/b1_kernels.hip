@@ -234,25 +234,35 @@ __device__ __forceinline__ void count_nonfinite(int32_t *ctr, int bad) {
 // ---------------------------------------------------------------- exact --
 
 constexpr int kExTN = 256; // output columns per work-group (one per thread)
-constexpr int kExTM = 4;   // output rows per work-group
 constexpr int kExKC = 256; // K staged in LDS per pass
 
+// EXACT mode: every output in the reference's scalar order
+// (src/b1_0_kernel.h:253-277): block_sum takes +-a over the block's 32
+// elements in order, then sum += scale * block_sum (an fp32 multiply and
+// an fp32 add, no contraction).  Each +-a step is fma(a, s, block_sum) with
+// s = +-1.0: the product is exact, so the fma rounds once, exactly as the
+// add or the subtract does, to the same value (signed zeros included; a
+// NaN may carry another payload).  The 32 signs of a block are formed once
+// (a shift and a bit op each) for the work-group's TM rows, which share
+// them: about 1 + 2 / TM VALU operations per multiply-accumulate, where a
+// select between a and -a and an add made 2 + 2 / TM.
+template <int TM>
 __global__ __launch_bounds__(kExTN) void b1_exact_kernel(LinearArgs p) {
 #pragma clang fp contract(off)
-    __shared__ float As[kExTM][kExKC];
+    __shared__ __attribute__((aligned(16))) float As[TM][kExKC];
     const int n = blockIdx.x * kExTN + threadIdx.x;
-    const int m0 = blockIdx.y * kExTM;
+    const int m0 = blockIdx.y * TM;
     const int nb = p.K / 32;
     const int nrow = n < p.N ? n : p.N - 1;
     const uint16_t *wr = reinterpret_cast<const uint16_t *>(p.w + (size_t)nrow * nb * 6);
-    float sum[kExTM];
+    float sum[TM];
 #pragma unroll
-    for (int r = 0; r < kExTM; ++r) sum[r] = 0.0f;
+    for (int r = 0; r < TM; ++r) sum[r] = 0.0f;
 
     for (int kc = 0; kc < p.K; kc += kExKC) {
         const int klen = min(kExKC, p.K - kc);
         __syncthreads();
-        for (int i = threadIdx.x; i < kExTM * kExKC; i += kExTN) {
+        for (int i = threadIdx.x; i < TM * kExKC; i += kExTN) {
             const int r = i / kExKC, c = i - r * kExKC;
             As[r][c] = (m0 + r < p.M && c < klen)
                            ? p.act[(size_t)(m0 + r) * p.lda + kc + c]
@@ -264,22 +274,33 @@ __global__ __launch_bounds__(kExTN) void b1_exact_kernel(LinearArgs p) {
             const uint16_t *blk = wr + (size_t)(kc / 32 + b) * 3;
             const float scale = (float)__builtin_bit_cast(_Float16, blk[0]);
             const uint32_t bits = (uint32_t)blk[1] | ((uint32_t)blk[2] << 16);
+            float bs[TM];
 #pragma unroll
-            for (int r = 0; r < kExTM; ++r) {
-                float bs = 0.0f;
+            for (int r = 0; r < TM; ++r) bs[r] = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    const float a = As[r][b * 32 + i];
-                    bs = ((bits >> i) & 1u) ? bs + a : bs - a;
+            for (int i4 = 0; i4 < 8; ++i4) {
+                // +1.0 for a set bit, -1.0 for a clear one
+                float sg[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 4 * i4 + j;
+                    sg[j] = __builtin_bit_cast(float, ((bits << (31 - i)) & 0x80000000u) ^ 0xBF800000u);
                 }
-                sum[r] = sum[r] + scale * bs;
+#pragma unroll
+                for (int r = 0; r < TM; ++r) {
+                    const floatx4 a = *reinterpret_cast<const floatx4 *>(&As[r][b * 32 + 4 * i4]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) bs[r] = __builtin_fmaf(a[j], sg[j], bs[r]);
+                }
             }
+#pragma unroll
+            for (int r = 0; r < TM; ++r) sum[r] = sum[r] + scale * bs[r];
         }
     }
     if (n >= p.N) return;
     int bad = 0;
 #pragma unroll
-    for (int r = 0; r < kExTM; ++r) {
+    for (int r = 0; r < TM; ++r) {
         if (m0 + r < p.M) {
             bad += !__builtin_isfinite(sum[r]);
             p.out[(size_t)(m0 + r) * p.ldo + n] = sum[r];
@@ -3525,9 +3546,22 @@ __global__ __launch_bounds__(kGvWaves * 64, WL == kG4WL2 ? 4 : 2) void b1_gemv_g
 
 // ------------------------------------------------------------- launchers --
 
-hipError_t launch_exact(const LinearArgs &a, hipStream_t s) {
-    dim3 grid((a.N + kExTN - 1) / kExTN, (a.M + kExTM - 1) / kExTM);
-    hipLaunchKernelGGL(b1_exact_kernel, grid, dim3(kExTN), 0, s, a);
+hipError_t launch_exact(const LinearArgs &a, int num_cus, hipStream_t s) {
+    // rows a work-group shares its signs over: 16 or 8 while that leaves
+    // at least 4 work-groups (16 waves) a CU, else 4 (a small grid needs
+    // the work-groups more than the shared signs)
+    const int64_t cols = (a.N + kExTN - 1) / kExTN;
+    const int64_t want = 4 * (int64_t)(num_cus > 0 ? num_cus : 256);
+    auto go = [&](auto kernel, int tm) {
+        const dim3 grid((unsigned)cols, (unsigned)((a.M + tm - 1) / tm));
+        hipLaunchKernelGGL(kernel, grid, dim3(kExTN), 0, s, a);
+    };
+    if (a.M > 8 && cols * ((a.M + 15) / 16) >= want)
+        go(b1_exact_kernel<16>, 16);
+    else if (a.M > 4 && cols * ((a.M + 7) / 8) >= want)
+        go(b1_exact_kernel<8>, 8);
+    else
+        go(b1_exact_kernel<4>, 4);
     return hipGetLastError();
 }
 
