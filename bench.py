@@ -944,7 +944,7 @@ def main():
     ap.add_argument("--all", action="store_true", help="also time the secondary legs (stderr and JSON)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1/C3/C4/C5 config legs")
-    ap.add_argument("--only", choices=["gemm", "gemv", "copy", "c5chain", "tiles16", "c4"], default=None,
+    ap.add_argument("--only", choices=["gemm", "gemv", "copy", "c5chain", "tiles16", "c4", "exact"], default=None,
                     help="run one leg only (profiler runs); prints that leg's numbers")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -970,6 +970,9 @@ def main():
         del a, w
         t16 = bench_tiles16(torch, b1, synth, args.steps, args.warmup)
         print(json.dumps({"tiles16": t16, "sclk_mhz": sclk}), flush=True)
+        return
+    if args.only == "exact":
+        print(json.dumps({"exact": bench_exact(torch, b1, synth)}), flush=True)
         return
     if args.only == "c4":
         c4 = bench_c4_mlp(torch, b1, synth, reps=max(4, args.steps // 10))
